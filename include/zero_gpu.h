@@ -1,0 +1,222 @@
+/*
+ * zero_gpu.h -- C ABI of the MI355X (gfx950) quantized-matmul path.
+ *
+ * Drop-in for the decode-time matmul boundary of silicatetech/zero.  Every
+ * entry point names the reference interface it replaces (paths relative to
+ * the reference repository).  Plain pointers and sizes only; no C++ or torch
+ * types cross this boundary.  Status codes, never exceptions or aborts.
+ *
+ * Threading: one caller thread per context (the reference calls its
+ * dispatchers only from the BSP, kernel/src/smp.rs:1567-1712).  A context is
+ * not re-entrant.  Host-pointer calls are synchronous; *_dev calls are
+ * asynchronous on the stream given (NULL = the context's stream).
+ */
+#ifndef ZERO_GPU_H
+#define ZERO_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The reference returns Result enums and panics on an
+ * unsupported quant (crates/zero-llm-inference/src/ops.rs:486-523,
+ * kernel/src/inference_avx512.rs:1122-1184); here both are codes. */
+typedef int32_t zg_status;
+#define ZG_OK 0
+#define ZG_ERR_INVALID_ARG -1       /* null pointer, bad shape, bad interleave */
+#define ZG_ERR_UNSUPPORTED_QUANT -2 /* LinearDispatchError::UnsupportedQuant  */
+#define ZG_ERR_NOT_REGISTERED -3    /* weight pointer not uploaded            */
+#define ZG_ERR_HIP -4               /* HIP runtime error; see zg_last_error    */
+#define ZG_ERR_NONFINITE_LOGITS -5  /* LmHeadError::NonFiniteLogits (lm_head.rs:32-38) */
+#define ZG_ERR_ARGMAX_IN_PADDING -6 /* LmHeadError::ArgmaxInPaddingRegion      */
+#define ZG_ERR_REGISTRY_FULL -7     /* weight_layout::register returned false  */
+#define ZG_ERR_OUT_OF_MEMORY -8
+#define ZG_ERR_ATTENTION -9         /* AttentionError::NumericalInstability    */
+#define ZG_ERR_CONTEXT_FULL -10     /* KvCache position out of range           */
+
+/* GgmlType ids (crates/zero-gguf-parser/src/lib.rs:95-126). */
+#define ZG_Q4_0 2u
+#define ZG_Q8_0 8u
+#define ZG_Q4K 12u
+#define ZG_Q6K 14u
+
+typedef struct zg_ctx zg_ctx;
+
+/* Create a context on HIP device `device` with its own stream.  Replaces
+ * the SMP bring-up that the reference performs before its first dispatch
+ * (kernel/src/main.rs:979-1113, smp::set_active_cores). */
+zg_status zg_init(int device, zg_ctx **out);
+void zg_destroy(zg_ctx *ctx);
+/* Human-readable message of the last failing call on this context. */
+const char *zg_last_error(const zg_ctx *ctx);
+/* The context's hipStream_t, as an opaque pointer. */
+void *zg_stream(zg_ctx *ctx);
+
+/* ------------------------------------------------------------------ */
+/* Weight registry.                                                     */
+/* ------------------------------------------------------------------ */
+
+/* Upload `bytes` bytes at `host_ptr` and register them under that address
+ * with layout `interleave` (1 = plain row-major, 4 = .smodel-v2 X4).
+ * Replaces weight_layout::register (kernel/src/weight_layout.rs:94) plus
+ * the SIDX dtype decode 100/101 -> (Q4_0|Q8_0, 4)
+ * (kernel/src/model_loader.rs:82-90).  Lookups are by exact start address
+ * or by an address inside a plain tensor (weight_layout.rs:133 semantics:
+ * an interior pointer is never interleaved). */
+zg_status zg_register_weight(zg_ctx *ctx, const void *host_ptr, size_t bytes, uint32_t ggml_type,
+                             uint32_t interleave);
+/* Same, but the bytes are already on the device at `dev_ptr` (borrowed,
+ * not freed by the context). `key` is the host-side address to register. */
+zg_status zg_register_weight_device(zg_ctx *ctx, const void *key, const void *dev_ptr,
+                                    size_t bytes, uint32_t ggml_type, uint32_t interleave);
+/* weight_layout::group_of (weight_layout.rs:133): 4 for a registered X4
+ * tensor start, else 1. */
+uint32_t zg_group_of(const zg_ctx *ctx, const void *host_ptr);
+/* weight_layout::rebase (weight_layout.rs:76): shift every key by delta. */
+void zg_rebase(zg_ctx *ctx, int64_t delta);
+/* weight_layout::clear (weight_layout.rs:57); frees owned uploads. */
+void zg_clear(zg_ctx *ctx);
+/* Number of registered tensors (weight_layout::count). */
+size_t zg_registered_count(const zg_ctx *ctx);
+
+/* ------------------------------------------------------------------ */
+/* Operator API: host pointers, synchronous.                            */
+/* ------------------------------------------------------------------ */
+
+/* out[0..out_dim) = W . x.  Replaces linear_dispatch (ops.rs:486-523) and
+ * linear_dispatch_avx512 (inference_avx512.rs:1147-1184).  The layout
+ * (plain or X4) comes from the registry, as the reference's comes from
+ * weight_layout::group_of (inference_avx512.rs:638,690). */
+zg_status zg_linear(zg_ctx *ctx, const float *x, const void *w, float *out, size_t in_dim,
+                    size_t out_dim, uint32_t ggml_type);
+/* Rows [start,end) only (the RowRange kernels, linear.rs:909,1096,...);
+ * out is the full out_dim vector, rows outside the range are untouched. */
+zg_status zg_linear_range(zg_ctx *ctx, const float *x, const void *w, float *out, size_t in_dim,
+                          size_t out_dim, uint32_t ggml_type, size_t start, size_t end);
+
+/* One projection of a fused same-input dispatch: FusedSegment
+ * (inference_avx512.rs:743-764). */
+typedef struct {
+    const void *w;      /* registered weight (host key) or device ptr for _dev */
+    float *out;         /* host output (or device output for _dev)           */
+    size_t out_dim;
+    uint32_t ggml_type;
+    uint32_t interleave; /* used by the _dev variant only                     */
+} zg_segment;
+/* linear_fused_dispatch (inference_avx512.rs:890-945): up to 3 segments
+ * sharing x, one launch over the concatenated row space. */
+zg_status zg_linear_fused(zg_ctx *ctx, const float *x, const zg_segment *segs, size_t n_segs,
+                          size_t in_dim);
+
+/* lm_head_argmax_avx512 (inference_avx512.rs:1200-1270): rmsnorm(hidden,
+ * norm_w) -> GEMV over vocab_padded rows -> first-max argmax with NaN
+ * suppressed.  logits may be NULL.  Returns ZG_ERR_NONFINITE_LOGITS or
+ * ZG_ERR_ARGMAX_IN_PADDING (index >= vocab_real) like LmHeadError. */
+zg_status zg_lm_head_argmax(zg_ctx *ctx, const float *hidden, const float *norm_w, const void *w,
+                            uint32_t ggml_type, float eps, size_t dim, size_t vocab_padded,
+                            size_t vocab_real, float *logits, uint32_t *token, float *max_val);
+
+/* ------------------------------------------------------------------ */
+/* Device-pointer API: asynchronous on `stream` (NULL = ctx stream).    */
+/* No registry; the caller states the layout.                           */
+/* ------------------------------------------------------------------ */
+
+zg_status zg_linear_dev(zg_ctx *ctx, const float *d_x, const void *d_w, float *d_out,
+                        size_t in_dim, size_t out_dim, uint32_t ggml_type, uint32_t interleave,
+                        size_t start, size_t end, void *stream);
+zg_status zg_linear_fused_dev(zg_ctx *ctx, const float *d_x, const zg_segment *segs,
+                              size_t n_segs, size_t in_dim, void *stream);
+/* GEMV + argmax; writes the packed candidate (see zg_argmax_unpack) to
+ * d_best (uint64, reset by this call) and optionally logits. */
+zg_status zg_lm_head_dev(zg_ctx *ctx, const float *d_x, const void *d_w, float *d_logits,
+                         size_t in_dim, size_t out_dim, uint32_t ggml_type, uint32_t interleave,
+                         uint64_t *d_best, void *stream);
+/* Decode the packed argmax candidate. Returns 0 when no finite candidate. */
+int zg_argmax_unpack(uint64_t packed, uint32_t *index, float *value);
+/* Bit-exact dequantization of a device tensor into fp32 rows (test hook for
+ * dequant parity with crates/zero-gguf-parser/src/dequant.rs). */
+zg_status zg_dequant_dev(zg_ctx *ctx, const void *d_w, float *d_out, size_t rows, size_t in_dim,
+                         uint32_t ggml_type, uint32_t interleave, void *stream);
+/* fp16 bits -> f32 on the device (dequant.rs:28-61), n values. */
+zg_status zg_fp16_to_f32_dev(zg_ctx *ctx, const uint16_t *d_in, float *d_out, size_t n,
+                             void *stream);
+
+/* On-the-fly Q8_0 activation quantization of rows x k values (k % 32 == 0):
+ * the packer's quantize_q8_0_block (tools/silicatepack.py:893-907) bit for
+ * bit: d = amax/127 and q = round-half-even(x/d) computed in double, d stored
+ * as the round-to-nearest-even binary16 of the double d (:854-861).  A block
+ * holding a non-finite value (a ValueError in the packer) is written with
+ * q = 0 and d = NaN (0x7E00).
+ * zg_quantize_q8_0_dev writes standard 34-byte blocks (fp16 d + 32 i8);
+ * zg_quantize_q8_0_split_dev writes the same bytes as two arrays, int8
+ * qs[rows][k] (16-byte aligned) and fp16 d[rows][k/32], the layout the
+ * prefill GEMM reads. */
+zg_status zg_quantize_q8_0_dev(zg_ctx *ctx, const float *d_x, void *d_q, size_t rows, size_t k,
+                               void *stream);
+zg_status zg_quantize_q8_0_split_dev(zg_ctx *ctx, const float *d_x, int8_t *d_qs, uint16_t *d_d,
+                                     size_t rows, size_t k, void *stream);
+/* Prefill GEMM, any M: Y[m][n] = sum_b dX[m][b]*dW[n][b]*(int8 dot of block b)
+ * over Q4_0/Q8_0 weights (plain or X4) and split Q8_0 activations, on int8
+ * MFMA; Y is fp32 row-major [m][n].  No reference counterpart: the
+ * reference prefills token by token (kernel/src/inference.rs:1188-1330). */
+zg_status zg_gemm_q8act_dev(zg_ctx *ctx, const int8_t *d_qs, const uint16_t *d_d, const void *d_w,
+                            float *d_y, size_t m, size_t n, size_t k, uint32_t w_type,
+                            uint32_t interleave, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Forward pass.                                                        */
+/* ------------------------------------------------------------------ */
+
+/* LayerWeights (crates/zero-llm-inference/src/forward_pass.rs:227-239):
+ * host keys of registered tensors (or device pointers when
+ * zg_model_desc.device_pointers != 0). */
+typedef struct {
+    const void *attn_q, *attn_k, *attn_v, *attn_o;
+    const void *ffn_gate, *ffn_up, *ffn_down;
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm; /* host fp32 arrays */
+} zg_layer_weights;
+
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_q_heads, n_kv_heads, head_dim;
+    uint32_t vocab_padded, vocab_real, max_ctx;
+    float rms_eps, rope_theta;
+    uint32_t lin_type, lin_interleave;   /* ForwardPassDispatch quants (forward_pass.rs:191-207) */
+    uint32_t embd_type;                  /* token_embd quant (plain layout) */
+    uint32_t head_type, head_interleave; /* output.weight quant + layout */
+    const void *token_embd;
+    const void *lm_head;
+    const float *output_norm;
+    const zg_layer_weights *layers;
+    uint32_t device_pointers;            /* weights are device pointers, not keys */
+} zg_model_desc;
+
+typedef struct zg_model zg_model;
+
+/* Builds device state (KV cache [L][K|V][t][kv_head][d] fp32 as
+ * kv_cache.rs:17-31, scratch, norm weights) and captures the per-token
+ * layer sequence of forward_single_token_avx512
+ * (inference_avx512.rs:1826-1987) + lm_head_argmax_avx512 into a hipGraph. */
+zg_status zg_model_create(zg_ctx *ctx, const zg_model_desc *desc, zg_model **out);
+void zg_model_destroy(zg_model *m);
+/* One token through all layers at position pos, then the LM head.
+ * hidden_out (dim floats) and logits (vocab_padded floats) may be NULL.
+ * Returns the LmHeadError codes like zg_lm_head_argmax. */
+zg_status zg_model_step(zg_model *m, uint32_t token, uint32_t pos, float *hidden_out,
+                        float *logits, uint32_t *next_token, float *max_logit);
+/* The caller loop of run_forward_pass (kernel/src/inference.rs:1188-1330,
+ * 1644-1705, 1817-): prefill the prompt token by token, then n_gen greedy
+ * tokens, with the token id fed back on the device (no host round trip).
+ * out_tokens receives n_gen ids. *seconds (optional) = wall time of the
+ * generation phase. */
+zg_status zg_model_generate(zg_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                            uint32_t *out_tokens, double *prefill_seconds, double *gen_seconds);
+/* Position reset (new sequence). */
+void zg_model_reset(zg_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,274 @@
+"""GPU parity of the GEMV path, called through the C ABI.
+
+Bar: dequantized weights bit-exact with the oracle's restatement of
+dequant.rs; GEMV outputs within rel 1e-3 (max |gpu - oracle| <= 1e-3 *
+max |oracle| per vector) of the oracle's AVX-512-order kernels, and no
+further from an f64 brute force than the oracle itself is (x 4).
+"""
+import numpy as np
+import pytest
+import torch
+
+import zero_amd
+from golden import kats
+from zero_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4K, Q6K = 2, 8, 12, 14
+REL_TOL = 1e-3  # north-star bar for dot products / logits
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def same_bits(got, want):
+    """Bitwise equality; NaN results only need to be NaN on both sides
+    (the NaN-scale decode itself is checked bitwise by the fp16 test)."""
+    g, w = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan = np.isnan(w)
+    return np.array_equal(np.isnan(g), nan) and np.array_equal(g[~nan].view(np.uint32), w[~nan].view(np.uint32))
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def test_fp16_exhaustive_on_gpu(ctx, zo):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    src = dev(bits.view(np.int16))
+    out = torch.empty(65536, dtype=torch.float32, device="cuda")
+    ctx.fp16_to_f32_dev(src, out, 65536, stream=torch.cuda.current_stream().cuda_stream)
+    got = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, zo.fp16_to_f32(bits).view(np.uint32))
+
+
+DEQ_CASES = [(Q4_0, 4, 64, 2048), (Q8_0, 4, 64, 2048), (Q4_0, 4, 8, 96), (Q8_0, 4, 8, 32),
+             (Q4_0, 1, 9, 256), (Q8_0, 1, 7, 64), (Q4K, 1, 6, 1024), (Q6K, 1, 5, 768)]
+
+
+@pytest.mark.parametrize("quant,il,rows,k", DEQ_CASES)
+def test_dequant_bit_exact(ctx, zo, quant, il, rows, k):
+    rng = np.random.default_rng(rows * 7 + k + quant)
+    w = synth.weight(rng, quant, rows, k, il)
+    # all 65,536 fp16 scale patterns appear across the scale slots
+    if quant in (Q4_0, Q8_0):
+        bb = 18 if quant == Q4_0 else 34
+        nblk = w.size // bb
+        sc = rng.integers(0, 65536, nblk, dtype=np.uint32).astype(np.uint16)
+        if il == 4:
+            g = w.reshape(rows // 4, k // 32, 4 * bb)
+            g[..., :8] = sc.view(np.uint8).reshape(rows // 4, k // 32, 4, 2).reshape(rows // 4, k // 32, 8)
+        else:
+            w.reshape(nblk, bb)[:, :2] = sc.view(np.uint8).reshape(nblk, 2)
+    out = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+    ctx.dequant_dev(dev(w), out, rows, k, quant, il, stream=torch.cuda.current_stream().cuda_stream)
+    got = out.cpu().numpy()
+    want = zo.dequant(w, rows, k, quant, il)
+    assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("case", kats.DEQUANT, ids=lambda c: c[4])
+def test_dequant_kats_on_gpu(ctx, case):
+    quant, blk, checks, tol, src = case
+    w = np.frombuffer(blk, np.uint8).copy()
+    be, bb = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[quant]
+    k = (w.size // bb) * be
+    out = torch.empty((1, k), dtype=torch.float32, device="cuda")
+    ctx.dequant_dev(dev(w), out, 1, k, quant, 1, stream=torch.cuda.current_stream().cuda_stream)
+    kats.check_dequant(out.cpu().numpy()[0], checks, tol)
+
+
+@pytest.mark.parametrize("case", kats.LINEAR, ids=lambda c: c[7])
+def test_linear_kats_through_abi(ctx, case):
+    quant, k, n, x, wb, want, tol, src = case
+    w = np.frombuffer(wb, np.uint8).copy()
+    ctx.register(w, quant, 1)
+    out = np.empty(n, np.float32)
+    ctx.linear_dispatch(x, w, out, k, n, quant)
+    np.testing.assert_allclose(out, want, atol=tol, rtol=0, err_msg=src)
+    ctx.clear()
+
+
+GEMV_CASES = [
+    # (quant, interleave, rows, k)
+    (Q4_0, 4, 6144, 2048),   # Qwen3-1.7B FFN up-proj (pair path)
+    (Q4_0, 4, 2048, 6144),   # down-proj
+    (Q8_0, 4, 4096, 2048),   # fused-QKV-sized Q8_0X4
+    (Q4_0, 4, 4, 64),
+    (Q4_0, 4, 12, 96),       # odd blocks per row: generic path
+    (Q8_0, 4, 8, 32),
+    (Q4_0, 1, 7, 256),       # plain layouts
+    (Q8_0, 1, 100, 512),
+    (Q4K, 1, 64, 4096),
+    (Q6K, 1, 48, 1024),
+]
+
+
+@pytest.mark.parametrize("quant,il,rows,k", GEMV_CASES)
+def test_gemv_parity_host_api(ctx, zo, quant, il, rows, k):
+    rng = np.random.default_rng(rows + 3 * k + quant)
+    w = synth.weight(rng, quant, rows, k, il)
+    x = synth.activations(rng, k)
+    ctx.register(w, quant, il)
+    assert ctx.group_of(w) == il
+    out = np.empty(rows, np.float32)
+    ctx.linear_dispatch(x, w, out, k, rows, quant)
+    ref = zo.linear_range(x, w, k, rows, quant, il)
+    f64 = zo.linear_f64(x, w, k, rows, quant, il)
+    e_gpu, e_ref = rel_err(out, ref), rel_err(ref, f64)
+    print(f"quant={quant} il={il} {rows}x{k}: rel err vs oracle {e_gpu:.2e}, oracle vs f64 {e_ref:.2e}, "
+          f"gpu vs f64 {rel_err(out, f64):.2e}")
+    assert e_gpu <= REL_TOL
+    assert rel_err(out, f64) <= 4 * e_ref + 1e-6
+    ctx.clear()
+
+
+def test_gemv_device_api_matches_host_api(ctx, zo):
+    rng = np.random.default_rng(1)
+    rows, k = 6144, 2048
+    w = synth.weight(rng, Q4_0, rows, k, 4)
+    x = synth.activations(rng, k)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.linear_dev(dev(x), dev(w), y, k, rows, Q4_0, 4, stream=torch.cuda.current_stream().cuda_stream)
+    ctx.register(w, Q4_0, 4)
+    out = np.empty(rows, np.float32)
+    ctx.linear_dispatch(x, w, out, k, rows, Q4_0)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), out.view(np.uint32))
+    ctx.clear()
+
+
+@pytest.mark.parametrize("quant,il", [(Q4_0, 4), (Q8_0, 4), (Q6K, 1)])
+def test_row_ranges(ctx, zo, quant, il):
+    rng = np.random.default_rng(2)
+    rows, k = 40, 1024
+    w = synth.weight(rng, quant, rows, k, il)
+    x = synth.activations(rng, k)
+    ctx.register(w, quant, il)
+    ref = zo.linear_range(x, w, k, rows, quant, il)
+    for s, e in ((0, 40), (1, 7), (13, 14), (20, 40), (5, 5)):
+        out = np.full(rows, -7.0, np.float32)
+        ctx.linear_range(x, w, out, k, rows, quant, s, e)
+        assert np.all(out[:s] == -7.0) and np.all(out[e:] == -7.0)
+        assert rel_err(out[s:e], ref[s:e]) <= REL_TOL if e > s else True
+    ctx.clear()
+
+
+def test_fused_qkv_q8_0(ctx, zo):
+    """Config 2: fused Q|K|V Q8_0X4, Qwen3-1.7B attention (2048 + 1024 + 1024) x 2048."""
+    rng = np.random.default_rng(3)
+    k = 2048
+    ws = [synth.weight(rng, Q8_0, n, k, 4) for n in (2048, 1024, 1024)]
+    x = synth.activations(rng, k)
+    outs = [np.empty(w.size // (k // 32 * 34), np.float32) for w in ws]
+    for w in ws:
+        ctx.register(w, Q8_0, 4)
+    ctx.linear_fused_dispatch(x, [(w, o, Q8_0) for w, o in zip(ws, outs)], k)
+    for w, o in zip(ws, outs):
+        ref = zo.linear_range(x, w, k, o.size, Q8_0, 4)
+        assert rel_err(o, ref) <= REL_TOL
+    ctx.clear()
+
+
+@pytest.fixture(scope="module")
+def lm_head():
+    rng = np.random.default_rng(4)
+    V, H = kats.VOCAB_SIZE_PADDED, 2048
+    plain = synth.weight(rng, Q8_0, V, H, 1)
+    plain.reshape(V, -1)[kats.VOCAB_SIZE_REAL:] = 0  # padding rows
+    w = synth.interleave_x4(plain, V, H, Q8_0)
+    hidden = synth.activations(rng, H)
+    norm = (1 + 0.05 * rng.standard_normal(H)).astype(np.float32)
+    return w, hidden, norm
+
+
+def test_lm_head_argmax(ctx, zo, lm_head):
+    """Config 2: LM head Q8_0X4 151936 x 2048 with fused rmsnorm + argmax."""
+    w, hidden, norm = lm_head
+    V, H = kats.VOCAB_SIZE_PADDED, 2048
+    ctx.register(w, Q8_0, 4)
+    logits = np.empty(V, np.float32)
+    tok = ctx.lm_head_argmax(hidden, norm, w, Q8_0, 1e-6, H, logits_buf=logits)
+    xn = np.empty(H, np.float32)
+    zo.load().zo_rmsnorm(hidden.ctypes.data, norm.ctypes.data, xn.ctypes.data, H, 1e-6)
+    with zo.Pool(8):
+        ref = zo.linear_parallel(xn, w, H, V, Q8_0, 4)
+    assert rel_err(logits, ref) <= REL_TOL
+    idx, val = zo.argmax(ref)
+    top2 = np.sort(ref)[-2:]
+    print(f"LM head: argmax {tok} (oracle {idx}), margin {top2[1] - top2[0]:.4f}, rel err {rel_err(logits, ref):.2e}")
+    assert tok == idx and tok == int(np.argmax(logits))
+    ctx.clear()
+
+
+def test_lm_head_errors(ctx, lm_head):
+    w, hidden, norm = lm_head
+    V, H = kats.VOCAB_SIZE_PADDED, 2048
+    ctx.register(w, Q8_0, 4)
+    bad = hidden.copy()
+    bad[3] = np.nan
+    with pytest.raises(zero_amd.NonFiniteLogits):
+        ctx.lm_head_argmax(bad, norm, w, Q8_0, 1e-6, H)
+    # a vocab_real below the argmax puts it in the padding region
+    tok = ctx.lm_head_argmax(hidden, norm, w, Q8_0, 1e-6, H)
+    with pytest.raises(zero_amd.ArgmaxInPaddingRegion) as ei:
+        ctx.lm_head_argmax(hidden, norm, w, Q8_0, 1e-6, H, vocab_real=tok)
+    assert ei.value.index == tok
+    ctx.clear()
+
+
+def test_registry_semantics(ctx):
+    """weight_layout.rs:155-170: sorted registry, exact-start lookups,
+    interior pointers are plain, clear() empties it; rebase shifts keys."""
+    fake = torch.empty(64, dtype=torch.uint8, device="cuda")
+    for key in (0x5000, 0x1000, 0x3000):
+        ctx.register_device(key, fake.data_ptr(), 36, Q4_0, 4)
+    assert ctx.registered_count() == 3
+    for key in (0x1000, 0x3000, 0x5000):
+        assert ctx.group_of(key) == 4
+    assert ctx.group_of(0x3010) == 1 and ctx.group_of(0) == 1
+    ctx.rebase(0x100)
+    assert ctx.group_of(0x1100) == 4 and ctx.group_of(0x1000) == 1
+    ctx.clear()
+    assert ctx.group_of(0x1100) == 1 and ctx.registered_count() == 0
+
+
+def test_dispatch_errors(ctx):
+    w = synth.weight(np.random.default_rng(0), Q4_0, 4, 64, 1)
+    x = np.zeros(64, np.float32)
+    out = np.empty(4, np.float32)
+    with pytest.raises(zero_amd.LinearDispatchError):  # ops.rs:513-521 panics on F16
+        ctx.linear_dispatch(x, w, out, 64, 4, zero_amd.GgmlType.F16)
+    with pytest.raises(zero_amd.ZgError) as ei:  # not uploaded
+        ctx.linear_dispatch(x, w, out, 64, 4, Q4_0)
+    assert ei.value.code == -3
+    ctx.register(w, Q4_0, 1)
+    with pytest.raises(zero_amd.ZgError):  # registered as Q4_0, called as Q8_0
+        ctx.linear_dispatch(x, w, out, 64, 4, Q8_0)
+    # interior pointer of a plain tensor resolves to that row (weight_layout.rs:13-19)
+    row = w[36:]
+    x = synth.activations(np.random.default_rng(1), 64)
+    full = np.empty(4, np.float32)
+    ctx.linear_dispatch(x, w, full, 64, 4, Q4_0)
+    tail = np.empty(3, np.float32)
+    ctx.linear_dispatch(x, row, tail, 64, 3, Q4_0)
+    assert np.array_equal(tail, full[1:])
+    ctx.clear()
+
+
+@pytest.mark.parametrize("quant,rows,k", [(Q4K, 14336, 4096), (Q6K, 4096, 14336)])
+def test_kquant_llama3_shapes(ctx, zo, quant, rows, k):
+    """Config 4: Q4_K gate/up 14336x4096 and Q6_K down 4096x14336."""
+    rng = np.random.default_rng(rows)
+    w = synth.weight(rng, quant, rows, k, 1)
+    x = synth.activations(rng, k)
+    ctx.register(w, quant, 1)
+    out = np.empty(rows, np.float32)
+    ctx.linear_dispatch(x, w, out, k, rows, quant)
+    with zo.Pool(8):
+        ref = zo.linear_parallel(x, w, k, rows, quant, 1)
+    print(f"quant={quant} {rows}x{k}: rel err {rel_err(out, ref):.2e}")
+    assert rel_err(out, ref) <= REL_TOL
+    ctx.clear()

@@ -1,0 +1,538 @@
+// zg_abi.hip -- C ABI of include/zero_gpu.h: context, weight registry and
+// operator dispatch for the gfx950 kernels.
+//
+// The registry restates kernel/src/weight_layout.rs (sorted table keyed by
+// the tensor's host start address, exact-match group lookup, uniform
+// rebase) and adds what a GPU needs on top: every registered key maps to a
+// device copy of the tensor bytes (byte-identical to the host bytes).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/zero_gpu.h"
+#include "zg_internal.h"
+#include "zg_kernels.h"
+
+using namespace zg;
+
+// ---------------------------------------------------------------------------
+// Context helpers
+// ---------------------------------------------------------------------------
+
+zg_status zg::set_error(zg_ctx* ctx, zg_status code, const char* fmt, ...) {
+  if (ctx) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    ctx->last_error = buf;
+  }
+  return code;
+}
+
+zg_status zg::hip_check(zg_ctx* ctx, hipError_t e, const char* what) {
+  if (e == hipSuccess) return ZG_OK;
+  return set_error(ctx, ZG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static bool type_geom(uint32_t qt, size_t* be, size_t* bb) {
+  switch (qt) {
+    case ZG_Q4_0: *be = 32; *bb = 18; return true;
+    case ZG_Q8_0: *be = 32; *bb = 34; return true;
+    case ZG_Q4K: *be = 256; *bb = 144; return true;
+    case ZG_Q6K: *be = 256; *bb = 210; return true;
+    default: return false;
+  }
+}
+
+size_t zg::tensor_bytes(uint32_t qt, size_t rows, size_t k) {
+  size_t be, bb;
+  if (!type_geom(qt, &be, &bb)) return 0;
+  return rows * (k / be) * bb;
+}
+
+zg_status zg::ensure_buf(zg_ctx* ctx, DevBuf& b, size_t bytes) {
+  if (b.bytes >= bytes) return ZG_OK;
+  if (b.ptr) hipFree(b.ptr);
+  b.ptr = nullptr;
+  b.bytes = 0;
+  hipError_t e = hipMalloc(&b.ptr, bytes);
+  if (e != hipSuccess) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  b.bytes = bytes;
+  return ZG_OK;
+}
+
+static hipStream_t pick_stream(zg_ctx* ctx, void* stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+// ---------------------------------------------------------------------------
+// Lifecycle
+// ---------------------------------------------------------------------------
+
+extern "C" zg_status zg_init(int device, zg_ctx** out) {
+  if (!out) return ZG_ERR_INVALID_ARG;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return ZG_ERR_HIP;
+  if (hipSetDevice(device) != hipSuccess) return ZG_ERR_HIP;
+  zg_ctx* ctx = new zg_ctx();
+  ctx->device = device;
+  // A blocking stream: work on it is ordered against the legacy null stream,
+  // so callers that stage data with null-stream copies need no extra sync.
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamDefault) != hipSuccess) {
+    delete ctx;
+    return ZG_ERR_HIP;
+  }
+  if (hipMalloc(&ctx->d_best, sizeof(uint64_t) * 4) != hipSuccess) {
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ZG_ERR_OUT_OF_MEMORY;
+  }
+  *out = ctx;
+  return ZG_OK;
+}
+
+extern "C" void zg_destroy(zg_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  zg_clear(ctx);
+  for (DevBuf* b : {&ctx->d_x, &ctx->d_out, &ctx->d_aux}) {
+    if (b->ptr) hipFree(b->ptr);
+  }
+  if (ctx->h_pinned) hipHostFree(ctx->h_pinned);
+  if (ctx->d_best) hipFree(ctx->d_best);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" const char* zg_last_error(const zg_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
+
+extern "C" void* zg_stream(zg_ctx* ctx) { return ctx ? reinterpret_cast<void*>(ctx->stream) : nullptr; }
+
+// ---------------------------------------------------------------------------
+// Registry (kernel/src/weight_layout.rs)
+// ---------------------------------------------------------------------------
+
+static zg_status do_register(zg_ctx* ctx, uintptr_t key, const void* host, const void* dev, size_t bytes,
+                             uint32_t qt, uint32_t il) {
+  if (!ctx || !key || bytes == 0) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: null key or zero bytes");
+  size_t be, bb;
+  if (!type_geom(qt, &be, &bb)) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "register: unsupported quant %u", qt);
+  if (il != 1 && il != 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: interleave %u not in {1,4}", il);
+  // The packer only interleaves Q4_0/Q8_0 (silicatepack.py:836-851).
+  if (il == 4 && qt != ZG_Q4_0 && qt != ZG_Q8_0)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "register: interleave 4 needs Q4_0 or Q8_0");
+  if (ctx->reg.size() >= kMaxEntries) return set_error(ctx, ZG_ERR_REGISTRY_FULL, "register: registry full");
+  for (const RegEntry& e : ctx->reg)
+    if (e.key == key) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: key already registered");
+  hipSetDevice(ctx->device);
+  RegEntry e;
+  e.key = key;
+  e.bytes = bytes;
+  e.qt = qt;
+  e.il = il;
+  if (dev) {
+    e.dev = const_cast<void*>(dev);
+    e.owned = false;
+  } else {
+    hipError_t he = hipMalloc(&e.dev, bytes);
+    if (he != hipSuccess) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "register: hipMalloc(%zu): %s", bytes, hipGetErrorString(he));
+    he = hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice);
+    if (he != hipSuccess) {
+      hipFree(e.dev);
+      return hip_check(ctx, he, "register: upload");
+    }
+    e.owned = true;
+  }
+  auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), key,
+                             [](uintptr_t k, const RegEntry& r) { return k < r.key; });
+  ctx->reg.insert(it, e);
+  return ZG_OK;
+}
+
+extern "C" zg_status zg_register_weight(zg_ctx* ctx, const void* host_ptr, size_t bytes, uint32_t ggml_type,
+                                        uint32_t interleave) {
+  if (!host_ptr) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: null host pointer");
+  return do_register(ctx, reinterpret_cast<uintptr_t>(host_ptr), host_ptr, nullptr, bytes, ggml_type, interleave);
+}
+
+extern "C" zg_status zg_register_weight_device(zg_ctx* ctx, const void* key, const void* dev_ptr, size_t bytes,
+                                               uint32_t ggml_type, uint32_t interleave) {
+  if (!dev_ptr) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: null device pointer");
+  return do_register(ctx, reinterpret_cast<uintptr_t>(key), nullptr, dev_ptr, bytes, ggml_type, interleave);
+}
+
+extern "C" uint32_t zg_group_of(const zg_ctx* ctx, const void* host_ptr) {
+  if (!ctx) return 1;
+  const uintptr_t k = reinterpret_cast<uintptr_t>(host_ptr);
+  auto it = std::lower_bound(ctx->reg.begin(), ctx->reg.end(), k,
+                             [](const RegEntry& r, uintptr_t key) { return r.key < key; });
+  if (it != ctx->reg.end() && it->key == k) return it->il;
+  return 1;
+}
+
+extern "C" void zg_rebase(zg_ctx* ctx, int64_t delta) {
+  if (!ctx || delta == 0) return;
+  for (RegEntry& e : ctx->reg) e.key = (uintptr_t)((int64_t)e.key + delta);
+}
+
+extern "C" void zg_clear(zg_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  for (RegEntry& e : ctx->reg)
+    if (e.owned && e.dev) hipFree(e.dev);
+  ctx->reg.clear();
+}
+
+extern "C" size_t zg_registered_count(const zg_ctx* ctx) { return ctx ? ctx->reg.size() : 0; }
+
+// Resolve a host weight pointer to its device bytes.  Exact start match
+// gives the tensor and its layout; an interior pointer resolves only inside
+// a plain (interleave 1) tensor, as weight_layout::group_of treats interior
+// pointers as plain (weight_layout.rs:13-19).
+zg_status zg::resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il) {
+  const uintptr_t k = reinterpret_cast<uintptr_t>(w);
+  auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), k,
+                             [](uintptr_t key, const RegEntry& r) { return key < r.key; });
+  if (it == ctx->reg.begin()) return set_error(ctx, ZG_ERR_NOT_REGISTERED, "weight %p is not registered", w);
+  --it;
+  const size_t off = k - it->key;
+  if (off >= it->bytes) return set_error(ctx, ZG_ERR_NOT_REGISTERED, "weight %p is not registered", w);
+  if (it->qt != qt)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "weight %p registered as quant %u, called with %u", w, it->qt, qt);
+  if (off != 0 && it->il != 1)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "interior pointer into an interleaved tensor");
+  if (off + need > it->bytes)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "weight %p: %zu bytes needed, %zu registered", w, need, it->bytes - off);
+  *dev = static_cast<const uint8_t*>(it->dev) + off;
+  *il = off ? 1u : it->il;
+  return ZG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch core (device pointers)
+// ---------------------------------------------------------------------------
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool zg::pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
+  return il == 4 && (qt == ZG_Q4_0 || qt == ZG_Q8_0) && k % 64 == 0 && k <= kMaxPairK && n % 4 == 0 &&
+         aligned16(w) && aligned16(x);
+}
+
+zg_status zg::check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n) {
+  size_t be, bb;
+  if (!type_geom(qt, &be, &bb)) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "unsupported quant type %u", qt);
+  if (k == 0 || k % be) return set_error(ctx, ZG_ERR_INVALID_ARG, "in_dim %zu not a multiple of %zu", k, be);
+  if (il != 1 && il != 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave %u", il);
+  if (il == 4 && ((qt != ZG_Q4_0 && qt != ZG_Q8_0) || n % 4))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave 4 needs Q4_0/Q8_0 and out_dim %% 4 == 0");
+  if (k > (size_t)INT32_MAX || n > (size_t)UINT32_MAX / 2) return set_error(ctx, ZG_ERR_INVALID_ARG, "shape too large");
+  return ZG_OK;
+}
+
+// One GEMV (optionally a row range, residual or argmax epilogue).
+zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,
+                         uint32_t il, size_t start, size_t end, int epi, const float* resid, uint64_t* best,
+                         int pro, const float* norm_w, float eps, hipStream_t st) {
+  if (start >= end) return ZG_OK;
+  if (pair_path_ok(qt, il, k, n, w, x)) {
+    const size_t gbytes = (k / 32) * (qt == ZG_Q4_0 ? 72 : 136);
+    const size_t g0 = start / 4, g1 = (end + 3) / 4;
+    GemvArgs a{};
+    a.nseg = 1;
+    a.k = (int)k;
+    a.total_groups = (uint32_t)(g1 - g0);
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.best = best;
+    a.seg[0].w = w + g0 * gbytes;
+    a.seg[0].y = y ? y + 4 * g0 : nullptr;
+    a.seg[0].resid = resid ? resid + 4 * g0 : nullptr;
+    a.seg[0].g_begin = 0;
+    a.seg[0].row_lo = (uint32_t)(start - 4 * g0);
+    a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
+    return hip_check(ctx, launch_gemv_x4_pair(a, qt, pro, epi, st), "gemv_x4_pair launch");
+  }
+  const float* xin = x;
+  if (pro == PRO_RMSNORM) {
+    // generic path: normalize into the context's aux buffer first
+    zg_status s = ensure_buf(ctx, ctx->d_aux, k * sizeof(float));
+    if (s) return s;
+    hipError_t e = launch_rmsnorm(x, norm_w, static_cast<float*>(ctx->d_aux.ptr), (int)k, eps, st);
+    if (e != hipSuccess) return hip_check(ctx, e, "rmsnorm launch");
+    xin = static_cast<float*>(ctx->d_aux.ptr);
+  }
+  GenericArgs g{};
+  g.w = w;
+  g.x = xin;
+  g.y = y;
+  g.resid = resid;
+  g.best = best;
+  g.k = k;
+  g.row_lo = start;
+  g.row_hi = end;
+  g.qt = qt;
+  g.il = (int)il;
+  g.epi = epi;
+  return hip_check(ctx, launch_gemv_generic(g, st), "gemv_generic launch");
+}
+
+// Fused same-x dispatch: one pair launch over the concatenated group space
+// when every segment qualifies, else one launch per segment.
+zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
+                        const float* norm_w, float eps, int epi, hipStream_t st) {
+  bool pair = nseg >= 1 && nseg <= 3;
+  for (size_t i = 0; i < nseg && pair; i++)
+    pair = pair_path_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
+  if (epi == EPI_SWIGLU && !(pair && nseg == 2 && segs[0].n == segs[1].n))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "swiglu fusion needs two equal X4 segments");
+  if (pair) {
+    GemvArgs a{};
+    a.nseg = (int)nseg;
+    a.k = (int)k;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    uint32_t g = 0;
+    for (size_t i = 0; i < nseg; i++) {
+      a.seg[i].w = segs[i].w;
+      a.seg[i].y = segs[i].y;
+      a.seg[i].resid = nullptr;
+      a.seg[i].g_begin = g;
+      a.seg[i].row_lo = 0;
+      a.seg[i].row_hi = (uint32_t)segs[i].n;
+      g += (uint32_t)(segs[i].n / 4);
+    }
+    a.total_groups = g;
+    return hip_check(ctx, launch_gemv_x4_pair(a, segs[0].qt, pro, epi, st), "fused gemv launch");
+  }
+  for (size_t i = 0; i < nseg; i++) {
+    zg_status s = run_linear(ctx, x, segs[i].w, segs[i].y, k, segs[i].n, segs[i].qt, segs[i].il, 0, segs[i].n,
+                             EPI_STORE, nullptr, nullptr, pro, norm_w, eps, st);
+    if (s) return s;
+  }
+  return ZG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Host-pointer operator API
+// ---------------------------------------------------------------------------
+
+zg_status zg::stage_in(zg_ctx* ctx, const void* src, size_t bytes, DevBuf& dst) {
+  zg_status s = ensure_buf(ctx, dst, bytes);
+  if (s) return s;
+  return hip_check(ctx, hipMemcpyAsync(dst.ptr, src, bytes, hipMemcpyHostToDevice, ctx->stream), "upload");
+}
+
+extern "C" zg_status zg_linear_range(zg_ctx* ctx, const float* x, const void* w, float* out, size_t in_dim,
+                                     size_t out_dim, uint32_t ggml_type, size_t start, size_t end) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!x || !w || !out) return set_error(ctx, ZG_ERR_INVALID_ARG, "linear: null pointer");
+  if (start > end || end > out_dim) return set_error(ctx, ZG_ERR_INVALID_ARG, "linear: bad range [%zu,%zu)", start, end);
+  hipSetDevice(ctx->device);
+  size_t be, bb;
+  if (!type_geom(ggml_type, &be, &bb))
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "linear_dispatch: unsupported quant type %u", ggml_type);
+  const uint8_t* dw;
+  uint32_t il;
+  zg_status s = resolve(ctx, w, tensor_bytes(ggml_type, out_dim, in_dim), ggml_type, &dw, &il);
+  if (s) return s;
+  if ((s = check_shape(ctx, ggml_type, il, in_dim, out_dim))) return s;
+  if ((s = stage_in(ctx, x, in_dim * sizeof(float), ctx->d_x))) return s;
+  if ((s = ensure_buf(ctx, ctx->d_out, out_dim * sizeof(float)))) return s;
+  float* dout = static_cast<float*>(ctx->d_out.ptr);
+  s = run_linear(ctx, static_cast<const float*>(ctx->d_x.ptr), dw, dout, in_dim, out_dim, ggml_type, il, start, end,
+                 EPI_STORE, nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, ctx->stream);
+  if (s) return s;
+  if (end > start) {
+    s = hip_check(ctx, hipMemcpyAsync(out + start, dout + start, (end - start) * sizeof(float), hipMemcpyDeviceToHost,
+                                      ctx->stream), "download");
+    if (s) return s;
+  }
+  return hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync");
+}
+
+extern "C" zg_status zg_linear(zg_ctx* ctx, const float* x, const void* w, float* out, size_t in_dim, size_t out_dim,
+                               uint32_t ggml_type) {
+  return zg_linear_range(ctx, x, w, out, in_dim, out_dim, ggml_type, 0, out_dim);
+}
+
+extern "C" zg_status zg_linear_fused(zg_ctx* ctx, const float* x, const zg_segment* segs, size_t n_segs,
+                                     size_t in_dim) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!x || !segs || n_segs == 0 || n_segs > 3) return set_error(ctx, ZG_ERR_INVALID_ARG, "fused: bad segments");
+  hipSetDevice(ctx->device);
+  FusedDev fd[3];
+  size_t total = 0;
+  for (size_t i = 0; i < n_segs; i++) {
+    if (!segs[i].w || !segs[i].out) return set_error(ctx, ZG_ERR_INVALID_ARG, "fused: null segment pointer");
+    size_t be, bb;
+    if (!type_geom(segs[i].ggml_type, &be, &bb))
+      return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "fused: unsupported quant type %u", segs[i].ggml_type);
+    zg_status s = resolve(ctx, segs[i].w, tensor_bytes(segs[i].ggml_type, segs[i].out_dim, in_dim), segs[i].ggml_type,
+                          &fd[i].w, &fd[i].il);
+    if (s) return s;
+    if ((s = check_shape(ctx, segs[i].ggml_type, fd[i].il, in_dim, segs[i].out_dim))) return s;
+    fd[i].qt = segs[i].ggml_type;
+    fd[i].n = segs[i].out_dim;
+    total += segs[i].out_dim;
+  }
+  zg_status s = stage_in(ctx, x, in_dim * sizeof(float), ctx->d_x);
+  if (s) return s;
+  if ((s = ensure_buf(ctx, ctx->d_out, total * sizeof(float)))) return s;
+  float* dout = static_cast<float*>(ctx->d_out.ptr);
+  size_t off = 0;
+  for (size_t i = 0; i < n_segs; i++) {
+    fd[i].y = dout + off;
+    off += fd[i].n;
+  }
+  s = run_fused(ctx, static_cast<const float*>(ctx->d_x.ptr), fd, n_segs, in_dim, PRO_PLAIN, nullptr, 0.0f, EPI_STORE,
+                ctx->stream);
+  if (s) return s;
+  off = 0;
+  for (size_t i = 0; i < n_segs; i++) {
+    s = hip_check(ctx, hipMemcpyAsync(segs[i].out, dout + off, fd[i].n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                  "download");
+    if (s) return s;
+    off += fd[i].n;
+  }
+  return hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync");
+}
+
+extern "C" int zg_argmax_unpack(uint64_t packed, uint32_t* index, float* value) {
+  if (packed == 0) {
+    if (index) *index = 0;
+    if (value) *value = -INFINITY;
+    return 0;
+  }
+  const uint32_t k = (uint32_t)(packed >> 32);
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  float v;
+  memcpy(&v, &b, 4);
+  if (index) *index = 0xFFFFFFFFu - (uint32_t)(packed & 0xFFFFFFFFu);
+  if (value) *value = v;
+  return 1;
+}
+
+zg_status zg::lm_head_status(zg_ctx* ctx, uint64_t packed, size_t vocab_real, uint32_t* token, float* max_val) {
+  uint32_t idx;
+  float v;
+  const int have = zg_argmax_unpack(packed, &idx, &v);
+  if (token) *token = idx;
+  if (max_val) *max_val = v;
+  if (!have || !std::isfinite(v)) return set_error(ctx, ZG_ERR_NONFINITE_LOGITS, "LM head: non-finite logits");
+  if (idx >= vocab_real) return set_error(ctx, ZG_ERR_ARGMAX_IN_PADDING, "LM head: argmax %u in padding region", idx);
+  return ZG_OK;
+}
+
+extern "C" zg_status zg_lm_head_argmax(zg_ctx* ctx, const float* hidden, const float* norm_w, const void* w,
+                                       uint32_t ggml_type, float eps, size_t dim, size_t vocab_padded,
+                                       size_t vocab_real, float* logits, uint32_t* token, float* max_val) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!hidden || !norm_w || !w) return set_error(ctx, ZG_ERR_INVALID_ARG, "lm_head: null pointer");
+  if (vocab_real > vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "lm_head: vocab_real > vocab_padded");
+  hipSetDevice(ctx->device);
+  size_t be, bb;
+  if (!type_geom(ggml_type, &be, &bb))
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "lm_head: unsupported quant type %u", ggml_type);
+  const uint8_t* dw;
+  uint32_t il;
+  zg_status s = resolve(ctx, w, tensor_bytes(ggml_type, vocab_padded, dim), ggml_type, &dw, &il);
+  if (s) return s;
+  if ((s = check_shape(ctx, ggml_type, il, dim, vocab_padded))) return s;
+  // d_x holds [hidden | norm_w]
+  if ((s = ensure_buf(ctx, ctx->d_x, 2 * dim * sizeof(float) + 64))) return s;
+  float* dx = static_cast<float*>(ctx->d_x.ptr);
+  float* dn = dx + ((dim + 15) & ~size_t(15));
+  if ((s = hip_check(ctx, hipMemcpyAsync(dx, hidden, dim * 4, hipMemcpyHostToDevice, ctx->stream), "upload"))) return s;
+  if ((s = hip_check(ctx, hipMemcpyAsync(dn, norm_w, dim * 4, hipMemcpyHostToDevice, ctx->stream), "upload"))) return s;
+  if ((s = ensure_buf(ctx, ctx->d_out, vocab_padded * sizeof(float)))) return s;
+  float* dl = static_cast<float*>(ctx->d_out.ptr);
+  if ((s = hip_check(ctx, launch_fill_u64(ctx->d_best, 0, ctx->stream), "reset"))) return s;
+  s = run_linear(ctx, dx, dw, dl, dim, vocab_padded, ggml_type, il, 0, vocab_padded, EPI_ARGMAX, nullptr, ctx->d_best,
+                 PRO_RMSNORM, dn, eps, ctx->stream);
+  if (s) return s;
+  uint64_t packed = 0;
+  if ((s = hip_check(ctx, hipMemcpyAsync(&packed, ctx->d_best, 8, hipMemcpyDeviceToHost, ctx->stream), "download")))
+    return s;
+  if (logits &&
+      (s = hip_check(ctx, hipMemcpyAsync(logits, dl, vocab_padded * 4, hipMemcpyDeviceToHost, ctx->stream), "download")))
+    return s;
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  return lm_head_status(ctx, packed, vocab_real, token, max_val);
+}
+
+// ---------------------------------------------------------------------------
+// Device-pointer API
+// ---------------------------------------------------------------------------
+
+extern "C" zg_status zg_linear_dev(zg_ctx* ctx, const float* d_x, const void* d_w, float* d_out, size_t in_dim,
+                                   size_t out_dim, uint32_t ggml_type, uint32_t interleave, size_t start, size_t end,
+                                   void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_x || !d_w || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_dev: null pointer");
+  if (start > end || end > out_dim) return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_dev: bad range");
+  zg_status s = check_shape(ctx, ggml_type, interleave, in_dim, out_dim);
+  if (s) return s;
+  return run_linear(ctx, d_x, static_cast<const uint8_t*>(d_w), d_out, in_dim, out_dim, ggml_type, interleave, start,
+                    end, EPI_STORE, nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, pick_stream(ctx, stream));
+}
+
+extern "C" zg_status zg_linear_fused_dev(zg_ctx* ctx, const float* d_x, const zg_segment* segs, size_t n_segs,
+                                         size_t in_dim, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_x || !segs || n_segs == 0 || n_segs > 3) return set_error(ctx, ZG_ERR_INVALID_ARG, "fused_dev: bad segments");
+  FusedDev fd[3];
+  for (size_t i = 0; i < n_segs; i++) {
+    if (!segs[i].w || !segs[i].out) return set_error(ctx, ZG_ERR_INVALID_ARG, "fused_dev: null pointer");
+    zg_status s = check_shape(ctx, segs[i].ggml_type, segs[i].interleave, in_dim, segs[i].out_dim);
+    if (s) return s;
+    fd[i].w = static_cast<const uint8_t*>(segs[i].w);
+    fd[i].y = segs[i].out;
+    fd[i].n = segs[i].out_dim;
+    fd[i].qt = segs[i].ggml_type;
+    fd[i].il = segs[i].interleave;
+  }
+  return run_fused(ctx, d_x, fd, n_segs, in_dim, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, pick_stream(ctx, stream));
+}
+
+extern "C" zg_status zg_lm_head_dev(zg_ctx* ctx, const float* d_x, const void* d_w, float* d_logits, size_t in_dim,
+                                    size_t out_dim, uint32_t ggml_type, uint32_t interleave, uint64_t* d_best,
+                                    void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_x || !d_w || !d_best) return set_error(ctx, ZG_ERR_INVALID_ARG, "lm_head_dev: null pointer");
+  zg_status s = check_shape(ctx, ggml_type, interleave, in_dim, out_dim);
+  if (s) return s;
+  hipStream_t st = pick_stream(ctx, stream);
+  if ((s = hip_check(ctx, launch_fill_u64(d_best, 0, st), "reset"))) return s;
+  return run_linear(ctx, d_x, static_cast<const uint8_t*>(d_w), d_logits, in_dim, out_dim, ggml_type, interleave, 0,
+                    out_dim, EPI_ARGMAX, nullptr, d_best, PRO_PLAIN, nullptr, 0.0f, st);
+}
+
+extern "C" zg_status zg_dequant_dev(zg_ctx* ctx, const void* d_w, float* d_out, size_t rows, size_t in_dim,
+                                    uint32_t ggml_type, uint32_t interleave, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_w || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "dequant_dev: null pointer");
+  zg_status s = check_shape(ctx, ggml_type, interleave, in_dim, rows);
+  if (s) return s;
+  DequantArgs a{static_cast<const uint8_t*>(d_w), d_out, rows, in_dim, ggml_type, (int)interleave};
+  const bool pair = pair_path_ok(ggml_type, interleave, in_dim, rows, d_w, d_out);
+  return hip_check(ctx, launch_dequant(a, pair, pick_stream(ctx, stream)), "dequant launch");
+}
+
+extern "C" zg_status zg_fp16_to_f32_dev(zg_ctx* ctx, const uint16_t* d_in, float* d_out, size_t n, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_in || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "fp16_dev: null pointer");
+  return hip_check(ctx, launch_fp16(d_in, d_out, n, pick_stream(ctx, stream)), "fp16 launch");
+}

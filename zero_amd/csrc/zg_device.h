@@ -1,0 +1,52 @@
+// zg_device.h -- device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zg {
+
+// GgmlType ids (crates/zero-gguf-parser/src/lib.rs:95-126).
+enum QType : uint32_t { Q4_0 = 2, Q8_0 = 8, Q4K = 12, Q6K = 14 };
+
+// IEEE binary16 bits -> f32, bit-exact with fp16_to_f32
+// (crates/zero-gguf-parser/src/dequant.rs:28-61): normals and subnormals
+// through v_cvt_f32_f16 (exact; fp16 denormals are not flushed in the HIP
+// default float mode), inf/NaN rebuilt from the bits so that a signalling
+// NaN keeps its payload exactly as the reference's bit construction does
+// (the hardware conversion would quiet it).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+  h &= 0xFFFFu;
+  const float f = (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+  const uint32_t special = ((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13);
+  return ((h & 0x7C00u) == 0x7C00u) ? __uint_as_float(special) : f;
+}
+
+// Native 128-bit vector for global loads (nontemporal builtins need a
+// clang vector type, not HIP's uint4 wrapper).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Wave64 butterfly sum over aligned lane segments of width W (power of 2,
+// W <= 64).  Every lane of the segment ends with the segment total.
+template <int W>
+__device__ __forceinline__ float seg_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Order-preserving encoding of an argmax candidate into one u64 so that a
+// single atomicMax implements lm_argmax_propose
+// (kernel/src/inference_avx512.rs:1027-1044): larger value wins, equal
+// values go to the smaller index.  NaN is never encoded (callers skip it).
+// 0 means "no candidate".
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  uint32_t b = __float_as_uint(v);
+  // monotone float -> uint map: negative values flip all bits, positive set sign
+  uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  // -0.0 and +0.0 compare equal in IEEE; map both to the same key
+  if ((b & 0x7FFFFFFFu) == 0) k = 0x80000000u;
+  return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+
+}  // namespace zg

@@ -1,0 +1,74 @@
+// zg_internal.h -- host-side internals shared by the C ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "../../include/zero_gpu.h"
+
+namespace zg {
+
+// weight_layout.rs:45 caps the registry at 512 interleaved tensors; this
+// registry also holds plain tensors, so it is larger.
+constexpr size_t kMaxEntries = 4096;
+// Largest in_dim the LDS-staged pair kernel accepts (x plus block sums must
+// fit one workgroup's LDS allocation).
+constexpr size_t kMaxPairK = 15360;
+
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+struct RegEntry {
+  uintptr_t key = 0;  // host start address (weight_layout.rs ADDRS)
+  size_t bytes = 0;
+  uint32_t qt = 0;
+  uint32_t il = 1;    // weight_layout.rs GROUPS
+  void* dev = nullptr;
+  bool owned = false;
+};
+
+struct FusedDev {
+  const uint8_t* w;
+  float* y;
+  size_t n;
+  uint32_t qt;
+  uint32_t il;
+};
+
+}  // namespace zg
+
+struct zg_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<zg::RegEntry> reg;  // sorted by key
+  zg::DevBuf d_x, d_out, d_aux;
+  void* h_pinned = nullptr;
+  uint64_t* d_best = nullptr;
+  std::string last_error;
+};
+
+namespace zg {
+
+zg_status set_error(zg_ctx* ctx, zg_status code, const char* fmt, ...);
+zg_status hip_check(zg_ctx* ctx, hipError_t e, const char* what);
+size_t tensor_bytes(uint32_t qt, size_t rows, size_t k);
+zg_status ensure_buf(zg_ctx* ctx, DevBuf& b, size_t bytes);
+zg_status resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il);
+bool pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
+zg_status check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n);
+zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,
+                     uint32_t il, size_t start, size_t end, int epi, const float* resid, uint64_t* best, int pro,
+                     const float* norm_w, float eps, hipStream_t st);
+zg_status run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
+                    const float* norm_w, float eps, int epi, hipStream_t st);
+zg_status stage_in(zg_ctx* ctx, const void* src, size_t bytes, DevBuf& dst);
+zg_status lm_head_status(zg_ctx* ctx, uint64_t packed, size_t vocab_real, uint32_t* token, float* max_val);
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t st);
+
+}  // namespace zg

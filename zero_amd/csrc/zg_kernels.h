@@ -1,0 +1,62 @@
+// zg_kernels.h -- kernel argument blocks and host launchers (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace zg {
+
+enum Prologue : int { PRO_PLAIN = 0, PRO_RMSNORM = 1 };
+enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3 };
+
+// One projection of a (possibly fused) X4 GEMV launch.  Groups
+// [g_begin, g_begin + rows/4) of the launch's group space belong to it;
+// only local rows in [row_lo, row_hi) are stored.
+struct GemvSeg {
+  const uint8_t* w;
+  float* y;
+  const float* resid;  // EPI_RESID: y[row] = resid[row] + dot
+  uint32_t g_begin;
+  uint32_t row_lo, row_hi;
+};
+
+struct GemvArgs {
+  GemvSeg seg[3];
+  int nseg;
+  int k;                  // in_dim (multiple of 64 on the pair path)
+  uint32_t total_groups;  // groups over all segments
+  const float* x;         // activation (16-byte aligned)
+  const float* norm_w;    // PRO_RMSNORM gain
+  float eps;
+  uint64_t* best;         // EPI_ARGMAX packed candidate slot
+};
+
+struct GenericArgs {
+  const uint8_t* w;
+  const float* x;
+  float* y;
+  const float* resid;
+  uint64_t* best;
+  size_t k;
+  size_t row_lo, row_hi;
+  uint32_t qt;
+  int il;
+  int epi;
+};
+
+struct DequantArgs {
+  const uint8_t* w;
+  float* out;
+  size_t rows, k;
+  uint32_t qt;
+  int il;
+};
+
+hipError_t launch_gemv_x4_pair(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
+hipError_t launch_gemv_generic(const GenericArgs& a, hipStream_t st);
+hipError_t launch_dequant(const DequantArgs& a, bool pair_path, hipStream_t st);
+hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);
+hipError_t launch_fill_u64(uint64_t* p, uint64_t v, hipStream_t st);
+
+}  // namespace zg

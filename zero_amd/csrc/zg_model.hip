@@ -1,0 +1,608 @@
+// zg_model.hip -- single-token forward pass on the GPU, captured as HIP
+// graphs.
+//
+// Restates forward_single_token_avx512 (kernel/src/inference_avx512.rs:
+// 1826-1987) and lm_head_argmax_avx512 (:1200-1270) as a fixed sequence of
+// launches that reads the token id and position from device memory, so the
+// whole per-token sequence is one graph replay and greedy decoding feeds the
+// argmax back to the next step without a host round trip (the reference's
+// caller loop is kernel/src/inference.rs:1188-1330, 1644-1705, 1817-).
+//
+// Per layer:
+//   1. fused Q|K|V GEMV with rmsnorm(attn_norm) in the prologue
+//   2. attention partials: QK-norm + RoPE + KV-cache store + scores/softmax
+//      over one 32-token chunk of the context per workgroup (split-T)
+//   3. combine the chunks of each head
+//   4. O GEMV with the residual add in the epilogue
+//   5. fused gate|up GEMV with rmsnorm(ffn_norm) and SiLU(gate)*up epilogue
+//   6. down GEMV with the residual add in the epilogue
+// LM head: GEMV with rmsnorm(output_norm) prologue and argmax epilogue, then
+// a one-thread finalize kernel.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstring>
+#include <vector>
+
+#include "../../include/zero_gpu.h"
+#include "zg_device.h"
+#include "zg_internal.h"
+#include "zg_kernels.h"
+
+using namespace zg;
+
+namespace zg {
+
+constexpr int kChunk = 32;  // context tokens per attention workgroup
+constexpr int kMaxG = 8;    // max query heads per KV head
+
+// Device-resident decode state.
+struct DevState {
+  uint32_t token;    // token fed to the next forward pass
+  uint32_t pos;      // its position
+  uint32_t gen;      // tokens produced by finalize so far
+  uint32_t err;      // bit 0 non-finite logits, 1 argmax in padding, 2 attention
+  uint32_t n_prompt;
+  uint32_t gen_cap;
+  uint32_t err_step; // gen index at the first error (valid if err != 0)
+  uint32_t pad;
+  uint64_t best;     // last packed argmax (copy of the LM head slot)
+};
+
+// embed_lookup_dispatch (forward_pass.rs:311-370) for plain Q4_0/Q8_0 rows;
+// also clears the LM-head argmax slot for this step.
+__global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
+                             DevState* __restrict__ st, uint64_t* __restrict__ best,
+                             float* __restrict__ out) {
+  const uint32_t tok = st->token;
+  const int nb = hidden / 32;
+  const int bb = (qt == Q4_0) ? 18 : 34;
+  const uint8_t* row = embd + (size_t)tok * nb * bb;
+  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
+    const uint8_t* blk = row + (e / 32) * bb;
+    const float d = half_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    const int j = e & 31;
+    float v;
+    if (qt == Q4_0) {
+      const int q = (j < 16) ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
+      v = (float)(q - 8) * d;
+    } else {
+      v = (float)(int8_t)blk[2 + j] * d;
+    }
+    out[e] = v;
+  }
+  if (threadIdx.x == 0) *best = 0;
+}
+
+struct AttnArgs {
+  const float* q;      // raw Q projection [nq*HD]
+  const float* k;      // raw K projection [nkv*HD]
+  const float* v;      // raw V projection [nkv*HD]
+  const float* q_norm; // [HD]
+  const float* k_norm; // [HD]
+  const float* inv_freq;  // [HD/2]
+  float* kcache;       // this layer's K rows [max_ctx][nkv*HD]
+  float* vcache;       // this layer's V rows
+  float* part;         // partials [nq][nchunks][HD+2]
+  DevState* st;
+  int nkv, g, nchunks;
+  float eps, scale;
+};
+
+// QK-norm (rmsnorm over one head, ops.rs:29-52) then NeoX RoPE
+// (ops.rs:111-132) of one head held in LDS, by one wave.
+template <int HD>
+__device__ __forceinline__ void norm_rope_head(float* h, const float* w, const float* inv_freq, float pos_f,
+                                               float eps, int lane) {
+  constexpr int HALF = HD / 2;
+  float a = 0.0f, b = 0.0f;
+  if (lane < HALF) {
+    a = h[lane];
+    b = h[lane + HALF];
+  }
+  const float ssq = seg_sum<64>(a * a + b * b);
+  const float rinv = 1.0f / sqrtf(ssq / (float)HD + eps);
+  if (lane < HALF) {
+    const float x = a * rinv * w[lane];
+    const float y = b * rinv * w[lane + HALF];
+    const float th = pos_f * inv_freq[lane];
+    const float c = cosf(th), s = sinf(th);
+    h[lane] = x * c - y * s;
+    h[lane + HALF] = x * s + y * c;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  const int kvh = blockIdx.x, ch = blockIdx.y;
+  const int pos = (int)a.st->pos;
+  const int T = pos + 1;
+  const int c0 = ch * kChunk;
+  if (c0 >= T) return;  // uniform per workgroup
+  const int c1 = min(c0 + kChunk, T);
+  const int G = a.g;
+  const int kvd = a.nkv * HD;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float qs[kMaxG][HD];
+  __shared__ float knew[HD];
+  __shared__ float sc[kMaxG][kChunk];
+  __shared__ float mx[kMaxG], sm[kMaxG];
+  const bool has_pos = pos < c1;  // this chunk holds the current token
+  const float pos_f = (float)pos;
+
+  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = a.q[(kvh * G) * HD + i];
+  if (has_pos)
+    for (int i = tid; i < HD; i += 256) knew[i] = a.k[kvh * HD + i];
+  __syncthreads();
+  for (int hh = wave; hh < G + (has_pos ? 1 : 0); hh += 4) {
+    if (hh < G) norm_rope_head<HD>(qs[hh], a.q_norm, a.inv_freq, pos_f, a.eps, lane);
+    else norm_rope_head<HD>(knew, a.k_norm, a.inv_freq, pos_f, a.eps, lane);
+  }
+  __syncthreads();
+  if (has_pos) {
+    // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
+    for (int i = tid; i < HD; i += 256) {
+      a.kcache[(size_t)pos * kvd + kvh * HD + i] = knew[i];
+      a.vcache[(size_t)pos * kvd + kvh * HD + i] = a.v[kvh * HD + i];
+    }
+  }
+  // scores: 16 lanes per (head, token) dot product, 4 dots per wave
+  const int n_t = c1 - c0;
+  const int sub = lane >> 4, l16 = lane & 15;
+  for (int base = wave * 4; base < G * kChunk; base += 16) {
+    const int idx = base + sub;
+    const int g = idx / kChunk, tt = idx % kChunk;
+    float part = 0.0f;
+    if (g < G && tt < n_t) {
+      const int t = c0 + tt;
+      const float* krow = (t == pos) ? knew : a.kcache + (size_t)t * kvd + kvh * HD;
+#pragma unroll
+      for (int e = l16; e < HD; e += 16) part = fmaf(qs[g][e], krow[e], part);
+    }
+    part = seg_sum<16>(part);
+    if (l16 == 0 && g < G && tt < n_t) sc[g][tt] = part * a.scale;
+  }
+  __syncthreads();
+  // per-head chunk max and exp-sum (softmax, attention.rs:48-84)
+  if (wave == 0) {
+    for (int g = 0; g < G; g++) {
+      float m = (lane < n_t) ? sc[g][lane] : -INFINITY;
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      float e = (lane < n_t) ? expf(sc[g][lane] - m) : 0.0f;
+      if (lane < n_t) sc[g][lane] = e;
+      const float l = seg_sum<64>(e);
+      if (lane == 0) {
+        mx[g] = m;
+        sm[g] = l;
+        if (!isfinite(m)) atomicOr(&a.st->err, 4u);
+      }
+    }
+  }
+  __syncthreads();
+  // o[g][d] = sum_t e_t * v_t[d], ascending t (weighted_add order)
+  for (int i = tid; i < G * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    float o = 0.0f;
+    for (int tt = 0; tt < n_t; tt++) {
+      const int t = c0 + tt;
+      const float vv = (t == pos) ? a.v[kvh * HD + d] : a.vcache[(size_t)t * kvd + kvh * HD + d];
+      o = fmaf(sc[g][tt], vv, o);
+    }
+    float* p = a.part + ((size_t)(kvh * G + g) * a.nchunks + ch) * (HD + 2);
+    p[2 + d] = o;
+    if (d == 0) {
+      p[0] = mx[g];
+      p[1] = sm[g];
+    }
+  }
+}
+
+// Merge the chunk partials of one query head.
+template <int HD>
+__global__ void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out, int nchunks,
+                                    const DevState* __restrict__ st) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const int T = (int)st->pos + 1;
+  const int nc = (T + kChunk - 1) / kChunk;
+  const float* p = part + (size_t)h * nchunks * (HD + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < nc; c++) M = fmaxf(M, p[c * (HD + 2)]);
+  float L = 0.0f, o = 0.0f;
+  for (int c = 0; c < nc; c++) {
+    const float w = expf(p[c * (HD + 2)] - M);
+    L = fmaf(w, p[c * (HD + 2) + 1], L);
+    o = fmaf(w, p[c * (HD + 2) + 2 + d], o);
+  }
+  out[h * HD + d] = o * (1.0f / L);
+}
+
+__global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
+                               int n, float eps) {
+  __shared__ float red[4];
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) ssq += x[i] * x[i];
+  ssq = seg_sum<64>(ssq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ssq;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rinv = 1.0f / sqrtf(tot / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += 256) out[i] = x[i] * rinv * w[i];
+}
+
+// After the LM head: argmax -> next token, error bits, output record.
+__global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t vocab_real, uint32_t* out_tokens) {
+  const uint64_t key = *best;
+  uint32_t idx = 0;
+  uint32_t err = 0;
+  if (key == 0) {
+    err = 1;
+  } else {
+    const uint32_t k = (uint32_t)(key >> 32);
+    const uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    const float v = __uint_as_float(b);
+    idx = 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu);
+    if (!isfinite(v)) err = 1;
+    else if (idx >= vocab_real) err = 2;
+  }
+  if (err && st->err == 0) st->err_step = st->gen;
+  st->err |= err;
+  st->best = key;
+  st->token = idx;
+  if (out_tokens && st->gen < st->gen_cap) out_tokens[st->gen] = idx;
+  st->gen += 1;
+}
+
+// Move to the next position; during the prompt, feed the next prompt token.
+__global__ void advance_kernel(DevState* st, const uint32_t* prompt) {
+  const uint32_t p = st->pos + 1;
+  st->pos = p;
+  if (p < st->n_prompt) st->token = prompt[p];
+}
+
+}  // namespace zg
+
+hipError_t zg::launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, n, eps);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Model object
+// ---------------------------------------------------------------------------
+
+struct ZLayer {
+  const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+  float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+};
+
+struct zg_model {
+  zg_ctx* ctx = nullptr;
+  zg_model_desc d{};
+  std::vector<ZLayer> layers;
+  const uint8_t* embd = nullptr;
+  const uint8_t* head = nullptr;
+  float* out_norm = nullptr;
+  float* inv_freq = nullptr;
+  float* kv = nullptr;
+  float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
+  float* logits = nullptr;
+  float* part = nullptr;
+  uint64_t* best = nullptr;
+  zg::DevState* st = nullptr;
+  uint32_t* prompt = nullptr;  // device prompt buffer
+  size_t prompt_cap = 0;
+  uint32_t* out_tokens = nullptr;
+  size_t out_cap = 0;
+  int nchunks = 0;
+  std::vector<void*> owned;  // device allocations to free
+  hipGraphExec_t g_layers = nullptr, g_head = nullptr, g_adv = nullptr;
+};
+
+static zg_status model_alloc(zg_model* m, void** p, size_t bytes) {
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  m->owned.push_back(*p);
+  e = hipMemset(*p, 0, bytes);
+  return hip_check(m->ctx, e, "model: memset");
+}
+
+static zg_status upload_f32(zg_model* m, float** dst, const float* src, size_t n) {
+  zg_status s = model_alloc(m, reinterpret_cast<void**>(dst), n * sizeof(float));
+  if (s) return s;
+  return hip_check(m->ctx, hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice), "model: upload");
+}
+
+static zg_status weight_dev(zg_model* m, const void* key, uint32_t qt, uint32_t il, size_t rows, size_t k,
+                            const uint8_t** out) {
+  if (!key) return set_error(m->ctx, ZG_ERR_INVALID_ARG, "model: null weight");
+  if (m->d.device_pointers) {
+    *out = static_cast<const uint8_t*>(key);
+    return ZG_OK;
+  }
+  uint32_t got_il;
+  zg_status s = resolve(m->ctx, key, tensor_bytes(qt, rows, k), qt, out, &got_il);
+  if (s) return s;
+  if (got_il != il) return set_error(m->ctx, ZG_ERR_INVALID_ARG, "model: weight %p layout %u, expected %u", key, got_il, il);
+  return ZG_OK;
+}
+
+// Record the per-token sequence on the context stream.
+static zg_status record_layers(zg_model* m, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
+  const int qd = (int)(d.n_q_heads * d.head_dim), kvd = (int)(d.n_kv_heads * d.head_dim);
+  zg_ctx* ctx = m->ctx;
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, m->embd, d.embd_type, H, m->st, m->best, m->hidden);
+  zg_status s = hip_check(ctx, hipGetLastError(), "embed launch");
+  if (s) return s;
+  const float scale = 1.0f / sqrtf((float)HD);
+  for (uint32_t l = 0; l < d.n_layers; l++) {
+    const ZLayer& L = m->layers[l];
+    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, d.lin_type, 4},
+                       {L.k, m->k, (size_t)kvd, d.lin_type, 4},
+                       {L.v, m->v, (size_t)kvd, d.lin_type, 4}};
+    if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
+    AttnArgs aa{};
+    aa.q = m->q;
+    aa.k = m->k;
+    aa.v = m->v;
+    aa.q_norm = L.q_norm;
+    aa.k_norm = L.k_norm;
+    aa.inv_freq = m->inv_freq;
+    aa.kcache = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
+    aa.vcache = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
+    aa.part = m->part;
+    aa.st = m->st;
+    aa.nkv = (int)d.n_kv_heads;
+    aa.g = (int)(d.n_q_heads / d.n_kv_heads);
+    aa.nchunks = m->nchunks;
+    aa.eps = d.rms_eps;
+    aa.scale = scale;
+    if (HD == 128) {
+      hipLaunchKernelGGL(attn_partial_kernel<128>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
+      hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(d.n_q_heads), dim3(128), 0, st, m->part, m->attn, m->nchunks,
+                         m->st);
+    } else {
+      hipLaunchKernelGGL(attn_partial_kernel<64>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
+      hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(d.n_q_heads), dim3(64), 0, st, m->part, m->attn, m->nchunks,
+                         m->st);
+    }
+    if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
+    if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
+                        PRO_PLAIN, nullptr, 0.0f, st)))
+      return s;
+    FusedDev gu[2] = {{L.gate, m->act, (size_t)F, d.lin_type, 4}, {L.up, nullptr, (size_t)F, d.lin_type, 4}};
+    if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
+    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
+                        PRO_PLAIN, nullptr, 0.0f, st)))
+      return s;
+  }
+  return ZG_OK;
+}
+
+static zg_status record_head(zg_model* m, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  zg_status s = run_linear(m->ctx, m->hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
+                           d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM,
+                           m->out_norm, d.rms_eps, st);
+  if (s) return s;
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
+  return hip_check(m->ctx, hipGetLastError(), "finalize launch");
+}
+
+static zg_status record_advance(zg_model* m, hipStream_t st) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->st, m->prompt);
+  return hip_check(m->ctx, hipGetLastError(), "advance launch");
+}
+
+static zg_status capture(zg_model* m, zg_status (*rec)(zg_model*, hipStream_t), hipGraphExec_t* out) {
+  zg_ctx* ctx = m->ctx;
+  hipGraph_t g = nullptr;
+  zg_status s = hip_check(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+  if (s) return s;
+  zg_status rs = rec(m, ctx->stream);
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+  if (rs) {
+    if (g) hipGraphDestroy(g);
+    return rs;
+  }
+  if ((s = hip_check(ctx, e, "end capture"))) return s;
+  e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  return hip_check(ctx, e, "graph instantiate");
+}
+
+extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_model** out) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!desc || !out || !desc->layers) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: null descriptor");
+  *out = nullptr;
+  const zg_model_desc& d = *desc;
+  if (d.n_layers == 0 || d.hidden == 0 || d.ffn == 0 || d.n_kv_heads == 0 || d.n_q_heads % d.n_kv_heads ||
+      d.n_q_heads / d.n_kv_heads > (uint32_t)kMaxG || (d.head_dim != 128 && d.head_dim != 64) || d.max_ctx == 0 ||
+      d.vocab_real > d.vocab_padded || d.vocab_padded == 0)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "model: unsupported dimensions");
+  if (d.lin_interleave != 4 || (d.lin_type != ZG_Q4_0 && d.lin_type != ZG_Q8_0))
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: layer linears must be Q4_0X4 or Q8_0X4");
+  if (d.embd_type != ZG_Q4_0 && d.embd_type != ZG_Q8_0)
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: token_embd must be plain Q4_0 or Q8_0");
+  const size_t qd = (size_t)d.n_q_heads * d.head_dim, kvd = (size_t)d.n_kv_heads * d.head_dim;
+  for (size_t kk : {(size_t)d.hidden, qd, (size_t)d.ffn})
+    if (kk % 64 || kk > kMaxPairK) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: in_dim %zu not supported", kk);
+  if (qd % 4 || kvd % 4 || d.ffn % 4 || d.hidden % 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: rows % 4");
+  hipSetDevice(ctx->device);
+  zg_model* m = new zg_model();
+  m->ctx = ctx;
+  m->d = d;
+  m->d.layers = nullptr;
+  zg_status s = ZG_OK;
+  const size_t H = d.hidden, F = d.ffn;
+  m->layers.resize(d.n_layers);
+  for (uint32_t l = 0; l < d.n_layers && !s; l++) {
+    const zg_layer_weights& W = d.layers[l];
+    ZLayer& L = m->layers[l];
+    if (!W.attn_norm || !W.ffn_norm || !W.q_norm || !W.k_norm) {
+      s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null norm weight");
+      break;
+    }
+    if ((s = weight_dev(m, W.attn_q, d.lin_type, 4, qd, H, &L.q))) break;
+    if ((s = weight_dev(m, W.attn_k, d.lin_type, 4, kvd, H, &L.k))) break;
+    if ((s = weight_dev(m, W.attn_v, d.lin_type, 4, kvd, H, &L.v))) break;
+    if ((s = weight_dev(m, W.attn_o, d.lin_type, 4, H, qd, &L.o))) break;
+    if ((s = weight_dev(m, W.ffn_gate, d.lin_type, 4, F, H, &L.gate))) break;
+    if ((s = weight_dev(m, W.ffn_up, d.lin_type, 4, F, H, &L.up))) break;
+    if ((s = weight_dev(m, W.ffn_down, d.lin_type, 4, H, F, &L.down))) break;
+    if ((s = upload_f32(m, &L.attn_norm, W.attn_norm, H))) break;
+    if ((s = upload_f32(m, &L.ffn_norm, W.ffn_norm, H))) break;
+    if ((s = upload_f32(m, &L.q_norm, W.q_norm, d.head_dim))) break;
+    if ((s = upload_f32(m, &L.k_norm, W.k_norm, d.head_dim))) break;
+  }
+  if (!s) s = weight_dev(m, d.token_embd, d.embd_type, 1, d.vocab_padded, H, &m->embd);
+  if (!s) s = weight_dev(m, d.lm_head, d.head_type, d.head_interleave, d.vocab_padded, H, &m->head);
+  if (!s && !d.output_norm) s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null output_norm");
+  if (!s) s = upload_f32(m, &m->out_norm, d.output_norm, H);
+  if (!s) {
+    // RopeContext::new (ops.rs:79-93): inv_freq[i] = theta^(-2i/head_dim) in f32
+    std::vector<float> inv(d.head_dim / 2);
+    for (uint32_t i = 0; i < d.head_dim / 2; i++) {
+      const float ex = -2.0f * (float)i / (float)d.head_dim;
+      inv[i] = powf(d.rope_theta, ex);
+    }
+    s = upload_f32(m, &m->inv_freq, inv.data(), inv.size());
+  }
+  m->nchunks = (int)((d.max_ctx + kChunk - 1) / kChunk);
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->kv), (size_t)d.n_layers * 2 * d.max_ctx * kvd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->hidden), H * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->q), qd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->k), kvd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->v), kvd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->attn), qd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->act), F * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->logits), (size_t)d.vocab_padded * sizeof(float));
+  if (!s)
+    s = model_alloc(m, reinterpret_cast<void**>(&m->part),
+                    (size_t)d.n_q_heads * m->nchunks * (d.head_dim + 2) * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
+  m->prompt_cap = d.max_ctx;
+  m->out_cap = d.max_ctx;
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->prompt), m->prompt_cap * sizeof(uint32_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->out_tokens), m->out_cap * sizeof(uint32_t));
+  // the generic LM-head path normalizes into the context's aux buffer;
+  // allocate it before capture (no allocation inside a captured stream)
+  if (!s) s = ensure_buf(ctx, ctx->d_aux, H * sizeof(float));
+  if (!s) s = capture(m, record_layers, &m->g_layers);
+  if (!s) s = capture(m, record_head, &m->g_head);
+  if (!s) s = capture(m, record_advance, &m->g_adv);
+  if (s) {
+    zg_model_destroy(m);
+    return s;
+  }
+  *out = m;
+  return ZG_OK;
+}
+
+extern "C" void zg_model_destroy(zg_model* m) {
+  if (!m) return;
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+  for (hipGraphExec_t g : {m->g_layers, m->g_head, m->g_adv})
+    if (g) hipGraphExecDestroy(g);
+  for (void* p : m->owned) hipFree(p);
+  delete m;
+}
+
+static zg_status set_state(zg_model* m, uint32_t token, uint32_t pos, uint32_t n_prompt, uint32_t gen_cap) {
+  DevState h{};
+  h.token = token;
+  h.pos = pos;
+  h.n_prompt = n_prompt;
+  h.gen_cap = gen_cap;
+  return hip_check(m->ctx, hipMemcpyAsync(m->st, &h, sizeof h, hipMemcpyHostToDevice, m->ctx->stream), "state upload");
+}
+
+static zg_status state_status(zg_model* m, const DevState& h) {
+  if (h.err & 4u) return set_error(m->ctx, ZG_ERR_ATTENTION, "attention: non-finite scores");
+  if (h.err & 1u) return set_error(m->ctx, ZG_ERR_NONFINITE_LOGITS, "LM head: non-finite logits (step %u)", h.err_step);
+  if (h.err & 2u) return set_error(m->ctx, ZG_ERR_ARGMAX_IN_PADDING, "LM head: argmax in padding (step %u)", h.err_step);
+  return ZG_OK;
+}
+
+// Every step writes KV row `pos` before any read of rows <= pos, and every
+// step or generate call uploads its own position, so a new sequence needs
+// no device work: reset only waits for in-flight work.
+extern "C" void zg_model_reset(zg_model* m) {
+  if (!m) return;
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+}
+
+extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, float* hidden_out, float* logits,
+                                   uint32_t* next_token, float* max_logit) {
+  if (!m) return ZG_ERR_INVALID_ARG;
+  zg_ctx* ctx = m->ctx;
+  if (pos >= m->d.max_ctx) return set_error(ctx, ZG_ERR_CONTEXT_FULL, "position %u >= max_ctx %u", pos, m->d.max_ctx);
+  if (token >= m->d.vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "token %u out of range", token);
+  hipSetDevice(ctx->device);
+  zg_status s = set_state(m, token, pos, 0, 0);
+  if (s) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
+  zg::DevState h{};
+  if ((s = hip_check(ctx, hipMemcpyAsync(&h, m->st, sizeof h, hipMemcpyDeviceToHost, ctx->stream), "state download")))
+    return s;
+  if (hidden_out &&
+      (s = hip_check(ctx, hipMemcpyAsync(hidden_out, m->hidden, m->d.hidden * 4, hipMemcpyDeviceToHost, ctx->stream),
+                     "download")))
+    return s;
+  if (logits && (s = hip_check(ctx, hipMemcpyAsync(logits, m->logits, (size_t)m->d.vocab_padded * 4,
+                                                   hipMemcpyDeviceToHost, ctx->stream), "download")))
+    return s;
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  if ((s = state_status(m, h))) return s;
+  return lm_head_status(ctx, h.best, m->d.vocab_real, next_token, max_logit);
+}
+
+extern "C" zg_status zg_model_generate(zg_model* m, const uint32_t* prompt, size_t n_prompt, size_t n_gen,
+                                       uint32_t* out_tokens, double* prefill_seconds, double* gen_seconds) {
+  if (!m) return ZG_ERR_INVALID_ARG;
+  zg_ctx* ctx = m->ctx;
+  if (!prompt || n_prompt == 0 || n_gen == 0 || !out_tokens) return set_error(ctx, ZG_ERR_INVALID_ARG, "generate: bad args");
+  if (n_prompt + n_gen - 1 > m->d.max_ctx || n_prompt > m->prompt_cap || n_gen > m->out_cap)
+    return set_error(ctx, ZG_ERR_CONTEXT_FULL, "generate: %zu + %zu tokens exceed max_ctx %u", n_prompt, n_gen,
+                     m->d.max_ctx);
+  for (size_t i = 0; i < n_prompt; i++)
+    if (prompt[i] >= m->d.vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "generate: prompt token out of range");
+  hipSetDevice(ctx->device);
+  zg_status s = hip_check(ctx, hipMemcpyAsync(m->prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice, ctx->stream),
+                          "prompt upload");
+  if (s) return s;
+  if ((s = set_state(m, prompt[0], 0, (uint32_t)n_prompt, (uint32_t)n_gen))) return s;
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  auto t0 = std::chrono::steady_clock::now();
+  // prefill: prompt tokens 0..n-2 through the layers; the last one also
+  // through the LM head, producing generated token 0
+  for (size_t i = 0; i + 1 < n_prompt; i++) {
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
+  }
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  auto t1 = std::chrono::steady_clock::now();
+  // greedy decode: each generated token goes back through the layers
+  for (size_t j = 1; j < n_gen; j++) {
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
+  }
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  auto t2 = std::chrono::steady_clock::now();
+  if (prefill_seconds) *prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+  if (gen_seconds) *gen_seconds = std::chrono::duration<double>(t2 - t1).count();
+  zg::DevState h{};
+  if ((s = hip_check(ctx, hipMemcpy(&h, m->st, sizeof h, hipMemcpyDeviceToHost), "state download"))) return s;
+  if ((s = hip_check(ctx, hipMemcpy(out_tokens, m->out_tokens, n_gen * 4, hipMemcpyDeviceToHost), "tokens download")))
+    return s;
+  return state_status(m, h);
+}

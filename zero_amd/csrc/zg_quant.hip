@@ -1,0 +1,336 @@
+// zg_quant.hip -- on-the-fly Q8_0 activation quantization and the M >= 64
+// prefill GEMM (int8 MFMA) for gfx950.
+//
+// The reference has no batched prefill (kernel/src/inference.rs:1188-1330
+// runs the prompt token by token) and never quantizes activations on its
+// Q4_0/Q8_0 path.  The quantizer restates the packer's Q8_0 block encoder
+// (tools/silicatepack.py:893-907, fp16 bytes :854-861) bit for bit: the
+// amax, d = amax/127, 1/d and x/d are computed in double as Python does,
+// round() is round-half-even (rint), and d is stored as the
+// round-to-nearest-even binary16 of the double d.
+#include <hip/hip_runtime.h>
+
+#include "../../include/zero_gpu.h"
+#include "zg_device.h"
+#include "zg_internal.h"
+
+using namespace zg;
+
+namespace zg {
+
+// binary64 -> binary16, round to nearest even, for finite |v| <= 65504
+// (the packer clamps to that range first, silicatepack.py:854-861).
+__device__ __forceinline__ uint32_t f64_to_f16_rne(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t sign = (uint32_t)(u >> 48) & 0x8000u;
+  const uint64_t a = u & 0x7FFFFFFFFFFFFFFFull;
+  if (a == 0) return sign;
+  const int e = (int)(a >> 52) - 1023;
+  const uint64_t mant = (a & ((1ull << 52) - 1)) | (1ull << 52);
+  if (e < -14) {
+    // subnormal half: count units of 2^-24
+    const int s = 28 - e;
+    if (s >= 64) return sign;
+    const uint64_t q = mant >> s;
+    const uint64_t rem = mant & ((1ull << s) - 1);
+    const uint64_t half = 1ull << (s - 1);
+    const uint64_t r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+    return sign | (uint32_t)r;  // r == 1024 encodes the smallest normal
+  }
+  uint64_t q = mant >> 42;
+  const uint64_t rem = mant & ((1ull << 42) - 1);
+  const uint64_t half = 1ull << 41;
+  if (rem > half || (rem == half && (q & 1))) q++;
+  int eb = e + 15;
+  if (q == 2048) {
+    q = 1024;
+    eb++;
+  }
+  return sign | ((uint32_t)eb << 10) | ((uint32_t)q & 0x3FFu);
+}
+
+struct QuantArgs {
+  const float* x;   // [rows][k]
+  uint8_t* blocks;  // optional: [rows][k/32] x 34-byte Q8_0 blocks
+  int8_t* qs;       // optional: [rows][k] int8
+  uint16_t* d;      // optional: [rows][k/32] fp16 bits
+  size_t rows, k;
+};
+
+// One thread per 32-element block.  A block holding a non-finite value (the
+// packer raises ValueError there, silicatepack.py:877-887) is written with
+// q = 0 and d = NaN (0x7E00) so that it cannot pass unnoticed.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(QuantArgs a) {
+  const size_t nb = a.k / 32;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.rows * nb) return;
+  const size_t row = t / nb, b = t % nb;
+  const float4* src = reinterpret_cast<const float4*>(a.x + row * a.k + b * 32);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float4 f = src[i];
+    v[4 * i] = f.x;
+    v[4 * i + 1] = f.y;
+    v[4 * i + 2] = f.z;
+    v[4 * i + 3] = f.w;
+  }
+  bool finite = true;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    finite = finite && isfinite(v[i]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  uint32_t dbits = 0;
+  int8_t q[32];
+  if (!finite) {
+    dbits = 0x7E00u;
+#pragma unroll
+    for (int i = 0; i < 32; i++) q[i] = 0;
+  } else if (amax == 0.0f) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) q[i] = 0;
+  } else {
+    const double dd = (double)amax / 127.0;
+    const double inv = 1.0 / dd;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      double r = rint((double)v[i] * inv);
+      r = fmin(127.0, fmax(-127.0, r));
+      q[i] = (int8_t)(int)r;
+    }
+    dbits = f64_to_f16_rne(fmin(dd, 65504.0));
+  }
+  if (a.qs) {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      w[i] = (uint32_t)(uint8_t)q[4 * i] | ((uint32_t)(uint8_t)q[4 * i + 1] << 8) |
+             ((uint32_t)(uint8_t)q[4 * i + 2] << 16) | ((uint32_t)(uint8_t)q[4 * i + 3] << 24);
+    u32x4* dst = reinterpret_cast<u32x4*>(a.qs + row * a.k + b * 32);
+    dst[0] = u32x4{w[0], w[1], w[2], w[3]};
+    dst[1] = u32x4{w[4], w[5], w[6], w[7]};
+  }
+  if (a.d) a.d[row * nb + b] = (uint16_t)dbits;
+  if (a.blocks) {
+    uint8_t* o = a.blocks + (row * nb + b) * 34;
+    // 34-byte blocks are only 2-byte aligned: 17 halfword stores
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(o);
+    o16[0] = (uint16_t)dbits;
+#pragma unroll
+    for (int i = 0; i < 16; i++) o16[1 + i] = (uint16_t)((uint8_t)q[2 * i] | ((uint16_t)(uint8_t)q[2 * i + 1] << 8));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM: Y[m][n] = sum_b dX[m][b] * dW[n][b] * sum_{k in b} qX*qW.
+// v_mfma_i32_16x16x32_i8: one MFMA is exactly one 32-element block of a
+// 16x16 output tile, so each block's int32 dot is scaled once by its two
+// fp16 scales and accumulated in fp32 as acc = fma(dX*dW, isum, acc) in
+// ascending block order (the operation order of the oracle's
+// zo_gemm_q8act, so results match it bit for bit).  Workgroup tile 64 (m) x 64 (n), 4 waves of
+// 32 x 32 (2 x 2 MFMA tiles), 4 blocks (128 K) staged in LDS per step.
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+  const int8_t* xq;    // [m][k]
+  const uint16_t* xd;  // [m][k/32]
+  const uint8_t* w;    // weights, Q4_0/Q8_0, plain or X4
+  float* y;            // [m][n]
+  int m, n, k;
+};
+
+constexpr int kBM = 64, kBN = 64, kBK = 4;  // kBK blocks of 32 per stage
+constexpr int kRow = kBK * 32 + 16;         // LDS row stride in bytes (padded, 16-B aligned)
+
+template <uint32_t WT, int IL>
+__global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t As[kBM * kRow];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[kBN * kRow];
+  __shared__ float Ad[kBM][kBK];
+  __shared__ float Bd[kBN][kBK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int nb = a.k / 32;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  float acc[2][2][4];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
+
+  for (int b0 = 0; b0 < nb; b0 += kBK) {
+    __syncthreads();
+    // A tile: 64 rows x kBK blocks of 32 int8 (row-major, 16-B chunks)
+    for (int c = tid; c < kBM * kBK * 2; c += 256) {
+      const int row = c / (kBK * 2), ch = c % (kBK * 2);
+      const int gm = m0 + row, kb = b0 + ch / 2;
+      u32x4 v = {0, 0, 0, 0};
+      if (gm < a.m && kb < nb) v = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
+      *reinterpret_cast<u32x4*>(As + row * kRow + ch * 16) = v;
+    }
+    {
+      const int row = tid / kBK, kk = tid % kBK;
+      const int gm = m0 + row, kb = b0 + kk;
+      Ad[row][kk] = (gm < a.m && kb < nb) ? half_bits_to_f32(a.xd[(size_t)gm * nb + kb]) : 0.0f;
+    }
+    // B tile: 64 weight rows x kBK blocks, unpacked to signed int8
+    {
+      const int row = tid / kBK, kk = tid % kBK;
+      const int gn = n0 + row, kb = b0 + kk;
+      uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float dw = 0.0f;
+      if (gn < a.n && kb < nb) {
+        const uint8_t* dp;
+        const uint8_t* qp;
+        if (IL == 4) {
+          const size_t gb = (WT == Q4_0) ? 72 : 136;
+          const uint8_t* g = a.w + (size_t)(gn >> 2) * nb * gb + (size_t)kb * gb;
+          dp = g + 2 * (gn & 3);
+          qp = g + 8 + (gn & 3) * ((WT == Q4_0) ? 16 : 32);
+        } else {
+          const size_t bb = (WT == Q4_0) ? 18 : 34;
+          dp = a.w + ((size_t)gn * nb + kb) * bb;
+          qp = dp + 2;
+        }
+        dw = half_bits_to_f32((uint32_t)dp[0] | ((uint32_t)dp[1] << 8));
+        if (WT == Q4_0) {
+          uint32_t raw[4];
+          if (IL == 4) {
+            const uint2 lo = *reinterpret_cast<const uint2*>(qp);
+            const uint2 hi = *reinterpret_cast<const uint2*>(qp + 8);
+            raw[0] = lo.x; raw[1] = lo.y; raw[2] = hi.x; raw[3] = hi.y;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              raw[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
+                       ((uint32_t)qp[4 * i + 3] << 24);
+          }
+          // (nibble - 8) as a signed byte == nibble XOR 8 sign-extended:
+          // (n ^ 8) - 8 in 4 bits; compute bytewise via (n | 0xF0) when n < 8
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const uint32_t lo = raw[i] & 0x0F0F0F0Fu;          // elements 4i..4i+3
+            const uint32_t hi = (raw[i] >> 4) & 0x0F0F0F0Fu;   // elements 16+4i..
+            // bytewise n - 8 without borrow across bytes: (n + 0x78) ^ 0x80
+            q[i] = ((lo + 0x78787878u) ^ 0x80808080u);
+            q[4 + i] = ((hi + 0x78787878u) ^ 0x80808080u);
+          }
+        } else {
+          if (IL == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * i);
+              q[2 * i] = v.x;
+              q[2 * i + 1] = v.y;
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+              q[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
+                     ((uint32_t)qp[4 * i + 3] << 24);
+          }
+        }
+      }
+      u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * kRow + kk * 32);
+      dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+      dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+      Bd[row][kk] = dw;
+    }
+    __syncthreads();
+    const int r16 = lane & 15, kq = (lane >> 4) * 8;
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk++) {
+      long av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) av[i] = *reinterpret_cast<const long*>(As + (wm + 16 * i + r16) * kRow + kk * 32 + kq);
+#pragma unroll
+      for (int j = 0; j < 2; j++) bv[j] = *reinterpret_cast<const long*>(Bs + (wn + 16 * j + r16) * kRow + kk * 32 + kq);
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+          const float dwv = Bd[wn + 16 * j + r16][kk];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float s = __fmul_rn(Ad[wm + 16 * i + (lane >> 4) * 4 + r][kk], dwv);
+            acc[i][j][r] = fmaf(s, (float)c[r], acc[i][j][r]);
+          }
+        }
+    }
+  }
+  // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int gm = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
+        const int gn = n0 + wn + 16 * j + (lane & 15);
+        if (gm < a.m && gn < a.n) a.y[(size_t)gm * a.n + gn] = acc[i][j][r];
+      }
+}
+
+}  // namespace zg
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+static hipStream_t qstream(zg_ctx* ctx, void* s) { return s ? reinterpret_cast<hipStream_t>(s) : ctx->stream; }
+
+static zg_status launch_quant(zg_ctx* ctx, const float* x, uint8_t* blocks, int8_t* qs, uint16_t* d, size_t rows,
+                              size_t k, void* stream) {
+  if (!x || (!blocks && !qs && !d)) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize: null pointer");
+  if (k == 0 || k % 32) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize: k %% 32 != 0");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (qs && (reinterpret_cast<uintptr_t>(qs) & 15)) ||
+      (blocks && (reinterpret_cast<uintptr_t>(blocks) & 1)) || (d && (reinterpret_cast<uintptr_t>(d) & 1)))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize: misaligned buffer");
+  if (rows == 0) return ZG_OK;
+  QuantArgs a{x, blocks, qs, d, rows, k};
+  const size_t n = rows * (k / 32);
+  hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, qstream(ctx, stream), a);
+  return hip_check(ctx, hipGetLastError(), "quantize launch");
+}
+
+extern "C" zg_status zg_quantize_q8_0_dev(zg_ctx* ctx, const float* d_x, void* d_q, size_t rows, size_t k,
+                                         void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  return launch_quant(ctx, d_x, static_cast<uint8_t*>(d_q), nullptr, nullptr, rows, k, stream);
+}
+
+extern "C" zg_status zg_quantize_q8_0_split_dev(zg_ctx* ctx, const float* d_x, int8_t* d_qs, uint16_t* d_d,
+                                               size_t rows, size_t k, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_qs || !d_d) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize: null output");
+  return launch_quant(ctx, d_x, nullptr, d_qs, d_d, rows, k, stream);
+}
+
+extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const uint16_t* d_d, const void* d_w,
+                                      float* d_y, size_t m, size_t n, size_t k, uint32_t w_type, uint32_t interleave,
+                                      void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_qs || !d_d || !d_w || !d_y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: null pointer");
+  if (w_type != ZG_Q4_0 && w_type != ZG_Q8_0) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "gemm: weights must be Q4_0/Q8_0");
+  zg_status s = check_shape(ctx, w_type, interleave, k, n);
+  if (s) return s;
+  if (m == 0) return ZG_OK;
+  if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: shape too large");
+  if (reinterpret_cast<uintptr_t>(d_qs) & 15) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: activations misaligned");
+  if (interleave == 4 && (reinterpret_cast<uintptr_t>(d_w) & 7))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: weights misaligned");
+  GemmArgs a{d_qs, d_d, static_cast<const uint8_t*>(d_w), d_y, (int)m, (int)n, (int)k};
+  dim3 grid((unsigned)((n + kBN - 1) / kBN), (unsigned)((m + kBM - 1) / kBM));
+  hipStream_t st = qstream(ctx, stream);
+  if (w_type == ZG_Q4_0 && interleave == 4) hipLaunchKernelGGL((gemm_q8act_kernel<Q4_0, 4>), grid, dim3(256), 0, st, a);
+  else if (w_type == ZG_Q4_0) hipLaunchKernelGGL((gemm_q8act_kernel<Q4_0, 1>), grid, dim3(256), 0, st, a);
+  else if (interleave == 4) hipLaunchKernelGGL((gemm_q8act_kernel<Q8_0, 4>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((gemm_q8act_kernel<Q8_0, 1>), grid, dim3(256), 0, st, a);
+  return hip_check(ctx, hipGetLastError(), "gemm launch");
+}

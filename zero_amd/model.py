@@ -1,0 +1,90 @@
+"""Forward pass over the C ABI: the GPU counterpart of
+forward_single_token_avx512 + lm_head_argmax_avx512
+(kernel/src/inference_avx512.rs:1200-1270, 1826-1987) and of the caller's
+prefill/greedy loop (kernel/src/inference.rs:1188-1330, 1817-).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .ops import ArgmaxInPaddingRegion, Context, NonFiniteLogits, ZgError
+from .synth import RandomModel
+
+
+class GpuModel:
+    """Uploads a model's tensors through the weight registry and builds the
+    per-token HIP graphs (zg_model_create)."""
+
+    def __init__(self, ctx: Context, model: RandomModel):
+        self.ctx = ctx
+        self.cfg = cfg = model.cfg
+        self.model = model
+        for L in model.layers:
+            for w in (L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down):
+                ctx.register(w, cfg.lin_type, 4)
+        ctx.register(model.token_embd, cfg.embd_type, 1)
+        ctx.register(model.lm_head, cfg.head_type, 4)
+        self._layers = (_lib.zg_layer_weights * cfg.n_layers)()
+        for i, L in enumerate(model.layers):
+            self._layers[i] = _lib.zg_layer_weights(
+                L.attn_q.ctypes.data, L.attn_k.ctypes.data, L.attn_v.ctypes.data, L.attn_o.ctypes.data,
+                L.ffn_gate.ctypes.data, L.ffn_up.ctypes.data, L.ffn_down.ctypes.data,
+                L.attn_norm.ctypes.data, L.ffn_norm.ctypes.data, L.q_norm.ctypes.data, L.k_norm.ctypes.data)
+        d = _lib.zg_model_desc()
+        d.n_layers, d.hidden, d.ffn = cfg.n_layers, cfg.hidden, cfg.ffn
+        d.n_q_heads, d.n_kv_heads, d.head_dim = cfg.n_q_heads, cfg.n_kv_heads, cfg.head_dim
+        d.vocab_padded, d.vocab_real, d.max_ctx = cfg.vocab_padded, cfg.vocab_real, cfg.max_ctx
+        d.rms_eps, d.rope_theta = cfg.rms_eps, cfg.rope_theta
+        d.lin_type, d.lin_interleave = cfg.lin_type, 4
+        d.embd_type = cfg.embd_type
+        d.head_type, d.head_interleave = cfg.head_type, 4
+        d.token_embd = model.token_embd.ctypes.data
+        d.lm_head = model.lm_head.ctypes.data
+        d.output_norm = model.output_norm.ctypes.data
+        d.layers = self._layers
+        d.device_pointers = 0
+        self._desc = d
+        h = C.c_void_p()
+        ctx.check(ctx.lib.zg_model_create(ctx.h, C.byref(d), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.zg_model_destroy(self.h)
+            self.h = None
+
+    def _raise(self, rc, tok):
+        if rc == _lib.ZG_ERR_ARGMAX_IN_PADDING:
+            raise ArgmaxInPaddingRegion(rc, self.ctx.last_error(), tok)
+        if rc == _lib.ZG_ERR_NONFINITE_LOGITS:
+            raise NonFiniteLogits(rc, self.ctx.last_error())
+        if rc != _lib.ZG_OK:
+            raise ZgError(rc, self.ctx.last_error())
+
+    def step(self, token: int, pos: int, want_hidden=False, want_logits=False):
+        """One token through all layers and the LM head.  Returns
+        (next_token, max_logit, hidden or None, logits or None)."""
+        cfg = self.cfg
+        hid = np.empty(cfg.hidden, np.float32) if want_hidden else None
+        lg = np.empty(cfg.vocab_padded, np.float32) if want_logits else None
+        tok = C.c_uint32()
+        mv = C.c_float()
+        rc = self.ctx.lib.zg_model_step(self.h, token, pos, hid.ctypes.data if hid is not None else None,
+                                        lg.ctypes.data if lg is not None else None, C.byref(tok), C.byref(mv))
+        self._raise(rc, int(tok.value))
+        return int(tok.value), float(mv.value), hid, lg
+
+    def generate(self, prompt: np.ndarray, n_gen: int):
+        """Prefill `prompt` token by token, then n_gen greedy tokens.
+        Returns (tokens, prefill_seconds, generation_seconds)."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(n_gen, np.uint32)
+        t_pre = C.c_double()
+        t_gen = C.c_double()
+        rc = self.ctx.lib.zg_model_generate(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data, C.byref(t_pre),
+                                            C.byref(t_gen))
+        self._raise(rc, -1)
+        return out, float(t_pre.value), float(t_gen.value)
