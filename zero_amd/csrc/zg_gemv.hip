@@ -217,26 +217,31 @@ __global__ __launch_bounds__(NW * 64) void gemv_x4_pair_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < 4; r++) acc[r] = seg_sum<LPG>(acc[r]);
 
+  // Every lane of the group holds all four row sums; row r is stored by
+  // lane r % LPG of the group (one row per lane when LPG >= 4).
   uint64_t key = 0;
-  // lane lig (< 4) of the group owns row 4*lg + lig
-  const float v = (lig == 0) ? acc[0] : (lig == 1) ? acc[1] : (lig == 2) ? acc[2] : acc[3];
+  float up[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (EPI == EPI_SWIGLU) {
-    // up value of the same row sits LPG lanes higher (next group)
-    const float up = __shfl(v, (lane + LPG) & 63, 64);
-    if (active && s == 0 && lig < 4) {
-      const uint32_t row = 4 * lg + (uint32_t)lig;
+    // up rows of the same local group sit LPG lanes higher (next group)
+#pragma unroll
+    for (int r = 0; r < 4; r++) up[r] = __shfl(acc[r], (lane + LPG) & 63, 64);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t row = 4 * lg + (uint32_t)r;
+    const bool owner = active && lig == (r & (LPG - 1)) && row >= sg.row_lo && row < sg.row_hi;
+    if (!owner) continue;
+    const float v = acc[r];
+    if (EPI == EPI_SWIGLU) {
       // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
-      const float silu = v / (1.0f + expf(-v));
-      if (row >= sg.row_lo && row < sg.row_hi) sg.y[row] = silu * up;
-    }
-  } else if (active && lig < 4) {
-    const uint32_t row = 4 * lg + (uint32_t)lig;
-    if (row >= sg.row_lo && row < sg.row_hi) {
-      if (EPI == EPI_RESID) {
-        sg.y[row] = sg.resid[row] + v;
-      } else {
-        if (sg.y) sg.y[row] = v;
-        if (EPI == EPI_ARGMAX && !(v != v)) key = argmax_key(v, row);
+      if (s == 0) sg.y[row] = (v / (1.0f + expf(-v))) * up[r];
+    } else if (EPI == EPI_RESID) {
+      sg.y[row] = sg.resid[row] + v;
+    } else {
+      if (sg.y) sg.y[row] = v;
+      if (EPI == EPI_ARGMAX && !(v != v)) {
+        const uint64_t kk = argmax_key(v, row);
+        key = kk > key ? kk : key;
       }
     }
   }
