@@ -32,6 +32,11 @@ ROWS, K = 6144, 2048
 # W (6144 x 2048 Q4_0 = 7,077,888 B) + x fp32 (8,192 B) + y fp32 (24,576 B)
 GEMV_BYTES = ROWS * (K // 32) * 18 + 4 * K + 4 * ROWS
 ROTATE_BYTES = 512 << 20
+# HBM bytes per launch of the GEMV kernel, from rocprofv3 --pmc FETCH_SIZE
+# (3,538.5 KiB x 2.00) and WRITE_SIZE (24.0 KiB x 1.00); the factors come from
+# the same counters read on an elementwise kernel that reads and writes 256 MiB
+# (--pmc-calib).  1.02 x GEMV_BYTES: the weights are read exactly once.
+GEMV_TRAFFIC_BYTES = 7_271_424
 
 
 def log(*a):
@@ -168,6 +173,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-calib", action="store_true",
+                    help="first run one elementwise kernel that reads 256 MiB and writes 256 MiB, the "
+                         "known-size reference for FETCH_SIZE/WRITE_SIZE counter scaling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1",
@@ -181,6 +189,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     ctx = zero_amd.Context(0)
     torch.cuda.synchronize()
+    if args.pmc_calib:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.add(src, 1, out=dst)  # one kernel: reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
     g = bench_gemv(ctx, args.steps, args.warmup)
     log(f"gemv: {g['launches']} launches, {g['ms_per_gemv'] * 1e3:.2f} us/GEMV, {g['gbs']:.0f} GB/s")
     out = {
@@ -199,7 +213,7 @@ def main():
         "config": {"workload": "Q4_0X4 GEMV 6144x2048 (Qwen3-1.7B FFN up-proj), x fp32, y fp32",
                    "rotating_weight_copies": g["copies"], "bytes_per_step": GEMV_BYTES},
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES},
     }
     dec = None
     if not args.no_decode:

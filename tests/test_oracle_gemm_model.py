@@ -1,0 +1,114 @@
+"""Pins the oracle pieces with no reference counterpart.
+
+* zo_gemm_q8act (the prefill GEMM semantics) against an f64 brute force over
+  the same dequantized Q8_0 activations and dequantized weights, and a
+  closed-form KAT;
+* zo_model_forward (the composition of the pinned operators in the order of
+  forward_single_token_avx512, kernel/src/inference_avx512.rs:1826-1987)
+  against an independent numpy restatement written from the Qwen3 block
+  definition, on a tiny random model.
+"""
+import numpy as np
+import pytest
+
+from zero_amd import synth
+
+
+@pytest.mark.parametrize("m,n,k,wt,il", [(3, 8, 64, 2, 4), (5, 12, 96, 8, 1), (2, 4, 256, 2, 1), (4, 16, 128, 8, 4)])
+def test_gemm_q8act_vs_f64(zo, m, n, k, wt, il):
+    rng = np.random.default_rng(m * n + k)
+    w = synth.weight(rng, wt, n, k, il)
+    x = synth.activations(rng, m, k)
+    xq = zo.quantize_q8_0(x.reshape(-1))
+    y = zo.gemm_q8act(xq, w, m, n, k, wt, il)
+    xd = zo.dequant(xq, m, k, 8, 1).astype(np.float64)
+    wd = zo.dequant(w, n, k, wt, il).astype(np.float64)
+    ref = xd @ wd.T
+    err = np.max(np.abs(y - ref)) / np.max(np.abs(ref))
+    assert err < 1e-5, err
+
+
+def test_gemm_q8act_kat(zo):
+    # all-ones activations (d = 1/127, q = 127) against the Q4_0 unit row
+    # (ops.rs:955-965, every weight +1): y = 32 * 127 * (1/127 rounded to fp16)
+    x = np.ones((1, 32), np.float32)
+    xq = zo.quantize_q8_0(x.reshape(-1))
+    from golden import kats
+    w = np.frombuffer(kats.Q4_0_UNIT, np.uint8).copy()
+    y = zo.gemm_q8act(xq, w, 1, 1, 32, 2, 1)
+    d = float(np.float16(1.0 / 127.0))
+    assert y[0, 0] == np.float32(d) * np.float32(32 * 127)
+
+
+def _np_forward(model, tokens):
+    """Qwen3 decoder restated in numpy float64: pre-norm GQA with QK-norm,
+    NeoX RoPE, causal softmax attention, SwiGLU MLP, residuals, final norm,
+    LM head."""
+    cfg = model.cfg
+    H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q_heads, cfg.n_kv_heads
+
+    def deq(w, rows, k, q, il):
+        from oracle import zo
+        return zo.dequant(w, rows, k, q, il).astype(np.float64)
+
+    def rms(v, g):
+        return v / np.sqrt(np.mean(v * v) + cfg.rms_eps) * g
+
+    inv = cfg.rope_theta ** (-2.0 * np.arange(hd // 2) / hd)
+    emb = deq(model.token_embd, cfg.vocab_padded, H, cfg.embd_type, 1)
+    head = deq(model.lm_head, cfg.vocab_padded, H, cfg.head_type, 4)
+    Ws = [{k: deq(getattr(L, k), *shape, cfg.lin_type, 4) for k, shape in
+           (("attn_q", (cfg.q_dim, H)), ("attn_k", (cfg.kv_dim, H)), ("attn_v", (cfg.kv_dim, H)),
+            ("attn_o", (H, cfg.q_dim)), ("ffn_gate", (cfg.ffn, H)), ("ffn_up", (cfg.ffn, H)),
+            ("ffn_down", (H, cfg.ffn)))} for L in model.layers]
+    kc = [[] for _ in model.layers]
+    vc = [[] for _ in model.layers]
+    logits = []
+    for pos, tok in enumerate(tokens):
+        h = emb[tok].copy()
+        c, s = np.cos(pos * inv), np.sin(pos * inv)
+
+        def rope(v):
+            a, b = v[:hd // 2], v[hd // 2:]
+            return np.concatenate([a * c - b * s, a * s + b * c])
+
+        for li, (L, W) in enumerate(zip(model.layers, Ws)):
+            xn = rms(h, L.attn_norm)
+            q = (W["attn_q"] @ xn).reshape(nq, hd)
+            k = (W["attn_k"] @ xn).reshape(nkv, hd)
+            v = (W["attn_v"] @ xn).reshape(nkv, hd)
+            q = np.stack([rope(rms(qh, L.q_norm)) for qh in q])
+            k = np.stack([rope(rms(kh, L.k_norm)) for kh in k])
+            kc[li].append(k)
+            vc[li].append(v)
+            K, V = np.stack(kc[li]), np.stack(vc[li])
+            out = np.empty((nq, hd))
+            for hh in range(nq):
+                g = hh // (nq // nkv)
+                sc = K[:, g] @ q[hh] / np.sqrt(hd)
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                out[hh] = p @ V[:, g]
+            h = h + W["attn_o"] @ out.reshape(-1)
+            xn = rms(h, L.ffn_norm)
+            gt, up = W["ffn_gate"] @ xn, W["ffn_up"] @ xn
+            h = h + W["ffn_down"] @ (gt / (1 + np.exp(-gt)) * up)
+        logits.append(head @ rms(h, model.output_norm))
+    return np.array(logits)
+
+
+def test_model_forward_vs_numpy(zo):
+    cfg = synth.ModelConfig(n_layers=2, hidden=128, ffn=256, n_q_heads=4, n_kv_heads=2, head_dim=32,
+                            vocab_padded=256, vocab_real=250, max_ctx=16)
+    model = synth.random_model(cfg, seed=2)
+    toks = [3, 17, 101, 5, 5, 42]
+    ref = _np_forward(model, toks)
+    om = zo.OracleModel(model)
+    for pos, t in enumerate(toks):
+        om.forward(t, pos)
+        rc, tok, mv, lg = om.lm_head()
+        assert rc == 0
+        err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
+        assert err < 1e-4, (pos, err)
+        assert tok == int(np.argmax(ref[pos][:cfg.vocab_real]))
+    om.close()

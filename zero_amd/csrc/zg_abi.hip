@@ -226,7 +226,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 bool zg::pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
   return il == 4 && (qt == ZG_Q4_0 || qt == ZG_Q8_0) && k % 64 == 0 && k <= kMaxPairK && n % 4 == 0 &&
-         aligned16(w) && aligned16(x);
+         aligned16(w) && aligned16(x) && gemv_x4_lds_bytes(qt, (int)k) <= 65536;
 }
 
 zg_status zg::check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n) {
@@ -262,7 +262,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].g_begin = 0;
     a.seg[0].row_lo = (uint32_t)(start - 4 * g0);
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
-    return hip_check(ctx, launch_gemv_x4_pair(a, qt, pro, epi, st), "gemv_x4_pair launch");
+    return hip_check(ctx, launch_gemv_x4(a, qt, pro, epi, st), "gemv_x4 launch");
   }
   const float* xin = x;
   if (pro == PRO_RMSNORM) {
@@ -315,7 +315,7 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
       g += (uint32_t)(segs[i].n / 4);
     }
     a.total_groups = g;
-    return hip_check(ctx, launch_gemv_x4_pair(a, segs[0].qt, pro, epi, st), "fused gemv launch");
+    return hip_check(ctx, launch_gemv_x4(a, segs[0].qt, pro, epi, st), "fused gemv launch");
   }
   for (size_t i = 0; i < nseg; i++) {
     zg_status s = run_linear(ctx, x, segs[i].w, segs[i].y, k, segs[i].n, segs[i].qt, segs[i].il, 0, segs[i].n,

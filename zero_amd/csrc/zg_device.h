@@ -35,6 +35,27 @@ __device__ __forceinline__ float seg_sum(float v) {
   return v;
 }
 
+// DPP move (row_mask/bank_mask all rows/banks, bound_ctrl off).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Full wave64 sum, wave-uniform result: xor-1 and xor-2 within quads
+// (quad_perm), half-row and row mirrors give every lane its 16-lane row
+// sum, then the four row sums are read out with v_readlane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // Order-preserving encoding of an argmax candidate into one u64 so that a
 // single atomicMax implements lm_argmax_propose
 // (kernel/src/inference_avx512.rs:1027-1044): larger value wins, equal

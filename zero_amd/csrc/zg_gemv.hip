@@ -5,14 +5,13 @@
 // SMP row partitioning that fans them out (kernel/src/smp.rs:1567-1712):
 // output rows map to the launch grid instead of to cores.
 //
-// Fast path (X4 pair kernel): .smodel-v2 Q4_0X4 / Q8_0X4 tensors whose
-// blocks-per-row is even.  Two consecutive 4-row group-blocks (2 x 72 B or
-// 2 x 136 B) form a 16-byte aligned "pair" that a lane fetches with
-// 9 (Q4_0) or 17 (Q8_0) 128-bit loads.  The activation vector is staged in
-// LDS once per workgroup (after the lane's first weight loads are already in
-// flight) and broadcast from there; nibbles/bytes are unpacked in registers
+// Fast path (X4 streaming kernel): .smodel-v2 Q4_0X4 / Q8_0X4 tensors
+// whose blocks-per-row is even.  Waves stream the weight bytes with fully
+// coalesced 128-bit loads into LDS and decode them there (see gemv_x4_kernel
+// below); the activation vector is staged in LDS once per workgroup and
+// broadcast from there; nibbles/bytes are unpacked in registers
 // (v_cvt_f32_ubyte*), each block sum is scaled by its fp16 d once, and the
-// LPG lanes that share a group finish with a butterfly reduction.  No MFMA:
+// 64 lanes that share a group finish with a butterfly reduction.  No MFMA:
 // the GEMV is HBM-bound.
 //
 // Generic path: any layout / block type, one wave per output row, byte
@@ -27,17 +26,49 @@ namespace zg {
 // Prologue: how the kernel forms the activation vector in LDS.
 // ---------------------------------------------------------------------------
 
+// ---------------------------------------------------------------------------
+// X4 streaming kernel.
+//
+// A group is 4 output rows; its .smodel-v2 stream is K/32 group-blocks of
+// GB bytes (72 for Q4_0X4, 136 for Q8_0X4), contiguous, and consecutive
+// groups are contiguous too.  Work unit = one "segment" of up to 64
+// group-blocks of one group.  A wave
+//   1. streams the segment with lane-contiguous 128-bit loads (a wave
+//      instruction covers 1 KiB of consecutive bytes: fully coalesced),
+//   2. parks it in its own LDS slot,
+//   3. issues the loads of its next segment (they fly while it computes),
+//   4. lane l decodes group-block l from LDS (ds_read_b64 at a 72/136-byte
+//      stride, conflict-free) against x-block l broadcast from LDS.
+// At the end of a group the 64 lane partials are reduced with a butterfly
+// and lanes 0..3 write rows 0..3.  Waves loop persistently over groups; the
+// workgroup stages the activation vector in LDS once.
+// ---------------------------------------------------------------------------
+template <uint32_t QT>
+struct X4 {
+  static constexpr int GB = (QT == Q4_0) ? 72 : 136;  // group-block bytes
+  static constexpr int QDW = (QT == Q4_0) ? 4 : 8;     // qs dwords per row
+  static constexpr int SEG = 64;                       // group-blocks per segment
+  static constexpr int SEG_BYTES = SEG * GB;           // 4608 or 8704
+  static constexpr int NL = (SEG_BYTES / 16 + 63) / 64;  // 128-bit loads per lane: 5 or 9
+};
+
+constexpr int kNW = 4;     // waves per workgroup
+constexpr int kXBlk = 36;  // LDS floats per 32-float x-block (padded: lane stride 144 B)
+
+__device__ __forceinline__ int x_off(int e) { return (e >> 5) * kXBlk + (e & 31); }
+
 // Stage x (K floats) into LDS, applying the prologue.  rmsnorm follows
 // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w.
-template <int PRO, int NT>
+template <int PRO>
 __device__ __forceinline__ void stage_x(float* xs, float* red, const GemvArgs& a) {
+  constexpr int NT = kNW * 64;
   const int tid = threadIdx.x;
   const int K = a.k;
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
   float ssq = 0.0f;
   for (int i = tid; i < K / 4; i += NT) {
     const float4 v = x4[i];
-    reinterpret_cast<float4*>(xs)[i] = v;
+    *reinterpret_cast<float4*>(xs + x_off(4 * i)) = v;
     if (PRO == PRO_RMSNORM) ssq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
   if (PRO == PRO_RMSNORM) {
@@ -46,32 +77,27 @@ __device__ __forceinline__ void stage_x(float* xs, float* red, const GemvArgs& a
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NT / 64; i++) tot += red[i];
+    for (int i = 0; i < kNW; i++) tot += red[i];
     const float rinv = 1.0f / sqrtf(tot / (float)K + a.eps);
-    for (int i = tid; i < K; i += NT) xs[i] = xs[i] * rinv * a.norm_w[i];
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+    for (int i = tid; i < K / 4; i += NT) {
+      float4* p = reinterpret_cast<float4*>(xs + x_off(4 * i));
+      float4 v = *p;
+      const float4 g = w4[i];
+      v.x = v.x * rinv * g.x;
+      v.y = v.y * rinv * g.y;
+      v.z = v.z * rinv * g.z;
+      v.w = v.w * rinv * g.w;
+      *p = v;
+    }
   }
 }
 
-// ---------------------------------------------------------------------------
-// X4 pair kernel.
-//   QT = Q4_0 or Q8_0;  LPG = lanes per 4-row group (power of 2, <= 64);
-//   NW = waves per workgroup.
-// Group g of segment s covers rows 4g..4g+3 of that segment; a lane owns
-// pairs p = lane_in_group, +LPG, ... (blocks 2p, 2p+1) of its group.
-// ---------------------------------------------------------------------------
-template <uint32_t QT>
-struct X4 {
-  static constexpr int GB = (QT == Q4_0) ? 72 : 136;  // group-block bytes
-  static constexpr int PU4 = (2 * GB) / 16;            // uint4 per pair: 9 or 17
-  static constexpr int BDW = GB / 4;                   // dwords per group-block
-  static constexpr int QDW = (QT == Q4_0) ? 4 : 8;     // qs dwords per row
-};
-
-// Sum over one Q4_0 block of row r: returns sum_j q_j * x_j with q the raw
-// nibble (0..15); the caller applies d * (s - 8 * sum(x)).  Low nibbles of
-// byte j are element j, high nibbles element j+16 (dequant.rs:186-216).
-// High nibbles are masked in place (value 16*q) and rescaled by 1/16, an
-// exact power-of-two scaling.
+// Sum over one Q4_0 block of one row: sum_j q_j * x_j with q the raw nibble
+// (0..15); the caller applies d * (s - 8 * sum(x)).  Low nibbles of byte j
+// are element j, high nibbles element j+16 (dequant.rs:186-216).  High
+// nibbles are masked in place (value 16*q) and rescaled by 1/16, an exact
+// power-of-two scaling.
 __device__ __forceinline__ float q4_block_dot(const uint32_t* qs, const float4* xb) {
   float s_lo = 0.0f, s_hi = 0.0f;
 #pragma unroll
@@ -93,7 +119,7 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* qs, const float4* 
   return fmaf(s_hi, 0.0625f, s_lo);
 }
 
-// Sum over one Q8_0 block of row r: sum_j q_j * x_j, q signed bytes
+// Sum over one Q8_0 block of one row: sum_j q_j * x_j, q signed bytes
 // (dequant.rs:247-275).
 __device__ __forceinline__ float q8_block_dot(const uint32_t* qs, const float4* xb) {
   float s0 = 0.0f, s1 = 0.0f;
@@ -110,156 +136,195 @@ __device__ __forceinline__ float q8_block_dot(const uint32_t* qs, const float4* 
   return s0 + s1;
 }
 
-template <uint32_t QT, int LPG, int NW, int PRO, int EPI>
-__global__ __launch_bounds__(NW * 64) void gemv_x4_pair_kernel(GemvArgs a) {
-  constexpr int NT = NW * 64;
-  constexpr int GPW = 64 / LPG;
-  constexpr int PU4 = X4<QT>::PU4;
-  constexpr int BDW = X4<QT>::BDW;
-  constexpr int QDW = X4<QT>::QDW;
-  extern __shared__ float smem[];
-  float* xs = smem;             // K floats
-  float* sx = smem + a.k;       // K/32 block sums (Q4_0 only)
-  __shared__ float red[NW];
-  __shared__ uint64_t wbest[NW];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int lig = lane % LPG;
-  const uint32_t group = (blockIdx.x * NW + wave) * GPW + lane / LPG;
-  const bool active = group < a.total_groups;
-
-  // Locate the segment owning this group (<= 3 segments, fused Q|K|V).
-  // SwiGLU mode interleaves two equal segments group by group (gate g, up
-  // g, gate g+1, ...) so one wave holds matching gate and up rows.
-  int s = 0;
-  uint32_t lg;
-  if (EPI == EPI_SWIGLU) {
-    s = (int)(group & 1u);
-    lg = group >> 1;
-  } else {
-    if (a.nseg > 1 && group >= a.seg[1].g_begin) s = 1;
-    if (a.nseg > 2 && group >= a.seg[2].g_begin) s = 2;
-    lg = group - a.seg[s].g_begin;
+// One group-block (GB bytes, 8-byte aligned in LDS) -> its 4 scales and
+// 4 x QDW quant dwords.
+template <uint32_t QT>
+__device__ __forceinline__ void lds_group_block(const uint8_t* src, uint32_t* dw) {
+  const uint2* p = reinterpret_cast<const uint2*>(src);
+#pragma unroll
+  for (int i = 0; i < X4<QT>::GB / 8; i++) {
+    const uint2 v = p[i];
+    dw[2 * i] = v.x;
+    dw[2 * i + 1] = v.y;
   }
-  const GemvSeg& sg = a.seg[s];
+}
+
+// Issue the 128-bit loads of one segment (nbytes, a multiple of 16) into
+// registers: load i of lane l is bytes [16*(64*i + l), +16).
+template <uint32_t QT>
+__device__ __forceinline__ void seg_load(const uint8_t* src, int nbytes, int lane, u32x4* r) {
+  const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+  for (int i = 0; i < X4<QT>::NL; i++) {
+    const int c = 64 * i + lane;
+    if (16 * c < nbytes) r[i] = __builtin_nontemporal_load(s4 + c);
+  }
+}
+
+template <uint32_t QT>
+__device__ __forceinline__ void seg_park(uint8_t* dst, int nbytes, int lane, const u32x4* r) {
+  u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+  for (int i = 0; i < X4<QT>::NL; i++) {
+    const int c = 64 * i + lane;
+    if (16 * c < nbytes) d4[c] = r[i];
+  }
+}
+
+// LDS order point for one wave: its own LDS writes become visible to its
+// other lanes, and no LDS access moves across it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Work decomposition shared by the GEMV and its dequant test hook.
+//   item  = logical group (SwiGLU: a gate group and its up group)
+//   part  = which of the item's groups (0 unless SwiGLU)
+//   seg   = segment of that group's K stream
+struct UnitIter {
+  int item, part, seg;
+};
+
+template <uint32_t QT, int PRO, int EPI>
+__global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
+  constexpr int GB = X4<QT>::GB, QDW = X4<QT>::QDW, SEG = X4<QT>::SEG, SEGB = X4<QT>::SEG_BYTES;
+  constexpr int NL = X4<QT>::NL;
+  constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ float red[kNW];
   const int nb = a.k / 32;
-  const int npairs = nb / 2;
-  const u32x4* gp = reinterpret_cast<const u32x4*>(sg.w + (size_t)lg * (size_t)nb * X4<QT>::GB);
+  const int nseg = (nb + SEG - 1) / SEG;
+  float* xs = smem;  // nb padded x-blocks
+  uint8_t* wslot = reinterpret_cast<uint8_t*>(xs + nb * kXBlk) + (threadIdx.x >> 6) * SEGB;
 
-  // Issue the first pair's loads before staging x so that HBM latency
-  // overlaps the LDS staging.
-  u32x4 cur[PU4];
-  if (active && lig < npairs) {
-#pragma unroll
-    for (int i = 0; i < PU4; i++) cur[i] = __builtin_nontemporal_load(gp + (size_t)lig * PU4 + i);
-  }
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int items = (int)(EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups);
+  const int wave_id = blockIdx.x * kNW + wave;
+  const int wave_stride = gridDim.x * kNW;
 
-  stage_x<PRO, NT>(xs, red, a);
-  __syncthreads();
-  if (QT == Q4_0) {
-    for (int b = tid; b < nb; b += NT) {
-      const float4* xb = reinterpret_cast<const float4*>(xs + 32 * b);
-      float t = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        const float4 v = xb[c];
-        t += (v.x + v.y) + (v.z + v.w);
-      }
-      sx[b] = t;
+  // group stream of (item, part): segment table lookup (<= 3 segments)
+  auto locate = [&](int item, int part, int& s, uint32_t& lg) {
+    if (EPI == EPI_SWIGLU) {
+      s = part;
+      lg = (uint32_t)item;
+    } else {
+      s = 0;
+      if (a.nseg > 1 && (uint32_t)item >= a.seg[1].g_begin) s = 1;
+      if (a.nseg > 2 && (uint32_t)item >= a.seg[2].g_begin) s = 2;
+      lg = (uint32_t)item - a.seg[s].g_begin;
     }
-    __syncthreads();
+  };
+  auto seg_src = [&](const UnitIter& u, int& nbytes) -> const uint8_t* {
+    int s;
+    uint32_t lg;
+    locate(u.item, u.part, s, lg);
+    const int blocks = min(SEG, nb - u.seg * SEG);
+    nbytes = blocks * GB;
+    return a.seg[s].w + ((size_t)lg * nb + (size_t)u.seg * SEG) * GB;
+  };
+  auto advance = [&](UnitIter& u) {
+    if (++u.seg == nseg) {
+      u.seg = 0;
+      if (++u.part == PARTS) {
+        u.part = 0;
+        u.item += wave_stride;
+      }
+    }
+  };
+
+  UnitIter u{wave_id, 0, 0};
+  u32x4 r[NL];
+  int nbytes = 0;
+  const uint8_t* src = nullptr;
+  if (u.item < items) {
+    src = seg_src(u, nbytes);
+    seg_load<QT>(src, nbytes, lane, r);  // first loads fly during x staging
   }
+  stage_x<PRO>(xs, red, a);
+  __syncthreads();
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (active) {
-    for (int p = lig; p < npairs; p += LPG) {
-      u32x4 nxt[PU4];
-      const bool more = (p + LPG) < npairs;
-      if (more) {
+  float gate[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint64_t key = 0;
+  while (u.item < items) {
+    const int cur_bytes = nbytes;
+    const UnitIter cu = u;
+    seg_park<QT>(wslot, cur_bytes, lane, r);
+    wave_lds_sync();
+    advance(u);
+    if (u.item < items) {
+      src = seg_src(u, nbytes);
+      seg_load<QT>(src, nbytes, lane, r);
+    }
+    // lane l: group-block l of the segment
+    const int b = cu.seg * SEG + lane;
+    if (lane * GB < cur_bytes) {
+      uint32_t dw[GB / 4];
+      lds_group_block<QT>(wslot + lane * GB, dw);
+      float4 xb[8];
 #pragma unroll
-        for (int i = 0; i < PU4; i++)
-          nxt[i] = __builtin_nontemporal_load(gp + (size_t)(p + LPG) * PU4 + i);
+      for (int c = 0; c < 8; c++) xb[c] = reinterpret_cast<const float4*>(xs + b * kXBlk)[c];
+      float d[4];
+      d[0] = half_bits_to_f32(dw[0]);
+      d[1] = half_bits_to_f32(dw[0] >> 16);
+      d[2] = half_bits_to_f32(dw[1]);
+      d[3] = half_bits_to_f32(dw[1] >> 16);
+      if (QT == Q4_0) {
+        float t = 0.0f;  // sum of this x-block, for the -8 offset of every row
+#pragma unroll
+        for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+        const float m8 = -8.0f * t;
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) acc[rr] = fmaf(d[rr], q4_block_dot(dw + 2 + QDW * rr, xb) + m8, acc[rr]);
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) acc[rr] = fmaf(d[rr], q8_block_dot(dw + 2 + QDW * rr, xb), acc[rr]);
       }
-      const uint32_t* dw = reinterpret_cast<const uint32_t*>(cur);
+    }
+    wave_lds_sync();  // the slot is rewritten next iteration
+    if (cu.seg != nseg - 1) continue;
+    // group finished: reduce and write
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int kb = 2 * p + h;
-        const float4* xb = reinterpret_cast<const float4*>(xs + 32 * kb);
-        const uint32_t* blk = dw + h * BDW;
-        float d[4];
-        d[0] = half_bits_to_f32(blk[0]);
-        d[1] = half_bits_to_f32(blk[0] >> 16);
-        d[2] = half_bits_to_f32(blk[1]);
-        d[3] = half_bits_to_f32(blk[1] >> 16);
-        if (QT == Q4_0) {
-          const float m8 = -8.0f * sx[kb];
+    for (int rr = 0; rr < 4; rr++) acc[rr] = wave_sum(acc[rr]);
+    int s;
+    uint32_t lg;
+    locate(cu.item, cu.part, s, lg);
+    const GemvSeg& sg = a.seg[s];
+    if (EPI == EPI_SWIGLU && cu.part == 0) {
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float t = q4_block_dot(blk + 2 + QDW * r, xb);
-            acc[r] = fmaf(d[r], t + m8, acc[r]);
-          }
+      for (int rr = 0; rr < 4; rr++) gate[rr] = acc[rr];
+    } else if (lane < 4) {
+      const float v = (lane == 0) ? acc[0] : (lane == 1) ? acc[1] : (lane == 2) ? acc[2] : acc[3];
+      const uint32_t row = 4 * lg + (uint32_t)lane;
+      if (row >= sg.row_lo && row < sg.row_hi) {
+        if (EPI == EPI_SWIGLU) {
+          const float g = (lane == 0) ? gate[0] : (lane == 1) ? gate[1] : (lane == 2) ? gate[2] : gate[3];
+          // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
+          a.seg[0].y[row] = (g / (1.0f + expf(-g))) * v;
+        } else if (EPI == EPI_RESID) {
+          sg.y[row] = sg.resid[row] + v;
         } else {
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float t = q8_block_dot(blk + 2 + QDW * r, xb);
-            acc[r] = fmaf(d[r], t, acc[r]);
+          if (sg.y) sg.y[row] = v;
+          if (EPI == EPI_ARGMAX && !(v != v)) {
+            const uint64_t kk = argmax_key(v, row);
+            key = kk > key ? kk : key;
           }
         }
       }
-      if (more) {
-#pragma unroll
-        for (int i = 0; i < PU4; i++) cur[i] = nxt[i];
-      }
     }
-  }
 #pragma unroll
-  for (int r = 0; r < 4; r++) acc[r] = seg_sum<LPG>(acc[r]);
-
-  // Every lane of the group holds all four row sums; row r is stored by
-  // lane r % LPG of the group (one row per lane when LPG >= 4).
-  uint64_t key = 0;
-  float up[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (EPI == EPI_SWIGLU) {
-    // up rows of the same local group sit LPG lanes higher (next group)
-#pragma unroll
-    for (int r = 0; r < 4; r++) up[r] = __shfl(acc[r], (lane + LPG) & 63, 64);
-  }
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const uint32_t row = 4 * lg + (uint32_t)r;
-    const bool owner = active && lig == (r & (LPG - 1)) && row >= sg.row_lo && row < sg.row_hi;
-    if (!owner) continue;
-    const float v = acc[r];
-    if (EPI == EPI_SWIGLU) {
-      // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
-      if (s == 0) sg.y[row] = (v / (1.0f + expf(-v))) * up[r];
-    } else if (EPI == EPI_RESID) {
-      sg.y[row] = sg.resid[row] + v;
-    } else {
-      if (sg.y) sg.y[row] = v;
-      if (EPI == EPI_ARGMAX && !(v != v)) {
-        const uint64_t kk = argmax_key(v, row);
-        key = kk > key ? kk : key;
-      }
-    }
+    for (int rr = 0; rr < 4; rr++) acc[rr] = 0.0f;
   }
   if (EPI == EPI_ARGMAX) {
-    // wave max, then workgroup max, then one global atomic per workgroup
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const uint64_t other = __shfl_xor(key, o, 64);
       key = other > key ? other : key;
     }
-    if (lane == 0) wbest[wave] = key;
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t b = 0;
-#pragma unroll
-      for (int i = 0; i < NW; i++) b = wbest[i] > b ? wbest[i] : b;
-      if (b) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)b);
-    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
   }
 }
 
@@ -394,39 +459,43 @@ __global__ void dequant_kernel(DequantArgs a) {
   for (int e = 0; e < be; e++) o[e] = deq_elem(br, a.qt, d, e);
 }
 
-// Dequantize X4 tensors through the pair kernel's own register mapping
-// (one lane per pair), so the fast path's byte->element map is checked
-// bit for bit.
+// Dequantize X4 tensors through the streaming kernel's own path (segment
+// loads, LDS slot, per-lane group-block decode), so the fast path's
+// byte -> element map is checked bit for bit.  One wave per segment.
 template <uint32_t QT>
-__global__ void dequant_x4_pair_kernel(DequantArgs a) {
-  constexpr int PU4 = X4<QT>::PU4, BDW = X4<QT>::BDW, QDW = X4<QT>::QDW;
-  const size_t nb = a.k / 32, npairs = nb / 2;
-  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (a.rows / 4) * npairs) return;
-  const size_t g = t / npairs, p = t % npairs;
-  const u32x4* gp = reinterpret_cast<const u32x4*>(a.w + g * nb * X4<QT>::GB);
-  u32x4 cur[PU4];
-#pragma unroll
-  for (int i = 0; i < PU4; i++) cur[i] = gp[p * PU4 + i];
-  const uint32_t* dw = reinterpret_cast<const uint32_t*>(cur);
-  for (int h = 0; h < 2; h++) {
-    const uint32_t* blk = dw + h * BDW;
-    for (int r = 0; r < 4; r++) {
-      const float d = half_bits_to_f32(blk[r >> 1] >> (16 * (r & 1)));
-      float* o = a.out + (4 * g + r) * a.k + (2 * p + h) * 32;
-      const uint32_t* qs = blk + 2 + QDW * r;
-      for (int e = 0; e < 32; e++) {
-        float v;
-        if (QT == Q4_0) {
-          const uint32_t word = qs[(e & 15) >> 2];
-          const uint32_t nib = (e < 16) ? ((word >> (8 * (e & 3))) & 0xF) : ((word >> (8 * (e & 3) + 4)) & 0xF);
-          v = (float)((int)nib - 8) * d;
-        } else {
-          const uint32_t word = qs[e >> 2];
-          v = (float)(int8_t)((word >> (8 * (e & 3))) & 0xFF) * d;
-        }
-        o[e] = v;
+__global__ __launch_bounds__(kNW * 64) void dequant_x4_stream_kernel(DequantArgs a) {
+  constexpr int GB = X4<QT>::GB, QDW = X4<QT>::QDW, SEG = X4<QT>::SEG, SEGB = X4<QT>::SEG_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t slots[kNW * SEGB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nb = (int)(a.k / 32), nseg = (nb + SEG - 1) / SEG;
+  const size_t unit = (size_t)blockIdx.x * kNW + wave;
+  if (unit >= (a.rows / 4) * (size_t)nseg) return;  // wave-uniform
+  const size_t g = unit / nseg;
+  const int seg = (int)(unit % nseg);
+  const int nbytes = min(SEG, nb - seg * SEG) * GB;
+  u32x4 r[X4<QT>::NL];
+  seg_load<QT>(a.w + (g * nb + (size_t)seg * SEG) * GB, nbytes, lane, r);
+  uint8_t* slot = slots + wave * SEGB;
+  seg_park<QT>(slot, nbytes, lane, r);
+  wave_lds_sync();
+  if (lane * GB >= nbytes) return;
+  uint32_t dw[GB / 4];
+  lds_group_block<QT>(slot + lane * GB, dw);
+  const int b = seg * SEG + lane;
+  for (int rr = 0; rr < 4; rr++) {
+    const float d = half_bits_to_f32(dw[rr >> 1] >> (16 * (rr & 1)));
+    float* o = a.out + (4 * g + rr) * a.k + (size_t)b * 32;
+    const uint32_t* qs = dw + 2 + QDW * rr;
+    for (int e = 0; e < 32; e++) {
+      float v;
+      if (QT == Q4_0) {
+        const uint32_t word = qs[(e & 15) >> 2];
+        const uint32_t nib = (word >> (8 * (e & 3) + (e < 16 ? 0 : 4))) & 0xF;
+        v = (float)((int)nib - 8) * d;
+      } else {
+        v = (float)(int8_t)((qs[e >> 2] >> (8 * (e & 3))) & 0xFF) * d;
       }
+      o[e] = v;
     }
   }
 }
@@ -442,44 +511,55 @@ __global__ void fill_u64_kernel(uint64_t* p, uint64_t v) { *p = v; }
 // Host-side launchers.
 // ---------------------------------------------------------------------------
 
-template <uint32_t QT, int LPG, int NW, int PRO, int EPI>
-static hipError_t launch_pair(const GemvArgs& a, hipStream_t st) {
-  constexpr int GPB = NW * (64 / LPG);
-  const uint32_t grid = (a.total_groups + GPB - 1) / GPB;
-  const size_t shm = (size_t)a.k * sizeof(float) + (QT == Q4_0 ? (size_t)(a.k / 32) * sizeof(float) : 0);
-  hipLaunchKernelGGL((gemv_x4_pair_kernel<QT, LPG, NW, PRO, EPI>), dim3(grid), dim3(NW * 64), shm, st, a);
-  return hipGetLastError();
+static int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+size_t gemv_x4_lds_bytes(uint32_t qt, int k) {
+  const int nb = k / 32;
+  const size_t segb = (qt == Q4_0) ? X4<Q4_0>::SEG_BYTES : X4<Q8_0>::SEG_BYTES;
+  return (size_t)nb * kXBlk * sizeof(float) + kNW * segb;
 }
 
 template <uint32_t QT, int PRO, int EPI>
-static hipError_t pick_lpg(const GemvArgs& a, hipStream_t st) {
-  // Lanes per group: enough lanes that every lane owns at least one pair,
-  // up to 32 (two groups per wave keep the reduction short).
-  const int npairs = a.k / 64;
-  // SwiGLU pairs two groups per wave, so LPG <= 32 always holds here.
-  if (npairs >= 32) return launch_pair<QT, 32, 4, PRO, EPI>(a, st);
-  if (npairs >= 16) return launch_pair<QT, 16, 4, PRO, EPI>(a, st);
-  if (npairs >= 8) return launch_pair<QT, 8, 4, PRO, EPI>(a, st);
-  if (npairs >= 4) return launch_pair<QT, 4, 4, PRO, EPI>(a, st);
-  if (npairs >= 2) return launch_pair<QT, 2, 4, PRO, EPI>(a, st);
-  return launch_pair<QT, 1, 4, PRO, EPI>(a, st);
+static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
+  constexpr int SEG = X4<QT>::SEG;
+  const int nb = a.k / 32, nseg = (nb + SEG - 1) / SEG;
+  const size_t units = (size_t)a.total_groups * nseg;
+  const size_t shm = gemv_x4_lds_bytes(QT, a.k);
+  // enough workgroups that every wave has work, capped at a few resident
+  // workgroups per CU (the waves loop over the remaining groups)
+  const size_t want = (units + kNW - 1) / kNW;
+  const size_t per_cu = shm <= 32768 ? 4 : (shm <= 53248 ? 3 : 2);
+  const size_t grid = want < (size_t)cu_count() * per_cu ? want : (size_t)cu_count() * per_cu;
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemv_x4_kernel<QT, PRO, EPI>), dim3((unsigned)grid), dim3(kNW * 64), shm, st, a);
+  return hipGetLastError();
 }
 
 template <uint32_t QT>
-static hipError_t dispatch_pair_qt(const GemvArgs& a, int pro, int epi, hipStream_t st) {
-  if (pro == PRO_PLAIN && epi == EPI_STORE) return pick_lpg<QT, PRO_PLAIN, EPI_STORE>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_RESID) return pick_lpg<QT, PRO_PLAIN, EPI_RESID>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return pick_lpg<QT, PRO_PLAIN, EPI_ARGMAX>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_STORE) return pick_lpg<QT, PRO_RMSNORM, EPI_STORE>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return pick_lpg<QT, PRO_RMSNORM, EPI_ARGMAX>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return pick_lpg<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return pick_lpg<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
+static hipError_t dispatch_x4_qt(const GemvArgs& a, int pro, int epi, hipStream_t st) {
+  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_x4<QT, PRO_PLAIN, EPI_STORE>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_x4<QT, PRO_PLAIN, EPI_RESID>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_x4<QT, PRO_PLAIN, EPI_ARGMAX>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_x4<QT, PRO_RMSNORM, EPI_STORE>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_x4<QT, PRO_RMSNORM, EPI_ARGMAX>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv_x4_pair(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st) {
-  if (qt == Q4_0) return dispatch_pair_qt<Q4_0>(a, pro, epi, st);
-  if (qt == Q8_0) return dispatch_pair_qt<Q8_0>(a, pro, epi, st);
+hipError_t launch_gemv_x4(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st) {
+  if (qt == Q4_0) return dispatch_x4_qt<Q4_0>(a, pro, epi, st);
+  if (qt == Q8_0) return dispatch_x4_qt<Q8_0>(a, pro, epi, st);
   return hipErrorInvalidValue;
 }
 
@@ -493,10 +573,11 @@ hipError_t launch_gemv_generic(const GenericArgs& a, hipStream_t st) {
 
 hipError_t launch_dequant(const DequantArgs& a, bool pair_path, hipStream_t st) {
   if (pair_path && (a.qt == Q4_0 || a.qt == Q8_0)) {
-    const size_t n = (a.rows / 4) * (a.k / 64);
-    const uint32_t grid = (uint32_t)((n + 255) / 256);
-    if (a.qt == Q4_0) hipLaunchKernelGGL(dequant_x4_pair_kernel<Q4_0>, dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(dequant_x4_pair_kernel<Q8_0>, dim3(grid), dim3(256), 0, st, a);
+    const size_t nseg = (a.k / 32 + 63) / 64;
+    const size_t units = (a.rows / 4) * nseg;
+    const uint32_t grid = (uint32_t)((units + kNW - 1) / kNW);
+    if (a.qt == Q4_0) hipLaunchKernelGGL(dequant_x4_stream_kernel<Q4_0>, dim3(grid), dim3(kNW * 64), 0, st, a);
+    else hipLaunchKernelGGL(dequant_x4_stream_kernel<Q8_0>, dim3(grid), dim3(kNW * 64), 0, st, a);
     return hipGetLastError();
   }
   const int be = (a.qt == Q4_0 || a.qt == Q8_0) ? 32 : 256;

@@ -14,9 +14,10 @@ namespace zg {
 // weight_layout.rs:45 caps the registry at 512 interleaved tensors; this
 // registry also holds plain tensors, so it is larger.
 constexpr size_t kMaxEntries = 4096;
-// Largest in_dim the LDS-staged pair kernel accepts (x plus block sums must
-// fit one workgroup's LDS allocation).
-constexpr size_t kMaxPairK = 15360;
+// Largest in_dim the LDS-staged pair kernel accepts: the padded x copy
+// (36 floats per 32) plus the block sums must fit a 64 KiB workgroup LDS
+// allocation.
+constexpr size_t kMaxPairK = 14080;
 
 struct DevBuf {
   void* ptr = nullptr;

@@ -53,7 +53,9 @@ struct DequantArgs {
   int il;
 };
 
-hipError_t launch_gemv_x4_pair(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
+hipError_t launch_gemv_x4(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
+// LDS bytes the X4 streaming kernel needs for in_dim k.
+size_t gemv_x4_lds_bytes(uint32_t qt, int k);
 hipError_t launch_gemv_generic(const GenericArgs& a, hipStream_t st);
 hipError_t launch_dequant(const DequantArgs& a, bool pair_path, hipStream_t st);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);

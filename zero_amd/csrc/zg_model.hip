@@ -10,14 +10,14 @@
 //
 // Per layer:
 //   1. fused Q|K|V GEMV with rmsnorm(attn_norm) in the prologue
-//   2. attention partials: QK-norm + RoPE + KV-cache store + scores/softmax
-//      over one 32-token chunk of the context per workgroup (split-T)
-//   3. combine the chunks of each head
-//   4. O GEMV with the residual add in the epilogue
-//   5. fused gate|up GEMV with rmsnorm(ffn_norm) and SiLU(gate)*up epilogue
-//   6. down GEMV with the residual add in the epilogue
+//   2. attention: QK-norm + RoPE + KV-cache store + scores/softmax over one
+//      32-token chunk of the context per workgroup (split-T); the last
+//      workgroup of each KV head merges its chunks
+//   3. O GEMV with the residual add in the epilogue
+//   4. fused gate|up GEMV with rmsnorm(ffn_norm) and SiLU(gate)*up epilogue
+//   5. down GEMV with the residual add in the epilogue
 // LM head: GEMV with rmsnorm(output_norm) prologue and argmax epilogue, then
-// a one-thread finalize kernel.
+// a one-thread finalize kernel that feeds the argmax to the next step.
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -84,6 +84,8 @@ struct AttnArgs {
   float* kcache;       // this layer's K rows [max_ctx][nkv*HD]
   float* vcache;       // this layer's V rows
   float* part;         // partials [nq][nchunks][HD+2]
+  float* out;          // merged attention output [nq*HD]
+  uint32_t* counters;  // per KV head: chunk workgroups finished (self-resetting)
   DevState* st;
   int nkv, g, nchunks;
   float eps, scale;
@@ -195,25 +197,36 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       p[1] = sm[g];
     }
   }
-}
-
-// Merge the chunk partials of one query head.
-template <int HD>
-__global__ void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out, int nchunks,
-                                    const DevState* __restrict__ st) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  const int T = (int)st->pos + 1;
-  const int nc = (T + kChunk - 1) / kChunk;
-  const float* p = part + (size_t)h * nchunks * (HD + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < nc; c++) M = fmaxf(M, p[c * (HD + 2)]);
-  float L = 0.0f, o = 0.0f;
-  for (int c = 0; c < nc; c++) {
-    const float w = expf(p[c * (HD + 2)] - M);
-    L = fmaf(w, p[c * (HD + 2) + 1], L);
-    o = fmaf(w, p[c * (HD + 2) + 2 + d], o);
+  // The workgroup that finishes last for this KV head merges the chunks of
+  // its G query heads (split-T reduction without a second launch).  Release:
+  // partials reach device scope before the count; acquire: the last
+  // workgroup sees every other chunk's partials.
+  __shared__ int is_last;
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned nc = (unsigned)((T + kChunk - 1) / kChunk);
+    is_last = atomicAdd(&a.counters[kvh], 1u) == nc - 1;
   }
-  out[h * HD + d] = o * (1.0f / L);
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  const int nc = (T + kChunk - 1) / kChunk;
+  for (int i = tid; i < G * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    const float* p = a.part + (size_t)(kvh * G + g) * a.nchunks * (HD + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < nc; c++) M = fmaxf(M, p[c * (HD + 2)]);
+    float L = 0.0f, o = 0.0f;
+    for (int c = 0; c < nc; c++) {
+      const float w = expf(p[c * (HD + 2)] - M);
+      L = fmaf(w, p[c * (HD + 2) + 1], L);
+      o = fmaf(w, p[c * (HD + 2) + 2 + d], o);
+    }
+    // softmax normalization as attention.rs:76-81: multiply by 1/sum
+    a.out[(kvh * G + g) * HD + d] = o * (1.0f / L);
+  }
+  if (tid == 0) a.counters[kvh] = 0;  // ready for the next launch
 }
 
 __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
@@ -229,7 +242,8 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
   for (int i = threadIdx.x; i < n; i += 256) out[i] = x[i] * rinv * w[i];
 }
 
-// After the LM head: argmax -> next token, error bits, output record.
+// After the LM head: argmax -> next token, error bits, output record, then
+// move to the next position.
 __global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t vocab_real, uint32_t* out_tokens) {
   const uint64_t key = *best;
   uint32_t idx = 0;
@@ -250,6 +264,7 @@ __global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t voc
   st->token = idx;
   if (out_tokens && st->gen < st->gen_cap) out_tokens[st->gen] = idx;
   st->gen += 1;
+  st->pos += 1;
 }
 
 // Move to the next position; during the prompt, feed the next prompt token.
@@ -287,6 +302,7 @@ struct zg_model {
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
   float* logits = nullptr;
   float* part = nullptr;
+  uint32_t* counters = nullptr;
   uint64_t* best = nullptr;
   zg::DevState* st = nullptr;
   uint32_t* prompt = nullptr;  // device prompt buffer
@@ -295,7 +311,9 @@ struct zg_model {
   size_t out_cap = 0;
   int nchunks = 0;
   std::vector<void*> owned;  // device allocations to free
-  hipGraphExec_t g_layers = nullptr, g_head = nullptr, g_adv = nullptr;
+  // g_prefill: embed + layers + advance (prompt tokens before the last);
+  // g_step: embed + layers + LM head + finalize (every step that emits a token)
+  hipGraphExec_t g_prefill = nullptr, g_step = nullptr;
 };
 
 static zg_status model_alloc(zg_model* m, void** p, size_t bytes) {
@@ -352,21 +370,18 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.kcache = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
     aa.vcache = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
     aa.part = m->part;
+    aa.out = m->attn;
+    aa.counters = m->counters;
     aa.st = m->st;
     aa.nkv = (int)d.n_kv_heads;
     aa.g = (int)(d.n_q_heads / d.n_kv_heads);
     aa.nchunks = m->nchunks;
     aa.eps = d.rms_eps;
     aa.scale = scale;
-    if (HD == 128) {
+    if (HD == 128)
       hipLaunchKernelGGL(attn_partial_kernel<128>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
-      hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(d.n_q_heads), dim3(128), 0, st, m->part, m->attn, m->nchunks,
-                         m->st);
-    } else {
+    else
       hipLaunchKernelGGL(attn_partial_kernel<64>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
-      hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(d.n_q_heads), dim3(64), 0, st, m->part, m->attn, m->nchunks,
-                         m->st);
-    }
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
     if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
                         PRO_PLAIN, nullptr, 0.0f, st)))
@@ -380,19 +395,23 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
   return ZG_OK;
 }
 
-static zg_status record_head(zg_model* m, hipStream_t st) {
+static zg_status record_prefill(zg_model* m, hipStream_t st) {
+  zg_status s = record_layers(m, st);
+  if (s) return s;
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->st, m->prompt);
+  return hip_check(m->ctx, hipGetLastError(), "advance launch");
+}
+
+static zg_status record_step(zg_model* m, hipStream_t st) {
   const zg_model_desc& d = m->d;
-  zg_status s = run_linear(m->ctx, m->hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
+  zg_status s = record_layers(m, st);
+  if (s) return s;
+  s = run_linear(m->ctx, m->hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
                            d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM,
                            m->out_norm, d.rms_eps, st);
   if (s) return s;
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
   return hip_check(m->ctx, hipGetLastError(), "finalize launch");
-}
-
-static zg_status record_advance(zg_model* m, hipStream_t st) {
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->st, m->prompt);
-  return hip_check(m->ctx, hipGetLastError(), "advance launch");
 }
 
 static zg_status capture(zg_model* m, zg_status (*rec)(zg_model*, hipStream_t), hipGraphExec_t* out) {
@@ -481,6 +500,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s)
     s = model_alloc(m, reinterpret_cast<void**>(&m->part),
                     (size_t)d.n_q_heads * m->nchunks * (d.head_dim + 2) * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->counters), d.n_kv_heads * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
   m->prompt_cap = d.max_ctx;
@@ -490,9 +510,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   // the generic LM-head path normalizes into the context's aux buffer;
   // allocate it before capture (no allocation inside a captured stream)
   if (!s) s = ensure_buf(ctx, ctx->d_aux, H * sizeof(float));
-  if (!s) s = capture(m, record_layers, &m->g_layers);
-  if (!s) s = capture(m, record_head, &m->g_head);
-  if (!s) s = capture(m, record_advance, &m->g_adv);
+  if (!s) s = capture(m, record_prefill, &m->g_prefill);
+  if (!s) s = capture(m, record_step, &m->g_step);
   if (s) {
     zg_model_destroy(m);
     return s;
@@ -505,7 +524,7 @@ extern "C" void zg_model_destroy(zg_model* m) {
   if (!m) return;
   hipSetDevice(m->ctx->device);
   hipStreamSynchronize(m->ctx->stream);
-  for (hipGraphExec_t g : {m->g_layers, m->g_head, m->g_adv})
+  for (hipGraphExec_t g : {m->g_prefill, m->g_step})
     if (g) hipGraphExecDestroy(g);
   for (void* p : m->owned) hipFree(p);
   delete m;
@@ -545,8 +564,7 @@ extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, fl
   hipSetDevice(ctx->device);
   zg_status s = set_state(m, token, pos, 0, 0);
   if (s) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
   zg::DevState h{};
   if ((s = hip_check(ctx, hipMemcpyAsync(&h, m->st, sizeof h, hipMemcpyDeviceToHost, ctx->stream), "state download")))
     return s;
@@ -581,21 +599,14 @@ extern "C" zg_status zg_model_generate(zg_model* m, const uint32_t* prompt, size
   auto t0 = std::chrono::steady_clock::now();
   // prefill: prompt tokens 0..n-2 through the layers; the last one also
   // through the LM head, producing generated token 0
-  for (size_t i = 0; i + 1 < n_prompt; i++) {
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
-  }
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
+  for (size_t i = 0; i + 1 < n_prompt; i++)
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_prefill, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t1 = std::chrono::steady_clock::now();
   // greedy decode: each generated token goes back through the layers
-  for (size_t j = 1; j < n_gen; j++) {
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_layers, ctx->stream), "graph launch"))) return s;
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_head, ctx->stream), "graph launch"))) return s;
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_adv, ctx->stream), "graph launch"))) return s;
-  }
+  for (size_t j = 1; j < n_gen; j++)
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t2 = std::chrono::steady_clock::now();
   if (prefill_seconds) *prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
