@@ -28,6 +28,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "Q4_0 GEMV HBM GB/s (% of peak); bs1 decode tok/s, Qwen3-1.7B-shape, 1 GPU"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 ROWS, K = 6144, 2048
 # W (6144 x 2048 Q4_0 = 7,077,888 B) + x fp32 (8,192 B) + y fp32 (24,576 B)
 GEMV_BYTES = ROWS * (K // 32) * 18 + 4 * K + 4 * ROWS
@@ -43,36 +44,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def bench_gemv(ctx, steps: int, warmup: int):
-    import numpy as np
+def _graph_time(launch, n_launch: int, steps: int, warmup: int):
+    """Mean device time per launch of `launch(i)` for i in 0..n_launch-1,
+    captured once into a graph on a side stream and replayed; HIP events on
+    that stream bracket the timed replays."""
     import torch
 
-    from zero_amd import synth
-
-    rng = np.random.default_rng(0)
-    w_host = synth.weight(rng, synth.Q4_0, ROWS, K, 4)
-    copies = math.ceil(ROTATE_BYTES / w_host.nbytes) + 1
-    w_dev = [torch.from_numpy(w_host).cuda() for _ in range(copies)]
-    x = torch.from_numpy(synth.activations(rng, K)).cuda()
-    y = torch.empty(ROWS, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    # all GEMVs run on one side stream: it is captured into a graph, and the
-    # timing events are recorded on it
     stream = torch.cuda.Stream()
     st = stream.cuda_stream
-
-    def launch_all():
-        for w in w_dev:
-            ctx.linear_dev(x, w, y, K, ROWS, synth.Q4_0, 4, stream=st)
-
     with torch.cuda.stream(stream):
-        launch_all()  # eager warm-up outside capture
+        for i in range(n_launch):  # eager warm-up outside capture
+            launch(i, st)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
-        launch_all()
-    reps = max(1, math.ceil(steps / copies))
-    wreps = max(1, math.ceil(warmup / copies))
+        for i in range(n_launch):
+            launch(i, st)
+    reps = max(1, math.ceil(steps / n_launch))
+    wreps = max(1, math.ceil(warmup / n_launch))
     with torch.cuda.stream(stream):
         for _ in range(wreps):
             g.replay()
@@ -84,12 +73,140 @@ def bench_gemv(ctx, steps: int, warmup: int):
         e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
-    n = reps * copies
-    per = ms / n
-    gbs = GEMV_BYTES / (per * 1e-3) / 1e9
     del g
-    return {"launches": n, "warmup": wreps * copies, "copies": copies, "ms_per_gemv": per, "gbs": gbs,
+    return ms / (reps * n_launch), reps * n_launch, wreps * n_launch
+
+
+def _copies(nbytes: int) -> int:
+    return math.ceil(ROTATE_BYTES / nbytes) + 1
+
+
+def bench_gemv(ctx, steps: int, warmup: int):
+    import numpy as np
+    import torch
+
+    from zero_amd import synth
+
+    rng = np.random.default_rng(0)
+    w_host = synth.weight(rng, synth.Q4_0, ROWS, K, 4)
+    copies = _copies(w_host.nbytes)
+    w0 = torch.from_numpy(w_host).cuda()
+    w_dev = [w0] + [w0.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(synth.activations(rng, K)).cuda()
+    y = torch.empty(ROWS, dtype=torch.float32, device="cuda")
+
+    def launch(i, st):
+        ctx.linear_dev(x, w_dev[i], y, K, ROWS, synth.Q4_0, 4, stream=st)
+
+    per, n, nw = _graph_time(launch, copies, steps, warmup)
+    gbs = GEMV_BYTES / (per * 1e-3) / 1e9
+    return {"launches": n, "warmup": nw, "copies": copies, "ms_per_gemv": per, "gbs": gbs,
             "w_host": w_host, "x_host": x.cpu().numpy()}
+
+
+def _row(name, per_ms, nbytes, n, copies, **extra):
+    gbs = nbytes / (per_ms * 1e-3) / 1e9
+    d = {"workload": name, "us_per_launch": round(per_ms * 1e3, 3), "launches": n, "rotating_copies": copies,
+         "bytes_per_launch": nbytes, "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    d.update(extra)
+    log(f"{name}: {per_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    return d
+
+
+def bench_rows(ctx, steps: int):
+    """The other hot-path workloads, each timed like the headline GEMV:
+    fused Q|K|V Q8_0X4, LM head Q8_0X4 + argmax, Q4_K and Q6_K GEMVs at
+    Llama-3-8B FFN shapes, and the M=512 int8-MFMA prefill GEMM."""
+    import numpy as np
+    import torch
+
+    from zero_amd import synth
+
+    rng = np.random.default_rng(7)
+    out = {}
+    H = 2048
+
+    def rotating(w_host):
+        c = _copies(w_host.nbytes)
+        w0 = torch.from_numpy(w_host).cuda()
+        return [w0] + [w0.clone() for _ in range(c - 1)], c
+
+    # fused Q|K|V, Q8_0X4, 2048 + 1024 + 1024 rows x 2048
+    segs = [(2048, synth.weight(rng, synth.Q8_0, 2048, H, 4)), (1024, synth.weight(rng, synth.Q8_0, 1024, H, 4)),
+            (1024, synth.weight(rng, synth.Q8_0, 1024, H, 4))]
+    per_copy = sum(w.nbytes for _, w in segs)
+    c = _copies(per_copy)
+    sd = [[torch.from_numpy(w).cuda() for _, w in segs]]
+    sd += [[t.clone() for t in sd[0]] for _ in range(c - 1)]
+    x = torch.from_numpy(synth.activations(rng, H)).cuda()
+    ys = [torch.empty(n, device="cuda") for n, _ in segs]
+
+    def qkv(i, st):
+        ctx.linear_fused_dev(x, [(sd[i][j], ys[j], segs[j][0], synth.Q8_0, 4) for j in range(3)], H, stream=st)
+
+    per, n, _ = _graph_time(qkv, c, steps, steps // 10)
+    out["fused_qkv_q8_0x4"] = _row("fused Q|K|V Q8_0X4 (2048+1024+1024)x2048", per, per_copy + 4 * H + 4 * 4096, n, c)
+    del sd
+
+    # LM head Q8_0X4 151936 x 2048 + argmax, logits written
+    V = 151_936
+    wl = synth.weight(rng, synth.Q8_0, V, H, 4)
+    wd, c = rotating(wl)
+    logits = torch.empty(V, device="cuda")
+    best = torch.zeros(1, dtype=torch.int64, device="cuda")
+
+    def head(i, st):
+        ctx.lm_head_dev(x, wd[i], logits, H, V, synth.Q8_0, 4, best, stream=st)
+
+    per, n, _ = _graph_time(head, c, max(20, steps // 40), 4)
+    out["lm_head_q8_0x4_argmax"] = _row("LM head Q8_0X4 151936x2048 + argmax", per, wl.nbytes + 4 * H + 4 * V, n, c)
+    del wd, wl
+
+    # k-quants at Llama-3-8B FFN shapes
+    for name, qt, rows, k in (("Q4_K 14336x4096 (gate/up)", synth.Q4K, 14336, 4096),
+                              ("Q6_K 4096x14336 (down)", synth.Q6K, 4096, 14336)):
+        wh = synth.weight(rng, qt, rows, k, 1)
+        wd, c = rotating(wh)
+        xk = torch.from_numpy(synth.activations(rng, k)).cuda()
+        yk = torch.empty(rows, device="cuda")
+
+        def kq(i, st, wd=wd, xk=xk, yk=yk, qt=qt, rows=rows, k=k):
+            ctx.linear_dev(xk, wd[i], yk, k, rows, qt, 1, stream=st)
+
+        per, n, _ = _graph_time(kq, c, max(40, steps // 10), 20)
+        key = "q4_k_14336x4096" if qt == synth.Q4K else "q6_k_4096x14336"
+        out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
+        del wd
+
+    # prefill GEMM, M = 512, both FFN shapes, Q4_0X4 weights, Q8_0 activations
+    M = 512
+    for name, n_out, k in (("up", 6144, 2048), ("down", 2048, 6144)):
+        wh = synth.weight(rng, synth.Q4_0, n_out, k, 4)
+        wd = torch.from_numpy(wh).cuda()
+        xm = torch.from_numpy(synth.activations(rng, M, k)).cuda()
+        qs = torch.empty((M, k), dtype=torch.int8, device="cuda")
+        dd = torch.empty((M, k // 32), dtype=torch.int16, device="cuda")
+        ym = torch.empty((M, n_out), device="cuda")
+        ctx.quantize_q8_0_split_dev(xm, qs, dd, M, k)
+
+        def gemm(i, st, wd=wd, qs=qs, dd=dd, ym=ym, n_out=n_out, k=k):
+            ctx.gemm_q8act_dev(qs, dd, wd, ym, M, n_out, k, synth.Q4_0, 4, stream=st)
+
+        def quant(i, st, xm=xm, qs=qs, dd=dd, k=k):
+            ctx.quantize_q8_0_split_dev(xm, qs, dd, M, k, stream=st)
+
+        per, n, _ = _graph_time(gemm, 1, max(40, steps // 20), 10)
+        perq, _, _ = _graph_time(quant, 1, max(40, steps // 20), 10)
+        ops = 2 * M * n_out * k
+        tops = ops / (per * 1e-3) / 1e12
+        nbytes = wh.nbytes + M * k + M * (k // 32) * 2 + 4 * M * n_out
+        out[f"prefill_gemm_{name}"] = {
+            "workload": f"prefill GEMM M=512 x {n_out}x{k} Q4_0X4, Q8_0 activations, int8 MFMA",
+            "us_per_launch": round(per * 1e3, 2), "int8_TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "ops_per_launch": ops, "bytes_per_launch": nbytes,
+            "quantize_us": round(perq * 1e3, 2)}
+        log(f"prefill GEMM {name}: {per * 1e3:.1f} us, {tops:.0f} TOPS; quantize {perq * 1e3:.1f} us")
+    return out
 
 
 def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
@@ -173,6 +290,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-rows", action="store_true", help="skip the fused-QKV, LM-head, k-quant and GEMM lines")
     ap.add_argument("--pmc-calib", action="store_true",
                     help="first run one elementwise kernel that reads 256 MiB and writes 256 MiB, the "
                          "known-size reference for FETCH_SIZE/WRITE_SIZE counter scaling")
@@ -215,6 +333,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES},
     }
+    if not args.no_rows:
+        out["rows"] = bench_rows(ctx, args.steps)
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx)

@@ -104,6 +104,9 @@ GEMV_CASES = [
     (Q8_0, 1, 100, 512),
     (Q4K, 1, 64, 4096),
     (Q6K, 1, 48, 1024),
+    (Q4K, 1, 33, 2304),      # 9 superblocks per row: a partial 8-superblock step
+    (Q6K, 1, 17, 2304),      # odd superblocks per row: unaligned Q6_K row starts
+    (Q6K, 1, 8, 16384),      # in_dim above the LDS-staged limit: generic path
 ]
 
 
@@ -200,6 +203,26 @@ def test_lm_head_argmax(ctx, zo, lm_head):
     top2 = np.sort(ref)[-2:]
     print(f"LM head: argmax {tok} (oracle {idx}), margin {top2[1] - top2[0]:.4f}, rel err {rel_err(logits, ref):.2e}")
     assert tok == idx and tok == int(np.argmax(logits))
+    ctx.clear()
+
+
+def test_lm_head_argmax_q6_k(ctx, zo):
+    """LM head in Q6_K (the output.weight type of Q4_K_M GGUF artifacts)."""
+    rng = np.random.default_rng(5)
+    V, H = 32000, 4096
+    w = synth.weight(rng, Q6K, V, H, 1)
+    hidden = synth.activations(rng, H)
+    norm = (1 + 0.05 * rng.standard_normal(H)).astype(np.float32)
+    ctx.register(w, Q6K, 1)
+    logits = np.empty(V, np.float32)
+    tok = ctx.lm_head_argmax(hidden, norm, w, Q6K, 1e-6, H, vocab_padded=V, vocab_real=V, logits_buf=logits)
+    xn = np.empty(H, np.float32)
+    zo.load().zo_rmsnorm(hidden.ctypes.data, norm.ctypes.data, xn.ctypes.data, H, 1e-6)
+    with zo.Pool(8):
+        ref = zo.linear_parallel(xn, w, H, V, Q6K, 1)
+    assert rel_err(logits, ref) <= REL_TOL
+    idx, _ = zo.argmax(ref)
+    assert tok == idx
     ctx.clear()
 
 

@@ -285,6 +285,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
   g.qt = qt;
   g.il = (int)il;
   g.epi = epi;
+  if (kq_path_ok(qt, il, k, w, xin)) return hip_check(ctx, launch_gemv_kq(g, st), "gemv_kq launch");
   return hip_check(ctx, launch_gemv_generic(g, st), "gemv_generic launch");
 }
 

@@ -58,6 +58,12 @@ hipError_t launch_gemv_x4(const GemvArgs& a, uint32_t qt, int pro, int epi, hipS
 size_t gemv_x4_lds_bytes(uint32_t qt, int k);
 hipError_t launch_gemv_generic(const GenericArgs& a, hipStream_t st);
 hipError_t launch_dequant(const DequantArgs& a, bool pair_path, hipStream_t st);
+// Q4_K / Q6_K fast path (row-major superblocks, in_dim a multiple of 256
+// and at most kMaxKqK so that x and its 16-element sums fit 64 KiB of LDS).
+constexpr size_t kMaxKqK = 15360;
+bool kq_path_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x);
+size_t kq_lds_bytes(int k);
+hipError_t launch_gemv_kq(const GenericArgs& a, hipStream_t st);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t v, hipStream_t st);
 
