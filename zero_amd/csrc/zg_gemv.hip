@@ -43,6 +43,17 @@ namespace zg {
 // and lanes 0..3 write rows 0..3.  Waves loop persistently over groups; the
 // workgroup stages the activation vector in LDS once.
 // ---------------------------------------------------------------------------
+// Segment of a group index.  The fields are picked with constant indices so
+// that they stay in scalar registers: a dynamically indexed a.seg[s] is
+// re-read from the kernel-argument segment with a vector load, a full
+// memory round trip in front of every weight load that depends on it.
+__device__ __forceinline__ GemvSeg seg_of(const GemvArgs& a, uint32_t item) {
+  GemvSeg s = a.seg[0];
+  if (a.nseg > 1 && item >= a.seg[1].g_begin) s = a.seg[1];
+  if (a.nseg > 2 && item >= a.seg[2].g_begin) s = a.seg[2];
+  return s;
+}
+
 template <uint32_t QT>
 struct X4 {
   static constexpr int GB = (QT == Q4_0) ? 72 : 136;  // group-block bytes
@@ -200,30 +211,27 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
   uint8_t* wslot = reinterpret_cast<uint8_t*>(xs + nb * kXBlk) + (threadIdx.x >> 6) * SEGB;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int items = (int)(EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups);
   const int wave_id = blockIdx.x * kNW + wave;
   const int wave_stride = gridDim.x * kNW;
 
   // group stream of (item, part): segment table lookup (<= 3 segments)
-  auto locate = [&](int item, int part, int& s, uint32_t& lg) {
+  auto locate = [&](int item, int part, uint32_t& lg) -> GemvSeg {
     if (EPI == EPI_SWIGLU) {
-      s = part;
       lg = (uint32_t)item;
-    } else {
-      s = 0;
-      if (a.nseg > 1 && (uint32_t)item >= a.seg[1].g_begin) s = 1;
-      if (a.nseg > 2 && (uint32_t)item >= a.seg[2].g_begin) s = 2;
-      lg = (uint32_t)item - a.seg[s].g_begin;
+      return part ? a.seg[1] : a.seg[0];
     }
+    const GemvSeg sg = seg_of(a, (uint32_t)item);
+    lg = (uint32_t)item - sg.g_begin;
+    return sg;
   };
   auto seg_src = [&](const UnitIter& u, int& nbytes) -> const uint8_t* {
-    int s;
     uint32_t lg;
-    locate(u.item, u.part, s, lg);
+    const GemvSeg sg = locate(u.item, u.part, lg);
     const int blocks = min(SEG, nb - u.seg * SEG);
     nbytes = blocks * GB;
-    return a.seg[s].w + ((size_t)lg * nb + (size_t)u.seg * SEG) * GB;
+    return sg.w + ((size_t)lg * nb + (size_t)u.seg * SEG) * GB;
   };
   auto advance = [&](UnitIter& u) {
     if (++u.seg == nseg) {
@@ -289,10 +297,8 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
     // group finished: reduce and write
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) acc[rr] = wave_sum(acc[rr]);
-    int s;
     uint32_t lg;
-    locate(cu.item, cu.part, s, lg);
-    const GemvSeg& sg = a.seg[s];
+    const GemvSeg sg = locate(cu.item, cu.part, lg);
     if (EPI == EPI_SWIGLU && cu.part == 0) {
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) gate[rr] = acc[rr];
@@ -317,6 +323,232 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
     }
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) acc[rr] = 0.0f;
+  }
+  if (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// X4 strip kernel (in_dim a multiple of 512, at most 8192).
+//
+// The K axis is cut into strips of 16 blocks (512 values).  A wave owns one
+// strip and keeps that strip's activations in registers: lane (b, r) holds
+// x-block b of the strip (32 floats) and decodes row r of that block for
+// every group the wave visits, loading its own 16 (Q4_0) or 32 (Q8_0) quant
+// bytes and its fp16 d straight from HBM (lanes 4b..4b+3 cover one
+// group-block's quant bytes contiguously, so a wave instruction spans
+// ~1.1-2.2 KB of consecutive bytes).  A workgroup has one wave per strip
+// (times 1, 2 or 4 when there are fewer than 4 strips) and walks batches of
+// groups; per group a lane's partial is reduced over the 4 lanes of a DPP
+// row with the same r (row_ror 4, 8), the 16-lane row sums go to LDS, and
+// after one barrier per batch each row's total is summed over strips and
+// rows in a fixed order, then the epilogue runs.  Every lane loads all of
+// its batch's weight bytes before the first of them is used.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <uint32_t QT>
+struct StripGeom {
+  static constexpr int GB = (QT == Q4_0) ? 72 : 136;  // group-block bytes
+  static constexpr int QW = (QT == Q4_0) ? 4 : 8;     // quant dwords per row-block
+};
+
+template <uint32_t QT>
+struct LaneW {
+  uint32_t q[StripGeom<QT>::QW];
+  uint32_t d;
+};
+
+template <uint32_t QT>
+__device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int r) {
+  constexpr int QW = StripGeom<QT>::QW;
+  const u32x2* p = reinterpret_cast<const u32x2*>(blk + 8 + 4 * QW * r);
+#pragma unroll
+  for (int i = 0; i < QW / 2; i++) {
+    const u32x2 v = __builtin_nontemporal_load(p + i);
+    L.q[2 * i] = v.x;
+    L.q[2 * i + 1] = v.y;
+  }
+  L.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(blk + 2 * r));
+}
+
+// Q8_0 block sum with the int8 quants read as unsigned bytes (q ^ 0x80 =
+// q + 128); the caller subtracts 128 * sum(x).
+__device__ __forceinline__ float q8u_block_dot(const uint32_t* qs, const float4* xb) {
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    const uint32_t v = qs[c] ^ 0x80808080u;
+    const float4 xv = xb[c];
+    float& s = (c & 1) ? s1 : s0;
+    s = fmaf(xv.x, (float)(v & 0xFFu), s);
+    s = fmaf(xv.y, (float)((v >> 8) & 0xFFu), s);
+    s = fmaf(xv.z, (float)((v >> 16) & 0xFFu), s);
+    s = fmaf(xv.w, (float)(v >> 24), s);
+  }
+  return s0 + s1;
+}
+
+template <uint32_t QT>
+__device__ __forceinline__ float strip_dot(const LaneW<QT>& L, const float4* xb, float mterm) {
+  const float d = half_bits_to_f32(L.d);
+  if (QT == Q4_0) return d * (q4_block_dot(L.q, xb) + mterm);
+  return d * (q8u_block_dot(L.q, xb) + mterm);
+}
+
+// partial sums over the 4 lanes of each DPP row that share lane & 3
+__device__ __forceinline__ float row_sum4(float v) {
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x128>(v);  // row_ror:8
+  return v;
+}
+
+template <uint32_t QT, int PRO, int EPI, int GBATCH>
+__global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
+  constexpr int GBY = StripGeom<QT>::GB;
+  constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) float part[];  // [2][NW][GBATCH][PARTS][16]
+  __shared__ float red[16];
+  const int NW = blockDim.x >> 6;
+  const int WPS = NW / S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = wave % S, sub = wave / S;
+  const int b = lane >> 2, r = lane & 3;
+  const int nb = a.k >> 5;
+  const int kb = strip * 16 + b;  // this lane's K-block
+  const int items = (int)(EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups);
+  const int per_batch = WPS * GBATCH;
+  const int nbatch = (items + per_batch - 1) / per_batch;
+
+  auto locate = [&](int item, int p, uint32_t& lg) -> GemvSeg {
+    if (EPI == EPI_SWIGLU) {
+      lg = (uint32_t)item;
+      return p ? a.seg[1] : a.seg[0];
+    }
+    const GemvSeg sg = seg_of(a, (uint32_t)item);
+    lg = (uint32_t)item - sg.g_begin;
+    return sg;
+  };
+
+  auto load_batch = [&](LaneW<QT> (&L)[GBATCH][PARTS], int batch) {
+    const int base = batch * per_batch + sub * GBATCH;
+#pragma unroll
+    for (int j = 0; j < GBATCH; j++) {
+      if (base + j < items) {
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+          uint32_t lg;
+          const GemvSeg sg = locate(base + j, p, lg);
+          strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
+        }
+      }
+    }
+  };
+
+  // activation block of this lane, then the first batch's weights: all
+  // loads are issued before any of them is waited for, x first because it
+  // is consumed first
+  float4 xb[8];
+  {
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
+#pragma unroll
+    for (int c = 0; c < 8; c++) xb[c] = x4[c];
+  }
+  LaneW<QT> L[GBATCH][PARTS];
+  if ((int)blockIdx.x < nbatch) load_batch(L, blockIdx.x);
+
+  // prologue and block sum
+  if (PRO == PRO_RMSNORM) {
+    // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w, sum of squares over
+    // the whole vector (each wave's strip blocks, 4 lanes per block: lane
+    // r < 1 of each block contributes)
+    float ssq = 0.0f;
+    if (sub == 0 && r == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; c++) ssq += xb[c].x * xb[c].x + xb[c].y * xb[c].y + xb[c].z * xb[c].z + xb[c].w * xb[c].w;
+    }
+    ssq = wave_sum(ssq);
+    if (lane == 0) red[wave] = ssq;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < S; i++) tot += red[i];
+    const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const float4 g = g4[c];
+      xb[c].x = xb[c].x * rinv * g.x;
+      xb[c].y = xb[c].y * rinv * g.y;
+      xb[c].z = xb[c].z * rinv * g.z;
+      xb[c].w = xb[c].w * rinv * g.w;
+    }
+  }
+  float t = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+  const float mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
+
+  uint64_t key = 0;
+  int buf = 0;
+  for (int batch = blockIdx.x; batch < nbatch; batch += gridDim.x, buf ^= 1) {
+    const int base = batch * per_batch + sub * GBATCH;
+    float* pb = part + (size_t)buf * NW * GBATCH * PARTS * 16;
+#pragma unroll
+    for (int j = 0; j < GBATCH; j++) {
+      if (base + j < items) {
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+          const float v = row_sum4(strip_dot<QT>(L[j][p], xb, mterm));
+          if ((lane & 15) < 4) pb[((wave * GBATCH + j) * PARTS + p) * 16 + (lane >> 4) * 4 + r] = v;
+        }
+      }
+    }
+    // next batch's loads fly during the barrier and the combine
+    if (batch + (int)gridDim.x < nbatch) load_batch(L, batch + gridDim.x);
+    __syncthreads();
+    const int tt = threadIdx.x;
+    if (tt < per_batch * 4) {
+      const int su = tt / (GBATCH * 4), j = (tt >> 2) % GBATCH, rr = tt & 3;
+      const int item = batch * per_batch + su * GBATCH + j;
+      if (item < items) {
+        float tot[PARTS];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+          float acc = 0.0f;
+          for (int st = 0; st < S; st++) {
+            const float* q = pb + (((su * S + st) * GBATCH + j) * PARTS + p) * 16 + rr;
+            acc += (q[0] + q[4]) + (q[8] + q[12]);
+          }
+          tot[p] = acc;
+        }
+        uint32_t lg;
+        const GemvSeg sg = locate(item, 0, lg);
+        const uint32_t row = 4 * lg + (uint32_t)rr;
+        if (row >= sg.row_lo && row < sg.row_hi) {
+          const float v = tot[PARTS - 1];
+          if (EPI == EPI_SWIGLU) {
+            const float g = tot[0];
+            // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
+            a.seg[0].y[row] = (g / (1.0f + expf(-g))) * v;
+          } else if (EPI == EPI_RESID) {
+            sg.y[row] = sg.resid[row] + v;
+          } else {
+            if (sg.y) sg.y[row] = v;
+            if (EPI == EPI_ARGMAX && !(v != v)) {
+              const uint64_t kk = argmax_key(v, row);
+              key = kk > key ? kk : key;
+            }
+          }
+        }
+      }
+    }
   }
   if (EPI == EPI_ARGMAX) {
 #pragma unroll
@@ -545,15 +777,60 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Tuning constants of the strip launch (overridable at build time).
+#ifndef ZG_STRIP_WAVES_PER_CU
+#define ZG_STRIP_WAVES_PER_CU 16
+#endif
+#ifndef ZG_STRIP_SMALL_ITEMS_PER_CU
+#define ZG_STRIP_SMALL_ITEMS_PER_CU 8
+#endif
+#ifndef ZG_STRIP_ENABLE
+#define ZG_STRIP_ENABLE 1
+#endif
+
+bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
+
+template <uint32_t QT, int PRO, int EPI, int GBATCH>
+static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
+  constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  const int wps = nw / S;
+  const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
+  // about 16 resident waves per CU; the remaining batches are looped over
+  const size_t per_cu = nw >= ZG_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_STRIP_WAVES_PER_CU / nw);
+  const size_t cap = (size_t)cu_count() * per_cu;
+  const size_t grid = nbatch < cap ? nbatch : cap;
+  if (grid == 0) return hipSuccess;
+  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float);
+  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH>), dim3((unsigned)grid), dim3(nw * 64), shm, st, a, S);
+  return hipGetLastError();
+}
+
+template <uint32_t QT, int PRO, int EPI>
+static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
+  const int S = a.k / 512;
+  const int nw = S >= 4 ? S : 4;  // S in {1, 2} -> 4 waves: 4 / S waves per strip
+  const size_t items = EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups;
+  // small launches use short batches so that more workgroups share the work
+  const size_t wps = nw / S;
+  if (items <= (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps) return launch_strip_gb<QT, PRO, EPI, 2>(a, S, nw, items, st);
+  return launch_strip_gb<QT, PRO, EPI, 4>(a, S, nw, items, st);
+}
+
+template <uint32_t QT, int PRO, int EPI>
+static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
+  if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+  return launch_x4<QT, PRO, EPI>(a, st);
+}
+
 template <uint32_t QT>
 static hipError_t dispatch_x4_qt(const GemvArgs& a, int pro, int epi, hipStream_t st) {
-  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_x4<QT, PRO_PLAIN, EPI_STORE>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_x4<QT, PRO_PLAIN, EPI_RESID>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_x4<QT, PRO_PLAIN, EPI_ARGMAX>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_x4<QT, PRO_RMSNORM, EPI_STORE>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_x4<QT, PRO_RMSNORM, EPI_ARGMAX>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
-  if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_x4_any<QT, PRO_PLAIN, EPI_STORE>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_x4_any<QT, PRO_PLAIN, EPI_RESID>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_x4_any<QT, PRO_PLAIN, EPI_ARGMAX>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_x4_any<QT, PRO_RMSNORM, EPI_STORE>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_x4_any<QT, PRO_RMSNORM, EPI_ARGMAX>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
   return hipErrorInvalidValue;
 }
 
