@@ -50,6 +50,45 @@ def test_tiny_model_stepwise(ctx, zo, tiny):
     ctx.clear()
 
 
+@pytest.mark.parametrize("n_q,n_kv,hd", [(8, 1, 64), (4, 4, 64), (8, 2, 128)])
+def test_attention_head_groupings(ctx, zo, n_q, n_kv, hd):
+    """Query heads per KV head G = 8, 1 and 4 (the Qwen shape has G = 2)."""
+    cfg = synth.ModelConfig(n_layers=1, hidden=256, ffn=512, n_q_heads=n_q, n_kv_heads=n_kv, head_dim=hd,
+                            vocab_padded=512, vocab_real=500, max_ctx=72)
+    model = synth.random_model(cfg, seed=n_q + 3 * n_kv + hd)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    tok, worst = 3, 0.0
+    for pos in range(40):
+        nxt, _, hid, _ = gm.step(tok, pos, want_hidden=True, want_logits=False)
+        h_ref = om.forward(tok, pos)
+        rc, t_ref, _, _ = om.lm_head()
+        worst = max(worst, rel_err(hid, h_ref))
+        assert nxt == t_ref, pos
+        tok = nxt
+    print(f"G={n_q // n_kv} hd={hd}: worst hidden rel err {worst:.2e}")
+    assert worst <= REL_TOL
+    om.close()
+    gm.close()
+    ctx.clear()
+
+
+def test_attention_split_context(ctx, zo):
+    """max_ctx above one workgroup's split (2048 positions): positions past
+    2048 are merged across two workgroups per KV head."""
+    cfg = synth.ModelConfig(n_layers=1, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=512, vocab_real=500, max_ctx=2100)
+    model = synth.random_model(cfg, seed=11)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    prompt = synth.prompt(12, 8, cfg.vocab_real)
+    toks, _, _ = gm.generate(prompt, 2090)
+    assert np.array_equal(toks, om.generate(prompt, 2090))
+    om.close()
+    gm.close()
+    ctx.clear()
+
+
 def test_tiny_model_generate_matches_oracle(ctx, zo, tiny):
     gm = GpuModel(ctx, tiny)
     om = zo.OracleModel(tiny)

@@ -56,6 +56,36 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Full wave64 max, wave-uniform result (same DPP pattern as wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Sum over aligned groups of W lanes (W = 16 or 32).  Within a 16-lane DPP
+// row: quad swaps, then rotations by 4 and 8 (every lane of the row gets the
+// row total).  W = 32 then adds row 0's total into row 1 and row 2's into
+// row 3 (row_bcast:15); the group total is valid in the upper row of each
+// pair only (lanes 16..31 and 48..63).  Returns, for W = 16, the total in
+// every lane.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x128>(v);  // row_ror:8
+  if (W == 32)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  return v;
+}
+
 // Order-preserving encoding of an argmax candidate into one u64 so that a
 // single atomicMax implements lm_argmax_propose
 // (kernel/src/inference_avx512.rs:1027-1044): larger value wins, equal

@@ -33,8 +33,9 @@ using namespace zg;
 
 namespace zg {
 
-constexpr int kChunk = 32;  // context tokens per attention workgroup
-constexpr int kMaxG = 8;    // max query heads per KV head
+constexpr int kMaxG = 8;          // max query heads per KV head
+constexpr int kAttnThreads = 1024;
+constexpr int kSplitMax = 2048;   // positions per attention workgroup (one split below this)
 
 // Device-resident decode state.
 struct DevState {
@@ -51,10 +52,19 @@ struct DevState {
 
 // embed_lookup_dispatch (forward_pass.rs:311-370) for plain Q4_0/Q8_0 rows;
 // also clears the LM-head argmax slot for this step.
+// It also fills this position's RoPE table once for all layers, as the
+// reference builds its sin/cos table once per token (trig.rs:148-216):
+// cs[i] = cos(pos * inv_freq[i]), cs[half + i] = sin(pos * inv_freq[i]).
 __global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
                              DevState* __restrict__ st, uint64_t* __restrict__ best,
-                             float* __restrict__ out) {
+                             float* __restrict__ out, const float* __restrict__ inv_freq, int half,
+                             float* __restrict__ rope_cs) {
   const uint32_t tok = st->token;
+  if ((int)threadIdx.x < half) {
+    const float th = (float)st->pos * inv_freq[threadIdx.x];
+    rope_cs[threadIdx.x] = cosf(th);
+    rope_cs[half + threadIdx.x] = sinf(th);
+  }
   const int nb = hidden / 32;
   const int bb = (qt == Q4_0) ? 18 : 34;
   const uint8_t* row = embd + (size_t)tok * nb * bb;
@@ -80,150 +90,258 @@ struct AttnArgs {
   const float* v;      // raw V projection [nkv*HD]
   const float* q_norm; // [HD]
   const float* k_norm; // [HD]
-  const float* inv_freq;  // [HD/2]
+  const float* rope_cs;   // [HD]: cos then sin of pos * inv_freq
   float* kcache;       // this layer's K rows [max_ctx][nkv*HD]
   float* vcache;       // this layer's V rows
-  float* part;         // partials [nq][nchunks][HD+2]
+  float* part;         // partials [nq][nsplit][HD+2] (nsplit > 1 only)
   float* out;          // merged attention output [nq*HD]
   uint32_t* counters;  // per KV head: chunk workgroups finished (self-resetting)
   DevState* st;
-  int nkv, g, nchunks;
+  int nkv, g, nsplit, split_len;
   float eps, scale;
 };
 
-// QK-norm (rmsnorm over one head, ops.rs:29-52) then NeoX RoPE
-// (ops.rs:111-132) of one head held in LDS, by one wave.
-template <int HD>
-__device__ __forceinline__ void norm_rope_head(float* h, const float* w, const float* inv_freq, float pos_f,
-                                               float eps, int lane) {
-  constexpr int HALF = HD / 2;
-  float a = 0.0f, b = 0.0f;
-  if (lane < HALF) {
-    a = h[lane];
-    b = h[lane + HALF];
-  }
-  const float ssq = seg_sum<64>(a * a + b * b);
-  const float rinv = 1.0f / sqrtf(ssq / (float)HD + eps);
-  if (lane < HALF) {
-    const float x = a * rinv * w[lane];
-    const float y = b * rinv * w[lane + HALF];
-    const float th = pos_f * inv_freq[lane];
-    const float c = cosf(th), s = sinf(th);
-    h[lane] = x * c - y * s;
-    h[lane + HALF] = x * s + y * c;
-  }
-}
-
-template <int HD>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
-  const int kvh = blockIdx.x, ch = blockIdx.y;
+// Decode attention for one KV head (grid: KV heads x splits; one split
+// unless the context exceeds kSplitMax positions).  1024 threads walk the
+// split in chunks of kTile positions with an online softmax; each chunk's
+// K and V rows are loaded into registers one chunk ahead in the coalesced
+// (row, float4 column) order, and both products work in that order:
+//   scores  thread (row, column c) dots its float4 of k_row with q_g's
+//           float4 c; the F4 lanes of a row are summed with DPP
+//   softmax one wave per head updates the running max and exp-sum
+//           (attention.rs:48-84, rescaled online)
+//   P.V     the same thread adds e_row * v_row[c] to its column's
+//           accumulator; at the end the accumulators of each column are
+//           summed through LDS and divided by the exp-sum (attention.rs:
+//           76-81 multiplies by 1/sum)
+// With several splits each writes (max, sum, o) and the last workgroup of
+// the KV head merges them.
+template <int HD, int GM>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
+  constexpr int F4 = HD / 4;                      // float4 per head row (= lanes per row)
+  constexpr int RPI = kAttnThreads / F4;          // rows per load instruction of the workgroup
+  constexpr int kTile = GM <= 4 ? 128 : 64;       // positions per chunk (registers permitting)
+  constexpr int TL = kTile / RPI;                 // rows (float4) per thread per chunk
+  const int kvh = blockIdx.x, sp = blockIdx.y;
   const int pos = (int)a.st->pos;
   const int T = pos + 1;
-  const int c0 = ch * kChunk;
+  const int CH = a.split_len;
+  const int c0 = sp * CH;
   if (c0 >= T) return;  // uniform per workgroup
-  const int c1 = min(c0 + kChunk, T);
-  const int G = a.g;
-  const int kvd = a.nkv * HD;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float qs[kMaxG][HD];
-  __shared__ float knew[HD];
-  __shared__ float sc[kMaxG][kChunk];
-  __shared__ float mx[kMaxG], sm[kMaxG];
-  const bool has_pos = pos < c1;  // this chunk holds the current token
-  const float pos_f = (float)pos;
-
-  for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = a.q[(kvh * G) * HD + i];
-  if (has_pos)
-    for (int i = tid; i < HD; i += 256) knew[i] = a.k[kvh * HD + i];
-  __syncthreads();
-  for (int hh = wave; hh < G + (has_pos ? 1 : 0); hh += 4) {
-    if (hh < G) norm_rope_head<HD>(qs[hh], a.q_norm, a.inv_freq, pos_f, a.eps, lane);
-    else norm_rope_head<HD>(knew, a.k_norm, a.inv_freq, pos_f, a.eps, lane);
-  }
-  __syncthreads();
-  if (has_pos) {
-    // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
-    for (int i = tid; i < HD; i += 256) {
-      a.kcache[(size_t)pos * kvd + kvh * HD + i] = knew[i];
-      a.vcache[(size_t)pos * kvd + kvh * HD + i] = a.v[kvh * HD + i];
-    }
-  }
-  // scores: 16 lanes per (head, token) dot product, 4 dots per wave
+  const int c1 = min(c0 + CH, T);
   const int n_t = c1 - c0;
-  const int sub = lane >> 4, l16 = lane & 15;
-  for (int base = wave * 4; base < G * kChunk; base += 16) {
-    const int idx = base + sub;
-    const int g = idx / kChunk, tt = idx % kChunk;
-    float part = 0.0f;
-    if (g < G && tt < n_t) {
-      const int t = c0 + tt;
-      const float* krow = (t == pos) ? knew : a.kcache + (size_t)t * kvd + kvh * HD;
+  const int G = a.g;
+  const size_t rowf4 = (size_t)a.nkv * F4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = tid % F4, r0 = tid / F4;  // this thread's column, first row of each chunk
+  __shared__ __attribute__((aligned(16))) float red[RPI * HD];  // column sums of P.V
+  __shared__ __attribute__((aligned(16))) float qs[GM][HD];
+  __shared__ __attribute__((aligned(16))) float knew[HD];
+  __shared__ __attribute__((aligned(16))) float vnew[HD];
+  __shared__ float sc[GM][kTile];
+  __shared__ float mx[GM], sm[GM], al[GM];
+  const bool has_pos = pos < c1;  // this split holds the current token
+  const float4* K4 = reinterpret_cast<const float4*>(a.kcache);
+  const float4* V4 = reinterpret_cast<const float4*>(a.vcache);
+
+  // Every load below is unconditional (indices clamped to valid rows), so
+  // the compiler's wait counts stay exact and a chunk's loads remain in
+  // flight while the previous chunk is used.  The current row (written by
+  // this step) is read too and replaced by the LDS copy.
+  auto load_chunk = [&](float4 (&kr)[TL], float4 (&vr)[TL], int tb) {
 #pragma unroll
-      for (int e = l16; e < HD; e += 16) part = fmaf(qs[g][e], krow[e], part);
+    for (int i = 0; i < TL; i++) {
+      const int t = min(tb + r0 + RPI * i, n_t - 1);
+      const size_t off = (size_t)(c0 + t) * rowf4 + kvh * F4 + c;
+      kr[i] = K4[off];
+      vr[i] = V4[off];
     }
-    part = seg_sum<16>(part);
-    if (l16 == 0 && g < G && tt < n_t) sc[g][tt] = part * a.scale;
+  };
+  // prologue operands first: query heads, new k and v, norm gains and the
+  // rotation table (lane l of a wave needs elements l and l + HD/2)
+  constexpr int HALF = HD / 2;
+  const int hl = lane % HALF;
+  const float4 qv = reinterpret_cast<const float4*>(a.q)[kvh * G * F4 + min(tid, G * F4 - 1)];
+  const float4 knv = reinterpret_cast<const float4*>(a.k)[kvh * F4 + c];
+  const float4 vnv = reinterpret_cast<const float4*>(a.v)[kvh * F4 + c];
+  const float qw0 = a.q_norm[hl], qw1 = a.q_norm[hl + HALF];
+  const float kw0 = a.k_norm[hl], kw1 = a.k_norm[hl + HALF];
+  const float cs0 = a.rope_cs[hl], cs1 = a.rope_cs[hl + HALF];
+  float4 kr[TL], vr[TL], kn[TL], vn[TL];
+  load_chunk(kn, vn, 0);
+  // unconditional store (surplus threads repeat the last element): a
+  // conditional one lets the compiler sink the load behind the K/V loads
+  reinterpret_cast<float4*>(&qs[0][0])[min(tid, G * F4 - 1)] = qv;
+  // unconditional too: every workgroup keeps a copy of the new row
+  reinterpret_cast<float4*>(knew)[c] = knv;
+  reinterpret_cast<float4*>(vnew)[c] = vnv;
+  if (tid < GM) {
+    mx[tid] = -INFINITY;
+    sm[tid] = 0.0f;
   }
   __syncthreads();
-  // per-head chunk max and exp-sum (softmax, attention.rs:48-84)
-  if (wave == 0) {
-    for (int g = 0; g < G; g++) {
-      float m = (lane < n_t) ? sc[g][lane] : -INFINITY;
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      float e = (lane < n_t) ? expf(sc[g][lane] - m) : 0.0f;
-      if (lane < n_t) sc[g][lane] = e;
-      const float l = seg_sum<64>(e);
-      if (lane == 0) {
-        mx[g] = m;
-        sm[g] = l;
-        if (!isfinite(m)) atomicOr(&a.st->err, 4u);
+  // QK-norm (ops.rs:29-52) + NeoX RoPE (ops.rs:111-132), one wave per head
+  for (int hh = wave; hh < G + (has_pos ? 1 : 0); hh += kAttnThreads / 64) {
+    float* h = hh < G ? qs[hh] : knew;
+    const float w0 = hh < G ? qw0 : kw0, w1 = hh < G ? qw1 : kw1;
+    float x0 = 0.0f, x1 = 0.0f;
+    if (lane < HALF) {
+      x0 = h[lane];
+      x1 = h[lane + HALF];
+    }
+    const float ssq = wave_sum(x0 * x0 + x1 * x1);
+    const float rinv = 1.0f / sqrtf(ssq / (float)HD + a.eps);
+    if (lane < HALF) {
+      const float xa = x0 * rinv * w0;
+      const float xb = x1 * rinv * w1;
+      h[lane] = xa * cs0 - xb * cs1;
+      h[lane + HALF] = xa * cs1 + xb * cs0;
+    }
+  }
+  __syncthreads();
+  if (has_pos && tid < F4) {
+    // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
+    const size_t off = (size_t)pos * rowf4 + kvh * F4 + tid;
+    reinterpret_cast<float4*>(a.kcache)[off] = reinterpret_cast<const float4*>(knew)[tid];
+    reinterpret_cast<float4*>(a.vcache)[off] = reinterpret_cast<const float4*>(vnew)[tid];
+  }
+  float4 qc[GM];  // this thread's column of every query head
+#pragma unroll
+  for (int g = 0; g < GM; g++)
+    if (g < G) qc[g] = *reinterpret_cast<const float4*>(&qs[g][4 * c]);
+  float4 acc[GM];
+#pragma unroll
+  for (int g = 0; g < GM; g++) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+  const int nchunk = (n_t + kTile - 1) / kTile;
+  for (int ci = 0; ci < nchunk; ci++) {
+    const int tb = ci * kTile;
+    const int nc_t = min(kTile, n_t - tb);
+#pragma unroll
+    for (int i = 0; i < TL; i++) {
+      kr[i] = kn[i];
+      vr[i] = vn[i];
+    }
+    if (ci + 1 < nchunk) load_chunk(kn, vn, tb + kTile);
+    // scores of the chunk
+#pragma unroll
+    for (int i = 0; i < TL; i++) {
+      const int t = r0 + RPI * i;  // row in the chunk (uniform per F4-lane group)
+      if (c0 + tb + t == pos) {
+        kr[i] = reinterpret_cast<const float4*>(knew)[c];
+        vr[i] = reinterpret_cast<const float4*>(vnew)[c];
+      }
+#pragma unroll
+      for (int g = 0; g < GM; g++) {
+        if (g < G) {
+          float d = qc[g].x * kr[i].x;
+          d = fmaf(qc[g].y, kr[i].y, d);
+          d = fmaf(qc[g].z, kr[i].z, d);
+          d = fmaf(qc[g].w, kr[i].w, d);
+          d = group_sum<F4>(d);
+          // the row total sits in every lane (F4 = 16) or in the upper
+          // half of the 32 lanes (F4 = 32)
+          if (c == (F4 == 32 ? 16 : 0) && t < nc_t) sc[g][t] = d * a.scale;
+        }
       }
     }
-  }
-  __syncthreads();
-  // o[g][d] = sum_t e_t * v_t[d], ascending t (weighted_add order)
-  for (int i = tid; i < G * HD; i += 256) {
-    const int g = i / HD, d = i % HD;
-    float o = 0.0f;
-    for (int tt = 0; tt < n_t; tt++) {
-      const int t = c0 + tt;
-      const float vv = (t == pos) ? a.v[kvh * HD + d] : a.vcache[(size_t)t * kvd + kvh * HD + d];
-      o = fmaf(sc[g][tt], vv, o);
+    __syncthreads();
+    // online softmax: running max, rescale factor, exp-sum
+    for (int g = wave; g < G; g += kAttnThreads / 64) {
+      float s0 = -INFINITY, s1 = -INFINITY;
+      if (lane < nc_t) s0 = sc[g][lane];
+      if (lane + 64 < nc_t) s1 = sc[g][lane + 64];
+      const float m_old = mx[g];
+      const float m_new = fmaxf(m_old, wave_max(fmaxf(s0, s1)));
+      const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+      const float e0 = lane < nc_t ? expf(s0 - m_new) : 0.0f;
+      const float e1 = lane + 64 < nc_t ? expf(s1 - m_new) : 0.0f;
+      if (lane < nc_t) sc[g][lane] = e0;
+      if (lane + 64 < nc_t) sc[g][lane + 64] = e1;
+      const float l = wave_sum(e0 + e1);
+      if (lane == 0) {
+        mx[g] = m_new;
+        sm[g] = fmaf(sm[g], alpha, l);
+        al[g] = alpha;
+      }
     }
-    float* p = a.part + ((size_t)(kvh * G + g) * a.nchunks + ch) * (HD + 2);
-    p[2 + d] = o;
-    if (d == 0) {
-      p[0] = mx[g];
-      p[1] = sm[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+      if (g < G) {
+        const float alpha = al[g];
+        acc[g].x *= alpha;
+        acc[g].y *= alpha;
+        acc[g].z *= alpha;
+        acc[g].w *= alpha;
+      }
     }
+#pragma unroll
+    for (int i = 0; i < TL; i++) {
+      const int t = r0 + RPI * i;
+      if (t < nc_t) {
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+          if (g < G) {
+            const float p = sc[g][t];
+            acc[g].x = fmaf(p, vr[i].x, acc[g].x);
+            acc[g].y = fmaf(p, vr[i].y, acc[g].y);
+            acc[g].z = fmaf(p, vr[i].z, acc[g].z);
+            acc[g].w = fmaf(p, vr[i].w, acc[g].w);
+          }
+        }
+      }
+    }
+    __syncthreads();  // sc is rewritten by the next chunk
   }
-  // The workgroup that finishes last for this KV head merges the chunks of
-  // its G query heads (split-T reduction without a second launch).  Release:
-  // partials reach device scope before the count; acquire: the last
-  // workgroup sees every other chunk's partials.
+  if (tid < G && !isfinite(mx[tid])) atomicOr(&a.st->err, 4u);
+  // splits that hold positions this step; one split needs no merge
+  const int nsp = (T + CH - 1) / CH;
+  const bool single = nsp == 1;
+#pragma unroll
+  for (int g = 0; g < GM; g++) {
+    if (g >= G) break;
+    reinterpret_cast<float4*>(red)[r0 * F4 + c] = acc[g];
+    __syncthreads();
+    if (tid < HD) {
+      float o = 0.0f;
+      for (int j = 0; j < RPI; j++) o += red[j * HD + tid];
+      if (single) {
+        // softmax normalization as attention.rs:76-81: multiply by 1/sum
+        a.out[(kvh * G + g) * HD + tid] = o * (1.0f / sm[g]);
+      } else {
+        float* p = a.part + ((size_t)(kvh * G + g) * a.nsplit + sp) * (HD + 2);
+        p[2 + tid] = o;
+        if (tid == 0) {
+          p[0] = mx[g];
+          p[1] = sm[g];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (single) return;
+  // The workgroup that finishes last for this KV head merges the splits of
+  // its G query heads.  Release: partials reach device scope before the
+  // count; acquire: the last workgroup sees every other split's partials.
   __shared__ int is_last;
   __threadfence();
   __syncthreads();
-  if (tid == 0) {
-    const unsigned nc = (unsigned)((T + kChunk - 1) / kChunk);
-    is_last = atomicAdd(&a.counters[kvh], 1u) == nc - 1;
-  }
+  if (tid == 0) is_last = atomicAdd(&a.counters[kvh], 1u) == (unsigned)(nsp - 1);
   __syncthreads();
   if (!is_last) return;
   __threadfence();
-  const int nc = (T + kChunk - 1) / kChunk;
-  for (int i = tid; i < G * HD; i += 256) {
+  for (int i = tid; i < G * HD; i += kAttnThreads) {
     const int g = i / HD, d = i % HD;
-    const float* p = a.part + (size_t)(kvh * G + g) * a.nchunks * (HD + 2);
+    const float* p = a.part + (size_t)(kvh * G + g) * a.nsplit * (HD + 2);
     float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, p[c * (HD + 2)]);
+    for (int s2 = 0; s2 < nsp; s2++) M = fmaxf(M, p[s2 * (HD + 2)]);
     float L = 0.0f, o = 0.0f;
-    for (int c = 0; c < nc; c++) {
-      const float w = expf(p[c * (HD + 2)] - M);
-      L = fmaf(w, p[c * (HD + 2) + 1], L);
-      o = fmaf(w, p[c * (HD + 2) + 2 + d], o);
+    for (int s2 = 0; s2 < nsp; s2++) {
+      const float w = expf(p[s2 * (HD + 2)] - M);
+      L = fmaf(w, p[s2 * (HD + 2) + 1], L);
+      o = fmaf(w, p[s2 * (HD + 2) + 2 + d], o);
     }
-    // softmax normalization as attention.rs:76-81: multiply by 1/sum
     a.out[(kvh * G + g) * HD + d] = o * (1.0f / L);
   }
   if (tid == 0) a.counters[kvh] = 0;  // ready for the next launch
@@ -298,6 +416,7 @@ struct zg_model {
   const uint8_t* head = nullptr;
   float* out_norm = nullptr;
   float* inv_freq = nullptr;
+  float* rope_cs = nullptr;  // this position's RoPE cos/sin table [head_dim]
   float* kv = nullptr;
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
   float* logits = nullptr;
@@ -309,7 +428,7 @@ struct zg_model {
   size_t prompt_cap = 0;
   uint32_t* out_tokens = nullptr;
   size_t out_cap = 0;
-  int nchunks = 0;
+  int nsplit = 1, split_len = 0;
   std::vector<void*> owned;  // device allocations to free
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
@@ -350,7 +469,8 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
   const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
   const int qd = (int)(d.n_q_heads * d.head_dim), kvd = (int)(d.n_kv_heads * d.head_dim);
   zg_ctx* ctx = m->ctx;
-  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, m->embd, d.embd_type, H, m->st, m->best, m->hidden);
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, m->embd, d.embd_type, H, m->st, m->best, m->hidden,
+                     m->inv_freq, HD / 2, m->rope_cs);
   zg_status s = hip_check(ctx, hipGetLastError(), "embed launch");
   if (s) return s;
   const float scale = 1.0f / sqrtf((float)HD);
@@ -366,7 +486,7 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.v = m->v;
     aa.q_norm = L.q_norm;
     aa.k_norm = L.k_norm;
-    aa.inv_freq = m->inv_freq;
+    aa.rope_cs = m->rope_cs;
     aa.kcache = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
     aa.vcache = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
     aa.part = m->part;
@@ -375,13 +495,20 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.st = m->st;
     aa.nkv = (int)d.n_kv_heads;
     aa.g = (int)(d.n_q_heads / d.n_kv_heads);
-    aa.nchunks = m->nchunks;
+    aa.nsplit = m->nsplit;
+    aa.split_len = m->split_len;
     aa.eps = d.rms_eps;
     aa.scale = scale;
-    if (HD == 128)
-      hipLaunchKernelGGL(attn_partial_kernel<128>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
-    else
-      hipLaunchKernelGGL(attn_partial_kernel<64>, dim3(d.n_kv_heads, m->nchunks), dim3(256), 0, st, aa);
+    const dim3 ag(d.n_kv_heads, m->nsplit), ab(kAttnThreads);
+    if (HD == 128) {
+      if (aa.g <= 2) hipLaunchKernelGGL((attn_decode_kernel<128, 2>), ag, ab, 0, st, aa);
+      else if (aa.g <= 4) hipLaunchKernelGGL((attn_decode_kernel<128, 4>), ag, ab, 0, st, aa);
+      else hipLaunchKernelGGL((attn_decode_kernel<128, 8>), ag, ab, 0, st, aa);
+    } else {
+      if (aa.g <= 2) hipLaunchKernelGGL((attn_decode_kernel<64, 2>), ag, ab, 0, st, aa);
+      else if (aa.g <= 4) hipLaunchKernelGGL((attn_decode_kernel<64, 4>), ag, ab, 0, st, aa);
+      else hipLaunchKernelGGL((attn_decode_kernel<64, 8>), ag, ab, 0, st, aa);
+    }
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
     if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
                         PRO_PLAIN, nullptr, 0.0f, st)))
@@ -488,8 +615,13 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     }
     s = upload_f32(m, &m->inv_freq, inv.data(), inv.size());
   }
-  m->nchunks = (int)((d.max_ctx + kChunk - 1) / kChunk);
+  // one workgroup per KV head streams its whole context (a 1024-thread
+  // workgroup sustains ~100 GB/s); contexts above kSplitMax are split and
+  // merged by the last workgroup
+  m->split_len = (int)(d.max_ctx <= (uint32_t)kSplitMax ? d.max_ctx : (uint32_t)kSplitMax);
+  m->nsplit = (int)((d.max_ctx + m->split_len - 1) / m->split_len);
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->kv), (size_t)d.n_layers * 2 * d.max_ctx * kvd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->rope_cs), d.head_dim * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->hidden), H * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->q), qd * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->k), kvd * sizeof(float));
@@ -499,7 +631,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->logits), (size_t)d.vocab_padded * sizeof(float));
   if (!s)
     s = model_alloc(m, reinterpret_cast<void**>(&m->part),
-                    (size_t)d.n_q_heads * m->nchunks * (d.head_dim + 2) * sizeof(float));
+                    (size_t)d.n_q_heads * m->nsplit * (d.head_dim + 2) * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->counters), d.n_kv_heads * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
