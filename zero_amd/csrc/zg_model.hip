@@ -95,34 +95,44 @@ struct AttnArgs {
   float* vcache;       // this layer's V rows
   float* part;         // partials [nq][nsplit][HD+2] (nsplit > 1 only)
   float* out;          // merged attention output [nq*HD]
-  uint32_t* counters;  // per KV head: chunk workgroups finished (self-resetting)
+  uint32_t* counters;  // per query head: split workgroups finished (self-resetting)
   DevState* st;
   int nkv, g, nsplit, split_len;
   float eps, scale;
 };
 
-// Decode attention for one KV head (grid: KV heads x splits; one split
-// unless the context exceeds kSplitMax positions).  1024 threads walk the
-// split in chunks of kTile positions with an online softmax; each chunk's
-// K and V rows are loaded into registers one chunk ahead in the coalesced
-// (row, float4 column) order, and both products work in that order:
-//   scores  thread (row, column c) dots its float4 of k_row with q_g's
-//           float4 c; the F4 lanes of a row are summed with DPP
-//   softmax one wave per head updates the running max and exp-sum
-//           (attention.rs:48-84, rescaled online)
-//   P.V     the same thread adds e_row * v_row[c] to its column's
-//           accumulator; at the end the accumulators of each column are
-//           summed through LDS and divided by the exp-sum (attention.rs:
-//           76-81 multiplies by 1/sum)
-// With several splits each writes (max, sum, o) and the last workgroup of
-// the KV head merges them.
-template <int HD, int GM>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
-  constexpr int F4 = HD / 4;                      // float4 per head row (= lanes per row)
-  constexpr int RPI = kAttnThreads / F4;          // rows per load instruction of the workgroup
-  constexpr int kTile = GM <= 4 ? 128 : 64;       // positions per chunk (registers permitting)
-  constexpr int TL = kTile / RPI;                 // rows (float4) per thread per chunk
-  const int kvh = blockIdx.x, sp = blockIdx.y;
+// Decode attention for one query head (grid: query heads x splits; one
+// split unless the context exceeds kSplitMax positions), flash-decoding
+// inside the workgroup: each of the 16 waves owns 8 rows of every 128-row
+// chunk and keeps its own running max, exp-sum and output; the waves are
+// merged once at the end.  K and V rows are loaded one chunk ahead with
+// unconditional (clamped) loads so that the compiler's wait counts stay
+// exact; the current row, written by this step, comes from LDS.
+//   score   lane (row r, slice s) holds float4 columns s, s+8, ... of its K
+//           row; the partial dot is summed over the row's 8 lanes by DPP;
+//           softmax as attention.rs:48-84, rescaled online
+//   P.V     lane l holds dims VPL*l.. of all 8 rows of V; the row weights
+//           are read out with v_readlane, so every lane accumulates its own
+//           output dims and no cross-lane sum is needed at the end
+//   end     waves merged through LDS; o / sum written (attention.rs:76-81
+//           multiplies by 1/sum); several splits write (max, sum, o) and the
+//           last workgroup of the head merges them
+// The G query heads of a KV head run in G workgroups; the first stores the
+// new K/V row.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_head_kernel(AttnArgs a) {
+  constexpr int F4 = HD / 4;             // float4 per head row
+  constexpr int LPR = 8;                 // lanes per row in the score layout
+  constexpr int CPL = F4 / LPR;          // K float4 columns per lane
+  constexpr int RPW = 64 / LPR;          // rows per wave per chunk
+  constexpr int VPL = HD / 64;           // V dims per lane
+  constexpr int NWV = kAttnThreads / 64;
+  constexpr int CHUNK = RPW * NWV;       // rows per chunk
+  constexpr int HALF = HD / 2;
+  typedef float vlane_t __attribute__((ext_vector_type(VPL)));
+  const int qh = blockIdx.x, sp = blockIdx.y;
+  const int G = a.g;
+  const int kvh = qh / G;
   const int pos = (int)a.st->pos;
   const int T = pos + 1;
   const int CH = a.split_len;
@@ -130,60 +140,53 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
   if (c0 >= T) return;  // uniform per workgroup
   const int c1 = min(c0 + CH, T);
   const int n_t = c1 - c0;
-  const int G = a.g;
   const size_t rowf4 = (size_t)a.nkv * F4;
+  const size_t rowv = (size_t)a.nkv * HD / VPL;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = tid % F4, r0 = tid / F4;  // this thread's column, first row of each chunk
-  __shared__ __attribute__((aligned(16))) float red[RPI * HD];  // column sums of P.V
-  __shared__ __attribute__((aligned(16))) float qs[GM][HD];
+  const int r = lane / LPR, sl = lane % LPR;
+  __shared__ __attribute__((aligned(16))) float qs[HD];
   __shared__ __attribute__((aligned(16))) float knew[HD];
   __shared__ __attribute__((aligned(16))) float vnew[HD];
-  __shared__ float sc[GM][kTile];
-  __shared__ float mx[GM], sm[GM], al[GM];
+  __shared__ __attribute__((aligned(16))) float wo[NWV][HD];
+  __shared__ float wm[NWV], wl[NWV];
   const bool has_pos = pos < c1;  // this split holds the current token
   const float4* K4 = reinterpret_cast<const float4*>(a.kcache);
-  const float4* V4 = reinterpret_cast<const float4*>(a.vcache);
+  const vlane_t* VL = reinterpret_cast<const vlane_t*>(a.vcache);
 
-  // Every load below is unconditional (indices clamped to valid rows), so
-  // the compiler's wait counts stay exact and a chunk's loads remain in
-  // flight while the previous chunk is used.  The current row (written by
-  // this step) is read too and replaced by the LDS copy.
-  auto load_chunk = [&](float4 (&kr)[TL], float4 (&vr)[TL], int tb) {
+  auto load_chunk = [&](float4 (&kr)[CPL], vlane_t (&vr)[RPW], int tb) {
+    const int tk = min(tb + wave * RPW + r, n_t - 1);
+    const size_t ko = (size_t)(c0 + tk) * rowf4 + kvh * F4;
 #pragma unroll
-    for (int i = 0; i < TL; i++) {
-      const int t = min(tb + r0 + RPI * i, n_t - 1);
-      const size_t off = (size_t)(c0 + t) * rowf4 + kvh * F4 + c;
-      kr[i] = K4[off];
-      vr[i] = V4[off];
+    for (int i = 0; i < CPL; i++) kr[i] = K4[ko + sl + LPR * i];
+#pragma unroll
+    for (int j = 0; j < RPW; j++) {
+      const int tv = min(tb + wave * RPW + j, n_t - 1);
+      vr[j] = VL[(size_t)(c0 + tv) * rowv + kvh * (HD / VPL) + lane];
     }
   };
-  // prologue operands first: query heads, new k and v, norm gains and the
-  // rotation table (lane l of a wave needs elements l and l + HD/2)
-  constexpr int HALF = HD / 2;
+  // prologue operands, then chunk 0's K/V loads
+  const int cc = tid % F4;
+  const float4 qv = reinterpret_cast<const float4*>(a.q)[qh * F4 + cc];
+  const float4 knv = reinterpret_cast<const float4*>(a.k)[kvh * F4 + cc];
+  const float4 vnv = reinterpret_cast<const float4*>(a.v)[kvh * F4 + cc];
   const int hl = lane % HALF;
-  const float4 qv = reinterpret_cast<const float4*>(a.q)[kvh * G * F4 + min(tid, G * F4 - 1)];
-  const float4 knv = reinterpret_cast<const float4*>(a.k)[kvh * F4 + c];
-  const float4 vnv = reinterpret_cast<const float4*>(a.v)[kvh * F4 + c];
   const float qw0 = a.q_norm[hl], qw1 = a.q_norm[hl + HALF];
   const float kw0 = a.k_norm[hl], kw1 = a.k_norm[hl + HALF];
   const float cs0 = a.rope_cs[hl], cs1 = a.rope_cs[hl + HALF];
-  float4 kr[TL], vr[TL], kn[TL], vn[TL];
+  float4 kr[CPL], kn[CPL];
+  vlane_t vr[RPW], vn[RPW];
   load_chunk(kn, vn, 0);
-  // unconditional store (surplus threads repeat the last element): a
-  // conditional one lets the compiler sink the load behind the K/V loads
-  reinterpret_cast<float4*>(&qs[0][0])[min(tid, G * F4 - 1)] = qv;
-  // unconditional too: every workgroup keeps a copy of the new row
-  reinterpret_cast<float4*>(knew)[c] = knv;
-  reinterpret_cast<float4*>(vnew)[c] = vnv;
-  if (tid < GM) {
-    mx[tid] = -INFINITY;
-    sm[tid] = 0.0f;
-  }
+  // surplus threads repeat the same values (unconditional stores keep the
+  // operand loads ahead of the K/V loads)
+  reinterpret_cast<float4*>(qs)[cc] = qv;
+  reinterpret_cast<float4*>(knew)[cc] = knv;
+  reinterpret_cast<float4*>(vnew)[cc] = vnv;
   __syncthreads();
-  // QK-norm (ops.rs:29-52) + NeoX RoPE (ops.rs:111-132), one wave per head
-  for (int hh = wave; hh < G + (has_pos ? 1 : 0); hh += kAttnThreads / 64) {
-    float* h = hh < G ? qs[hh] : knew;
-    const float w0 = hh < G ? qw0 : kw0, w1 = hh < G ? qw1 : kw1;
+  // QK-norm (ops.rs:29-52) + NeoX RoPE (ops.rs:111-132): wave 0 the query
+  // head, wave 1 the new key
+  if (wave < 2) {
+    float* h = wave == 0 ? qs : knew;
+    const float w0 = wave == 0 ? qw0 : kw0, w1 = wave == 0 ? qw1 : kw1;
     float x0 = 0.0f, x1 = 0.0f;
     if (lane < HALF) {
       x0 = h[lane];
@@ -199,152 +202,110 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  if (has_pos && tid < F4) {
+  if (has_pos && qh % G == 0 && tid < F4) {
     // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
     const size_t off = (size_t)pos * rowf4 + kvh * F4 + tid;
     reinterpret_cast<float4*>(a.kcache)[off] = reinterpret_cast<const float4*>(knew)[tid];
     reinterpret_cast<float4*>(a.vcache)[off] = reinterpret_cast<const float4*>(vnew)[tid];
   }
-  float4 qc[GM];  // this thread's column of every query head
+  float4 q[CPL];
 #pragma unroll
-  for (int g = 0; g < GM; g++)
-    if (g < G) qc[g] = *reinterpret_cast<const float4*>(&qs[g][4 * c]);
-  float4 acc[GM];
-#pragma unroll
-  for (int g = 0; g < GM; g++) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-
-  const int nchunk = (n_t + kTile - 1) / kTile;
+  for (int i = 0; i < CPL; i++) q[i] = reinterpret_cast<const float4*>(qs)[sl + LPR * i];
+  vlane_t acc = (vlane_t)(0.0f);
+  float m_w = -INFINITY, l_w = 0.0f;
+  const int nchunk = (n_t + CHUNK - 1) / CHUNK;
   for (int ci = 0; ci < nchunk; ci++) {
-    const int tb = ci * kTile;
-    const int nc_t = min(kTile, n_t - tb);
 #pragma unroll
-    for (int i = 0; i < TL; i++) {
-      kr[i] = kn[i];
-      vr[i] = vn[i];
+    for (int i = 0; i < CPL; i++) kr[i] = kn[i];
+#pragma unroll
+    for (int j = 0; j < RPW; j++) vr[j] = vn[j];
+    if (ci + 1 < nchunk) load_chunk(kn, vn, (ci + 1) * CHUNK);
+    const int t0 = ci * CHUNK + wave * RPW;  // first row of this wave
+    const int t = t0 + r;
+    const bool valid = t < n_t;
+    if (c0 + t == pos) {
+#pragma unroll
+      for (int i = 0; i < CPL; i++) kr[i] = reinterpret_cast<const float4*>(knew)[sl + LPR * i];
     }
-    if (ci + 1 < nchunk) load_chunk(kn, vn, tb + kTile);
-    // scores of the chunk
+    float d = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TL; i++) {
-      const int t = r0 + RPI * i;  // row in the chunk (uniform per F4-lane group)
-      if (c0 + tb + t == pos) {
-        kr[i] = reinterpret_cast<const float4*>(knew)[c];
-        vr[i] = reinterpret_cast<const float4*>(vnew)[c];
-      }
-#pragma unroll
-      for (int g = 0; g < GM; g++) {
-        if (g < G) {
-          float d = qc[g].x * kr[i].x;
-          d = fmaf(qc[g].y, kr[i].y, d);
-          d = fmaf(qc[g].z, kr[i].z, d);
-          d = fmaf(qc[g].w, kr[i].w, d);
-          d = group_sum<F4>(d);
-          // the row total sits in every lane (F4 = 16) or in the upper
-          // half of the 32 lanes (F4 = 32)
-          if (c == (F4 == 32 ? 16 : 0) && t < nc_t) sc[g][t] = d * a.scale;
-        }
-      }
+    for (int i = 0; i < CPL; i++) {
+      d = fmaf(q[i].x, kr[i].x, d);
+      d = fmaf(q[i].y, kr[i].y, d);
+      d = fmaf(q[i].z, kr[i].z, d);
+      d = fmaf(q[i].w, kr[i].w, d);
     }
-    __syncthreads();
-    // online softmax: running max, rescale factor, exp-sum
-    for (int g = wave; g < G; g += kAttnThreads / 64) {
-      float s0 = -INFINITY, s1 = -INFINITY;
-      if (lane < nc_t) s0 = sc[g][lane];
-      if (lane + 64 < nc_t) s1 = sc[g][lane + 64];
-      const float m_old = mx[g];
-      const float m_new = fmaxf(m_old, wave_max(fmaxf(s0, s1)));
-      const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-      const float e0 = lane < nc_t ? expf(s0 - m_new) : 0.0f;
-      const float e1 = lane + 64 < nc_t ? expf(s1 - m_new) : 0.0f;
-      if (lane < nc_t) sc[g][lane] = e0;
-      if (lane + 64 < nc_t) sc[g][lane + 64] = e1;
-      const float l = wave_sum(e0 + e1);
-      if (lane == 0) {
-        mx[g] = m_new;
-        sm[g] = fmaf(sm[g], alpha, l);
-        al[g] = alpha;
-      }
-    }
-    __syncthreads();
+    d += dpp_f32<0xB1>(d);   // quad_perm [1,0,3,2]
+    d += dpp_f32<0x4E>(d);   // quad_perm [2,3,0,1]
+    d += dpp_f32<0x141>(d);  // row_half_mirror: the 8 lanes of the row
+    const float sc = valid ? d * a.scale : -INFINITY;
+    const float cm = wave_max(sc);
+    if (cm == -INFINITY) continue;  // no row of this wave in the chunk (uniform)
+    const float m_new = fmaxf(m_w, cm);
+    const float alpha = m_w == -INFINITY ? 0.0f : expf(m_w - m_new);
+    const float e = valid ? expf(sc - m_new) : 0.0f;
+    l_w = fmaf(l_w, alpha, wave_sum(sl == 0 ? e : 0.0f));
+    acc *= alpha;
 #pragma unroll
-    for (int g = 0; g < GM; g++) {
-      if (g < G) {
-        const float alpha = al[g];
-        acc[g].x *= alpha;
-        acc[g].y *= alpha;
-        acc[g].z *= alpha;
-        acc[g].w *= alpha;
-      }
+    for (int j = 0; j < RPW; j++) {
+      const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j * LPR));
+      const vlane_t v = (c0 + t0 + j == pos) ? reinterpret_cast<const vlane_t*>(vnew)[lane] : vr[j];
+      acc += ej * v;
     }
-#pragma unroll
-    for (int i = 0; i < TL; i++) {
-      const int t = r0 + RPI * i;
-      if (t < nc_t) {
-#pragma unroll
-        for (int g = 0; g < GM; g++) {
-          if (g < G) {
-            const float p = sc[g][t];
-            acc[g].x = fmaf(p, vr[i].x, acc[g].x);
-            acc[g].y = fmaf(p, vr[i].y, acc[g].y);
-            acc[g].z = fmaf(p, vr[i].z, acc[g].z);
-            acc[g].w = fmaf(p, vr[i].w, acc[g].w);
-          }
-        }
-      }
-    }
-    __syncthreads();  // sc is rewritten by the next chunk
+    m_w = m_new;
   }
-  if (tid < G && !isfinite(mx[tid])) atomicOr(&a.st->err, 4u);
-  // splits that hold positions this step; one split needs no merge
+  reinterpret_cast<vlane_t*>(wo[wave])[lane] = acc;
+  if (lane == 0) {
+    wm[wave] = m_w;
+    wl[wave] = l_w;
+  }
+  __syncthreads();
   const int nsp = (T + CH - 1) / CH;
-  const bool single = nsp == 1;
-#pragma unroll
-  for (int g = 0; g < GM; g++) {
-    if (g >= G) break;
-    reinterpret_cast<float4*>(red)[r0 * F4 + c] = acc[g];
-    __syncthreads();
-    if (tid < HD) {
-      float o = 0.0f;
-      for (int j = 0; j < RPI; j++) o += red[j * HD + tid];
-      if (single) {
-        // softmax normalization as attention.rs:76-81: multiply by 1/sum
-        a.out[(kvh * G + g) * HD + tid] = o * (1.0f / sm[g]);
-      } else {
-        float* p = a.part + ((size_t)(kvh * G + g) * a.nsplit + sp) * (HD + 2);
-        p[2 + tid] = o;
-        if (tid == 0) {
-          p[0] = mx[g];
-          p[1] = sm[g];
-        }
+  if (tid < HD) {
+    float M = -INFINITY;
+    for (int w = 0; w < NWV; w++) M = fmaxf(M, wm[w]);
+    float L = 0.0f, o = 0.0f;
+    for (int w = 0; w < NWV; w++) {
+      const float f = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
+      L = fmaf(f, wl[w], L);
+      o = fmaf(f, wo[w][tid], o);
+    }
+    if (tid == 0 && !isfinite(M)) atomicOr(&a.st->err, 4u);
+    if (nsp == 1) {
+      a.out[qh * HD + tid] = o * (1.0f / L);
+    } else {
+      float* p = a.part + ((size_t)qh * a.nsplit + sp) * (HD + 2);
+      p[2 + tid] = o;
+      if (tid == 0) {
+        p[0] = M;
+        p[1] = L;
       }
     }
-    __syncthreads();
   }
-  if (single) return;
-  // The workgroup that finishes last for this KV head merges the splits of
-  // its G query heads.  Release: partials reach device scope before the
-  // count; acquire: the last workgroup sees every other split's partials.
+  if (nsp == 1) return;
+  // The workgroup that finishes last for this head merges the splits.
+  // Release: partials reach device scope before the count; acquire: the
+  // last workgroup sees every other split's partials.
   __shared__ int is_last;
   __threadfence();
   __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&a.counters[kvh], 1u) == (unsigned)(nsp - 1);
+  if (tid == 0) is_last = atomicAdd(&a.counters[qh], 1u) == (unsigned)(nsp - 1);
   __syncthreads();
   if (!is_last) return;
   __threadfence();
-  for (int i = tid; i < G * HD; i += kAttnThreads) {
-    const int g = i / HD, d = i % HD;
-    const float* p = a.part + (size_t)(kvh * G + g) * a.nsplit * (HD + 2);
+  if (tid < HD) {
+    const float* p = a.part + (size_t)qh * a.nsplit * (HD + 2);
     float M = -INFINITY;
     for (int s2 = 0; s2 < nsp; s2++) M = fmaxf(M, p[s2 * (HD + 2)]);
     float L = 0.0f, o = 0.0f;
     for (int s2 = 0; s2 < nsp; s2++) {
       const float w = expf(p[s2 * (HD + 2)] - M);
       L = fmaf(w, p[s2 * (HD + 2) + 1], L);
-      o = fmaf(w, p[s2 * (HD + 2) + 2 + d], o);
+      o = fmaf(w, p[s2 * (HD + 2) + 2 + tid], o);
     }
-    a.out[(kvh * G + g) * HD + d] = o * (1.0f / L);
+    a.out[qh * HD + tid] = o * (1.0f / L);
   }
-  if (tid == 0) a.counters[kvh] = 0;  // ready for the next launch
+  if (tid == 0) a.counters[qh] = 0;  // ready for the next launch
 }
 
 __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
@@ -499,16 +460,9 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.split_len = m->split_len;
     aa.eps = d.rms_eps;
     aa.scale = scale;
-    const dim3 ag(d.n_kv_heads, m->nsplit), ab(kAttnThreads);
-    if (HD == 128) {
-      if (aa.g <= 2) hipLaunchKernelGGL((attn_decode_kernel<128, 2>), ag, ab, 0, st, aa);
-      else if (aa.g <= 4) hipLaunchKernelGGL((attn_decode_kernel<128, 4>), ag, ab, 0, st, aa);
-      else hipLaunchKernelGGL((attn_decode_kernel<128, 8>), ag, ab, 0, st, aa);
-    } else {
-      if (aa.g <= 2) hipLaunchKernelGGL((attn_decode_kernel<64, 2>), ag, ab, 0, st, aa);
-      else if (aa.g <= 4) hipLaunchKernelGGL((attn_decode_kernel<64, 4>), ag, ab, 0, st, aa);
-      else hipLaunchKernelGGL((attn_decode_kernel<64, 8>), ag, ab, 0, st, aa);
-    }
+    const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnThreads);
+    if (HD == 128) hipLaunchKernelGGL(attn_head_kernel<128>, ag, ab, 0, st, aa);
+    else hipLaunchKernelGGL(attn_head_kernel<64>, ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
     if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
                         PRO_PLAIN, nullptr, 0.0f, st)))
@@ -632,7 +586,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s)
     s = model_alloc(m, reinterpret_cast<void**>(&m->part),
                     (size_t)d.n_q_heads * m->nsplit * (d.head_dim + 2) * sizeof(float));
-  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->counters), d.n_kv_heads * sizeof(uint32_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->counters), d.n_q_heads * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
   m->prompt_cap = d.max_ctx;
