@@ -437,17 +437,18 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
     return sg;
   };
 
+  // unconditional loads (items past the end are clamped to the last one
+  // and their results dropped), so the compiler's wait counts stay exact
+  // and a batch's loads stay in flight while the previous batch is used
   auto load_batch = [&](LaneW<QT> (&L)[GBATCH][PARTS], int batch) {
     const int base = batch * per_batch + sub * GBATCH;
 #pragma unroll
     for (int j = 0; j < GBATCH; j++) {
-      if (base + j < items) {
 #pragma unroll
-        for (int p = 0; p < PARTS; p++) {
-          uint32_t lg;
-          const GemvSeg sg = locate(base + j, p, lg);
-          strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
-        }
+      for (int p = 0; p < PARTS; p++) {
+        uint32_t lg;
+        const GemvSeg sg = locate(min(base + j, items - 1), p, lg);
+        strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
       }
     }
   };
@@ -461,8 +462,11 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
 #pragma unroll
     for (int c = 0; c < 8; c++) xb[c] = x4[c];
   }
-  LaneW<QT> L[GBATCH][PARTS];
-  if ((int)blockIdx.x < nbatch) load_batch(L, blockIdx.x);
+  // two batches in flight: this workgroup's first and second
+  LaneW<QT> LA[GBATCH][PARTS], LB[GBATCH][PARTS];
+  const int b0 = blockIdx.x, bstep = gridDim.x;
+  if (b0 < nbatch) load_batch(LA, b0);
+  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
 
   // prologue and block sum
   if (PRO == PRO_RMSNORM) {
@@ -496,8 +500,9 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
   const float mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
 
   uint64_t key = 0;
-  int buf = 0;
-  for (int batch = blockIdx.x; batch < nbatch; batch += gridDim.x, buf ^= 1) {
+  // one batch: partials -> LDS, barrier, per-row totals over strips and
+  // DPP rows in a fixed order, epilogue
+  auto process = [&](const LaneW<QT> (&L)[GBATCH][PARTS], int batch, int buf) {
     const int base = batch * per_batch + sub * GBATCH;
     float* pb = part + (size_t)buf * NW * GBATCH * PARTS * 16;
 #pragma unroll
@@ -510,8 +515,6 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
         }
       }
     }
-    // next batch's loads fly during the barrier and the combine
-    if (batch + (int)gridDim.x < nbatch) load_batch(L, batch + gridDim.x);
     __syncthreads();
     const int tt = threadIdx.x;
     if (tt < per_batch * 4) {
@@ -548,6 +551,16 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
           }
         }
       }
+    }
+  };
+  // batches b0, b0 + bstep, ... alternate between the two register sets;
+  // a set is refilled with the batch two steps ahead as soon as it is used
+  for (int batch = b0; batch < nbatch; batch += 2 * bstep) {
+    process(LA, batch, 0);
+    if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
+    if (batch + bstep < nbatch) {
+      process(LB, batch + bstep, 1);
+      if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
     }
   }
   if (EPI == EPI_ARGMAX) {
@@ -810,15 +823,25 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   const int S = a.k / 512;
   const int nw = S >= 4 ? S : 4;  // S in {1, 2} -> 4 waves: 4 / S waves per strip
   const size_t items = EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups;
-  // small launches use short batches so that more workgroups share the work
+  // small launches use short batches so that more workgroups share the
+  // work; with SwiGLU or argmax epilogues two batches in flight only fit
+  // the register budget at two groups per batch
   const size_t wps = nw / S;
-  if (items <= (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps) return launch_strip_gb<QT, PRO, EPI, 2>(a, S, nw, items, st);
-  return launch_strip_gb<QT, PRO, EPI, 4>(a, S, nw, items, st);
+  if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
+    if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
+      return launch_strip_gb<QT, PRO, EPI, 4>(a, S, nw, items, st);
+  }
+  return launch_strip_gb<QT, PRO, EPI, 2>(a, S, nw, items, st);
 }
 
+// Q4_0X4 takes the strip kernel (measured faster at every decode shape);
+// Q8_0X4 keeps the segment-streaming kernel, whose coalesced LDS-parked
+// loads suit its 32-byte row blocks better than per-lane loads.
 template <uint32_t QT, int PRO, int EPI>
 static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
-  if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+  if constexpr (QT == Q4_0) {
+    if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+  }
   return launch_x4<QT, PRO, EPI>(a, st);
 }
 

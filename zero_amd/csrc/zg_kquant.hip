@@ -93,19 +93,54 @@ struct KqGeom<Q6K> {
   static constexpr int BB = 210;
 };
 
-// One lane's share of one superblock: 32 elements -> partial dot.
+// One lane's share of one superblock (32 elements): its bytes are loaded
+// first (kq_load) and decoded later (kq_dot), so that a wave keeps the next
+// unit's loads in flight while it computes the current one.
+//
 // Q4_K lane (j = sub-block pair 0..3, h = half 0..1): qs bytes
 // [32j + 16h, +16): low nibbles are elements 64j + 16h + i (sub-block 2j),
 // high nibbles elements 64j + 32 + 16h + i (sub-block 2j+1).
-__device__ __forceinline__ float q4k_lane(const uint8_t* blk, const float* xsb, const float* x16sb, int j, int h) {
-  const u32x4 hdr = *reinterpret_cast<const u32x4*>(blk);
-  const u32x4 qv = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * j + 16 * h);
-  const float d = half_bits_to_f32(hdr.x), dmin = half_bits_to_f32(hdr.x >> 16);
-  const uint32_t sb[3] = {hdr.y, hdr.z, hdr.w};
+//
+// Q6_K lane (n = half 0..1, is = 0..1, qp = quarter pair 0..1): l in
+// [16 is, 16 is + 16) of half n, quarters Q = 2 qp and 2 qp + 1
+// (dequant.rs:328-355 element map: quarter Q of l is element 128n + l + 32Q,
+// low 4 bits from ql[l] (Q even) or ql[l+32] (Q odd), nibble selected by
+// Q >= 2, high 2 bits qh[l] >> 2Q, scale sc[8n + is + 2Q]).
+template <uint32_t QT>
+struct KqLane;
+template <>
+struct KqLane<Q4K> {
+  u32x4 hdr, q;
+};
+template <>
+struct KqLane<Q6K> {
+  u32x4 la, lb, hb, sc;
+  uint32_t d;
+};
+
+__device__ __forceinline__ void kq_load(KqLane<Q4K>& L, const uint8_t* blk, int lane) {
+  const int j = (lane >> 1) & 3, h = lane & 1;
+  L.hdr = *reinterpret_cast<const u32x4*>(blk);
+  L.q = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * j + 16 * h);
+}
+
+__device__ __forceinline__ void kq_load(KqLane<Q6K>& L, const uint8_t* blk, int lane) {
+  const int n = (lane >> 2) & 1, is = (lane >> 1) & 1;
+  L.la = ld16u(blk + 64 * n + 16 * is);
+  L.lb = ld16u(blk + 64 * n + 32 + 16 * is);
+  L.hb = ld16u(blk + 128 + 32 * n + 16 * is);
+  L.sc = ld16u(blk + 192);
+  L.d = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208);
+}
+
+__device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const float* xsb, const float* x16sb, int lane) {
+  const int j = (lane >> 1) & 3, h = lane & 1;
+  const float d = half_bits_to_f32(L.hdr.x), dmin = half_bits_to_f32(L.hdr.x >> 16);
+  const uint32_t sb[3] = {L.hdr.y, L.hdr.z, L.hdr.w};
   float scA, mA, scB, mB;
   scale_min_k4(sb, 2 * j, scA, mA);
   scale_min_k4(sb, 2 * j + 1, scB, mB);
-  const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+  const uint32_t q[4] = {L.q.x, L.q.y, L.q.z, L.q.w};
   uint32_t lo[4], hi[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
@@ -122,21 +157,15 @@ __device__ __forceinline__ float q4k_lane(const uint8_t* blk, const float* xsb, 
   return fmaf(-(dmin * mB), xB, acc);
 }
 
-// Q6_K lane (n = half 0..1, is = 0..1, qp = quarter pair 0..1): l in
-// [16 is, 16 is + 16) of half n, quarters Q = 2 qp and 2 qp + 1
-// (dequant.rs:328-355 element map: quarter Q of l is element 128n + l + 32Q,
-// low 4 bits from ql[l] (Q even) or ql[l+32] (Q odd), nibble selected by
-// Q >= 2, high 2 bits qh[l] >> 2Q, scale sc[8n + is + 2Q]).
-__device__ __forceinline__ float q6k_lane(const uint8_t* blk, const float* xsb, const float* x16sb, int n, int is,
-                                          int qp) {
-  const u32x4 la = ld16u(blk + 64 * n + 16 * is);
-  const u32x4 lb = ld16u(blk + 64 * n + 32 + 16 * is);
-  const u32x4 hb = ld16u(blk + 128 + 32 * n + 16 * is);
-  const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * n + is);
-  const float scA = (float)sc[4 * qp], scB = (float)sc[4 * qp + 2];
-  const float d = half_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-  const uint32_t a[4] = {la.x, la.y, la.z, la.w}, b[4] = {lb.x, lb.y, lb.z, lb.w}, hh[4] = {hb.x, hb.y, hb.z, hb.w};
-  const int nsh = 4 * qp;  // nibble select
+__device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const float* xsb, const float* x16sb, int lane) {
+  const int n = (lane >> 2) & 1, is = (lane >> 1) & 1, qp = lane & 1;
+  const uint32_t scw[4] = {L.sc.x, L.sc.y, L.sc.z, L.sc.w};
+  const int ia = 8 * n + is + 4 * qp, ib = ia + 2;  // sc[8n + is + 2Q]
+  const float scA = (float)(int8_t)byte_of(scw, ia), scB = (float)(int8_t)byte_of(scw, ib);
+  const float d = half_bits_to_f32(L.d);
+  const uint32_t a[4] = {L.la.x, L.la.y, L.la.z, L.la.w}, b[4] = {L.lb.x, L.lb.y, L.lb.z, L.lb.w},
+                 hh[4] = {L.hb.x, L.hb.y, L.hb.z, L.hb.w};
+  const int nsh = 4 * qp;                  // nibble select
   const int hA = 4 * qp, hB = 4 * qp + 2;  // qh shift of quarters 2qp, 2qp+1
   uint32_t qA[4], qB[4];
 #pragma unroll
@@ -152,45 +181,59 @@ __device__ __forceinline__ float q6k_lane(const uint8_t* blk, const float* xsb, 
   return fmaf(d * scB, fmaf(-32.0f, xB, sB), acc);
 }
 
+// A wave walks units (row, step of 8 superblocks) of its rows; unit u + 1's
+// loads are issued before unit u is decoded.  Loads are unconditional, with
+// row and superblock indices clamped into the tensor (a clamped lane's
+// result is discarded), so the compiler's wait counts stay exact.
 template <uint32_t QT, int EPI>
 __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
   constexpr int BB = KqGeom<QT>::BB;
   extern __shared__ __attribute__((aligned(16))) float kq_smem[];
   const int k = (int)a.k;
-  float* xs = kq_smem;
-  float* x16 = kq_smem + k;
-  stage_x_kq(xs, x16, a.x, k);
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int sl = lane >> 3;  // superblock of the step
   const int nsb = k / 256;
+  const int steps = (nsb + 7) / 8;
   const size_t rowbytes = (size_t)nsb * BB;
   const size_t nrows = a.row_hi - a.row_lo;
   const size_t wave_id = (size_t)blockIdx.x * kKqWaves + (threadIdx.x >> 6);
   const size_t nwaves = (size_t)gridDim.x * kKqWaves;
+  const size_t my_rows = wave_id < nrows ? (nrows - wave_id + nwaves - 1) / nwaves : 0;
+  const size_t nunits = my_rows * steps;
+  auto unit_blk = [&](size_t u) -> const uint8_t* {
+    const size_t ri = u / steps;
+    const int st = (int)(u % steps);
+    const size_t row = a.row_lo + wave_id + ri * nwaves;
+    const int sb = min(st * 8 + sl, nsb - 1);
+    return a.w + row * rowbytes + (size_t)sb * BB;
+  };
+  KqLane<QT> cur, nxt;
+  if (nunits) kq_load(nxt, unit_blk(0), lane);
+  float* xs = kq_smem;
+  float* x16 = kq_smem + k;
+  stage_x_kq(xs, x16, a.x, k);
+  __syncthreads();
   uint64_t key = 0;
-  for (size_t r = wave_id; r < nrows; r += nwaves) {
-    const size_t row = a.row_lo + r;
-    const uint8_t* wrow = a.w + row * rowbytes;
-    float acc = 0.0f;
-    for (int s = sl; s < nsb; s += 8) {
-      const uint8_t* blk = wrow + (size_t)s * BB;
-      const float* xsb = xs + s * 256;
-      const float* x16sb = x16 + s * 16;
-      if (QT == Q4K)
-        acc += q4k_lane(blk, xsb, x16sb, (lane >> 1) & 3, lane & 1);
-      else
-        acc += q6k_lane(blk, xsb, x16sb, (lane >> 2) & 1, (lane >> 1) & 1, lane & 1);
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) {
-      if (EPI == EPI_RESID)
-        a.y[row] = a.resid[row] + acc;
-      else if (a.y)
-        a.y[row] = acc;
-      if (EPI == EPI_ARGMAX && !(acc != acc)) {
-        const uint64_t kk = argmax_key(acc, (uint32_t)row);
-        key = kk > key ? kk : key;
+  float acc = 0.0f;
+  for (size_t u = 0; u < nunits; u++) {
+    cur = nxt;
+    if (u + 1 < nunits) kq_load(nxt, unit_blk(u + 1), lane);
+    const int st = (int)(u % steps);
+    const int sb = st * 8 + sl;
+    if (sb < nsb) acc += kq_dot(cur, xs + sb * 256, x16 + sb * 16, lane);
+    if (st == steps - 1) {
+      const float v = wave_sum(acc);
+      acc = 0.0f;
+      const size_t row = a.row_lo + wave_id + (u / steps) * nwaves;
+      if (lane == 0) {
+        if (EPI == EPI_RESID)
+          a.y[row] = a.resid[row] + v;
+        else if (a.y)
+          a.y[row] = v;
+        if (EPI == EPI_ARGMAX && !(v != v)) {
+          const uint64_t kk = argmax_key(v, (uint32_t)row);
+          key = kk > key ? kk : key;
+        }
       }
     }
   }
