@@ -114,7 +114,8 @@ struct KqLane<Q4K> {
 };
 template <>
 struct KqLane<Q6K> {
-  u32x4 la, lb, hb, sc;
+  u32x4 la, lb, hb;
+  uint32_t sc0, sc1;  // scales sc[8n .. 8n+7] of the lane's half
   uint32_t d;
 };
 
@@ -129,12 +130,29 @@ __device__ __forceinline__ void kq_load(KqLane<Q6K>& L, const uint8_t* blk, int 
   L.la = ld16u(blk + 64 * n + 16 * is);
   L.lb = ld16u(blk + 64 * n + 32 + 16 * is);
   L.hb = ld16u(blk + 128 + 32 * n + 16 * is);
-  L.sc = ld16u(blk + 192);
+  uint32_t scw[2];
+  __builtin_memcpy(scw, blk + 192 + 8 * n, 8);
+  L.sc0 = scw[0];
+  L.sc1 = scw[1];
   L.d = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208);
 }
 
-__device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const float* xsb, const float* x16sb, int lane) {
-  const int j = (lane >> 1) & 3, h = lane & 1;
+// Element offset (within the superblock) of the lane's first 16-element run;
+// its second run starts 32 elements later.
+template <uint32_t QT>
+__device__ __forceinline__ int kq_lane_elem(int lane) {
+  if (QT == Q4K) return 64 * ((lane >> 1) & 3) + 16 * (lane & 1);
+  return 128 * ((lane >> 2) & 1) + 16 * ((lane >> 1) & 1) + 64 * (lane & 1);
+}
+
+// The lane's activations: runs A and B (16 values each) and their sums.
+struct KqX {
+  float4 a[4], b[4];
+  float sa, sb;
+};
+
+__device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const KqX& x, int lane) {
+  const int j = (lane >> 1) & 3;
   const float d = half_bits_to_f32(L.hdr.x), dmin = half_bits_to_f32(L.hdr.x >> 16);
   const uint32_t sb[3] = {L.hdr.y, L.hdr.z, L.hdr.w};
   float scA, mA, scB, mB;
@@ -147,20 +165,18 @@ __device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const float* xsb, 
     lo[c] = q[c] & 0x0F0F0F0Fu;
     hi[c] = (q[c] >> 4) & 0x0F0F0F0Fu;
   }
-  const int eA = 64 * j + 16 * h;
-  const float sA = u8_dot16(lo, reinterpret_cast<const float4*>(xsb + eA));
-  const float sB = u8_dot16(hi, reinterpret_cast<const float4*>(xsb + eA + 32));
-  const float xA = x16sb[eA >> 4], xB = x16sb[(eA >> 4) + 2];
+  const float sA = u8_dot16(lo, x.a);
+  const float sB = u8_dot16(hi, x.b);
   float acc = (d * scA) * sA;
-  acc = fmaf(-(dmin * mA), xA, acc);
+  acc = fmaf(-(dmin * mA), x.sa, acc);
   acc = fmaf(d * scB, sB, acc);
-  return fmaf(-(dmin * mB), xB, acc);
+  return fmaf(-(dmin * mB), x.sb, acc);
 }
 
-__device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const float* xsb, const float* x16sb, int lane) {
-  const int n = (lane >> 2) & 1, is = (lane >> 1) & 1, qp = lane & 1;
-  const uint32_t scw[4] = {L.sc.x, L.sc.y, L.sc.z, L.sc.w};
-  const int ia = 8 * n + is + 4 * qp, ib = ia + 2;  // sc[8n + is + 2Q]
+__device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const KqX& x, int lane) {
+  const int is = (lane >> 1) & 1, qp = lane & 1;
+  const uint32_t scw[2] = {L.sc0, L.sc1};
+  const int ia = is + 4 * qp, ib = ia + 2;  // sc[8n + is + 2Q] within the half's 8 scales
   const float scA = (float)(int8_t)byte_of(scw, ia), scB = (float)(int8_t)byte_of(scw, ib);
   const float d = half_bits_to_f32(L.d);
   const uint32_t a[4] = {L.la.x, L.la.y, L.la.z, L.la.w}, b[4] = {L.lb.x, L.lb.y, L.lb.z, L.lb.w},
@@ -173,12 +189,31 @@ __device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const float* xsb, 
     qA[c] = ((a[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hA) & 0x03030303u) << 4);
     qB[c] = ((b[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hB) & 0x03030303u) << 4);
   }
-  const int eA = 128 * n + 16 * is + 64 * qp;  // quarter 2qp
-  const float sA = u8_dot16(qA, reinterpret_cast<const float4*>(xsb + eA));
-  const float sB = u8_dot16(qB, reinterpret_cast<const float4*>(xsb + eA + 32));
-  const float xA = x16sb[eA >> 4], xB = x16sb[(eA >> 4) + 2];
-  float acc = (d * scA) * fmaf(-32.0f, xA, sA);
-  return fmaf(d * scB, fmaf(-32.0f, xB, sB), acc);
+  const float sA = u8_dot16(qA, x.a);
+  const float sB = u8_dot16(qB, x.b);
+  float acc = (d * scA) * fmaf(-32.0f, x.sa, sA);
+  return fmaf(d * scB, fmaf(-32.0f, x.sb, sB), acc);
+}
+
+// Activations of the lane's runs in superblock sb (from LDS or global).
+template <uint32_t QT>
+__device__ __forceinline__ KqX kq_x(const float* x, int sb, int lane) {
+  KqX r;
+  const float4* p = reinterpret_cast<const float4*>(x + sb * 256 + kq_lane_elem<QT>(lane));
+  float sa = 0.0f, sbs = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    r.a[c] = p[c];
+    r.b[c] = p[8 + c];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    sa += (r.a[c].x + r.a[c].y) + (r.a[c].z + r.a[c].w);
+    sbs += (r.b[c].x + r.b[c].y) + (r.b[c].z + r.b[c].w);
+  }
+  r.sa = sa;
+  r.sb = sbs;
+  return r;
 }
 
 // A wave walks units (row, step of 8 superblocks) of its rows; unit u + 1's
@@ -220,7 +255,7 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
     if (u + 1 < nunits) kq_load(nxt, unit_blk(u + 1), lane);
     const int st = (int)(u % steps);
     const int sb = st * 8 + sl;
-    if (sb < nsb) acc += kq_dot(cur, xs + sb * 256, x16 + sb * 16, lane);
+    if (sb < nsb) acc += kq_dot(cur, kq_x<QT>(xs, sb, lane), lane);
     if (st == steps - 1) {
       const float v = wave_sum(acc);
       acc = 0.0f;
@@ -241,6 +276,88 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
     atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
 }
 
+// Strip form (in_dim a multiple of 2048): the K axis is cut into strips of
+// 8 superblocks; a wave owns one strip and keeps its lanes' activations in
+// registers while it walks rows, so no activation is re-read per row.  A
+// workgroup has one wave per strip (times WPS when there are fewer than 4
+// strips) and walks batches of rows; two batches of loads are in flight
+// (clamped unconditional loads), a row's partials are summed over the wave
+// (DPP) and then over strips through LDS in a fixed order.
+template <uint32_t QT, int EPI, int RB>
+__global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
+  constexpr int BB = KqGeom<QT>::BB;
+  __shared__ float part[2][32][RB];  // [buffer][wave][row of the batch]
+  const int NW = blockDim.x >> 6;
+  const int WPS = NW / S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = wave % S, sub = wave / S;
+  const int nsb = (int)(a.k / 256);
+  const int sb = strip * 8 + (lane >> 3);  // this lane's superblock
+  const size_t rowbytes = (size_t)nsb * BB;
+  const int nrows = (int)(a.row_hi - a.row_lo);
+  const int per_batch = WPS * RB;
+  const int nbatch = (nrows + per_batch - 1) / per_batch;
+  auto load_batch = [&](KqLane<QT> (&L)[RB], int batch) {
+    const int base = batch * per_batch + sub * RB;
+#pragma unroll
+    for (int j = 0; j < RB; j++) {
+      const size_t row = a.row_lo + (size_t)min(base + j, nrows - 1);
+      kq_load(L[j], a.w + row * rowbytes + (size_t)sb * BB, lane);
+    }
+  };
+  KqLane<QT> LA[RB], LB[RB];
+  const int b0 = blockIdx.x, bstep = gridDim.x;
+  const KqX x = kq_x<QT>(a.x, sb, lane);
+  if (b0 < nbatch) load_batch(LA, b0);
+  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
+  uint64_t key = 0;
+  auto process = [&](const KqLane<QT> (&L)[RB], int batch, int buf) {
+    const int base = batch * per_batch + sub * RB;
+#pragma unroll
+    for (int j = 0; j < RB; j++) {
+      const float v = wave_sum(kq_dot(L[j], x, lane));
+      if (lane == 0) part[buf][wave][j] = v;
+    }
+    __syncthreads();
+    const int tt = threadIdx.x;
+    if (tt < per_batch) {
+      const int su = tt / RB, j = tt % RB;
+      const int ri = batch * per_batch + su * RB + j;
+      if (ri < nrows) {
+        float v = 0.0f;
+        for (int st = 0; st < S; st++) v += part[buf][su * S + st][j];
+        const size_t row = a.row_lo + ri;
+        if (EPI == EPI_RESID)
+          a.y[row] = a.resid[row] + v;
+        else if (a.y)
+          a.y[row] = v;
+        if (EPI == EPI_ARGMAX && !(v != v)) {
+          const uint64_t kk = argmax_key(v, (uint32_t)row);
+          key = kk > key ? kk : key;
+        }
+      }
+    }
+    (void)base;
+  };
+  for (int batch = b0; batch < nbatch; batch += 2 * bstep) {
+    process(LA, batch, 0);
+    if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
+    if (batch + bstep < nbatch) {
+      process(LB, batch + bstep, 1);
+      if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
+  }
+}
+
 size_t kq_lds_bytes(int k) { return (size_t)k * sizeof(float) + (size_t)(k / 16) * sizeof(float); }
 
 static int kq_cu_count() {
@@ -255,8 +372,29 @@ static int kq_cu_count() {
   return n;
 }
 
+#ifndef ZG_KQ_STRIP_WAVES_PER_CU
+#define ZG_KQ_STRIP_WAVES_PER_CU 16
+#endif
+
+template <uint32_t QT, int EPI>
+static hipError_t launch_kq_strip(const GenericArgs& a, hipStream_t st) {
+  constexpr int RB = QT == Q4K ? 4 : 2;  // rows per wave per batch (register budget)
+  const int S = (int)(a.k / 2048);
+  const int nw = S >= 4 ? S : (S == 3 ? 6 : 4);
+  const int wps = nw / S;
+  const size_t rows = a.row_hi - a.row_lo;
+  const size_t nbatch = (rows + (size_t)wps * RB - 1) / ((size_t)wps * RB);
+  const size_t per_cu = nw >= ZG_KQ_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_KQ_STRIP_WAVES_PER_CU / nw);
+  const size_t cap = (size_t)kq_cu_count() * per_cu;
+  const size_t grid = nbatch < cap ? nbatch : cap;
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((kq_strip_kernel<QT, EPI, RB>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
+  return hipGetLastError();
+}
+
 template <uint32_t QT, int EPI>
 static hipError_t launch_kq(const GenericArgs& a, hipStream_t st) {
+  if (a.k % 2048 == 0 && a.k / 2048 <= 16) return launch_kq_strip<QT, EPI>(a, st);
   const size_t rows = a.row_hi - a.row_lo;
   const size_t shm = kq_lds_bytes((int)a.k);
   // LDS decides how many workgroups fit a CU (160 KB per CU)
