@@ -145,16 +145,116 @@ struct GemmArgs {
 constexpr int kBM = 64, kBN = 64, kBK = 4;  // kBK blocks of 32 per stage
 constexpr int kRow = kBK * 32 + 16;         // LDS row stride in bytes (padded, 16-B aligned)
 
+// One stage's global operands held in registers between the load and the
+// LDS store (so that the next stage's loads fly while the current stage is
+// multiplied): two 16-byte activation chunks and one activation scale, one
+// weight block row (raw quants + scale) per thread.
+template <uint32_t WT>
+struct GemmStage {
+  u32x4 a[2];
+  uint32_t ad;
+  uint32_t q[WT == Q4_0 ? 4 : 8];
+  uint32_t wd;
+};
+
+template <uint32_t WT, int IL>
+__device__ __forceinline__ void gemm_stage_load(GemmStage<WT>& S, const GemmArgs& a, int m0, int n0, int b0, int tid) {
+  const int nb = a.k / 32;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
+    const int gm = m0 + row, kb = b0 + ch / 2;
+    S.a[i] = u32x4{0, 0, 0, 0};
+    if (gm < a.m && kb < nb) S.a[i] = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
+  }
+  {
+    const int row = tid / kBK, kk = tid % kBK;
+    const int gm = m0 + row, kb = b0 + kk;
+    S.ad = (gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
+  }
+  {
+    const int row = tid / kBK, kk = tid % kBK;
+    const int gn = n0 + row, kb = b0 + kk;
+    constexpr int QW = WT == Q4_0 ? 4 : 8;
+#pragma unroll
+    for (int i = 0; i < QW; i++) S.q[i] = 0;
+    S.wd = 0;
+    if (gn < a.n && kb < nb) {
+      const uint8_t* dp;
+      const uint8_t* qp;
+      if (IL == 4) {
+        const size_t gb = (WT == Q4_0) ? 72 : 136;
+        const uint8_t* g = a.w + (size_t)(gn >> 2) * nb * gb + (size_t)kb * gb;
+        dp = g + 2 * (gn & 3);
+        qp = g + 8 + (gn & 3) * ((WT == Q4_0) ? 16 : 32);
+#pragma unroll
+        for (int i = 0; i < QW / 2; i++) {
+          const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * i);
+          S.q[2 * i] = v.x;
+          S.q[2 * i + 1] = v.y;
+        }
+      } else {
+        const size_t bb = (WT == Q4_0) ? 18 : 34;
+        dp = a.w + ((size_t)gn * nb + kb) * bb;
+        qp = dp + 2;
+#pragma unroll
+        for (int i = 0; i < QW; i++)
+          S.q[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
+                   ((uint32_t)qp[4 * i + 3] << 24);
+      }
+      S.wd = (uint32_t)dp[0] | ((uint32_t)dp[1] << 8);
+    }
+  }
+}
+
+template <uint32_t WT>
+__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT>& S, int8_t* As, int8_t* Bs, float* Ad, float* Bd,
+                                                 int tid) {
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
+    *reinterpret_cast<u32x4*>(As + row * kRow + ch * 16) = S.a[i];
+  }
+  const int row = tid / kBK, kk = tid % kBK;
+  Ad[kk * kBM + row] = half_bits_to_f32(S.ad);
+  uint32_t q[8];
+  if (WT == Q4_0) {
+    // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
+    // bytes is (n + 0x78) ^ 0x80
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = S.q[i] & 0x0F0F0F0Fu;         // elements 4i..4i+3
+      const uint32_t hi = (S.q[i] >> 4) & 0x0F0F0F0Fu;  // elements 16+4i..
+      q[i] = ((lo + 0x78787878u) ^ 0x80808080u);
+      q[4 + i] = ((hi + 0x78787878u) ^ 0x80808080u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = S.q[i];
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * kRow + kk * 32);
+  dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+  dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+  Bd[kk * kBN + row] = half_bits_to_f32(S.wd);
+}
+
+// Workgroup tile 64 (m) x 64 (n), 4 waves of 32 x 32 (2 x 2 MFMA tiles).
+// kBK blocks (128 K) per stage, double-buffered in LDS; the next stage's
+// global loads are issued before the current stage is multiplied.  Per
+// 32-K block: v_mfma_i32_16x16x32_i8 gives the block's integer dots, and
+// every output adds dX*dW*isum with one fma, blocks in ascending order.
 template <uint32_t WT, int IL>
 __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t As[kBM * kRow];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[kBN * kRow];
-  __shared__ float Ad[kBM][kBK];
-  __shared__ float Bd[kBN][kBK];
+  __shared__ __attribute__((aligned(16))) int8_t As[2][kBM * kRow];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][kBN * kRow];
+  __shared__ __attribute__((aligned(16))) float Ad[2][kBK * kBM];  // [kk][row]
+  __shared__ __attribute__((aligned(16))) float Bd[2][kBK * kBN];  // [kk][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
   const int nb = a.k / 32;
+  const int nst = (nb + kBK - 1) / kBK;
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int r16 = lane & 15, kq = (lane >> 4) * 8, rq = (lane >> 4) * 4;
   float acc[2][2][4];
 #pragma unroll
   for (int i = 0; i < 2; i++)
@@ -163,106 +263,46 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
-  for (int b0 = 0; b0 < nb; b0 += kBK) {
-    __syncthreads();
-    // A tile: 64 rows x kBK blocks of 32 int8 (row-major, 16-B chunks)
-    for (int c = tid; c < kBM * kBK * 2; c += 256) {
-      const int row = c / (kBK * 2), ch = c % (kBK * 2);
-      const int gm = m0 + row, kb = b0 + ch / 2;
-      u32x4 v = {0, 0, 0, 0};
-      if (gm < a.m && kb < nb) v = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
-      *reinterpret_cast<u32x4*>(As + row * kRow + ch * 16) = v;
-    }
-    {
-      const int row = tid / kBK, kk = tid % kBK;
-      const int gm = m0 + row, kb = b0 + kk;
-      Ad[row][kk] = (gm < a.m && kb < nb) ? half_bits_to_f32(a.xd[(size_t)gm * nb + kb]) : 0.0f;
-    }
-    // B tile: 64 weight rows x kBK blocks, unpacked to signed int8
-    {
-      const int row = tid / kBK, kk = tid % kBK;
-      const int gn = n0 + row, kb = b0 + kk;
-      uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      float dw = 0.0f;
-      if (gn < a.n && kb < nb) {
-        const uint8_t* dp;
-        const uint8_t* qp;
-        if (IL == 4) {
-          const size_t gb = (WT == Q4_0) ? 72 : 136;
-          const uint8_t* g = a.w + (size_t)(gn >> 2) * nb * gb + (size_t)kb * gb;
-          dp = g + 2 * (gn & 3);
-          qp = g + 8 + (gn & 3) * ((WT == Q4_0) ? 16 : 32);
-        } else {
-          const size_t bb = (WT == Q4_0) ? 18 : 34;
-          dp = a.w + ((size_t)gn * nb + kb) * bb;
-          qp = dp + 2;
-        }
-        dw = half_bits_to_f32((uint32_t)dp[0] | ((uint32_t)dp[1] << 8));
-        if (WT == Q4_0) {
-          uint32_t raw[4];
-          if (IL == 4) {
-            const uint2 lo = *reinterpret_cast<const uint2*>(qp);
-            const uint2 hi = *reinterpret_cast<const uint2*>(qp + 8);
-            raw[0] = lo.x; raw[1] = lo.y; raw[2] = hi.x; raw[3] = hi.y;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-              raw[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
-                       ((uint32_t)qp[4 * i + 3] << 24);
-          }
-          // (nibble - 8) as a signed byte == nibble XOR 8 sign-extended:
-          // (n ^ 8) - 8 in 4 bits; compute bytewise via (n | 0xF0) when n < 8
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const uint32_t lo = raw[i] & 0x0F0F0F0Fu;          // elements 4i..4i+3
-            const uint32_t hi = (raw[i] >> 4) & 0x0F0F0F0Fu;   // elements 16+4i..
-            // bytewise n - 8 without borrow across bytes: (n + 0x78) ^ 0x80
-            q[i] = ((lo + 0x78787878u) ^ 0x80808080u);
-            q[4 + i] = ((hi + 0x78787878u) ^ 0x80808080u);
-          }
-        } else {
-          if (IL == 4) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * i);
-              q[2 * i] = v.x;
-              q[2 * i + 1] = v.y;
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-              q[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
-                     ((uint32_t)qp[4 * i + 3] << 24);
-          }
-        }
-      }
-      u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * kRow + kk * 32);
-      dst[0] = u32x4{q[0], q[1], q[2], q[3]};
-      dst[1] = u32x4{q[4], q[5], q[6], q[7]};
-      Bd[row][kk] = dw;
-    }
-    __syncthreads();
-    const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  GemmStage<WT> S;
+  gemm_stage_load<WT, IL>(S, a, m0, n0, 0, tid);
+  gemm_stage_store<WT>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
+  __syncthreads();
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gemm_stage_load<WT, IL>(S, a, m0, n0, (st + 1) * kBK, tid);
+    const int8_t* A = As[buf];
+    const int8_t* B = Bs[buf];
 #pragma unroll
     for (int kk = 0; kk < kBK; kk++) {
       long av[2], bv[2];
+      float4 da[2];
+      float db[2];
 #pragma unroll
-      for (int i = 0; i < 2; i++) av[i] = *reinterpret_cast<const long*>(As + (wm + 16 * i + r16) * kRow + kk * 32 + kq);
+      for (int i = 0; i < 2; i++) {
+        av[i] = *reinterpret_cast<const long*>(A + (wm + 16 * i + r16) * kRow + kk * 32 + kq);
+        da[i] = *reinterpret_cast<const float4*>(&Ad[buf][kk * kBM + wm + 16 * i + rq]);
+      }
 #pragma unroll
-      for (int j = 0; j < 2; j++) bv[j] = *reinterpret_cast<const long*>(Bs + (wn + 16 * j + r16) * kRow + kk * 32 + kq);
+      for (int j = 0; j < 2; j++) {
+        bv[j] = *reinterpret_cast<const long*>(B + (wn + 16 * j + r16) * kRow + kk * 32 + kq);
+        db[j] = Bd[buf][kk * kBN + wn + 16 * j + r16];
+      }
+      v4i c[2][2];
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-          const float dwv = Bd[wn + 16 * j + r16][kk];
+        for (int j = 0; j < 2; j++) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float s = __fmul_rn(Ad[wm + 16 * i + (lane >> 4) * 4 + r][kk], dwv);
-            acc[i][j][r] = fmaf(s, (float)c[r], acc[i][j][r]);
-          }
-        }
+      for (int i = 0; i < 2; i++) {
+        const float dai[4] = {da[i].x, da[i].y, da[i].z, da[i].w};
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(__fmul_rn(dai[r], db[j]), (float)c[i][j][r], acc[i][j][r]);
+      }
     }
+    if (st + 1 < nst) gemm_stage_store<WT>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
+    __syncthreads();
   }
   // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16
 #pragma unroll
@@ -271,8 +311,8 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int gm = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
-        const int gn = n0 + wn + 16 * j + (lane & 15);
+        const int gm = m0 + wm + 16 * i + rq + r;
+        const int gn = n0 + wn + 16 * j + r16;
         if (gm < a.m && gn < a.n) a.y[(size_t)gm * a.n + gn] = acc[i][j][r];
       }
 }
