@@ -130,19 +130,19 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* qs, const float4* 
   return fmaf(s_hi, 0.0625f, s_lo);
 }
 
-// Sum over one Q8_0 block of one row: sum_j q_j * x_j, q signed bytes
-// (dequant.rs:247-275).
-__device__ __forceinline__ float q8_block_dot(const uint32_t* qs, const float4* xb) {
+// Q8_0 block sum with the int8 quants read as unsigned bytes (q ^ 0x80 =
+// q + 128); the caller subtracts 128 * sum(x).
+__device__ __forceinline__ float q8u_block_dot(const uint32_t* qs, const float4* xb) {
   float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
   for (int c = 0; c < 8; c++) {
-    const uint32_t v = qs[c];
+    const uint32_t v = qs[c] ^ 0x80808080u;
     const float4 xv = xb[c];
     float& s = (c & 1) ? s1 : s0;
-    s = fmaf(xv.x, (float)(int32_t)((int8_t)(v & 0xFFu)), s);
-    s = fmaf(xv.y, (float)(int32_t)((int8_t)((v >> 8) & 0xFFu)), s);
-    s = fmaf(xv.z, (float)(int32_t)((int8_t)((v >> 16) & 0xFFu)), s);
-    s = fmaf(xv.w, (float)(int32_t)((int8_t)(v >> 24)), s);
+    s = fmaf(xv.x, (float)(v & 0xFFu), s);
+    s = fmaf(xv.y, (float)((v >> 8) & 0xFFu), s);
+    s = fmaf(xv.z, (float)((v >> 16) & 0xFFu), s);
+    s = fmaf(xv.w, (float)(v >> 24), s);
   }
   return s0 + s1;
 }
@@ -280,16 +280,19 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
       d[1] = half_bits_to_f32(dw[0] >> 16);
       d[2] = half_bits_to_f32(dw[1]);
       d[3] = half_bits_to_f32(dw[1] >> 16);
-      if (QT == Q4_0) {
-        float t = 0.0f;  // sum of this x-block, for the -8 offset of every row
+      // sum of this x-block: the -8 (Q4_0) or -128 (Q8_0 read as unsigned
+      // bytes) offset of every row
+      float t = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+      for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+      if (QT == Q4_0) {
         const float m8 = -8.0f * t;
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) acc[rr] = fmaf(d[rr], q4_block_dot(dw + 2 + QDW * rr, xb) + m8, acc[rr]);
       } else {
+        const float m128 = -128.0f * t;
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) acc[rr] = fmaf(d[rr], q8_block_dot(dw + 2 + QDW * rr, xb), acc[rr]);
+        for (int rr = 0; rr < 4; rr++) acc[rr] = fmaf(d[rr], q8u_block_dot(dw + 2 + QDW * rr, xb) + m128, acc[rr]);
       }
     }
     wave_lds_sync();  // the slot is rewritten next iteration
@@ -378,23 +381,6 @@ __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int
   L.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(blk + 2 * r));
 }
 
-// Q8_0 block sum with the int8 quants read as unsigned bytes (q ^ 0x80 =
-// q + 128); the caller subtracts 128 * sum(x).
-__device__ __forceinline__ float q8u_block_dot(const uint32_t* qs, const float4* xb) {
-  float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 8; c++) {
-    const uint32_t v = qs[c] ^ 0x80808080u;
-    const float4 xv = xb[c];
-    float& s = (c & 1) ? s1 : s0;
-    s = fmaf(xv.x, (float)(v & 0xFFu), s);
-    s = fmaf(xv.y, (float)((v >> 8) & 0xFFu), s);
-    s = fmaf(xv.z, (float)((v >> 16) & 0xFFu), s);
-    s = fmaf(xv.w, (float)(v >> 24), s);
-  }
-  return s0 + s1;
-}
-
 template <uint32_t QT>
 __device__ __forceinline__ float strip_dot(const LaneW<QT>& L, const float4* xb, float mterm) {
   const float d = half_bits_to_f32(L.d);
@@ -456,11 +442,18 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
   // activation block of this lane, then the first batch's weights: all
   // loads are issued before any of them is waited for, x first because it
   // is consumed first
-  float4 xb[8];
+  float4 xb[8], gw[8];
   {
     const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
 #pragma unroll
     for (int c = 0; c < 8; c++) xb[c] = x4[c];
+    if (PRO == PRO_RMSNORM) {
+      // the gain is loaded with x, ahead of the barrier that waits for the
+      // sum of squares
+      const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+#pragma unroll
+      for (int c = 0; c < 8; c++) gw[c] = g4[c];
+    }
   }
   // two batches in flight: this workgroup's first and second
   LaneW<QT> LA[GBATCH][PARTS], LB[GBATCH][PARTS];
@@ -484,10 +477,9 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
     float tot = 0.0f;
     for (int i = 0; i < S; i++) tot += red[i];
     const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
-    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-      const float4 g = g4[c];
+      const float4 g = gw[c];
       xb[c].x = xb[c].x * rinv * g.x;
       xb[c].y = xb[c].y * rinv * g.y;
       xb[c].z = xb[c].z * rinv * g.z;
