@@ -35,7 +35,7 @@ def test_tiny_model_stepwise(ctx, zo, tiny):
     om = zo.OracleModel(tiny)
     tok = 7
     worst_h = worst_l = 0.0
-    for pos in range(70):  # crosses the 32-token attention chunks twice
+    for pos in range(70):  # crosses the 32-row attention splits twice
         nxt, mx, hid, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
         h_ref = om.forward(tok, pos)
         rc, t_ref, m_ref, lg_ref = om.lm_head()
@@ -52,7 +52,9 @@ def test_tiny_model_stepwise(ctx, zo, tiny):
 
 @pytest.mark.parametrize("n_q,n_kv,hd", [(8, 1, 64), (4, 4, 64), (8, 2, 128)])
 def test_attention_head_groupings(ctx, zo, n_q, n_kv, hd):
-    """Query heads per KV head G = 8, 1 and 4 (the Qwen shape has G = 2)."""
+    """Query heads per KV head G = 8, 1 and 4 (the Qwen shape has G = 2).
+    Three 32-row splits; the 512- and 1024-wide attention outputs are merged
+    by the O GEMV's prologue, the 256-wide one by the separate merge kernel."""
     cfg = synth.ModelConfig(n_layers=1, hidden=256, ffn=512, n_q_heads=n_q, n_kv_heads=n_kv, head_dim=hd,
                             vocab_padded=512, vocab_real=500, max_ctx=72)
     model = synth.random_model(cfg, seed=n_q + 3 * n_kv + hd)
@@ -74,8 +76,8 @@ def test_attention_head_groupings(ctx, zo, n_q, n_kv, hd):
 
 
 def test_attention_split_context(ctx, zo):
-    """max_ctx above one workgroup's split (2048 positions): positions past
-    2048 are merged across two workgroups per KV head."""
+    """Long context: four 544-row splits per query head, each visited in
+    five 128-row rounds (online softmax across rounds)."""
     cfg = synth.ModelConfig(n_layers=1, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
                             vocab_padded=512, vocab_real=500, max_ctx=2100)
     model = synth.random_model(cfg, seed=11)
@@ -84,6 +86,24 @@ def test_attention_split_context(ctx, zo):
     prompt = synth.prompt(12, 8, cfg.vocab_real)
     toks, _, _ = gm.generate(prompt, 2090)
     assert np.array_equal(toks, om.generate(prompt, 2090))
+    om.close()
+    gm.close()
+    ctx.clear()
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,max_ctx,n_gen", [(8, 2, 128, 30, 26), (8, 2, 128, 520, 500), (8, 4, 64, 200, 190)])
+def test_attention_split_geometries(ctx, zo, n_q, n_kv, hd, max_ctx, n_gen):
+    """One split (max_ctx <= 32, the output written directly); four 160-row
+    splits of two rounds each, merged in the O GEMV; four 64-row splits at
+    head_dim 64, merged in the O GEMV."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=n_q, n_kv_heads=n_kv, head_dim=hd,
+                            vocab_padded=512, vocab_real=500, max_ctx=max_ctx)
+    model = synth.random_model(cfg, seed=max_ctx + hd)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    prompt = synth.prompt(max_ctx, 4, cfg.vocab_real)
+    toks, _, _ = gm.generate(prompt, n_gen)
+    assert np.array_equal(toks, om.generate(prompt, n_gen))
     om.close()
     gm.close()
     ctx.clear()

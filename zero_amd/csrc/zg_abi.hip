@@ -326,6 +326,29 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
   return ZG_OK;
 }
 
+// O projection of the decode step: y += W * merge(attention splits), the
+// split merge in the strip kernel's prologue.
+zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd,
+                         const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st) {
+  if (!attn_merge_gemv_ok(qt, il, k) || !pair_path_ok(qt, il, k, n, w, part_o))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0X4 and a strip-sized in_dim");
+  GemvArgs a{};
+  a.nseg = 1;
+  a.k = (int)k;
+  a.total_groups = (uint32_t)(n / 4);
+  a.x = part_o;
+  a.attn_ml = part_ml;
+  a.attn_nsplit = nsplit;
+  a.attn_hd = hd;
+  a.seg[0].w = w;
+  a.seg[0].y = y;
+  a.seg[0].resid = y;
+  a.seg[0].g_begin = 0;
+  a.seg[0].row_lo = 0;
+  a.seg[0].row_hi = (uint32_t)n;
+  return hip_check(ctx, launch_gemv_x4(a, qt, PRO_ATTN, EPI_RESID, st), "attention-merge gemv launch");
+}
+
 // ---------------------------------------------------------------------------
 // Host-pointer operator API
 // ---------------------------------------------------------------------------

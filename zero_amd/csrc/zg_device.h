@@ -86,6 +86,68 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Orders this wave's LDS writes before its later LDS reads (lanes of one
+// wave exchanging data through LDS; no workgroup barrier needed).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Split-context attention (flash-decoding).  Each split s of a query head's
+// context leaves its unnormalised output o_s (sum_t e_t v_t with
+// e_t = exp(score_t - m_s)), its running max m_s and its exp-sum l_s; a
+// split past the context leaves (o, m, l) = (0, -inf, 0).  The merged output
+// is sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s)
+// (attention.rs:48-84 softmax, regrouped by split).  One thread merges 8
+// consecutive dims of one head.
+constexpr int kAttnSplits = 4;  // max splits per query head
+
+struct AttnSplitIn {
+  float4 o[kAttnSplits][2];
+  float2 ml[kAttnSplits];
+};
+
+// part_o: [nsplit][k] split outputs; part_ml: [nsplit][k / hd] (m, l).
+__device__ __forceinline__ void attn_split_load(AttnSplitIn& in, const float* part_o, const float* part_ml, int k,
+                                                int hd, int nsplit, int e0) {
+  const int nh = k / hd, h = e0 / hd;
+#pragma unroll
+  for (int s = 0; s < kAttnSplits; s++) {
+    if (s < nsplit) {
+      const float4* p = reinterpret_cast<const float4*>(part_o + (size_t)s * k + e0);
+      in.o[s][0] = p[0];
+      in.o[s][1] = p[1];
+      in.ml[s] = reinterpret_cast<const float2*>(part_ml)[s * nh + h];
+    }
+  }
+}
+
+__device__ __forceinline__ float4 fma4(float w, float4 a, float4 acc) {
+  return make_float4(fmaf(w, a.x, acc.x), fmaf(w, a.y, acc.y), fmaf(w, a.z, acc.z), fmaf(w, a.w, acc.w));
+}
+
+__device__ __forceinline__ void attn_split_merge(const AttnSplitIn& in, int nsplit, float4& x0, float4& x1) {
+  float m = in.ml[0].x;
+#pragma unroll
+  for (int s = 1; s < kAttnSplits; s++)
+    if (s < nsplit) m = fmaxf(m, in.ml[s].x);
+  float l = 0.0f;
+  float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), a1 = a0;
+#pragma unroll
+  for (int s = 0; s < kAttnSplits; s++) {
+    if (s < nsplit) {
+      const float w = expf(in.ml[s].x - m);
+      l = fmaf(w, in.ml[s].y, l);
+      a0 = fma4(w, in.o[s][0], a0);
+      a1 = fma4(w, in.o[s][1], a1);
+    }
+  }
+  const float inv = 1.0f / l;
+  x0 = make_float4(a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv);
+  x1 = make_float4(a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv);
+}
+
 // Order-preserving encoding of an argmax candidate into one u64 so that a
 // single atomicMax implements lm_argmax_propose
 // (kernel/src/inference_avx512.rs:1027-1044): larger value wins, equal

@@ -182,14 +182,6 @@ __device__ __forceinline__ void seg_park(uint8_t* dst, int nbytes, int lane, con
   }
 }
 
-// LDS order point for one wave: its own LDS writes become visible to its
-// other lanes, and no LDS access moves across it.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Work decomposition shared by the GEMV and its dequant test hook.
 //   item  = logical group (SwiGLU: a gate group and its up group)
 //   part  = which of the item's groups (0 unless SwiGLU)
@@ -443,7 +435,11 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
   // loads are issued before any of them is waited for, x first because it
   // is consumed first
   float4 xb[8], gw[8];
-  {
+  AttnSplitIn am;
+  const int e0 = min(8 * (int)threadIdx.x, a.k - 8);  // PRO_ATTN: this thread's 8 merged dims
+  if (PRO == PRO_ATTN) {
+    attn_split_load(am, a.x, a.attn_ml, a.k, a.attn_hd, a.attn_nsplit, e0);
+  } else {
     const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
 #pragma unroll
     for (int c = 0; c < 8; c++) xb[c] = x4[c];
@@ -462,6 +458,22 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
 
   // prologue and block sum
+  if (PRO == PRO_ATTN) {
+    // the workgroup merges the attention splits into LDS (thread t: dims
+    // 8t..8t+7) while its weight loads are in flight; lanes then read their
+    // x-block from there
+    float* xs = part + (size_t)2 * NW * GBATCH * PARTS * 16;
+    float4 m0, m1;
+    attn_split_merge(am, a.attn_nsplit, m0, m1);
+    if (8 * (int)threadIdx.x < a.k) {
+      reinterpret_cast<float4*>(xs + e0)[0] = m0;
+      reinterpret_cast<float4*>(xs + e0)[1] = m1;
+    }
+    __syncthreads();
+    const float4* x4 = reinterpret_cast<const float4*>(xs + 32 * kb);
+#pragma unroll
+    for (int c = 0; c < 8; c++) xb[c] = x4[c];
+  }
   if (PRO == PRO_RMSNORM) {
     // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w, sum of squares over
     // the whole vector (each wave's strip blocks, 4 lanes per block: lane
@@ -805,7 +817,7 @@ static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items
   const size_t cap = (size_t)cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
-  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float);
+  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
   hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH>), dim3((unsigned)grid), dim3(nw * 64), shm, st, a, S);
   return hipGetLastError();
 }
@@ -831,10 +843,24 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
 // loads suit its 32-byte row blocks better than per-lane loads.
 template <uint32_t QT, int PRO, int EPI>
 static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
-  if constexpr (QT == Q4_0) {
-    if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+  if constexpr (PRO == PRO_ATTN) {
+    // only the Q4_0 strip kernel merges attention splits
+    if constexpr (QT == Q4_0) {
+      if (strip_path_ok(a.k) && a.attn_nsplit >= 1 && a.attn_nsplit <= kAttnSplits && a.attn_hd % 8 == 0 &&
+          a.k % a.attn_hd == 0)
+        return launch_strip<QT, PRO, EPI>(a, st);
+    }
+    return hipErrorInvalidValue;
+  } else {
+    if constexpr (QT == Q4_0) {
+      if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+    }
+    return launch_x4<QT, PRO, EPI>(a, st);
   }
-  return launch_x4<QT, PRO, EPI>(a, st);
+}
+
+bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k) {
+  return qt == Q4_0 && il == 4 && k <= 8192 && strip_path_ok((int)k);
 }
 
 template <uint32_t QT>
@@ -846,6 +872,7 @@ static hipError_t dispatch_x4_qt(const GemvArgs& a, int pro, int epi, hipStream_
   if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_x4_any<QT, PRO_RMSNORM, EPI_ARGMAX>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
+  if (pro == PRO_ATTN && epi == EPI_RESID) return launch_x4_any<QT, PRO_ATTN, EPI_RESID>(a, st);
   return hipErrorInvalidValue;
 }
 

@@ -67,6 +67,8 @@ zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, si
                      const float* norm_w, float eps, hipStream_t st);
 zg_status run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                     const float* norm_w, float eps, int epi, hipStream_t st);
+zg_status run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd, const uint8_t* w,
+                     float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st);
 zg_status stage_in(zg_ctx* ctx, const void* src, size_t bytes, DevBuf& dst);
 zg_status lm_head_status(zg_ctx* ctx, uint64_t packed, size_t vocab_real, uint32_t* token, float* max_val);
 

@@ -7,7 +7,9 @@
 
 namespace zg {
 
-enum Prologue : int { PRO_PLAIN = 0, PRO_RMSNORM = 1 };
+// PRO_ATTN: x holds split-context attention outputs and the kernel merges
+// them into the activation vector (strip path only).
+enum Prologue : int { PRO_PLAIN = 0, PRO_RMSNORM = 1, PRO_ATTN = 2 };
 enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3 };
 
 // One projection of a (possibly fused) X4 GEMV launch.  Groups
@@ -30,6 +32,10 @@ struct GemvArgs {
   const float* norm_w;    // PRO_RMSNORM gain
   float eps;
   uint64_t* best;         // EPI_ARGMAX packed candidate slot
+  // PRO_ATTN: x is [attn_nsplit][k] split outputs, attn_ml [attn_nsplit][k /
+  // attn_hd] their (max, exp-sum) pairs
+  const float* attn_ml;
+  int attn_nsplit, attn_hd;
 };
 
 struct GenericArgs {
@@ -64,6 +70,8 @@ constexpr size_t kMaxKqK = 15360;
 bool kq_path_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x);
 size_t kq_lds_bytes(int k);
 hipError_t launch_gemv_kq(const GenericArgs& a, hipStream_t st);
+// The strip GEMV can merge attention splits in its prologue (PRO_ATTN).
+bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t v, hipStream_t st);
 

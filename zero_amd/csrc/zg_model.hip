@@ -10,10 +10,10 @@
 //
 // Per layer:
 //   1. fused Q|K|V GEMV with rmsnorm(attn_norm) in the prologue
-//   2. attention: QK-norm + RoPE + KV-cache store + scores/softmax over one
-//      32-token chunk of the context per workgroup (split-T); the last
-//      workgroup of each KV head merges its chunks
-//   3. O GEMV with the residual add in the epilogue
+//   2. attention: QK-norm + RoPE + KV-cache store + scores/softmax, up to
+//      four workgroups per query head, each over its split of the context
+//   3. O GEMV with the split merge in the prologue and the residual add in
+//      the epilogue
 //   4. fused gate|up GEMV with rmsnorm(ffn_norm) and SiLU(gate)*up epilogue
 //   5. down GEMV with the residual add in the epilogue
 // LM head: GEMV with rmsnorm(output_norm) prologue and argmax epilogue, then
@@ -34,8 +34,6 @@ using namespace zg;
 namespace zg {
 
 constexpr int kMaxG = 8;          // max query heads per KV head
-constexpr int kAttnThreads = 1024;
-constexpr int kSplitMax = 2048;   // positions per attention workgroup (one split below this)
 
 // Device-resident decode state.
 struct DevState {
@@ -93,165 +91,189 @@ struct AttnArgs {
   const float* rope_cs;   // [HD]: cos then sin of pos * inv_freq
   float* kcache;       // this layer's K rows [max_ctx][nkv*HD]
   float* vcache;       // this layer's V rows
-  float* part;         // partials [nq][nsplit][HD+2] (nsplit > 1 only)
-  float* out;          // merged attention output [nq*HD]
-  uint32_t* counters;  // per query head: split workgroups finished (self-resetting)
+  float* out;          // one split: attention output [nq*HD]; else split outputs [nsplit][nq*HD]
+  float* part_ml;      // split (max, exp-sum) pairs [nsplit][nq] (nsplit > 1)
   DevState* st;
   int nkv, g, nsplit, split_len;
   float eps, scale;
 };
 
-// Decode attention for one query head (grid: query heads x splits; one
-// split unless the context exceeds kSplitMax positions), flash-decoding
-// inside the workgroup: each of the 16 waves owns 8 rows of every 128-row
-// chunk and keeps its own running max, exp-sum and output; the waves are
-// merged once at the end.  K and V rows are loaded one chunk ahead with
-// unconditional (clamped) loads so that the compiler's wait counts stay
-// exact; the current row, written by this step, comes from LDS.
-//   score   lane (row r, slice s) holds float4 columns s, s+8, ... of its K
-//           row; the partial dot is summed over the row's 8 lanes by DPP;
-//           softmax as attention.rs:48-84, rescaled online
-//   P.V     lane l holds dims VPL*l.. of all 8 rows of V; the row weights
-//           are read out with v_readlane, so every lane accumulates its own
-//           output dims and no cross-lane sum is needed at the end
-//   end     waves merged through LDS; o / sum written (attention.rs:76-81
-//           multiplies by 1/sum); several splits write (max, sum, o) and the
-//           last workgroup of the head merges them
-// The G query heads of a KV head run in G workgroups; the first stores the
-// new K/V row.
+constexpr int kAttnWaves = 4;
+
+// Decode attention, flash-decoding over splits: grid (query heads, splits),
+// one 4-wave workgroup per (head, split of split_len context rows).  Rows
+// are visited in rounds of 128 (4 passes of 32 rows, 8 rows per wave per
+// pass) whose K/V loads are all issued before any is used, so a split of up
+// to 128 rows costs one memory round trip; the splits spread a head's rows
+// over several CUs.
+//   prologue  every wave normalises and rotates the query head and the new
+//             key itself (QK-norm, ops.rs:29-52; NeoX RoPE, ops.rs:111-132)
+//             and parks them in its own LDS rows: no workgroup barrier
+//   score     lane (row r, slice s) holds float4 columns s, s+8, ... of its
+//             K row; the partial dot is summed over the row's 8 lanes by DPP;
+//             softmax as attention.rs:48-84, per wave, rescaled per round
+//   P.V       lane l holds dims VPL*l.. of the pass's 8 rows of V; the row
+//             weights are read out with v_readlane
+//   end       the 4 waves are merged through LDS.  A single split writes
+//             o / sum (attention.rs:76-81 multiplies by 1/sum); otherwise
+//             each split writes (o, max, sum) and the consumer merges them
+//             (attn_split_merge).  Splits past the context write the neutral
+//             (0, -inf, 0).
+// The current row (written by this step) comes from the wave's registers
+// and LDS, never from the cache: the first query head of each KV head
+// stores it, concurrently with the other workgroups' reads of older rows.
 template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_head_kernel(AttnArgs a) {
-  constexpr int F4 = HD / 4;             // float4 per head row
-  constexpr int LPR = 8;                 // lanes per row in the score layout
-  constexpr int CPL = F4 / LPR;          // K float4 columns per lane
-  constexpr int RPW = 64 / LPR;          // rows per wave per chunk
-  constexpr int VPL = HD / 64;           // V dims per lane
-  constexpr int NWV = kAttnThreads / 64;
-  constexpr int CHUNK = RPW * NWV;       // rows per chunk
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
+  constexpr int F4 = HD / 4;            // float4 per head row
+  constexpr int LPR = 8;                // lanes per row in the score layout
+  constexpr int CPL = F4 / LPR;         // K float4 columns per lane
+  constexpr int RPW = 64 / LPR;         // rows per wave per pass
+  constexpr int NWV = kAttnWaves;
+  constexpr int PASS = RPW * NWV;       // rows per pass
+  constexpr int NP = 4;                 // passes per round
+  constexpr int ROUND = NP * PASS;      // rows per round
+  constexpr int VPL = HD / 64;          // V dims per lane
   constexpr int HALF = HD / 2;
   typedef float vlane_t __attribute__((ext_vector_type(VPL)));
-  const int qh = blockIdx.x, sp = blockIdx.y;
-  const int G = a.g;
-  const int kvh = qh / G;
+  const int qh = blockIdx.x, sp = blockIdx.y, nq = gridDim.x;
+  const int kvh = qh / a.g;
   const int pos = (int)a.st->pos;
-  const int T = pos + 1;
-  const int CH = a.split_len;
-  const int c0 = sp * CH;
-  if (c0 >= T) return;  // uniform per workgroup
-  const int c1 = min(c0 + CH, T);
-  const int n_t = c1 - c0;
+  const int c0 = sp * a.split_len;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (c0 > pos) {
+    // split past the context: neutral partial (uniform per workgroup)
+    if (tid < HD) a.out[((size_t)sp * nq + qh) * HD + tid] = 0.0f;
+    if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(-INFINITY, 0.0f);
+    return;
+  }
+  const int n_t = min(a.split_len, pos + 1 - c0);
+  const bool has_pos = pos - c0 < a.split_len;  // this split holds the current row
   const size_t rowf4 = (size_t)a.nkv * F4;
-  const size_t rowv = (size_t)a.nkv * HD / VPL;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t rowv = (size_t)a.nkv * (HD / VPL);
   const int r = lane / LPR, sl = lane % LPR;
-  __shared__ __attribute__((aligned(16))) float qs[HD];
-  __shared__ __attribute__((aligned(16))) float knew[HD];
-  __shared__ __attribute__((aligned(16))) float vnew[HD];
+  __shared__ __attribute__((aligned(16))) float qk[NWV][2][HD];  // per wave: rotated q, new k
   __shared__ __attribute__((aligned(16))) float wo[NWV][HD];
   __shared__ float wm[NWV], wl[NWV];
-  const bool has_pos = pos < c1;  // this split holds the current token
   const float4* K4 = reinterpret_cast<const float4*>(a.kcache);
   const vlane_t* VL = reinterpret_cast<const vlane_t*>(a.vcache);
 
-  auto load_chunk = [&](float4 (&kr)[CPL], vlane_t (&vr)[RPW], int tb) {
-    const int tk = min(tb + wave * RPW + r, n_t - 1);
-    const size_t ko = (size_t)(c0 + tk) * rowf4 + kvh * F4;
+  float4 kr[NP][CPL];
+  vlane_t vr[NP][RPW];
+  // all passes of a round (rows past the split clamped to its last row)
+  auto load_round = [&](int rb) {
 #pragma unroll
-    for (int i = 0; i < CPL; i++) kr[i] = K4[ko + sl + LPR * i];
+    for (int p = 0; p < NP; p++) {
+      if (rb + p * PASS < n_t) {
+        const int tk = min(rb + p * PASS + wave * RPW + r, n_t - 1);
+        const size_t ko = (size_t)(c0 + tk) * rowf4 + kvh * F4;
 #pragma unroll
-    for (int j = 0; j < RPW; j++) {
-      const int tv = min(tb + wave * RPW + j, n_t - 1);
-      vr[j] = VL[(size_t)(c0 + tv) * rowv + kvh * (HD / VPL) + lane];
+        for (int i = 0; i < CPL; i++) kr[p][i] = K4[ko + sl + LPR * i];
+#pragma unroll
+        for (int j = 0; j < RPW; j++) {
+          const int tv = min(rb + p * PASS + wave * RPW + j, n_t - 1);
+          vr[p][j] = VL[(size_t)(c0 + tv) * rowv + kvh * (HD / VPL) + lane];
+        }
+      }
     }
   };
-  // prologue operands, then chunk 0's K/V loads
-  const int cc = tid % F4;
-  const float4 qv = reinterpret_cast<const float4*>(a.q)[qh * F4 + cc];
-  const float4 knv = reinterpret_cast<const float4*>(a.k)[kvh * F4 + cc];
-  const float4 vnv = reinterpret_cast<const float4*>(a.v)[kvh * F4 + cc];
+  // prologue operands, then round 0's K/V loads
   const int hl = lane % HALF;
+  const float qx0 = a.q[qh * HD + hl], qx1 = a.q[qh * HD + hl + HALF];
+  const float kx0 = a.k[kvh * HD + hl], kx1 = a.k[kvh * HD + hl + HALF];
   const float qw0 = a.q_norm[hl], qw1 = a.q_norm[hl + HALF];
   const float kw0 = a.k_norm[hl], kw1 = a.k_norm[hl + HALF];
   const float cs0 = a.rope_cs[hl], cs1 = a.rope_cs[hl + HALF];
-  float4 kr[CPL], kn[CPL];
-  vlane_t vr[RPW], vn[RPW];
-  load_chunk(kn, vn, 0);
-  // surplus threads repeat the same values (unconditional stores keep the
-  // operand loads ahead of the K/V loads)
-  reinterpret_cast<float4*>(qs)[cc] = qv;
-  reinterpret_cast<float4*>(knew)[cc] = knv;
-  reinterpret_cast<float4*>(vnew)[cc] = vnv;
-  __syncthreads();
-  // QK-norm (ops.rs:29-52) + NeoX RoPE (ops.rs:111-132): wave 0 the query
-  // head, wave 1 the new key
-  if (wave < 2) {
-    float* h = wave == 0 ? qs : knew;
-    const float w0 = wave == 0 ? qw0 : kw0, w1 = wave == 0 ? qw1 : kw1;
-    float x0 = 0.0f, x1 = 0.0f;
-    if (lane < HALF) {
-      x0 = h[lane];
-      x1 = h[lane + HALF];
-    }
-    const float ssq = wave_sum(x0 * x0 + x1 * x1);
+  const vlane_t vnew = reinterpret_cast<const vlane_t*>(a.v)[kvh * (HD / VPL) + lane];
+  load_round(0);
+
+  // QK-norm + RoPE of one head vector held as (x0, x1) = dims (l, l + HALF)
+  // by lanes l < HALF; result into this wave's LDS row
+  float* qrow = qk[wave][0];
+  float* krow = qk[wave][1];
+  auto norm_rope = [&](float x0, float x1, float w0, float w1, float* dst, float& y0, float& y1) {
+    const float ssq = wave_sum(lane < HALF ? x0 * x0 + x1 * x1 : 0.0f);
     const float rinv = 1.0f / sqrtf(ssq / (float)HD + a.eps);
+    const float xa = x0 * rinv * w0;
+    const float xb = x1 * rinv * w1;
+    y0 = xa * cs0 - xb * cs1;
+    y1 = xa * cs1 + xb * cs0;
     if (lane < HALF) {
-      const float xa = x0 * rinv * w0;
-      const float xb = x1 * rinv * w1;
-      h[lane] = xa * cs0 - xb * cs1;
-      h[lane + HALF] = xa * cs1 + xb * cs0;
+      dst[lane] = y0;
+      dst[lane + HALF] = y1;
     }
-  }
-  __syncthreads();
-  if (has_pos && qh % G == 0 && tid < F4) {
+  };
+  float q0, q1, k0, k1;
+  norm_rope(qx0, qx1, qw0, qw1, qrow, q0, q1);
+  norm_rope(kx0, kx1, kw0, kw1, krow, k0, k1);
+  if (has_pos && qh % a.g == 0 && wave == 0) {
     // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
-    const size_t off = (size_t)pos * rowf4 + kvh * F4 + tid;
-    reinterpret_cast<float4*>(a.kcache)[off] = reinterpret_cast<const float4*>(knew)[tid];
-    reinterpret_cast<float4*>(a.vcache)[off] = reinterpret_cast<const float4*>(vnew)[tid];
+    float* kc = a.kcache + (size_t)pos * rowf4 * 4 + kvh * HD;
+    if (lane < HALF) {
+      kc[lane] = k0;
+      kc[lane + HALF] = k1;
+    }
+    reinterpret_cast<vlane_t*>(a.vcache)[(size_t)pos * rowv + kvh * (HD / VPL) + lane] = vnew;
   }
+  wave_lds_sync();
   float4 q[CPL];
 #pragma unroll
-  for (int i = 0; i < CPL; i++) q[i] = reinterpret_cast<const float4*>(qs)[sl + LPR * i];
+  for (int i = 0; i < CPL; i++) q[i] = reinterpret_cast<const float4*>(qrow)[sl + LPR * i];
+
   vlane_t acc = (vlane_t)(0.0f);
   float m_w = -INFINITY, l_w = 0.0f;
-  const int nchunk = (n_t + CHUNK - 1) / CHUNK;
-  for (int ci = 0; ci < nchunk; ci++) {
+  for (int rb = 0; rb < n_t; rb += ROUND) {
+    if (rb > 0) load_round(rb);
+    float sc[NP];
+    float cmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < CPL; i++) kr[i] = kn[i];
+    for (int p = 0; p < NP; p++) {
+      sc[p] = -INFINITY;
+      if (rb + p * PASS < n_t) {
+        const int t = rb + p * PASS + wave * RPW + r;
+        float4 kk[CPL];
 #pragma unroll
-    for (int j = 0; j < RPW; j++) vr[j] = vn[j];
-    if (ci + 1 < nchunk) load_chunk(kn, vn, (ci + 1) * CHUNK);
-    const int t0 = ci * CHUNK + wave * RPW;  // first row of this wave
-    const int t = t0 + r;
-    const bool valid = t < n_t;
-    if (c0 + t == pos) {
+        for (int i = 0; i < CPL; i++) kk[i] = kr[p][i];
+        if (c0 + t == pos) {
 #pragma unroll
-      for (int i = 0; i < CPL; i++) kr[i] = reinterpret_cast<const float4*>(knew)[sl + LPR * i];
+          for (int i = 0; i < CPL; i++) kk[i] = reinterpret_cast<const float4*>(krow)[sl + LPR * i];
+        }
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+          d = fmaf(q[i].x, kk[i].x, d);
+          d = fmaf(q[i].y, kk[i].y, d);
+          d = fmaf(q[i].z, kk[i].z, d);
+          d = fmaf(q[i].w, kk[i].w, d);
+        }
+        d += dpp_f32<0xB1>(d);   // quad_perm [1,0,3,2]
+        d += dpp_f32<0x4E>(d);   // quad_perm [2,3,0,1]
+        d += dpp_f32<0x141>(d);  // row_half_mirror: the 8 lanes of the row
+        sc[p] = t < n_t ? d * a.scale : -INFINITY;
+        cmax = fmaxf(cmax, sc[p]);
+      }
     }
-    float d = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CPL; i++) {
-      d = fmaf(q[i].x, kr[i].x, d);
-      d = fmaf(q[i].y, kr[i].y, d);
-      d = fmaf(q[i].z, kr[i].z, d);
-      d = fmaf(q[i].w, kr[i].w, d);
-    }
-    d += dpp_f32<0xB1>(d);   // quad_perm [1,0,3,2]
-    d += dpp_f32<0x4E>(d);   // quad_perm [2,3,0,1]
-    d += dpp_f32<0x141>(d);  // row_half_mirror: the 8 lanes of the row
-    const float sc = valid ? d * a.scale : -INFINITY;
-    const float cm = wave_max(sc);
-    if (cm == -INFINITY) continue;  // no row of this wave in the chunk (uniform)
+    const float cm = wave_max(cmax);
+    if (cm == -INFINITY) continue;  // no row of this wave in the round (uniform)
     const float m_new = fmaxf(m_w, cm);
     const float alpha = m_w == -INFINITY ? 0.0f : expf(m_w - m_new);
-    const float e = valid ? expf(sc - m_new) : 0.0f;
-    l_w = fmaf(l_w, alpha, wave_sum(sl == 0 ? e : 0.0f));
     acc *= alpha;
+    float esum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < RPW; j++) {
-      const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j * LPR));
-      const vlane_t v = (c0 + t0 + j == pos) ? reinterpret_cast<const vlane_t*>(vnew)[lane] : vr[j];
-      acc += ej * v;
+    for (int p = 0; p < NP; p++) {
+      if (rb + p * PASS < n_t) {
+        const float e = sc[p] == -INFINITY ? 0.0f : expf(sc[p] - m_new);
+        esum += sl == 0 ? e : 0.0f;
+        const int t0 = rb + p * PASS + wave * RPW;
+#pragma unroll
+        for (int j = 0; j < RPW; j++) {
+          const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j * LPR));
+          const vlane_t v = (c0 + t0 + j == pos) ? vnew : vr[p][j];
+          acc += ej * v;
+        }
+      }
     }
+    l_w = fmaf(l_w, alpha, wave_sum(esum));
     m_w = m_new;
   }
   reinterpret_cast<vlane_t*>(wo[wave])[lane] = acc;
@@ -260,52 +282,39 @@ __global__ __launch_bounds__(kAttnThreads) void attn_head_kernel(AttnArgs a) {
     wl[wave] = l_w;
   }
   __syncthreads();
-  const int nsp = (T + CH - 1) / CH;
   if (tid < HD) {
     float M = -INFINITY;
+#pragma unroll
     for (int w = 0; w < NWV; w++) M = fmaxf(M, wm[w]);
     float L = 0.0f, o = 0.0f;
+#pragma unroll
     for (int w = 0; w < NWV; w++) {
       const float f = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
       L = fmaf(f, wl[w], L);
       o = fmaf(f, wo[w][tid], o);
     }
     if (tid == 0 && !isfinite(M)) atomicOr(&a.st->err, 4u);
-    if (nsp == 1) {
+    if (a.nsplit == 1) {
       a.out[qh * HD + tid] = o * (1.0f / L);
     } else {
-      float* p = a.part + ((size_t)qh * a.nsplit + sp) * (HD + 2);
-      p[2 + tid] = o;
-      if (tid == 0) {
-        p[0] = M;
-        p[1] = L;
-      }
+      a.out[((size_t)sp * nq + qh) * HD + tid] = o;
+      if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(M, L);
     }
   }
-  if (nsp == 1) return;
-  // The workgroup that finishes last for this head merges the splits.
-  // Release: partials reach device scope before the count; acquire: the
-  // last workgroup sees every other split's partials.
-  __shared__ int is_last;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&a.counters[qh], 1u) == (unsigned)(nsp - 1);
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (tid < HD) {
-    const float* p = a.part + (size_t)qh * a.nsplit * (HD + 2);
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < nsp; s2++) M = fmaxf(M, p[s2 * (HD + 2)]);
-    float L = 0.0f, o = 0.0f;
-    for (int s2 = 0; s2 < nsp; s2++) {
-      const float w = expf(p[s2 * (HD + 2)] - M);
-      L = fmaf(w, p[s2 * (HD + 2) + 1], L);
-      o = fmaf(w, p[s2 * (HD + 2) + 2 + tid], o);
-    }
-    a.out[qh * HD + tid] = o * (1.0f / L);
-  }
-  if (tid == 0) a.counters[qh] = 0;  // ready for the next launch
+}
+
+// Split merge for O projections that cannot take the merging GEMV: thread t
+// merges dims 8t..8t+7 of the attention output.
+__global__ void attn_merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml, int k, int hd,
+                                  int nsplit, float* __restrict__ out) {
+  const int e0 = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (e0 >= k) return;
+  AttnSplitIn in;
+  attn_split_load(in, part_o, part_ml, k, hd, nsplit, e0);
+  float4 x0, x1;
+  attn_split_merge(in, nsplit, x0, x1);
+  reinterpret_cast<float4*>(out + e0)[0] = x0;
+  reinterpret_cast<float4*>(out + e0)[1] = x1;
 }
 
 __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
@@ -381,8 +390,8 @@ struct zg_model {
   float* kv = nullptr;
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
   float* logits = nullptr;
-  float* part = nullptr;
-  uint32_t* counters = nullptr;
+  float* part_o = nullptr;   // attention split outputs [nsplit][nq*HD]
+  float* part_ml = nullptr;  // attention split (max, exp-sum) [nsplit][nq]
   uint64_t* best = nullptr;
   zg::DevState* st = nullptr;
   uint32_t* prompt = nullptr;  // device prompt buffer
@@ -390,6 +399,7 @@ struct zg_model {
   uint32_t* out_tokens = nullptr;
   size_t out_cap = 0;
   int nsplit = 1, split_len = 0;
+  bool o_merge = false;  // the O GEMV merges the attention splits itself
   std::vector<void*> owned;  // device allocations to free
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
@@ -450,9 +460,8 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.rope_cs = m->rope_cs;
     aa.kcache = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
     aa.vcache = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
-    aa.part = m->part;
-    aa.out = m->attn;
-    aa.counters = m->counters;
+    aa.out = m->nsplit == 1 ? m->attn : m->part_o;
+    aa.part_ml = m->part_ml;
     aa.st = m->st;
     aa.nkv = (int)d.n_kv_heads;
     aa.g = (int)(d.n_q_heads / d.n_kv_heads);
@@ -460,13 +469,24 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.split_len = m->split_len;
     aa.eps = d.rms_eps;
     aa.scale = scale;
-    const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnThreads);
-    if (HD == 128) hipLaunchKernelGGL(attn_head_kernel<128>, ag, ab, 0, st, aa);
-    else hipLaunchKernelGGL(attn_head_kernel<64>, ag, ab, 0, st, aa);
+    const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnWaves * 64);
+    if (HD == 128) hipLaunchKernelGGL(attn_split_kernel<128>, ag, ab, 0, st, aa);
+    else hipLaunchKernelGGL(attn_split_kernel<64>, ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
-    if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
-                        PRO_PLAIN, nullptr, 0.0f, st)))
-      return s;
+    if (m->o_merge) {
+      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, d.lin_type, 4, st)))
+        return s;
+    } else {
+      if (m->nsplit > 1) {
+        const int thr = 256, nthr = qd / 8;
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((nthr + thr - 1) / thr), dim3(thr), 0, st, m->part_o, m->part_ml,
+                           qd, HD, m->nsplit, m->attn);
+        if ((s = hip_check(ctx, hipGetLastError(), "attention merge launch"))) return s;
+      }
+      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
+                          PRO_PLAIN, nullptr, 0.0f, st)))
+        return s;
+    }
     FusedDev gu[2] = {{L.gate, m->act, (size_t)F, d.lin_type, 4}, {L.up, nullptr, (size_t)F, d.lin_type, 4}};
     if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
     if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
@@ -569,11 +589,15 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     }
     s = upload_f32(m, &m->inv_freq, inv.data(), inv.size());
   }
-  // one workgroup per KV head streams its whole context (a 1024-thread
-  // workgroup sustains ~100 GB/s); contexts above kSplitMax are split and
-  // merged by the last workgroup
-  m->split_len = (int)(d.max_ctx <= (uint32_t)kSplitMax ? d.max_ctx : (uint32_t)kSplitMax);
-  m->nsplit = (int)((d.max_ctx + m->split_len - 1) / m->split_len);
+  // up to kAttnSplits workgroups per query head share its context (one CU
+  // loads ~150 GB/s, so a head's K/V rows are spread over several CUs);
+  // splits are multiples of 32 rows
+  {
+    const uint32_t per = (d.max_ctx + kAttnSplits - 1) / kAttnSplits;
+    m->split_len = (int)(per < 32 ? 32 : (per + 31) / 32 * 32);
+    m->nsplit = (int)((d.max_ctx + m->split_len - 1) / m->split_len);
+    m->o_merge = m->nsplit > 1 && attn_merge_gemv_ok(d.lin_type, 4, qd);
+  }
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->kv), (size_t)d.n_layers * 2 * d.max_ctx * kvd * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->rope_cs), d.head_dim * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->hidden), H * sizeof(float));
@@ -583,10 +607,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->attn), qd * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->act), F * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->logits), (size_t)d.vocab_padded * sizeof(float));
-  if (!s)
-    s = model_alloc(m, reinterpret_cast<void**>(&m->part),
-                    (size_t)d.n_q_heads * m->nsplit * (d.head_dim + 2) * sizeof(float));
-  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->counters), d.n_q_heads * sizeof(uint32_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->part_o), (size_t)m->nsplit * qd * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->part_ml), (size_t)m->nsplit * d.n_q_heads * 2 * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
   m->prompt_cap = d.max_ctx;
