@@ -107,6 +107,9 @@ GEMV_CASES = [
     (Q4K, 1, 33, 2304),      # 9 superblocks per row: a partial 8-superblock step
     (Q6K, 1, 17, 2304),      # odd superblocks per row: unaligned Q6_K row starts
     (Q6K, 1, 8, 16384),      # in_dim above the LDS-staged limit: generic path
+    (Q8_0, 4, 32768, 512),   # tall Q8_0X4 (LM-head strip path): one strip, four waves per strip
+    (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
+    (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
 ]
 
 
@@ -156,6 +159,23 @@ def test_row_ranges(ctx, zo, quant, il):
         ctx.linear_range(x, w, out, k, rows, quant, s, e)
         assert np.all(out[:s] == -7.0) and np.all(out[e:] == -7.0)
         assert rel_err(out[s:e], ref[s:e]) <= REL_TOL if e > s else True
+    ctx.clear()
+
+
+def test_tall_q8_0_ranges(ctx, zo):
+    """Row ranges of a tall Q8_0X4 matrix (the LM head's strip path): rows
+    outside the range stay untouched, partial first and last groups."""
+    rng = np.random.default_rng(9)
+    rows, k = 32800, 1024
+    w = synth.weight(rng, Q8_0, rows, k, 4)
+    x = synth.activations(rng, k)
+    ctx.register(w, Q8_0, 4)
+    ref = zo.linear_range(x, w, k, rows, Q8_0, 4)
+    for s, e in ((0, rows), (1, 32799), (6, 32777)):
+        out = np.full(rows, -7.0, np.float32)
+        ctx.linear_range(x, w, out, k, rows, Q8_0, s, e)
+        assert np.all(out[:s] == -7.0) and np.all(out[e:] == -7.0)
+        assert rel_err(out[s:e], ref[s:e]) <= REL_TOL
     ctx.clear()
 
 

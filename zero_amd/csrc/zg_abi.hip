@@ -243,7 +243,7 @@ zg_status zg::check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_
 // One GEMV (optionally a row range, residual or argmax epilogue).
 zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,
                          uint32_t il, size_t start, size_t end, int epi, const float* resid, uint64_t* best,
-                         int pro, const float* norm_w, float eps, hipStream_t st) {
+                         int pro, const float* norm_w, float eps, hipStream_t st, uint32_t gemv_flags) {
   if (start >= end) return ZG_OK;
   if (pair_path_ok(qt, il, k, n, w, x)) {
     const size_t gbytes = (k / 32) * (qt == ZG_Q4_0 ? 72 : 136);
@@ -256,6 +256,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.norm_w = norm_w;
     a.eps = eps;
     a.best = best;
+    a.flags = gemv_flags;
     a.seg[0].w = w + g0 * gbytes;
     a.seg[0].y = y ? y + 4 * g0 : nullptr;
     a.seg[0].resid = resid ? resid + 4 * g0 : nullptr;

@@ -360,17 +360,53 @@ struct LaneW {
   uint32_t d;
 };
 
+// Quant loads of the strip kernels: 16-byte loads (8-byte aligned) or
+// 8-byte loads, nontemporal or not.  The scale load always uses the same
+// cache policy as the quant loads: the two share cache lines.
+#ifndef ZG_STRIP_LD16_Q8
+#define ZG_STRIP_LD16_Q8 1
+#endif
+#ifndef ZG_STRIP_LD16_Q4
+#define ZG_STRIP_LD16_Q4 0
+#endif
+#ifndef ZG_STRIP_NT_Q8
+#define ZG_STRIP_NT_Q8 0
+#endif
+#ifndef ZG_STRIP_NT_Q4
+#define ZG_STRIP_NT_Q4 1
+#endif
+typedef uint32_t u32x4a8 __attribute__((ext_vector_type(4), aligned(8)));
+
+// load through pointer p with the nontemporal hint when NT (a macro: the
+// pointee's alignment attribute must reach the load)
+#define ZG_LD_POL(NT, p) ((NT) ? __builtin_nontemporal_load(p) : *(p))
+
 template <uint32_t QT>
 __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int r) {
   constexpr int QW = StripGeom<QT>::QW;
-  const u32x2* p = reinterpret_cast<const u32x2*>(blk + 8 + 4 * QW * r);
+  constexpr bool LD16 = QT == Q8_0 ? ZG_STRIP_LD16_Q8 : ZG_STRIP_LD16_Q4;
+  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : ZG_STRIP_NT_Q4;
+  if (LD16) {
+    // row quants start at 8 + 16r (Q4_0) or 8 + 32r (Q8_0): 8-byte aligned
+    const u32x4a8* p = reinterpret_cast<const u32x4a8*>(blk + 8 + 4 * QW * r);
 #pragma unroll
-  for (int i = 0; i < QW / 2; i++) {
-    const u32x2 v = __builtin_nontemporal_load(p + i);
-    L.q[2 * i] = v.x;
-    L.q[2 * i + 1] = v.y;
+    for (int i = 0; i < QW / 4; i++) {
+      const u32x4a8 v = ZG_LD_POL(NT, p + i);
+      L.q[4 * i] = v.x;
+      L.q[4 * i + 1] = v.y;
+      L.q[4 * i + 2] = v.z;
+      L.q[4 * i + 3] = v.w;
+    }
+  } else {
+    const u32x2* p = reinterpret_cast<const u32x2*>(blk + 8 + 4 * QW * r);
+#pragma unroll
+    for (int i = 0; i < QW / 2; i++) {
+      const u32x2 v = ZG_LD_POL(NT, p + i);
+      L.q[2 * i] = v.x;
+      L.q[2 * i + 1] = v.y;
+    }
   }
-  L.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(blk + 2 * r));
+  L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk + 2 * r));
 }
 
 template <uint32_t QT>
@@ -387,8 +423,8 @@ __device__ __forceinline__ float row_sum4(float v) {
   return v;
 }
 
-template <uint32_t QT, int PRO, int EPI, int GBATCH>
-__global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false>
+__global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   constexpr int GBY = StripGeom<QT>::GB;
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) float part[];  // [2][NW][GBATCH][PARTS][16]
@@ -405,10 +441,15 @@ __global__ __launch_bounds__(1024) void gemv_strip_kernel(GemvArgs a, int S) {
   const int per_batch = WPS * GBATCH;
   const int nbatch = (items + per_batch - 1) / per_batch;
 
+  // SEG1: a single projection (g_begin 0), no per-item segment search
   auto locate = [&](int item, int p, uint32_t& lg) -> GemvSeg {
     if (EPI == EPI_SWIGLU) {
       lg = (uint32_t)item;
       return p ? a.seg[1] : a.seg[0];
+    }
+    if (SEG1) {
+      lg = (uint32_t)item;
+      return a.seg[0];
     }
     const GemvSeg sg = seg_of(a, (uint32_t)item);
     lg = (uint32_t)item - sg.g_begin;
@@ -807,19 +848,43 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
-template <uint32_t QT, int PRO, int EPI, int GBATCH>
-static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false>
+static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
-  // about 16 resident waves per CU; the remaining batches are looped over
-  const size_t per_cu = nw >= ZG_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_STRIP_WAVES_PER_CU / nw);
+  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
+  // about 16 resident waves per CU; the remaining batches are looped over.
+  // A 256-thread bound lets the compiler use more registers: the grid is
+  // then what the occupancy query says fits.
+  size_t per_cu = nw >= ZG_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_STRIP_WAVES_PER_CU / nw);
+  if (MAXT < 1024) {
+    static int resident = 0;
+    if (resident == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1>, nw * 64,
+                                                       shm) !=
+              hipSuccess ||
+          n <= 0)
+        n = 1;
+      resident = n;
+    }
+    if ((size_t)resident < per_cu) per_cu = (size_t)resident;
+  }
   const size_t cap = (size_t)cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
-  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
-  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH>), dim3((unsigned)grid), dim3(nw * 64), shm, st, a, S);
+  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1>), dim3((unsigned)grid), dim3(nw * 64), shm, st,
+                     a, S);
   return hipGetLastError();
+}
+
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024>
+static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    if (a.nseg == 1) return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, true>(a, S, nw, items, st);
+  }
+  return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, false>(a, S, nw, items, st);
 }
 
 template <uint32_t QT, int PRO, int EPI>
@@ -835,12 +900,31 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
     if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
       return launch_strip_gb<QT, PRO, EPI, 4>(a, S, nw, items, st);
   }
+  if constexpr (QT == Q8_0 && EPI != EPI_SWIGLU && PRO != PRO_ATTN) {
+    // tall Q8_0X4 (the LM head): four groups per batch with 16-byte loads
+    // need more than 128 registers, so these launches are 256-thread
+    // workgroups (in_dim at most 2048)
+    if (nw == 4 && items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
+      return launch_strip_gb<QT, PRO, EPI, 4, 256>(a, S, nw, items, st);
+  }
   return launch_strip_gb<QT, PRO, EPI, 2>(a, S, nw, items, st);
 }
 
-// Q4_0X4 takes the strip kernel (measured faster at every decode shape);
-// Q8_0X4 keeps the segment-streaming kernel, whose coalesced LDS-parked
-// loads suit its 32-byte row blocks better than per-lane loads.
+// Tall single-projection Q8_0X4 launches (the LM head: 37,984 groups) take
+// the strip kernel with four groups per batch and cache-allocating loads
+// (66 vs 85 us for 151936x2048 as a standalone call); smaller Q8_0X4
+// launches, and tall ones that stream their weights (kGemvStream: inside
+// the decode step the cache-allocating read would evict the KV cache, a net
+// loss there), keep the segment-streaming kernel and its nontemporal loads.
+#ifndef ZG_TALL_MIN_GROUPS
+#define ZG_TALL_MIN_GROUPS 8192
+#endif
+static bool tall_path_ok(const GemvArgs& a) {
+  return a.nseg == 1 && !(a.flags & kGemvStream) && a.k % 512 == 0 && a.k <= 2048 &&
+         a.total_groups >= ZG_TALL_MIN_GROUPS;
+}
+
+// Q4_0X4 takes the strip kernel (measured faster at every decode shape).
 template <uint32_t QT, int PRO, int EPI>
 static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
   if constexpr (PRO == PRO_ATTN) {
@@ -852,6 +936,9 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
     }
     return hipErrorInvalidValue;
   } else {
+    if constexpr (QT == Q8_0 && (EPI == EPI_STORE || EPI == EPI_ARGMAX)) {
+      if (tall_path_ok(a)) return launch_strip<QT, PRO, EPI>(a, st);
+    }
     if constexpr (QT == Q4_0) {
       if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
     }

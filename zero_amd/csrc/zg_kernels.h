@@ -36,7 +36,13 @@ struct GemvArgs {
   // attn_hd] their (max, exp-sum) pairs
   const float* attn_ml;
   int attn_nsplit, attn_hd;
+  uint32_t flags;  // kGemvStream
 };
+
+// The weights are streamed without allocating in the last-level cache:
+// set by the device-resident decode step, whose KV cache and activations
+// should stay cached across the 330 MB LM-head read.
+constexpr uint32_t kGemvStream = 1;
 
 struct GenericArgs {
   const uint8_t* w;

@@ -509,7 +509,7 @@ static zg_status record_step(zg_model* m, hipStream_t st) {
   if (s) return s;
   s = run_linear(m->ctx, m->hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
                            d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM,
-                           m->out_norm, d.rms_eps, st);
+                           m->out_norm, d.rms_eps, st, kGemvStream);
   if (s) return s;
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
   return hip_check(m->ctx, hipGetLastError(), "finalize launch");
