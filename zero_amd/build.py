@@ -3,7 +3,10 @@
 Every translation unit in zero_amd/csrc is compiled by hipcc for gfx950
 only, in parallel, then linked into one shared library that exports the C
 ABI of include/zero_gpu.h.  Packed FP32 VALU instructions are disabled
-(-target-feature -packed-fp32-ops) for every device compilation.
+(-target-feature -packed-fp32-ops) for every device compilation.  MFMA
+results are kept in ordinary VGPRs (-amdgpu-mfma-vgpr-form): the prefill
+GEMM reads every accumulator after each block, and the AGPR form would add
+one v_accvgpr_read per value.
 """
 from __future__ import annotations
 
@@ -28,6 +31,7 @@ DEVICE_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
     "-Wno-unused-value",
 ]

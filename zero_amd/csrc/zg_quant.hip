@@ -142,26 +142,27 @@ struct GemmArgs {
   int m, n, k;
 };
 
-constexpr int kBM = 64, kBN = 64, kBK = 4;  // kBK blocks of 32 per stage
+constexpr int kBN = 64, kBK = 4;  // tile columns; kBK blocks of 32 per stage (tile rows BM: 64 or 32)
 constexpr int kRow = kBK * 32 + 16;         // LDS row stride in bytes (padded, 16-B aligned)
 
 // One stage's global operands held in registers between the load and the
 // LDS store (so that the next stage's loads fly while the current stage is
-// multiplied): two 16-byte activation chunks and one activation scale, one
+// multiplied): BM/32 16-byte activation chunks and one activation scale, one
 // weight block row (raw quants + scale) per thread.
-template <uint32_t WT>
+template <uint32_t WT, int BM>
 struct GemmStage {
-  u32x4 a[2];
+  u32x4 a[BM / 32];
   uint32_t ad;
   uint32_t q[WT == Q4_0 ? 4 : 8];
   uint32_t wd;
 };
 
-template <uint32_t WT, int IL>
-__device__ __forceinline__ void gemm_stage_load(GemmStage<WT>& S, const GemmArgs& a, int m0, int n0, int b0, int tid) {
+template <uint32_t WT, int IL, int BM>
+__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const GemmArgs& a, int m0, int n0, int b0,
+                                                int tid) {
   const int nb = a.k / 32;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < BM / 32; i++) {
     const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
     const int gm = m0 + row, kb = b0 + ch / 2;
     S.a[i] = u32x4{0, 0, 0, 0};
@@ -170,7 +171,7 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT>& S, const GemmArgs
   {
     const int row = tid / kBK, kk = tid % kBK;
     const int gm = m0 + row, kb = b0 + kk;
-    S.ad = (gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
+    S.ad = (row < BM && gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
   }
   {
     const int row = tid / kBK, kk = tid % kBK;
@@ -207,16 +208,16 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT>& S, const GemmArgs
   }
 }
 
-template <uint32_t WT>
-__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT>& S, int8_t* As, int8_t* Bs, float* Ad, float* Bd,
-                                                 int tid) {
+template <uint32_t WT, int BM>
+__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM>& S, int8_t* As, int8_t* Bs, float* Ad,
+                                                 float* Bd, int tid) {
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < BM / 32; i++) {
     const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
     *reinterpret_cast<u32x4*>(As + row * kRow + ch * 16) = S.a[i];
   }
   const int row = tid / kBK, kk = tid % kBK;
-  Ad[kk * kBM + row] = half_bits_to_f32(S.ad);
+  if (row < BM) Ad[kk * BM + row] = half_bits_to_f32(S.ad);
   uint32_t q[8];
   if (WT == Q4_0) {
     // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
@@ -238,62 +239,67 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT>& S, int8_t*
   Bd[kk * kBN + row] = half_bits_to_f32(S.wd);
 }
 
-// Workgroup tile 64 (m) x 64 (n), 4 waves of 32 x 32 (2 x 2 MFMA tiles).
-// kBK blocks (128 K) per stage, double-buffered in LDS; the next stage's
-// global loads are issued before the current stage is multiplied.  Per
-// 32-K block: v_mfma_i32_16x16x32_i8 gives the block's integer dots, and
-// every output adds dX*dW*isum with one fma, blocks in ascending order.
-template <uint32_t WT, int IL>
+// Workgroup tile BM (m) x 64 (n), 4 waves of BM/2 x 32 (BM/32 x 2 MFMA
+// tiles): BM = 64, or 32 when the 64-row tiles would leave CUs idle.  kBK
+// blocks (128 K) per stage, double-buffered in LDS; the next stage's global
+// loads are issued before the current stage is multiplied.  Per 32-K block:
+// v_mfma_i32_16x16x32_i8 gives the block's integer dots, and every output
+// adds dX*dW*isum with one fma, blocks in ascending order.  The 64-row
+// tile's block loop is not unrolled: that keeps it near 100 VGPRs, four
+// workgroups per CU (M=512 x 6144: all 768 tiles resident at once; 34.7 vs
+// 41-43 us unrolled); the 32-row tile is unrolled (48.7 vs 54.3 us).
+template <uint32_t WT, int IL, int BM>
 __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t As[2][kBM * kRow];
+  constexpr int MI = BM / 32;  // 16-row MFMA tiles per wave
+  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * kRow];
   __shared__ __attribute__((aligned(16))) int8_t Bs[2][kBN * kRow];
-  __shared__ __attribute__((aligned(16))) float Ad[2][kBK * kBM];  // [kk][row]
+  __shared__ __attribute__((aligned(16))) float Ad[2][kBK * BM];   // [kk][row]
   __shared__ __attribute__((aligned(16))) float Bd[2][kBK * kBN];  // [kk][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
   const int nb = a.k / 32;
   const int nst = (nb + kBK - 1) / kBK;
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
   const int r16 = lane & 15, kq = (lane >> 4) * 8, rq = (lane >> 4) * 4;
-  float acc[2][2][4];
+  float acc[MI][2][4];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
-  GemmStage<WT> S;
-  gemm_stage_load<WT, IL>(S, a, m0, n0, 0, tid);
-  gemm_stage_store<WT>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
+  GemmStage<WT, BM> S;
+  gemm_stage_load<WT, IL, BM>(S, a, m0, n0, 0, tid);
+  gemm_stage_store<WT, BM>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
   for (int st = 0; st < nst; st++) {
     const int buf = st & 1;
-    if (st + 1 < nst) gemm_stage_load<WT, IL>(S, a, m0, n0, (st + 1) * kBK, tid);
+    if (st + 1 < nst) gemm_stage_load<WT, IL, BM>(S, a, m0, n0, (st + 1) * kBK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
-#pragma unroll
+#pragma unroll(BM == 64 ? 1 : kBK)
     for (int kk = 0; kk < kBK; kk++) {
-      long av[2], bv[2];
-      float4 da[2];
+      long av[MI], bv[2];
+      float4 da[MI];
       float db[2];
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
+      for (int i = 0; i < MI; i++) {
         av[i] = *reinterpret_cast<const long*>(A + (wm + 16 * i + r16) * kRow + kk * 32 + kq);
-        da[i] = *reinterpret_cast<const float4*>(&Ad[buf][kk * kBM + wm + 16 * i + rq]);
+        da[i] = *reinterpret_cast<const float4*>(&Ad[buf][kk * BM + wm + 16 * i + rq]);
       }
 #pragma unroll
       for (int j = 0; j < 2; j++) {
         bv[j] = *reinterpret_cast<const long*>(B + (wn + 16 * j + r16) * kRow + kk * 32 + kq);
         db[j] = Bd[buf][kk * kBN + wn + 16 * j + r16];
       }
-      v4i c[2][2];
+      v4i c[MI][2];
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
+      for (int i = 0; i < MI; i++) {
         const float dai[4] = {da[i].x, da[i].y, da[i].z, da[i].w};
 #pragma unroll
         for (int j = 0; j < 2; j++)
@@ -301,12 +307,12 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
           for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(__fmul_rn(dai[r], db[j]), (float)c[i][j][r], acc[i][j][r]);
       }
     }
-    if (st + 1 < nst) gemm_stage_store<WT>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
+    if (st + 1 < nst) gemm_stage_store<WT, BM>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
     __syncthreads();
   }
   // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -352,6 +358,24 @@ extern "C" zg_status zg_quantize_q8_0_split_dev(zg_ctx* ctx, const float* d_x, i
   return launch_quant(ctx, d_x, nullptr, d_qs, d_d, rows, k, stream);
 }
 
+static int gemm_cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+template <uint32_t WT, int IL, int BM>
+static void launch_gemm(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
+  hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM>), grid, dim3(256), 0, st, a);
+}
+
 extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const uint16_t* d_d, const void* d_w,
                                       float* d_y, size_t m, size_t n, size_t k, uint32_t w_type, uint32_t interleave,
                                       void* stream) {
@@ -366,11 +390,19 @@ extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const ui
   if (interleave == 4 && (reinterpret_cast<uintptr_t>(d_w) & 7))
     return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: weights misaligned");
   GemmArgs a{d_qs, d_d, static_cast<const uint8_t*>(d_w), d_y, (int)m, (int)n, (int)k};
-  dim3 grid((unsigned)((n + kBN - 1) / kBN), (unsigned)((m + kBM - 1) / kBM));
   hipStream_t st = qstream(ctx, stream);
-  if (w_type == ZG_Q4_0 && interleave == 4) hipLaunchKernelGGL((gemm_q8act_kernel<Q4_0, 4>), grid, dim3(256), 0, st, a);
-  else if (w_type == ZG_Q4_0) hipLaunchKernelGGL((gemm_q8act_kernel<Q4_0, 1>), grid, dim3(256), 0, st, a);
-  else if (interleave == 4) hipLaunchKernelGGL((gemm_q8act_kernel<Q8_0, 4>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((gemm_q8act_kernel<Q8_0, 1>), grid, dim3(256), 0, st, a);
+  // 64-row tiles unless they would not give every CU three workgroups
+  const size_t tiles64 = ((n + kBN - 1) / kBN) * ((m + 63) / 64);
+  if (tiles64 >= (size_t)3 * gemm_cu_count()) {
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 64>(a, st);
+    else launch_gemm<Q8_0, 1, 64>(a, st);
+  } else {
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 32>(a, st);
+    else launch_gemm<Q8_0, 1, 32>(a, st);
+  }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
 }
