@@ -22,6 +22,15 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return ((h & 0x7C00u) == 0x7C00u) ? __uint_as_float(special) : f;
 }
 
+// The value through an empty asm: the compiler can no longer see which
+// bits are zero.  Used on masked quant words, so that a byte conversion
+// stays one v_cvt_f32_ubyteN instead of being folded with the mask into a
+// bit-field extract plus a conversion.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // Native 128-bit vector for global loads (nontemporal builtins need a
 // clang vector type, not HIP's uint4 wrapper).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -114,8 +114,8 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* qs, const float4* 
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const uint32_t v = qs[c];
-    const uint32_t lo = v & 0x0F0F0F0Fu;
-    const uint32_t hi = v & 0xF0F0F0F0u;
+    const uint32_t lo = opaque_u32(v & 0x0F0F0F0Fu);
+    const uint32_t hi = opaque_u32(v & 0xF0F0F0F0u);
     const float4 xl = xb[c];
     const float4 xh = xb[4 + c];
     s_lo = fmaf(xl.x, (float)(lo & 0xFFu), s_lo);

@@ -160,8 +160,8 @@ __device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const KqX& x, int 
   uint32_t lo[4], hi[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    lo[c] = q[c] & 0x0F0F0F0Fu;
-    hi[c] = (q[c] >> 4) & 0x0F0F0F0Fu;
+    lo[c] = opaque_u32(q[c] & 0x0F0F0F0Fu);
+    hi[c] = opaque_u32((q[c] >> 4) & 0x0F0F0F0Fu);
   }
   const float sA = u8_dot16(lo, x.a);
   const float sB = u8_dot16(hi, x.b);
@@ -184,8 +184,8 @@ __device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const KqX& x, int 
   uint32_t qA[4], qB[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    qA[c] = ((a[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hA) & 0x03030303u) << 4);
-    qB[c] = ((b[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hB) & 0x03030303u) << 4);
+    qA[c] = opaque_u32(((a[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hA) & 0x03030303u) << 4));
+    qB[c] = opaque_u32(((b[c] >> nsh) & 0x0F0F0F0Fu) | (((hh[c] >> hB) & 0x03030303u) << 4));
   }
   const float sA = u8_dot16(qA, x.a);
   const float sB = u8_dot16(qB, x.b);
