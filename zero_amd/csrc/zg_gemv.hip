@@ -493,10 +493,14 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
     }
   }
   // two batches in flight: this workgroup's first and second
+  // The grid never exceeds the batch count, so the first batch exists and
+  // its loads are unconditional: the prologue's wait for x can then leave
+  // them in flight.  The second batch is issued after the prologue (a
+  // conditional load ahead of the prologue would make the compiler wait for
+  // every outstanding load before it uses x).
   LaneW<QT> LA[GBATCH][PARTS], LB[GBATCH][PARTS];
   const int b0 = blockIdx.x, bstep = gridDim.x;
-  if (b0 < nbatch) load_batch(LA, b0);
-  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
+  load_batch(LA, b0);
 
   // prologue and block sum
   if (PRO == PRO_ATTN) {
@@ -542,7 +546,9 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   float t = 0.0f;
 #pragma unroll
   for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
-  const float mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
+  float mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
+  asm volatile("" : "+v"(mterm));  // computed here, not sunk below the next load
+  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
 
   uint64_t key = 0;
   // one batch: partials -> LDS, barrier, per-row totals over strips and
