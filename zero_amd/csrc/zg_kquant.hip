@@ -274,8 +274,8 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
     atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
 }
 
-// Strip form (in_dim a multiple of 2048): the K axis is cut into strips of
-// 8 superblocks; a wave owns one strip and keeps its lanes' activations in
+// Strip form for Q4_K (in_dim a multiple of 2048): the K axis is cut into
+// strips of 8 superblocks; a wave owns one strip and keeps its lanes' activations in
 // registers while it walks rows, so no activation is re-read per row.  A
 // workgroup has one wave per strip (times WPS when there are fewer than 4
 // strips) and walks batches of rows; two batches of loads are in flight
@@ -304,10 +304,14 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
       kq_load(L[j], a.w + row * rowbytes + (size_t)sb * BB, lane);
     }
   };
+  // x first, then the first batch (unconditional: the grid never exceeds
+  // the batch count); the second batch is issued after the activation sums,
+  // so that their wait leaves the first batch's loads in flight
   KqLane<QT> LA[RB], LB[RB];
   const int b0 = blockIdx.x, bstep = gridDim.x;
-  const KqX x = kq_x<QT>(a.x, sb, lane);
-  if (b0 < nbatch) load_batch(LA, b0);
+  KqX x = kq_x<QT>(a.x, sb, lane);
+  load_batch(LA, b0);
+  asm volatile("" : "+v"(x.sa), "+v"(x.sb));
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
   uint64_t key = 0;
   auto process = [&](const KqLane<QT> (&L)[RB], int batch, int buf) {
@@ -356,6 +360,212 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   }
 }
 
+// Strip form for Q6_K (in_dim a multiple of 2048).  The K axis is cut into
+// strips of 8 superblocks; a wave owns one strip and keeps its lanes'
+// activations in registers while it walks rows.  Four lanes per superblock
+// decode 64
+// elements each, so a half-wave covers one row's strip and a wave decodes
+// two rows at a time:
+//   Q4_K lane jj (0..3): qs bytes [32 jj, 32 jj + 32); low nibbles are
+//        elements 64 jj + i (sub-block 2 jj), high nibbles 64 jj + 32 + i
+//        (sub-block 2 jj + 1)
+//   Q6_K lane (n, is): half n, l in [16 is, 16 is + 16), all four quarters
+//        Q: element 128 n + l + 32 Q, low 4 bits from ql[l] (Q even) or
+//        ql[l + 32] (Q odd), nibble selected by Q >= 2, high 2 bits
+//        qh[l] >> 2Q, scale sc[8 n + is + 2 Q] (dequant.rs:328-355)
+// A workgroup has one wave per strip (times WPS when there are fewer than 4
+// strips) and walks batches of row pairs with two batches of loads in
+// flight (clamped unconditional loads).  A row's partial is summed over its
+// half-wave with DPP, then over strips through LDS in a fixed order.
+template <uint32_t QT>
+struct Kq2Lane;
+template <>
+struct Kq2Lane<Q4K> {
+  u32x4 hdr, q0, q1;
+};
+template <>
+struct Kq2Lane<Q6K> {
+  u32x4 la, lb, hb;
+  uint32_t sc0, sc1, d;
+};
+
+__device__ __forceinline__ void kq2_load(Kq2Lane<Q4K>& L, const uint8_t* blk, int lane) {
+  const int jj = lane & 3;
+  L.hdr = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk));
+  L.q0 = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk + 16 + 32 * jj));
+  L.q1 = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk + 32 + 32 * jj));
+}
+
+__device__ __forceinline__ void kq2_load(Kq2Lane<Q6K>& L, const uint8_t* blk, int lane) {
+  const int n = (lane >> 1) & 1, is = lane & 1;
+  L.la = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 16 * is));
+  L.lb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 32 + 16 * is));
+  L.hb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * n + 16 * is));
+  const u32x2a2 scw = ZG_KQ_LD(reinterpret_cast<const u32x2a2*>(blk + 192 + 8 * n));
+  L.sc0 = scw.x;
+  L.sc1 = scw.y;
+  L.d = (uint32_t)ZG_KQ_LD(reinterpret_cast<const uint16_t*>(blk + 208));
+}
+
+// The lane's 64 activations as four runs of 16 and their sums.
+//   Q4_K runs: 64 jj + {0, 16, 32, 48}
+//   Q6_K runs: 128 n + 16 is + 32 Q, Q = 0..3
+struct Kq2X {
+  float4 r[4][4];
+  float s[4];
+};
+
+template <uint32_t QT>
+__device__ __forceinline__ int kq2_run_elem(int lane, int run) {
+  if (QT == Q4K) return 64 * (lane & 3) + 16 * run;
+  return 128 * ((lane >> 1) & 1) + 16 * (lane & 1) + 32 * run;
+}
+
+template <uint32_t QT>
+__device__ __forceinline__ Kq2X kq2_x(const float* x, int sb, int lane) {
+  Kq2X r;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float4* p = reinterpret_cast<const float4*>(x + sb * 256 + kq2_run_elem<QT>(lane, q));
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      r.r[q][c] = p[c];
+      s += (r.r[q][c].x + r.r[q][c].y) + (r.r[q][c].z + r.r[q][c].w);
+    }
+    r.s[q] = s;
+  }
+  return r;
+}
+
+__device__ __forceinline__ float kq2_dot(const Kq2Lane<Q4K>& L, const Kq2X& x, int lane) {
+  const int jj = lane & 3;
+  const float d = half_bits_to_f32(L.hdr.x), dmin = half_bits_to_f32(L.hdr.x >> 16);
+  const uint32_t sb[3] = {L.hdr.y, L.hdr.z, L.hdr.w};
+  float scA, mA, scB, mB;
+  scale_min_k4(sb, 2 * jj, scA, mA);
+  scale_min_k4(sb, 2 * jj + 1, scB, mB);
+  const uint32_t q0[4] = {L.q0.x, L.q0.y, L.q0.z, L.q0.w}, q1[4] = {L.q1.x, L.q1.y, L.q1.z, L.q1.w};
+  uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    lo0[c] = opaque_u32(q0[c] & 0x0F0F0F0Fu);
+    hi0[c] = opaque_u32((q0[c] >> 4) & 0x0F0F0F0Fu);
+    lo1[c] = opaque_u32(q1[c] & 0x0F0F0F0Fu);
+    hi1[c] = opaque_u32((q1[c] >> 4) & 0x0F0F0F0Fu);
+  }
+  // sub-block 2jj: runs 0, 1 (low nibbles); sub-block 2jj+1: runs 2, 3
+  const float sA = u8_dot16(lo0, x.r[0]) + u8_dot16(lo1, x.r[1]);
+  const float sB = u8_dot16(hi0, x.r[2]) + u8_dot16(hi1, x.r[3]);
+  float acc = (d * scA) * sA;
+  acc = fmaf(-(dmin * mA), x.s[0] + x.s[1], acc);
+  acc = fmaf(d * scB, sB, acc);
+  return fmaf(-(dmin * mB), x.s[2] + x.s[3], acc);
+}
+
+__device__ __forceinline__ float kq2_dot(const Kq2Lane<Q6K>& L, const Kq2X& x, int lane) {
+  const int is = lane & 1;
+  const uint32_t scw[2] = {L.sc0, L.sc1};
+  const float d = half_bits_to_f32(L.d);
+  const uint32_t a[4] = {L.la.x, L.la.y, L.la.z, L.la.w}, b[4] = {L.lb.x, L.lb.y, L.lb.z, L.lb.w},
+                 hh[4] = {L.hb.x, L.hb.y, L.hb.z, L.hb.w};
+  float acc = 0.0f;
+#pragma unroll
+  for (int Q = 0; Q < 4; Q++) {
+    uint32_t q[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const uint32_t lowsrc = (Q & 1) ? b[c] : a[c];
+      const uint32_t lo4 = (Q >= 2) ? ((lowsrc >> 4) & 0x0F0F0F0Fu) : (lowsrc & 0x0F0F0F0Fu);
+      q[c] = opaque_u32(lo4 | (((hh[c] >> (2 * Q)) & 0x03030303u) << 4));
+    }
+    const float sc = (float)(int8_t)byte_of(scw, is + 2 * Q);
+    const float sQ = u8_dot16(q, x.r[Q]);
+    acc = fmaf(d * sc, fmaf(-32.0f, x.s[Q], sQ), acc);
+  }
+  return acc;
+}
+
+template <uint32_t QT, int EPI, int RB>
+__global__ __launch_bounds__(1024) void kq2_strip_kernel(GenericArgs a, int S) {
+  constexpr int BB = KqGeom<QT>::BB;
+  constexpr int RPB = 2 * RB;                // rows per wave per batch
+  __shared__ float part[2][32][RPB];  // [buffer][wave][row of the batch]
+  const int NW = blockDim.x >> 6;
+  const int WPS = NW / S;
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = wave % S, sub = wave / S;
+  const int nsb = (int)(a.k / 256);
+  const int sb = strip * 8 + ((lane >> 2) & 7);  // this lane's superblock
+  const size_t rowbytes = (size_t)nsb * BB;
+  const int nrows = (int)(a.row_hi - a.row_lo);
+  const int per_batch = WPS * RPB;
+  const int nbatch = (nrows + per_batch - 1) / per_batch;
+  // row j of this wave's share of a batch: j = 2 * pair + half
+  auto load_batch = [&](Kq2Lane<QT> (&L)[RB], int batch) {
+    const int base = batch * per_batch + sub * RPB;
+#pragma unroll
+    for (int p = 0; p < RB; p++) {
+      const size_t row = a.row_lo + (size_t)min(base + 2 * p + half, nrows - 1);
+      kq2_load(L[p], a.w + row * rowbytes + (size_t)sb * BB, lane);
+    }
+  };
+  // x first, then the first batch (unconditional: the grid never exceeds
+  // the batch count); the second batch is issued after the activation sums
+  Kq2Lane<QT> LA[RB], LB[RB];
+  const int b0 = blockIdx.x, bstep = gridDim.x;
+  Kq2X x = kq2_x<QT>(a.x, sb, lane);
+  load_batch(LA, b0);
+  asm volatile("" : "+v"(x.s[0]), "+v"(x.s[1]), "+v"(x.s[2]), "+v"(x.s[3]));
+  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
+  uint64_t key = 0;
+  auto process = [&](const Kq2Lane<QT> (&L)[RB], int batch, int buf) {
+#pragma unroll
+    for (int p = 0; p < RB; p++) {
+      // sum over the half-wave: the row total lands in lanes 16..31 / 48..63
+      const float v = group_sum<32>(kq2_dot(L[p], x, lane));
+      if ((lane & 31) == 31) part[buf][wave][2 * p + half] = v;
+    }
+    __syncthreads();
+    const int tt = threadIdx.x;
+    if (tt < per_batch) {
+      const int su = tt / RPB, j = tt % RPB;
+      const int ri = batch * per_batch + su * RPB + j;
+      if (ri < nrows) {
+        float v = 0.0f;
+        for (int st = 0; st < S; st++) v += part[buf][su * S + st][j];
+        const size_t row = a.row_lo + ri;
+        if (EPI == EPI_RESID)
+          a.y[row] = a.resid[row] + v;
+        else if (a.y)
+          a.y[row] = v;
+        if (EPI == EPI_ARGMAX && !(v != v)) {
+          const uint64_t kk = argmax_key(v, (uint32_t)row);
+          key = kk > key ? kk : key;
+        }
+      }
+    }
+  };
+  for (int batch = b0; batch < nbatch; batch += 2 * bstep) {
+    process(LA, batch, 0);
+    if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
+    if (batch + bstep < nbatch) {
+      process(LB, batch + bstep, 1);
+      if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
+  }
+}
+
 size_t kq_lds_bytes(int k) { return (size_t)k * sizeof(float) + (size_t)(k / 16) * sizeof(float); }
 
 static int kq_cu_count() {
@@ -377,19 +587,24 @@ static int kq_cu_count() {
 
 template <uint32_t QT, int EPI>
 static hipError_t launch_kq_strip(const GenericArgs& a, hipStream_t st) {
-  // rows per wave per batch: 2 for Q6_K (register budget), 2 for Q4_K
-  // (13.3 vs 13.6 us at four)
-  constexpr int RB = 2;
+  // Q4_K: 32-element lanes, two rows per wave per batch.  Q6_K: 64-element
+  // lanes (half a wave per row), one row pair per wave per batch.  Measured
+  // on the Llama-3-8B shapes: Q4_K 12.6 us with 32-element lanes vs 14.6
+  // with 64 (the longer per-lane chains stall); Q6_K 18.1 vs 21.2 us.
+  constexpr int RPW = 2;  // rows per wave per batch
   const int S = (int)(a.k / 2048);
   const int nw = S >= 4 ? S : (S == 3 ? 6 : 4);
   const int wps = nw / S;
   const size_t rows = a.row_hi - a.row_lo;
-  const size_t nbatch = (rows + (size_t)wps * RB - 1) / ((size_t)wps * RB);
+  const size_t nbatch = (rows + (size_t)wps * RPW - 1) / ((size_t)wps * RPW);
   const size_t per_cu = nw >= ZG_KQ_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_KQ_STRIP_WAVES_PER_CU / nw);
   const size_t cap = (size_t)kq_cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((kq_strip_kernel<QT, EPI, RB>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
+  if constexpr (QT == Q4K)
+    hipLaunchKernelGGL((kq_strip_kernel<QT, EPI, 2>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
+  else
+    hipLaunchKernelGGL((kq2_strip_kernel<QT, EPI, 1>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
   return hipGetLastError();
 }
 
