@@ -116,23 +116,22 @@ struct KqLane<Q6K> {
 // dwordx2 loads (unaligned access mode).
 typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32x2a2 __attribute__((ext_vector_type(2), aligned(2)));
-#define ZG_KQ_LD(p) (*(p))
 
 __device__ __forceinline__ void kq_load(KqLane<Q4K>& L, const uint8_t* blk, int lane) {
   const int j = (lane >> 1) & 3, h = lane & 1;
-  L.hdr = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk));
-  L.q = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk + 16 + 32 * j + 16 * h));
+  L.hdr = *reinterpret_cast<const u32x4*>(blk);
+  L.q = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * j + 16 * h);
 }
 
 __device__ __forceinline__ void kq_load(KqLane<Q6K>& L, const uint8_t* blk, int lane) {
   const int n = (lane >> 2) & 1, is = (lane >> 1) & 1;
-  L.la = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 16 * is));
-  L.lb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 32 + 16 * is));
-  L.hb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * n + 16 * is));
-  const u32x2a2 scw = ZG_KQ_LD(reinterpret_cast<const u32x2a2*>(blk + 192 + 8 * n));
+  L.la = *reinterpret_cast<const u32x4a2*>(blk + 64 * n + 16 * is);
+  L.lb = *reinterpret_cast<const u32x4a2*>(blk + 64 * n + 32 + 16 * is);
+  L.hb = *reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * n + 16 * is);
+  const u32x2a2 scw = *reinterpret_cast<const u32x2a2*>(blk + 192 + 8 * n);
   L.sc0 = scw.x;
   L.sc1 = scw.y;
-  L.d = (uint32_t)ZG_KQ_LD(reinterpret_cast<const uint16_t*>(blk + 208));
+  L.d = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208);
 }
 
 // Element offset (within the superblock) of the lane's first 16-element run;
@@ -363,16 +362,11 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
 // Strip form for Q6_K (in_dim a multiple of 2048).  The K axis is cut into
 // strips of 8 superblocks; a wave owns one strip and keeps its lanes'
 // activations in registers while it walks rows.  Four lanes per superblock
-// decode 64
-// elements each, so a half-wave covers one row's strip and a wave decodes
-// two rows at a time:
-//   Q4_K lane jj (0..3): qs bytes [32 jj, 32 jj + 32); low nibbles are
-//        elements 64 jj + i (sub-block 2 jj), high nibbles 64 jj + 32 + i
-//        (sub-block 2 jj + 1)
-//   Q6_K lane (n, is): half n, l in [16 is, 16 is + 16), all four quarters
-//        Q: element 128 n + l + 32 Q, low 4 bits from ql[l] (Q even) or
-//        ql[l + 32] (Q odd), nibble selected by Q >= 2, high 2 bits
-//        qh[l] >> 2Q, scale sc[8 n + is + 2 Q] (dequant.rs:328-355)
+// decode 64 elements each, so a half-wave covers one row's strip and a wave
+// decodes two rows at a time.  Lane (n, is): half n, l in [16 is, 16 is +
+// 16), all four quarters Q: element 128 n + l + 32 Q, low 4 bits from ql[l]
+// (Q even) or ql[l + 32] (Q odd), nibble selected by Q >= 2, high 2 bits
+// qh[l] >> 2Q, scale sc[8 n + is + 2 Q] (dequant.rs:328-355).
 // A workgroup has one wave per strip (times WPS when there are fewer than 4
 // strips) and walks batches of row pairs with two batches of loads in
 // flight (clamped unconditional loads).  A row's partial is summed over its
@@ -380,53 +374,35 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
 template <uint32_t QT>
 struct Kq2Lane;
 template <>
-struct Kq2Lane<Q4K> {
-  u32x4 hdr, q0, q1;
-};
-template <>
 struct Kq2Lane<Q6K> {
   u32x4 la, lb, hb;
   uint32_t sc0, sc1, d;
 };
 
-__device__ __forceinline__ void kq2_load(Kq2Lane<Q4K>& L, const uint8_t* blk, int lane) {
-  const int jj = lane & 3;
-  L.hdr = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk));
-  L.q0 = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk + 16 + 32 * jj));
-  L.q1 = ZG_KQ_LD(reinterpret_cast<const u32x4*>(blk + 32 + 32 * jj));
-}
-
 __device__ __forceinline__ void kq2_load(Kq2Lane<Q6K>& L, const uint8_t* blk, int lane) {
   const int n = (lane >> 1) & 1, is = lane & 1;
-  L.la = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 16 * is));
-  L.lb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 64 * n + 32 + 16 * is));
-  L.hb = ZG_KQ_LD(reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * n + 16 * is));
-  const u32x2a2 scw = ZG_KQ_LD(reinterpret_cast<const u32x2a2*>(blk + 192 + 8 * n));
+  L.la = *reinterpret_cast<const u32x4a2*>(blk + 64 * n + 16 * is);
+  L.lb = *reinterpret_cast<const u32x4a2*>(blk + 64 * n + 32 + 16 * is);
+  L.hb = *reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * n + 16 * is);
+  const u32x2a2 scw = *reinterpret_cast<const u32x2a2*>(blk + 192 + 8 * n);
   L.sc0 = scw.x;
   L.sc1 = scw.y;
-  L.d = (uint32_t)ZG_KQ_LD(reinterpret_cast<const uint16_t*>(blk + 208));
+  L.d = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208);
 }
 
-// The lane's 64 activations as four runs of 16 and their sums.
-//   Q4_K runs: 64 jj + {0, 16, 32, 48}
-//   Q6_K runs: 128 n + 16 is + 32 Q, Q = 0..3
+// The lane's 64 activations as four runs of 16 (quarter Q: elements
+// 128 n + 16 is + 32 Q ..) and their sums.
 struct Kq2X {
   float4 r[4][4];
   float s[4];
 };
 
-template <uint32_t QT>
-__device__ __forceinline__ int kq2_run_elem(int lane, int run) {
-  if (QT == Q4K) return 64 * (lane & 3) + 16 * run;
-  return 128 * ((lane >> 1) & 1) + 16 * (lane & 1) + 32 * run;
-}
-
-template <uint32_t QT>
 __device__ __forceinline__ Kq2X kq2_x(const float* x, int sb, int lane) {
   Kq2X r;
+  const int e0 = 128 * ((lane >> 1) & 1) + 16 * (lane & 1);
 #pragma unroll
   for (int q = 0; q < 4; q++) {
-    const float4* p = reinterpret_cast<const float4*>(x + sb * 256 + kq2_run_elem<QT>(lane, q));
+    const float4* p = reinterpret_cast<const float4*>(x + sb * 256 + e0 + 32 * q);
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -436,31 +412,6 @@ __device__ __forceinline__ Kq2X kq2_x(const float* x, int sb, int lane) {
     r.s[q] = s;
   }
   return r;
-}
-
-__device__ __forceinline__ float kq2_dot(const Kq2Lane<Q4K>& L, const Kq2X& x, int lane) {
-  const int jj = lane & 3;
-  const float d = half_bits_to_f32(L.hdr.x), dmin = half_bits_to_f32(L.hdr.x >> 16);
-  const uint32_t sb[3] = {L.hdr.y, L.hdr.z, L.hdr.w};
-  float scA, mA, scB, mB;
-  scale_min_k4(sb, 2 * jj, scA, mA);
-  scale_min_k4(sb, 2 * jj + 1, scB, mB);
-  const uint32_t q0[4] = {L.q0.x, L.q0.y, L.q0.z, L.q0.w}, q1[4] = {L.q1.x, L.q1.y, L.q1.z, L.q1.w};
-  uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    lo0[c] = opaque_u32(q0[c] & 0x0F0F0F0Fu);
-    hi0[c] = opaque_u32((q0[c] >> 4) & 0x0F0F0F0Fu);
-    lo1[c] = opaque_u32(q1[c] & 0x0F0F0F0Fu);
-    hi1[c] = opaque_u32((q1[c] >> 4) & 0x0F0F0F0Fu);
-  }
-  // sub-block 2jj: runs 0, 1 (low nibbles); sub-block 2jj+1: runs 2, 3
-  const float sA = u8_dot16(lo0, x.r[0]) + u8_dot16(lo1, x.r[1]);
-  const float sB = u8_dot16(hi0, x.r[2]) + u8_dot16(hi1, x.r[3]);
-  float acc = (d * scA) * sA;
-  acc = fmaf(-(dmin * mA), x.s[0] + x.s[1], acc);
-  acc = fmaf(d * scB, sB, acc);
-  return fmaf(-(dmin * mB), x.s[2] + x.s[3], acc);
 }
 
 __device__ __forceinline__ float kq2_dot(const Kq2Lane<Q6K>& L, const Kq2X& x, int lane) {
@@ -516,7 +467,7 @@ __global__ __launch_bounds__(1024) void kq2_strip_kernel(GenericArgs a, int S) {
   // the batch count); the second batch is issued after the activation sums
   Kq2Lane<QT> LA[RB], LB[RB];
   const int b0 = blockIdx.x, bstep = gridDim.x;
-  Kq2X x = kq2_x<QT>(a.x, sb, lane);
+  Kq2X x = kq2_x(a.x, sb, lane);
   load_batch(LA, b0);
   asm volatile("" : "+v"(x.s[0]), "+v"(x.s[1]), "+v"(x.s[2]), "+v"(x.s[3]));
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
