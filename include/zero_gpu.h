@@ -36,6 +36,9 @@ typedef int32_t zg_status;
 #define ZG_ERR_OUT_OF_MEMORY -8
 #define ZG_ERR_ATTENTION -9         /* AttentionError::NumericalInstability    */
 #define ZG_ERR_CONTEXT_FULL -10     /* KvCache position out of range           */
+#define ZG_ERR_MAGIC_MISMATCH -11   /* LoadError::MagicMismatch (model_loader.rs:149-159)    */
+#define ZG_ERR_UNSUPPORTED_FORMAT -12 /* LoadError::UnsupportedFormat                        */
+#define ZG_ERR_INVALID_CONTAINER -13  /* LoadError::InvalidContainer                         */
 
 /* GgmlType ids (crates/zero-gguf-parser/src/lib.rs:95-126). */
 #define ZG_Q4_0 2u
@@ -215,6 +218,59 @@ zg_status zg_model_generate(zg_model *m, const uint32_t *prompt, size_t n_prompt
                             uint32_t *out_tokens, double *prefill_seconds, double *gen_seconds);
 /* Position reset (new sequence). */
 void zg_model_reset(zg_model *m);
+
+/* ------------------------------------------------------------------ */
+/* .smodel native container (SilicatePack SILM + SIDX).                 */
+/* ------------------------------------------------------------------ */
+
+typedef struct zg_smodel zg_smodel;
+
+/* Container header and SIDX model config (smodel_info,
+ * kernel/src/model_loader.rs:599-659; smodel_native_tensor_index :380-454).
+ * Optional u32 fields hold 0xFFFFFFFF when absent (SMODEL_NONE_U32). */
+typedef struct {
+    uint32_t version;      /* 1, or 2 (may carry row-interleaved dtypes) */
+    uint32_t payload_kind; /* 2 = native (1 = GGUF compatibility: rejected) */
+    uint32_t flags;        /* bit 0: payload 2 MiB aligned */
+    uint64_t manifest_offset, manifest_len, payload_offset, payload_len;
+    uint32_t architecture_id; /* 1 qwen3, 2 deepseek2, else unknown */
+    uint32_t block_count, context_length, embedding_length, feed_forward_length;
+    uint32_t head_count, head_count_kv, key_length, value_length;
+    float rope_freq_base, layer_norm_rms_epsilon;
+    uint32_t vocab_size, eos_token_id;
+    uint64_t tensor_count;
+} zg_smodel_info;
+
+/* One SIDX tensor entry (104 bytes, model_loader.rs:480-520). */
+typedef struct {
+    const char *name;       /* not NUL-terminated: name_len bytes */
+    size_t name_len;
+    uint32_t dtype;         /* SIDX dtype id as stored (100 = Q4_0X4, 101 = Q8_0X4) */
+    uint32_t ggml_type;     /* smodel_decode_dtype (model_loader.rs:82-90) */
+    uint32_t interleave;    /* 1, or 4 for the X4 dtypes */
+    uint32_t rank;
+    uint64_t dims[8];       /* source (HF) order: dims[0] = output rows */
+    uint64_t payload_offset;
+    const void *data;       /* inside the caller's bytes */
+    uint64_t byte_len;
+} zg_smodel_tensor;
+
+/* Validate a native .smodel held in memory (bytes..bytes+len, kept alive
+ * by the caller) with the reference loader's checks: header (smodel_info),
+ * SIDX magic/version/sizes, tensor count cap 10,000, names in range and
+ * UTF-8, dtype known, every tensor inside the payload, X4 tensors rank 2
+ * with rows % 4 == 0.  Errors are ZG_ERR_MAGIC_MISMATCH,
+ * ZG_ERR_UNSUPPORTED_FORMAT, ZG_ERR_INVALID_CONTAINER as LoadError. */
+zg_status zg_smodel_open(const void *bytes, size_t len, zg_smodel **out);
+void zg_smodel_close(zg_smodel *sm);
+zg_status zg_smodel_get_info(const zg_smodel *sm, zg_smodel_info *out);
+zg_status zg_smodel_get_tensor(const zg_smodel *sm, uint64_t index, zg_smodel_tensor *out);
+/* By exact name; ZG_ERR_INVALID_ARG when absent. */
+zg_status zg_smodel_find(const zg_smodel *sm, const char *name, zg_smodel_tensor *out);
+/* Register every quantized tensor (Q4_0/Q8_0 plain or X4, Q4_K, Q6_K) with
+ * its layout, as smodel_native_tensor_index registers the X4 ones in
+ * weight_layout (model_loader.rs:527-552); F32 tensors are skipped. */
+zg_status zg_smodel_register_all(zg_ctx *ctx, const zg_smodel *sm);
 
 #ifdef __cplusplus
 }

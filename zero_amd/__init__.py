@@ -17,8 +17,10 @@ from .ops import (  # noqa: F401
     ZgError,
     tensor_bytes,
 )
+from .smodel import InvalidContainer, LoadError, MagicMismatch, SModel, UnsupportedFormat  # noqa: F401
 
 __all__ = [
     "Context", "GgmlType", "LinearDispatchError", "LmHeadError", "NonFiniteLogits", "ArgmaxInPaddingRegion",
     "ZgError", "tensor_bytes", "VOCAB_SIZE_PADDED", "VOCAB_SIZE_REAL",
+    "SModel", "LoadError", "MagicMismatch", "UnsupportedFormat", "InvalidContainer",
 ]

@@ -32,6 +32,9 @@ ZG_ERR_REGISTRY_FULL = -7
 ZG_ERR_OUT_OF_MEMORY = -8
 ZG_ERR_ATTENTION = -9
 ZG_ERR_CONTEXT_FULL = -10
+ZG_ERR_MAGIC_MISMATCH = -11
+ZG_ERR_UNSUPPORTED_FORMAT = -12
+ZG_ERR_INVALID_CONTAINER = -13
 
 
 class zg_segment(C.Structure):
@@ -64,6 +67,32 @@ class zg_model_desc(C.Structure):
         ("token_embd", C.c_void_p), ("lm_head", C.c_void_p), ("output_norm", C.c_void_p),
         ("layers", C.POINTER(zg_layer_weights)),
         ("device_pointers", C.c_uint32),
+    ]
+
+
+class zg_smodel_info(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32), ("payload_kind", C.c_uint32), ("flags", C.c_uint32),
+        ("manifest_offset", C.c_uint64), ("manifest_len", C.c_uint64),
+        ("payload_offset", C.c_uint64), ("payload_len", C.c_uint64),
+        ("architecture_id", C.c_uint32), ("block_count", C.c_uint32), ("context_length", C.c_uint32),
+        ("embedding_length", C.c_uint32), ("feed_forward_length", C.c_uint32),
+        ("head_count", C.c_uint32), ("head_count_kv", C.c_uint32),
+        ("key_length", C.c_uint32), ("value_length", C.c_uint32),
+        ("rope_freq_base", C.c_float), ("layer_norm_rms_epsilon", C.c_float),
+        ("vocab_size", C.c_uint32), ("eos_token_id", C.c_uint32),
+        ("tensor_count", C.c_uint64),
+    ]
+
+
+class zg_smodel_tensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_void_p), ("name_len", C.c_size_t),
+        ("dtype", C.c_uint32), ("ggml_type", C.c_uint32), ("interleave", C.c_uint32), ("rank", C.c_uint32),
+        ("dims", C.c_uint64 * 8),
+        ("payload_offset", C.c_uint64),
+        ("data", C.c_void_p),
+        ("byte_len", C.c_uint64),
     ]
 
 
@@ -103,6 +132,12 @@ SIGNATURES = {
     "zg_model_step": (_ST, [_P, _U32, _U32, _P, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),
     "zg_model_generate": (_ST, [_P, _P, _S, _S, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "zg_model_reset": (None, [_P]),
+    "zg_smodel_open": (_ST, [_P, _S, C.POINTER(_P)]),
+    "zg_smodel_close": (None, [_P]),
+    "zg_smodel_get_info": (_ST, [_P, C.POINTER(zg_smodel_info)]),
+    "zg_smodel_get_tensor": (_ST, [_P, C.c_uint64, C.POINTER(zg_smodel_tensor)]),
+    "zg_smodel_find": (_ST, [_P, C.c_char_p, C.POINTER(zg_smodel_tensor)]),
+    "zg_smodel_register_all": (_ST, [_P, _P]),
 }
 
 _lib = None

@@ -18,15 +18,18 @@ class GpuModel:
     """Uploads a model's tensors through the weight registry and builds the
     per-token HIP graphs (zg_model_create)."""
 
-    def __init__(self, ctx: Context, model: RandomModel):
+    def __init__(self, ctx: Context, model: RandomModel, register: bool = True):
+        """``register=False`` when the weights are already in the context's
+        registry (``from_smodel``)."""
         self.ctx = ctx
         self.cfg = cfg = model.cfg
         self.model = model
-        for L in model.layers:
-            for w in (L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down):
-                ctx.register(w, cfg.lin_type, 4)
-        ctx.register(model.token_embd, cfg.embd_type, 1)
-        ctx.register(model.lm_head, cfg.head_type, 4)
+        if register:
+            for L in model.layers:
+                for w in (L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down):
+                    ctx.register(w, cfg.lin_type, 4)
+            ctx.register(model.token_embd, cfg.embd_type, 1)
+            ctx.register(model.lm_head, cfg.head_type, 4)
         self._layers = (_lib.zg_layer_weights * cfg.n_layers)()
         for i, L in enumerate(model.layers):
             self._layers[i] = _lib.zg_layer_weights(
@@ -50,6 +53,16 @@ class GpuModel:
         h = C.c_void_p()
         ctx.check(ctx.lib.zg_model_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h
+
+    @classmethod
+    def from_smodel(cls, ctx: Context, sm, max_ctx: int | None = None) -> "GpuModel":
+        """A packed ``.smodel`` (zero_amd.smodel.SModel): every quantized
+        tensor enters the registry with its SIDX layout
+        (zg_smodel_register_all), then the dense Qwen3 graph is built over
+        those registered views."""
+        model = sm.to_model(max_ctx)
+        sm.register_all(ctx)
+        return cls(ctx, model, register=False)
 
     def close(self):
         if getattr(self, "h", None):
