@@ -219,6 +219,27 @@ zg_status zg_model_generate(zg_model *m, const uint32_t *prompt, size_t n_prompt
 /* Position reset (new sequence). */
 void zg_model_reset(zg_model *m);
 
+/* Batched prefill.  No counterpart in the reference, which runs the prompt
+ * token by token through forward_single_token_avx512
+ * (kernel/src/inference.rs:1188-1330); this is the M >= 64 prefill of the
+ * int8-MFMA path: per layer the n prompt rows go through rmsnorm, Q8_0
+ * activation quantization (the packer's encoder, silicatepack.py:893-907)
+ * and zg_gemm_q8act_dev-style GEMMs (Q|K|V, O, gate|up, down), with the
+ * decode step's QK-norm, RoPE, causal attention and SwiGLU per row.  Writes
+ * KV rows pos0..pos0+n-1 (chunks of up to 512 rows attend to the rows
+ * before them), then runs the LM head on the last row.  Leaves the model
+ * ready to decode at position pos0 + n.  hidden_out (optional): the final
+ * hidden state of the last row.  Activations are quantized to 8 bits, so
+ * results differ from token-by-token prefill by that quantization. */
+zg_status zg_model_prefill(zg_model *m, const uint32_t *tokens, size_t n, uint32_t pos0,
+                           float *hidden_out, uint32_t *next_token, float *max_logit);
+#define ZG_GEN_BATCHED_PREFILL 1u
+/* zg_model_generate with flags: ZG_GEN_BATCHED_PREFILL runs the prompt
+ * through zg_model_prefill's batched path instead of token by token. */
+zg_status zg_model_generate_ex(zg_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                               uint32_t flags, uint32_t *out_tokens, double *prefill_seconds,
+                               double *gen_seconds);
+
 /* ------------------------------------------------------------------ */
 /* .smodel native container (SilicatePack SILM + SIDX).                 */
 /* ------------------------------------------------------------------ */

@@ -1052,11 +1052,34 @@ void zo_model_destroy(zo_model *m) {
     free(m);
 }
 
+/* All query heads of one token over cache rows 0..T-1
+ * (gqa_attention_single_token_avx512, inference_avx512.rs:1744-1800):
+ * scores q.k * scale, softmax, weighted sum of V rows in row order. */
+static int attend(const zo_model_desc *d, const float *kc, const float *vc, const float *q, size_t T,
+                  float scale, float *scores, float *out) {
+    size_t hd = (size_t)d->head_dim, nq = (size_t)d->n_q_heads, nkv = (size_t)d->n_kv_heads;
+    size_t kvd = nkv * hd, gqa = nq / nkv;
+    for (size_t h = 0; h < nq; h++) {
+        size_t kh = h / gqa;
+        const float *qv = q + h * hd;
+        for (size_t t = 0; t < T; t++) scores[t] = dot16(qv, kc + t * kvd + kh * hd, hd) * scale;
+        if (zo_softmax(scores, T)) return -4;
+        float *o = out + h * hd;
+        for (size_t i = 0; i < hd; i++) o[i] = 0.0f;
+        for (size_t t = 0; t < T; t++) {
+            const float *vv = vc + t * kvd + kh * hd;
+            float wgt = scores[t];
+            for (size_t i = 0; i < hd; i++) o[i] = fmaf(wgt, vv[i], o[i]);
+        }
+    }
+    return 0;
+}
+
 int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out) {
     const zo_model_desc *d = &m->d;
     size_t H = (size_t)d->hidden, F = (size_t)d->ffn, hd = (size_t)d->head_dim;
     size_t nq = (size_t)d->n_q_heads, nkv = (size_t)d->n_kv_heads;
-    size_t qd = nq * hd, kvd = nkv * hd, gqa = nq / nkv;
+    size_t qd = nq * hd, kvd = nkv * hd;
     if (pos >= d->max_ctx || token >= d->vocab_padded) return -3;
     /* embed_lookup_dispatch (forward_pass.rs:311-370) */
     size_t be, bb;
@@ -1088,19 +1111,7 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
         float *vc = m->kv + ((size_t)l * 2 + 1) * d->max_ctx * kvd;
         memcpy(kc + pos * kvd, m->k, kvd * 4);
         memcpy(vc + pos * kvd, m->v, kvd * 4);
-        for (size_t h = 0; h < nq; h++) {
-            size_t kh = h / gqa;
-            const float *qv = m->q + h * hd;
-            for (size_t t = 0; t < T; t++) m->scores[t] = dot16(qv, kc + t * kvd + kh * hd, hd) * scale;
-            if (zo_softmax(m->scores, T)) return -4;
-            float *o = m->attn + h * hd;
-            for (size_t i = 0; i < hd; i++) o[i] = 0.0f;
-            for (size_t t = 0; t < T; t++) {
-                const float *vv = vc + t * kvd + kh * hd;
-                float wgt = m->scores[t];
-                for (size_t i = 0; i < hd; i++) o[i] = fmaf(wgt, vv[i], o[i]);
-            }
-        }
+        if (attend(d, kc, vc, m->q, T, scale, m->scores, m->attn)) return -4;
         zo_linear_parallel(m->attn, L->attn_o, m->proj, qd, H, d->lin_type, d->lin_interleave);
         for (size_t i = 0; i < H; i++) m->hidden[i] = m->hidden[i] + m->proj[i];
         zo_rmsnorm(m->hidden, L->ffn_norm, m->norm, H, d->rms_eps);
@@ -1115,6 +1126,89 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
     }
     if (hidden_out) memcpy(hidden_out, m->hidden, H * 4);
     return 0;
+}
+
+/* Batched prefill with Q8_0 activations (no reference counterpart: the
+ * reference runs the prompt token by token).  n rows at positions
+ * pos0..pos0+n-1; per layer every row is rmsnormed, quantized with the
+ * packer's Q8_0 encoder (zo_quantize_q8_0_row) and multiplied by
+ * zo_gemm_q8act; QK-norm, RoPE, the cache store, attention, SwiGLU and the
+ * residual adds are the single-token pass's per row.  Leaves the last row's
+ * final hidden state in the model (for zo_model_lm_head). */
+int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t pos0, float *hidden_out) {
+    const zo_model_desc *d = &m->d;
+    size_t H = (size_t)d->hidden, F = (size_t)d->ffn, hd = (size_t)d->head_dim;
+    size_t nq = (size_t)d->n_q_heads, nkv = (size_t)d->n_kv_heads;
+    size_t qd = nq * hd, kvd = nkv * hd;
+    if (n == 0 || pos0 + n > d->max_ctx) return -3;
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= d->vocab_padded) return -3;
+    size_t be, bb;
+    if (type_geom(d->embd_type, &be, &bb) || H % be) return -3;
+    size_t km = H > qd ? H : qd;
+    if (F > km) km = F;
+    float *X = (float *)malloc(n * H * 4), *T = (float *)malloc(n * km * 4);
+    float *Q = (float *)malloc(n * qd * 4), *K = (float *)malloc(n * kvd * 4), *V = (float *)malloc(n * kvd * 4);
+    float *A = (float *)malloc(n * qd * 4), *P = (float *)malloc(n * H * 4);
+    float *G = (float *)malloc(n * F * 4), *U = (float *)malloc(n * F * 4);
+    uint8_t *xq = (uint8_t *)malloc(n * (km / 32) * 34);
+    float *scores = (float *)malloc((pos0 + n) * 4);
+    int rc = 0;
+    if (!X || !T || !Q || !K || !V || !A || !P || !G || !U || !xq || !scores) rc = -5;
+    for (size_t i = 0; i < n && !rc; i++)
+        zo_dequant_tensor(d->token_embd + (size_t)tokens[i] * (H / be) * bb, X + i * H, 1, H, d->embd_type, 1);
+    float scale = 1.0f / sqrtf((float)hd);
+    float tmp[512];
+    for (int l = 0; l < d->n_layers && !rc; l++) {
+        const zo_layer *L = &m->layers[l];
+        float *kc = m->kv + ((size_t)l * 2 + 0) * d->max_ctx * kvd;
+        float *vc = m->kv + ((size_t)l * 2 + 1) * d->max_ctx * kvd;
+        for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->attn_norm, T + i * H, H, d->rms_eps);
+        zo_quantize_q8_0_row(T, xq, n * H);
+        if (zo_gemm_q8act(xq, L->attn_q, Q, n, qd, H, d->lin_type, d->lin_interleave) ||
+            zo_gemm_q8act(xq, L->attn_k, K, n, kvd, H, d->lin_type, d->lin_interleave) ||
+            zo_gemm_q8act(xq, L->attn_v, V, n, kvd, H, d->lin_type, d->lin_interleave)) {
+            rc = -3;
+            break;
+        }
+        for (size_t i = 0; i < n; i++) {
+            size_t pos = pos0 + i;
+            for (size_t h = 0; h < nq; h++) {
+                float *x = Q + i * qd + h * hd;
+                zo_rmsnorm(x, L->q_norm, tmp, hd, d->rms_eps);
+                memcpy(x, tmp, hd * 4);
+                zo_rope(x, m->inv_freqs, (int)(hd / 2), pos);
+            }
+            for (size_t h = 0; h < nkv; h++) {
+                float *x = K + i * kvd + h * hd;
+                zo_rmsnorm(x, L->k_norm, tmp, hd, d->rms_eps);
+                memcpy(x, tmp, hd * 4);
+                zo_rope(x, m->inv_freqs, (int)(hd / 2), pos);
+            }
+            memcpy(kc + pos * kvd, K + i * kvd, kvd * 4);
+            memcpy(vc + pos * kvd, V + i * kvd, kvd * 4);
+        }
+        for (size_t i = 0; i < n && !rc; i++)
+            if (attend(d, kc, vc, Q + i * qd, pos0 + i + 1, scale, scores, A + i * qd)) rc = -4;
+        if (rc) break;
+        zo_quantize_q8_0_row(A, xq, n * qd);
+        zo_gemm_q8act(xq, L->attn_o, P, n, H, qd, d->lin_type, d->lin_interleave);
+        for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
+        for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->ffn_norm, T + i * H, H, d->rms_eps);
+        zo_quantize_q8_0_row(T, xq, n * H);
+        zo_gemm_q8act(xq, L->ffn_gate, G, n, F, H, d->lin_type, d->lin_interleave);
+        zo_gemm_q8act(xq, L->ffn_up, U, n, F, H, d->lin_type, d->lin_interleave);
+        zo_silu_mul(G, U, T, n * F);
+        zo_quantize_q8_0_row(T, xq, n * F);
+        zo_gemm_q8act(xq, L->ffn_down, P, n, H, F, d->lin_type, d->lin_interleave);
+        for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
+    }
+    if (!rc) {
+        memcpy(m->hidden, X + (n - 1) * H, H * 4);
+        if (hidden_out) memcpy(hidden_out, m->hidden, H * 4);
+    }
+    free(X); free(T); free(Q); free(K); free(V); free(A); free(P); free(G); free(U); free(xq); free(scores);
+    return rc;
 }
 
 int zo_model_lm_head(zo_model *m, float *logits_out, uint32_t *token, float *max_val) {

@@ -142,6 +142,11 @@ void zo_model_destroy(zo_model *m);
 /* Runs one token through all layers at position pos.  Returns 0 on success,
  * negative on error.  If hidden_out != NULL copies the final hidden state. */
 int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out);
+/* Batched prefill with Q8_0-quantized activations (the GPU's int8-MFMA
+ * prefill; no reference counterpart): n tokens at positions
+ * pos0..pos0+n-1, KV rows stored; the last row's final hidden state is left
+ * in the model for zo_model_lm_head and copied to hidden_out if non-NULL. */
+int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t pos0, float *hidden_out);
 /* final rmsnorm + LM head + argmax; returns 0 / -1 non-finite / -2 padding */
 int zo_model_lm_head(zo_model *m, float *logits_out, uint32_t *token, float *max_val);
 

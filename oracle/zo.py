@@ -74,6 +74,7 @@ _SIG = {
     "zo_model_destroy": (None, [_P]),
     "zo_model_forward": (_I, [_P, _U32, _S, _P]),
     "zo_model_lm_head": (_I, [_P, _P, C.POINTER(_U32), C.POINTER(_F)]),
+    "zo_model_prefill_q8": (_I, [_P, _P, _S, _S, _P]),
 }
 
 _lib = None
@@ -236,6 +237,30 @@ class OracleModel:
         rc = load().zo_model_forward(self.h, token, pos, _p(hid))
         assert rc == 0, rc
         return hid
+
+    def prefill_q8(self, tokens, pos0=0):
+        """Batched prefill with Q8_0 activations; returns the last row's
+        final hidden state (the model is then ready for lm_head())."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        hid = np.empty(self.cfg.hidden, np.float32)
+        rc = load().zo_model_prefill_q8(self.h, _p(t), t.size, pos0, _p(hid))
+        assert rc == 0, rc
+        return hid
+
+    def generate_batched(self, prompt, n_gen):
+        """prefill_q8 of the prompt, then the single-token greedy loop."""
+        self.prefill_q8(prompt, 0)
+        rc, tok, _, _ = self.lm_head()
+        assert rc == 0, rc
+        toks = [tok]
+        pos = len(prompt)
+        while len(toks) < n_gen:
+            self.forward(toks[-1], pos)
+            pos += 1
+            rc, tok, _, _ = self.lm_head()
+            assert rc == 0, rc
+            toks.append(tok)
+        return np.array(toks, np.uint32)
 
     def lm_head(self):
         lg = np.empty(self.cfg.vocab_padded, np.float32)

@@ -6,7 +6,10 @@
 * zo_model_forward (the composition of the pinned operators in the order of
   forward_single_token_avx512, kernel/src/inference_avx512.rs:1826-1987)
   against an independent numpy restatement written from the Qwen3 block
-  definition, on a tiny random model.
+  definition, on a tiny random model;
+* zo_model_prefill_q8 (batched prefill with Q8_0 activations) against the
+  same numpy restatement with each matmul input quantized to Q8_0 (numpy's
+  own round-half-even and binary16 rounding), and for chunk invariance.
 """
 import numpy as np
 import pytest
@@ -40,10 +43,21 @@ def test_gemm_q8act_kat(zo):
     assert y[0, 0] == np.float32(d) * np.float32(32 * 127)
 
 
-def _np_forward(model, tokens):
+def _np_q8(v):
+    """Q8_0 round trip of a vector: per 32 values d = amax/127, q =
+    round-half-even(v/d) clamped to +-127, value q * fp16(d)."""
+    b = v.reshape(-1, 32)
+    amax = np.abs(b).max(axis=1, keepdims=True)
+    d = amax / 127.0
+    q = np.clip(np.rint(np.divide(b, d, out=np.zeros_like(b), where=d > 0)), -127, 127)
+    return (q * d.astype(np.float16).astype(np.float64)).reshape(-1)
+
+
+def _np_forward(model, tokens, q8_rows=0):
     """Qwen3 decoder restated in numpy float64: pre-norm GQA with QK-norm,
     NeoX RoPE, causal softmax attention, SwiGLU MLP, residuals, final norm,
-    LM head."""
+    LM head.  Positions below q8_rows quantize every matmul input to Q8_0
+    first (the batched prefill's arithmetic)."""
     cfg = model.cfg
     H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q_heads, cfg.n_kv_heads
 
@@ -67,13 +81,14 @@ def _np_forward(model, tokens):
     for pos, tok in enumerate(tokens):
         h = emb[tok].copy()
         c, s = np.cos(pos * inv), np.sin(pos * inv)
+        a8 = _np_q8 if pos < q8_rows else (lambda v: v)
 
         def rope(v):
             a, b = v[:hd // 2], v[hd // 2:]
             return np.concatenate([a * c - b * s, a * s + b * c])
 
         for li, (L, W) in enumerate(zip(model.layers, Ws)):
-            xn = rms(h, L.attn_norm)
+            xn = a8(rms(h, L.attn_norm))
             q = (W["attn_q"] @ xn).reshape(nq, hd)
             k = (W["attn_k"] @ xn).reshape(nkv, hd)
             v = (W["attn_v"] @ xn).reshape(nkv, hd)
@@ -89,10 +104,10 @@ def _np_forward(model, tokens):
                 p = np.exp(sc - sc.max())
                 p /= p.sum()
                 out[hh] = p @ V[:, g]
-            h = h + W["attn_o"] @ out.reshape(-1)
-            xn = rms(h, L.ffn_norm)
+            h = h + W["attn_o"] @ a8(out.reshape(-1))
+            xn = a8(rms(h, L.ffn_norm))
             gt, up = W["ffn_gate"] @ xn, W["ffn_up"] @ xn
-            h = h + W["ffn_down"] @ (gt / (1 + np.exp(-gt)) * up)
+            h = h + W["ffn_down"] @ a8(gt / (1 + np.exp(-gt)) * up)
         logits.append(head @ rms(h, model.output_norm))
     return np.array(logits)
 
@@ -112,3 +127,53 @@ def test_model_forward_vs_numpy(zo):
         assert err < 1e-4, (pos, err)
         assert tok == int(np.argmax(ref[pos][:cfg.vocab_real]))
     om.close()
+
+
+PREFILL_CFG = synth.ModelConfig(n_layers=2, hidden=128, ffn=256, n_q_heads=4, n_kv_heads=2, head_dim=32,
+                                vocab_padded=256, vocab_real=250, max_ctx=24)
+
+
+def test_np_q8_matches_the_oracle_quantizer(zo):
+    x = synth.activations(np.random.default_rng(5), 4096)
+    want = zo.dequant(zo.quantize_q8_0(x), 1, 4096, 8, 1)[0]
+    assert np.array_equal(_np_q8(x.astype(np.float64)).astype(np.float32), want)
+
+
+def test_prefill_q8_vs_numpy(zo):
+    model = synth.random_model(PREFILL_CFG, seed=4)
+    toks = [3, 17, 101, 5, 5, 42, 9, 200, 7]
+    n = 7  # prefill 7 tokens, then decode the last two one by one
+    ref = _np_forward(model, toks, q8_rows=n)
+    om = zo.OracleModel(model)
+    om.prefill_q8(toks[:n])
+    for pos in range(n - 1, len(toks)):
+        if pos >= n:
+            om.forward(toks[pos], pos)
+        rc, tok, mv, lg = om.lm_head()
+        assert rc == 0
+        err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
+        assert err < 1e-3, (pos, err)
+        assert tok == int(np.argmax(ref[pos][:PREFILL_CFG.vocab_real]))
+    # the fp32 token-by-token pass differs by the activation quantization only
+    fp = _np_forward(model, toks)
+    q_err = np.max(np.abs(ref[n - 1] - fp[n - 1])) / np.max(np.abs(fp[n - 1]))
+    assert 1e-4 < q_err < 5e-2, q_err
+    om.close()
+
+
+def test_prefill_q8_chunks_are_invariant(zo):
+    """Rows are independent through the GEMMs and attend only to earlier
+    positions, so prefilling in chunks (pos0 > 0) gives the same bits."""
+    model = synth.random_model(PREFILL_CFG, seed=6)
+    toks = np.array([11, 2, 99, 140, 3, 3, 77, 18, 60, 201, 5], np.uint32)
+    a = zo.OracleModel(model)
+    ha = a.prefill_q8(toks)
+    la = a.lm_head()[3]
+    b = zo.OracleModel(model)
+    b.prefill_q8(toks[:4])
+    b.prefill_q8(toks[4:9], pos0=4)
+    hb = b.prefill_q8(toks[9:], pos0=9)
+    lb = b.lm_head()[3]
+    assert np.array_equal(ha, hb) and np.array_equal(la, lb)
+    a.close()
+    b.close()

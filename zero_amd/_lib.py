@@ -36,6 +36,8 @@ ZG_ERR_MAGIC_MISMATCH = -11
 ZG_ERR_UNSUPPORTED_FORMAT = -12
 ZG_ERR_INVALID_CONTAINER = -13
 
+ZG_GEN_BATCHED_PREFILL = 1
+
 
 class zg_segment(C.Structure):
     _fields_ = [
@@ -132,6 +134,8 @@ SIGNATURES = {
     "zg_model_step": (_ST, [_P, _U32, _U32, _P, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),
     "zg_model_generate": (_ST, [_P, _P, _S, _S, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "zg_model_reset": (None, [_P]),
+    "zg_model_prefill": (_ST, [_P, _P, _S, _U32, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),
+    "zg_model_generate_ex": (_ST, [_P, _P, _S, _S, _U32, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "zg_smodel_open": (_ST, [_P, _S, C.POINTER(_P)]),
     "zg_smodel_close": (None, [_P]),
     "zg_smodel_get_info": (_ST, [_P, C.POINTER(zg_smodel_info)]),

@@ -20,6 +20,7 @@
 // a one-thread finalize kernel that feeds the argmax to the next step.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <vector>
@@ -96,6 +97,11 @@ struct AttnArgs {
   DevState* st;
   int nkv, g, nsplit, split_len;
   float eps, scale;
+  // batched prefill: query row z of the chunk sits at position pos0 + z,
+  // its (already normalised and rotated) query at q + z * row_stride and
+  // its output at out + z * row_stride
+  int pos0;
+  int row_stride;
 };
 
 constexpr int kAttnWaves = 4;
@@ -122,7 +128,12 @@ constexpr int kAttnWaves = 4;
 // The current row (written by this step) comes from the wave's registers
 // and LDS, never from the cache: the first query head of each KV head
 // stores it, concurrently with the other workgroups' reads of older rows.
-template <int HD>
+//
+// Prefill form (PF): grid (query heads, 1, chunk rows), one split; query row
+// z attends to cache rows 0..pos0+z, all of which are in the cache already
+// (qk_rope_store_kernel ran first), and its query is already normalised and
+// rotated.  Everything else is the decode kernel's arithmetic.
+template <int HD, bool PF>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
   constexpr int F4 = HD / 4;            // float4 per head row
   constexpr int LPR = 8;                // lanes per row in the score layout
@@ -137,7 +148,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   typedef float vlane_t __attribute__((ext_vector_type(VPL)));
   const int qh = blockIdx.x, sp = blockIdx.y, nq = gridDim.x;
   const int kvh = qh / a.g;
-  const int pos = (int)a.st->pos;
+  const int pos = PF ? a.pos0 + (int)blockIdx.z : (int)a.st->pos;
+  if (PF) {
+    a.q += (size_t)blockIdx.z * a.row_stride;
+    a.out += (size_t)blockIdx.z * a.row_stride;
+  }
   const int c0 = sp * a.split_len;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -148,7 +163,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     return;
   }
   const int n_t = min(a.split_len, pos + 1 - c0);
-  const bool has_pos = pos - c0 < a.split_len;  // this split holds the current row
+  const bool has_pos = !PF && pos - c0 < a.split_len;  // this split holds the current row (decode)
   const size_t rowf4 = (size_t)a.nkv * F4;
   const size_t rowv = (size_t)a.nkv * (HD / VPL);
   const int r = lane / LPR, sl = lane % LPR;
@@ -180,11 +195,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   // prologue operands, then round 0's K/V loads
   const int hl = lane % HALF;
   const float qx0 = a.q[qh * HD + hl], qx1 = a.q[qh * HD + hl + HALF];
-  const float kx0 = a.k[kvh * HD + hl], kx1 = a.k[kvh * HD + hl + HALF];
-  const float qw0 = a.q_norm[hl], qw1 = a.q_norm[hl + HALF];
-  const float kw0 = a.k_norm[hl], kw1 = a.k_norm[hl + HALF];
-  const float cs0 = a.rope_cs[hl], cs1 = a.rope_cs[hl + HALF];
-  const vlane_t vnew = reinterpret_cast<const vlane_t*>(a.v)[kvh * (HD / VPL) + lane];
+  float kx0 = 0.0f, kx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f, cs0 = 0.0f, cs1 = 0.0f;
+  vlane_t vnew = (vlane_t)(0.0f);
+  if (!PF) {
+    kx0 = a.k[kvh * HD + hl];
+    kx1 = a.k[kvh * HD + hl + HALF];
+    qw0 = a.q_norm[hl];
+    qw1 = a.q_norm[hl + HALF];
+    kw0 = a.k_norm[hl];
+    kw1 = a.k_norm[hl + HALF];
+    cs0 = a.rope_cs[hl];
+    cs1 = a.rope_cs[hl + HALF];
+    vnew = reinterpret_cast<const vlane_t*>(a.v)[kvh * (HD / VPL) + lane];
+  }
   load_round(0);
 
   // QK-norm + RoPE of one head vector held as (x0, x1) = dims (l, l + HALF)
@@ -204,8 +227,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     }
   };
   float q0, q1, k0, k1;
-  norm_rope(qx0, qx1, qw0, qw1, qrow, q0, q1);
-  norm_rope(kx0, kx1, kw0, kw1, krow, k0, k1);
+  if (PF) {
+    if (lane < HALF) {
+      qrow[lane] = qx0;
+      qrow[lane + HALF] = qx1;
+    }
+  } else {
+    norm_rope(qx0, qx1, qw0, qw1, qrow, q0, q1);
+    norm_rope(kx0, kx1, kw0, kw1, krow, k0, k1);
+  }
   if (has_pos && qh % a.g == 0 && wave == 0) {
     // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
     float* kc = a.kcache + (size_t)pos * rowf4 * 4 + kvh * HD;
@@ -234,7 +264,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
         float4 kk[CPL];
 #pragma unroll
         for (int i = 0; i < CPL; i++) kk[i] = kr[p][i];
-        if (c0 + t == pos) {
+        if (!PF && c0 + t == pos) {
 #pragma unroll
           for (int i = 0; i < CPL; i++) kk[i] = reinterpret_cast<const float4*>(krow)[sl + LPR * i];
         }
@@ -268,7 +298,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
         for (int j = 0; j < RPW; j++) {
           const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j * LPR));
-          const vlane_t v = (c0 + t0 + j == pos) ? vnew : vr[p][j];
+          const vlane_t v = (!PF && c0 + t0 + j == pos) ? vnew : vr[p][j];
           acc += ej * v;
         }
       }
@@ -317,9 +347,12 @@ __global__ void attn_merge_kernel(const float* __restrict__ part_o, const float*
   reinterpret_cast<float4*>(out + e0)[1] = x1;
 }
 
+// One row of n per workgroup (row blockIdx.x).
 __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
                                int n, float eps) {
   __shared__ float red[4];
+  x += (size_t)blockIdx.x * n;
+  out += (size_t)blockIdx.x * n;
   float ssq = 0.0f;
   for (int i = threadIdx.x; i < n; i += 256) ssq += x[i] * x[i];
   ssq = seg_sum<64>(ssq);
@@ -360,6 +393,97 @@ __global__ void advance_kernel(DevState* st, const uint32_t* prompt) {
   const uint32_t p = st->pos + 1;
   st->pos = p;
   if (p < st->n_prompt) st->token = prompt[p];
+}
+
+// ---------------------------------------------------------------------------
+// Batched prefill support (no reference counterpart: the reference runs the
+// prompt token by token, kernel/src/inference.rs:1188-1330).  Each kernel
+// does per row what the decode step does for its one token.
+// ---------------------------------------------------------------------------
+
+// Rows of token_embd for tokens[0..rows) (embed_kernel per row); block 0 also
+// clears the LM-head argmax slot.
+__global__ void embed_rows_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
+                                  const uint32_t* __restrict__ tokens, float* __restrict__ out,
+                                  uint64_t* __restrict__ best) {
+  const uint32_t tok = tokens[blockIdx.x];
+  out += (size_t)blockIdx.x * hidden;
+  const int nb = hidden / 32;
+  const int bb = (qt == Q4_0) ? 18 : 34;
+  const uint8_t* row = embd + (size_t)tok * nb * bb;
+  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
+    const uint8_t* blk = row + (e / 32) * bb;
+    const float d = half_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    const int j = e & 31;
+    float v;
+    if (qt == Q4_0) {
+      const int q = (j < 16) ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
+      v = (float)(q - 8) * d;
+    } else {
+      v = (float)(int8_t)blk[2 + j] * d;
+    }
+    out[e] = v;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) *best = 0;
+}
+
+struct QkStoreArgs {
+  float* q;              // [rows][nq*HD], normalised and rotated in place
+  const float* k;        // [rows][nkv*HD]
+  const float* v;        // [rows][nkv*HD]
+  const float* q_norm;   // [HD]
+  const float* k_norm;   // [HD]
+  const float* inv_freq; // [HD/2]
+  float* kcache;         // this layer's K rows [max_ctx][nkv*HD]
+  float* vcache;
+  int nq, nkv, pos0;
+  float eps;
+};
+
+// grid (rows, nq + nkv), one wave: QK-norm + RoPE of one head of one row at
+// position pos0 + row, with the decode step's arithmetic (the cos/sin of
+// embed_kernel, the norm_rope of attn_split_kernel).  Query heads are
+// written back in place; KV heads go to the cache row with their V.
+template <int HD>
+__global__ __launch_bounds__(64) void qk_rope_store_kernel(QkStoreArgs a) {
+  constexpr int HALF = HD / 2;
+  const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int pos = a.pos0 + row;
+  const bool isq = h < a.nq;
+  const int kvh = h - a.nq;
+  const size_t qd = (size_t)a.nq * HD, kvd = (size_t)a.nkv * HD;
+  const float* x = isq ? a.q + row * qd + (size_t)h * HD : a.k + row * kvd + (size_t)kvh * HD;
+  const float* w = isq ? a.q_norm : a.k_norm;
+  const int hl = lane % HALF;
+  const float x0 = x[hl], x1 = x[hl + HALF];
+  const float th = (float)pos * a.inv_freq[hl];
+  const float c = cosf(th), sn = sinf(th);
+  const float ssq = wave_sum(lane < HALF ? x0 * x0 + x1 * x1 : 0.0f);
+  const float rinv = 1.0f / sqrtf(ssq / (float)HD + a.eps);
+  const float xa = x0 * rinv * w[hl];
+  const float xb = x1 * rinv * w[hl + HALF];
+  const float y0 = xa * c - xb * sn;
+  const float y1 = xa * sn + xb * c;
+  float* dst = isq ? a.q + row * qd + (size_t)h * HD : a.kcache + (size_t)pos * kvd + (size_t)kvh * HD;
+  if (lane < HALF) {
+    dst[lane] = y0;
+    dst[lane + HALF] = y1;
+  }
+  if (!isq) {
+    const float* vs = a.v + row * kvd + (size_t)kvh * HD;
+    float* vd = a.vcache + (size_t)pos * kvd + (size_t)kvh * HD;
+    for (int e = lane; e < HD; e += 64) vd[e] = vs[e];
+  }
+}
+
+// out[i] = silu(g[i]) * u[i] with the decode epilogue's operand order
+// (activation.rs:115-148: g / (1 + exp(-g)), then * up).
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out,
+                              size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gv = g[i];
+  out[i] = (gv / (1.0f + expf(-gv))) * u[i];
 }
 
 }  // namespace zg
@@ -404,7 +528,18 @@ struct zg_model {
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
   hipGraphExec_t g_prefill = nullptr, g_step = nullptr;
+  // batched prefill: row buffers for chunks of up to pf_cap tokens,
+  // allocated on first use
+  size_t pf_cap = 0;
+  float *pf_x = nullptr, *pf_t = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+  float *pf_a = nullptr, *pf_g = nullptr, *pf_u = nullptr;
+  int8_t* pf_qs = nullptr;
+  uint16_t* pf_qd = nullptr;
 };
+
+// Rows per batched-prefill chunk: longer prompts run in chunks, each
+// attending to the cache rows of the chunks before it.
+constexpr size_t kPrefillChunk = 512;
 
 static zg_status model_alloc(zg_model* m, void** p, size_t bytes) {
   hipError_t e = hipMalloc(p, bytes);
@@ -470,8 +605,8 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.eps = d.rms_eps;
     aa.scale = scale;
     const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnWaves * 64);
-    if (HD == 128) hipLaunchKernelGGL(attn_split_kernel<128>, ag, ab, 0, st, aa);
-    else hipLaunchKernelGGL(attn_split_kernel<64>, ag, ab, 0, st, aa);
+    if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), ag, ab, 0, st, aa);
+    else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
     if (m->o_merge) {
       if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, d.lin_type, 4, st)))
@@ -530,6 +665,122 @@ static zg_status capture(zg_model* m, zg_status (*rec)(zg_model*, hipStream_t), 
   e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   hipGraphDestroy(g);
   return hip_check(ctx, e, "graph instantiate");
+}
+
+static zg_status prefill_alloc(zg_model* m) {
+  if (m->pf_cap) return ZG_OK;
+  const zg_model_desc& d = m->d;
+  const size_t C = d.max_ctx < kPrefillChunk ? d.max_ctx : kPrefillChunk;
+  const size_t H = d.hidden, F = d.ffn, qd = (size_t)d.n_q_heads * d.head_dim, kvd = (size_t)d.n_kv_heads * d.head_dim;
+  const size_t kmax = std::max(H, std::max(qd, F));
+  zg_status s = ZG_OK;
+  auto al = [&](auto** p, size_t bytes) {
+    if (!s) s = model_alloc(m, reinterpret_cast<void**>(p), bytes);
+  };
+  al(&m->pf_x, C * H * 4);
+  al(&m->pf_t, C * std::max(H, qd) * 4);
+  al(&m->pf_q, C * qd * 4);
+  al(&m->pf_k, C * kvd * 4);
+  al(&m->pf_v, C * kvd * 4);
+  al(&m->pf_a, C * qd * 4);
+  al(&m->pf_g, C * F * 4);
+  al(&m->pf_u, C * F * 4);
+  al(&m->pf_qs, C * kmax);
+  al(&m->pf_qd, C * (kmax / 32) * 2);
+  if (!s) m->pf_cap = C;
+  return s;
+}
+
+// One chunk of n <= pf_cap prompt rows (device tokens) at positions
+// pos0..pos0+n-1 through every layer, leaving the final hidden states in
+// pf_x.  Per layer: rmsnorm rows -> Q8_0 -> Q|K|V GEMM -> QK-norm + RoPE +
+// cache store -> causal attention -> Q8_0 -> O GEMM (+= residual) ->
+// rmsnorm rows -> Q8_0 -> gate|up GEMM -> SwiGLU -> Q8_0 -> down GEMM
+// (+= residual).
+static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, uint32_t pos0, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  zg_ctx* ctx = m->ctx;
+  const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
+  const int nq = (int)d.n_q_heads, nkv = (int)d.n_kv_heads;
+  const size_t qd = (size_t)nq * HD, kvd = (size_t)nkv * HD;
+  const uint32_t lt = d.lin_type;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(256), 0, st, m->embd, d.embd_type, H, d_tokens,
+                     m->pf_x, m->best);
+  zg_status s = hip_check(ctx, hipGetLastError(), "prefill embed launch");
+  const float scale = 1.0f / sqrtf((float)HD);
+  for (uint32_t l = 0; l < d.n_layers && !s; l++) {
+    const ZLayer& L = m->layers[l];
+    float* kc = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
+    float* vc = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.attn_norm, m->pf_t, H,
+                       d.rms_eps);
+    if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
+    if ((s = run_quant_split(ctx, m->pf_t, m->pf_qs, m->pf_qd, n, H, st))) break;
+    const GemmSegDev qkv[3] = {{L.q, m->pf_q, qd}, {L.k, m->pf_k, kvd}, {L.v, m->pf_v, kvd}};
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, qkv, 3, n, H, lt, 4, false, st))) break;
+    QkStoreArgs qa{m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm, m->inv_freq, kc, vc, nq, nkv, (int)pos0, d.rms_eps};
+    const dim3 qg((unsigned)n, (unsigned)(nq + nkv));
+    if (HD == 128) hipLaunchKernelGGL(qk_rope_store_kernel<128>, qg, dim3(64), 0, st, qa);
+    else hipLaunchKernelGGL(qk_rope_store_kernel<64>, qg, dim3(64), 0, st, qa);
+    if ((s = hip_check(ctx, hipGetLastError(), "prefill qk-rope launch"))) break;
+    AttnArgs aa{};
+    aa.q = m->pf_q;
+    aa.kcache = kc;
+    aa.vcache = vc;
+    aa.out = m->pf_a;
+    aa.part_ml = m->part_ml;
+    aa.st = m->st;
+    aa.nkv = nkv;
+    aa.g = nq / nkv;
+    aa.nsplit = 1;
+    aa.split_len = (int)d.max_ctx;
+    aa.eps = d.rms_eps;
+    aa.scale = scale;
+    aa.pos0 = (int)pos0;
+    aa.row_stride = (int)qd;
+    const dim3 ag((unsigned)nq, 1, (unsigned)n), ab(kAttnWaves * 64);
+    if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, true>), ag, ab, 0, st, aa);
+    else hipLaunchKernelGGL((attn_split_kernel<64, true>), ag, ab, 0, st, aa);
+    if ((s = hip_check(ctx, hipGetLastError(), "prefill attention launch"))) break;
+    if ((s = run_quant_split(ctx, m->pf_a, m->pf_qs, m->pf_qd, n, qd, st))) break;
+    const GemmSegDev o{L.o, m->pf_x, (size_t)H};
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &o, 1, n, qd, lt, 4, true, st))) break;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_t, H, d.rms_eps);
+    if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
+    if ((s = run_quant_split(ctx, m->pf_t, m->pf_qs, m->pf_qd, n, H, st))) break;
+    const GemmSegDev gu[2] = {{L.gate, m->pf_g, (size_t)F}, {L.up, m->pf_u, (size_t)F}};
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, gu, 2, n, H, lt, 4, false, st))) break;
+    const size_t ne = n * (size_t)F;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_g,
+                       ne);
+    if ((s = hip_check(ctx, hipGetLastError(), "prefill swiglu launch"))) break;
+    if ((s = run_quant_split(ctx, m->pf_g, m->pf_qs, m->pf_qd, n, F, st))) break;
+    const GemmSegDev dn{L.down, m->pf_x, (size_t)H};
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &dn, 1, n, F, lt, 4, true, st))) break;
+  }
+  return s;
+}
+
+// The whole prompt (already in m->prompt[off..off+n)) in chunks, then the LM
+// head on the last row and finalize: the state must hold pos = pos0 + n - 1
+// (finalize advances it past the prompt).  Returns the last chunk's row count.
+static zg_status prefill_run(zg_model* m, size_t off, size_t n, uint32_t pos0, size_t* last_rows) {
+  const zg_model_desc& d = m->d;
+  hipStream_t st = m->ctx->stream;
+  zg_status s = prefill_alloc(m);
+  size_t rows = 0;
+  for (size_t c = 0; c < n && !s; c += rows) {
+    rows = std::min(m->pf_cap, n - c);
+    s = prefill_chunk(m, m->prompt + off + c, rows, pos0 + (uint32_t)c, st);
+  }
+  if (s) return s;
+  s = run_linear(m->ctx, m->pf_x + (rows - 1) * d.hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
+                 d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM, m->out_norm,
+                 d.rms_eps, st, kGemvStream);
+  if (s) return s;
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
+  *last_rows = rows;
+  return hip_check(m->ctx, hipGetLastError(), "finalize launch");
 }
 
 extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_model** out) {
@@ -688,8 +939,42 @@ extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, fl
   return lm_head_status(ctx, h.best, m->d.vocab_real, next_token, max_logit);
 }
 
+extern "C" zg_status zg_model_prefill(zg_model* m, const uint32_t* tokens, size_t n, uint32_t pos0, float* hidden_out,
+                                      uint32_t* next_token, float* max_logit) {
+  if (!m) return ZG_ERR_INVALID_ARG;
+  zg_ctx* ctx = m->ctx;
+  if (!tokens || n == 0) return set_error(ctx, ZG_ERR_INVALID_ARG, "prefill: no tokens");
+  if ((size_t)pos0 + n > m->d.max_ctx)
+    return set_error(ctx, ZG_ERR_CONTEXT_FULL, "prefill: positions %u..%zu exceed max_ctx %u", pos0, pos0 + n - 1,
+                     m->d.max_ctx);
+  for (size_t i = 0; i < n; i++)
+    if (tokens[i] >= m->d.vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "prefill: token %u out of range", tokens[i]);
+  hipSetDevice(ctx->device);
+  zg_status s = hip_check(ctx, hipMemcpyAsync(m->prompt, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream),
+                          "prompt upload");
+  if (!s) s = set_state(m, 0, pos0 + (uint32_t)n - 1, 0, 0);
+  size_t rows = 0;
+  if (!s) s = prefill_run(m, 0, n, pos0, &rows);
+  if (s) return s;
+  zg::DevState h{};
+  if ((s = hip_check(ctx, hipMemcpyAsync(&h, m->st, sizeof h, hipMemcpyDeviceToHost, ctx->stream), "state download")))
+    return s;
+  if (hidden_out && (s = hip_check(ctx, hipMemcpyAsync(hidden_out, m->pf_x + (rows - 1) * m->d.hidden, m->d.hidden * 4,
+                                                      hipMemcpyDeviceToHost, ctx->stream), "download")))
+    return s;
+  if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
+  if ((s = state_status(m, h))) return s;
+  return lm_head_status(ctx, h.best, m->d.vocab_real, next_token, max_logit);
+}
+
 extern "C" zg_status zg_model_generate(zg_model* m, const uint32_t* prompt, size_t n_prompt, size_t n_gen,
                                        uint32_t* out_tokens, double* prefill_seconds, double* gen_seconds) {
+  return zg_model_generate_ex(m, prompt, n_prompt, n_gen, 0, out_tokens, prefill_seconds, gen_seconds);
+}
+
+extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, size_t n_prompt, size_t n_gen,
+                                          uint32_t flags, uint32_t* out_tokens, double* prefill_seconds,
+                                          double* gen_seconds) {
   if (!m) return ZG_ERR_INVALID_ARG;
   zg_ctx* ctx = m->ctx;
   if (!prompt || n_prompt == 0 || n_gen == 0 || !out_tokens) return set_error(ctx, ZG_ERR_INVALID_ARG, "generate: bad args");
@@ -702,14 +987,24 @@ extern "C" zg_status zg_model_generate(zg_model* m, const uint32_t* prompt, size
   zg_status s = hip_check(ctx, hipMemcpyAsync(m->prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice, ctx->stream),
                           "prompt upload");
   if (s) return s;
-  if ((s = set_state(m, prompt[0], 0, (uint32_t)n_prompt, (uint32_t)n_gen))) return s;
+  const bool batched = (flags & ZG_GEN_BATCHED_PREFILL) != 0;
+  if (batched && (s = prefill_alloc(m))) return s;
+  if ((s = set_state(m, prompt[0], batched ? (uint32_t)n_prompt - 1 : 0, (uint32_t)n_prompt, (uint32_t)n_gen)))
+    return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t0 = std::chrono::steady_clock::now();
-  // prefill: prompt tokens 0..n-2 through the layers; the last one also
-  // through the LM head, producing generated token 0
-  for (size_t i = 0; i + 1 < n_prompt; i++)
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_prefill, ctx->stream), "graph launch"))) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
+  if (batched) {
+    // the whole prompt as Q8_0-activation GEMMs, then the LM head on its
+    // last row, producing generated token 0
+    size_t rows = 0;
+    if ((s = prefill_run(m, 0, n_prompt, 0, &rows))) return s;
+  } else {
+    // prompt tokens 0..n-2 through the layers one by one; the last one also
+    // through the LM head, producing generated token 0
+    for (size_t i = 0; i + 1 < n_prompt; i++)
+      if ((s = hip_check(ctx, hipGraphLaunch(m->g_prefill, ctx->stream), "graph launch"))) return s;
+    if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
+  }
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t1 = std::chrono::steady_clock::now();
   // greedy decode: each generated token goes back through the layers

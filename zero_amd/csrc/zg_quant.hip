@@ -134,12 +134,22 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(QuantArgs a) {
 // ---------------------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// Up to three weight matrices that share the activations (Q|K|V, gate|up)
+// in one launch: the output columns are the concatenation of the segments,
+// seg_end[s] is the end column of segment s, and every 64-column tile lies
+// in one segment (segment widths are multiples of 64 when there are
+// several).  Segment s writes y[s] as [m][width of s].
+constexpr int kGemmSegs = 3;
+
 struct GemmArgs {
   const int8_t* xq;    // [m][k]
   const uint16_t* xd;  // [m][k/32]
-  const uint8_t* w;    // weights, Q4_0/Q8_0, plain or X4
-  float* y;            // [m][n]
-  int m, n, k;
+  const uint8_t* w[kGemmSegs];  // weights, Q4_0/Q8_0, plain or X4
+  float* y[kGemmSegs];          // [m][n_s]
+  int seg_end[kGemmSegs];
+  int nseg;
+  int accumulate;  // 1: y += result (residual add), 0: y = result
+  int m, n, k;     // n: total columns
 };
 
 constexpr int kBN = 64, kBK = 4;  // tile columns; kBK blocks of 32 per stage (tile rows BM: 64 or 32)
@@ -158,8 +168,8 @@ struct GemmStage {
 };
 
 template <uint32_t WT, int IL, int BM>
-__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const GemmArgs& a, int m0, int n0, int b0,
-                                                int tid) {
+__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const GemmArgs& a, const uint8_t* w, int ns,
+                                                int m0, int n0, int b0, int tid) {
   const int nb = a.k / 32;
 #pragma unroll
   for (int i = 0; i < BM / 32; i++) {
@@ -180,12 +190,12 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const Gemm
 #pragma unroll
     for (int i = 0; i < QW; i++) S.q[i] = 0;
     S.wd = 0;
-    if (gn < a.n && kb < nb) {
+    if (gn < ns && kb < nb) {
       const uint8_t* dp;
       const uint8_t* qp;
       if (IL == 4) {
         const size_t gb = (WT == Q4_0) ? 72 : 136;
-        const uint8_t* g = a.w + (size_t)(gn >> 2) * nb * gb + (size_t)kb * gb;
+        const uint8_t* g = w + (size_t)(gn >> 2) * nb * gb + (size_t)kb * gb;
         dp = g + 2 * (gn & 3);
         qp = g + 8 + (gn & 3) * ((WT == Q4_0) ? 16 : 32);
 #pragma unroll
@@ -196,7 +206,7 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const Gemm
         }
       } else {
         const size_t bb = (WT == Q4_0) ? 18 : 34;
-        dp = a.w + ((size_t)gn * nb + kb) * bb;
+        dp = w + ((size_t)gn * nb + kb) * bb;
         qp = dp + 2;
 #pragma unroll
         for (int i = 0; i < QW; i++)
@@ -256,7 +266,14 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float Ad[2][kBK * BM];   // [kk][row]
   __shared__ __attribute__((aligned(16))) float Bd[2][kBK * kBN];  // [kk][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * BM;
+  // this tile's segment (uniform): its weights, output and local columns
+  const int nt0 = blockIdx.x * kBN;
+  const int sg = (a.nseg > 1 && nt0 >= a.seg_end[0]) ? ((a.nseg > 2 && nt0 >= a.seg_end[1]) ? 2 : 1) : 0;
+  const int base = sg == 0 ? 0 : a.seg_end[sg - 1];
+  const int ns = a.seg_end[sg] - base, n0 = nt0 - base;
+  const uint8_t* w = a.w[sg];
+  float* y = a.y[sg];
   const int nb = a.k / 32;
   const int nst = (nb + kBK - 1) / kBK;
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
@@ -270,12 +287,12 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
   GemmStage<WT, BM> S;
-  gemm_stage_load<WT, IL, BM>(S, a, m0, n0, 0, tid);
+  gemm_stage_load<WT, IL, BM>(S, a, w, ns, m0, n0, 0, tid);
   gemm_stage_store<WT, BM>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
   for (int st = 0; st < nst; st++) {
     const int buf = st & 1;
-    if (st + 1 < nst) gemm_stage_load<WT, IL, BM>(S, a, m0, n0, (st + 1) * kBK, tid);
+    if (st + 1 < nst) gemm_stage_load<WT, IL, BM>(S, a, w, ns, m0, n0, (st + 1) * kBK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
 #pragma unroll(BM == 64 ? 1 : kBK)
@@ -319,7 +336,10 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
       for (int r = 0; r < 4; r++) {
         const int gm = m0 + wm + 16 * i + rq + r;
         const int gn = n0 + wn + 16 * j + r16;
-        if (gm < a.m && gn < a.n) a.y[(size_t)gm * a.n + gn] = acc[i][j][r];
+        if (gm < a.m && gn < ns) {
+          float* o = y + (size_t)gm * ns + gn;
+          *o = a.accumulate ? *o + acc[i][j][r] : acc[i][j][r];
+        }
       }
 }
 
@@ -343,6 +363,11 @@ static zg_status launch_quant(zg_ctx* ctx, const float* x, uint8_t* blocks, int8
   const size_t n = rows * (k / 32);
   hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, qstream(ctx, stream), a);
   return hip_check(ctx, hipGetLastError(), "quantize launch");
+}
+
+zg_status zg::run_quant_split(zg_ctx* ctx, const float* x, int8_t* qs, uint16_t* d, size_t rows, size_t k,
+                             hipStream_t st) {
+  return launch_quant(ctx, x, nullptr, qs, d, rows, k, st);
 }
 
 extern "C" zg_status zg_quantize_q8_0_dev(zg_ctx* ctx, const float* d_x, void* d_q, size_t rows, size_t k,
@@ -376,21 +401,40 @@ static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM>), grid, dim3(256), 0, st, a);
 }
 
-extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const uint16_t* d_d, const void* d_w,
-                                      float* d_y, size_t m, size_t n, size_t k, uint32_t w_type, uint32_t interleave,
-                                      void* stream) {
-  if (!ctx) return ZG_ERR_INVALID_ARG;
-  if (!d_qs || !d_d || !d_w || !d_y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: null pointer");
+// Checks and launches one Q8_0-activation GEMM over 1..3 weight segments.
+zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const GemmSegDev* segs, int nseg, size_t m,
+                       size_t k, uint32_t w_type, uint32_t interleave, bool accumulate, hipStream_t st) {
+  if (!qs || !xd || !segs || nseg < 1 || nseg > kGemmSegs) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: bad arguments");
   if (w_type != ZG_Q4_0 && w_type != ZG_Q8_0) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "gemm: weights must be Q4_0/Q8_0");
-  zg_status s = check_shape(ctx, w_type, interleave, k, n);
-  if (s) return s;
+  if (reinterpret_cast<uintptr_t>(qs) & 15) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: activations misaligned");
+  GemmArgs a{};
+  a.xq = qs;
+  a.xd = xd;
+  size_t n = 0;
+  for (int i = 0; i < nseg; i++) {
+    if (!segs[i].w || !segs[i].y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: null pointer");
+    zg_status s = check_shape(ctx, w_type, interleave, k, segs[i].n);
+    if (s) return s;
+    if (nseg > 1 && segs[i].n % kBN) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: segment width %% %d", kBN);
+    if (interleave == 4 && (reinterpret_cast<uintptr_t>(segs[i].w) & 7))
+      return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: weights misaligned");
+    n += segs[i].n;
+    a.w[i] = segs[i].w;
+    a.y[i] = segs[i].y;
+    a.seg_end[i] = (int)n;
+  }
   if (m == 0) return ZG_OK;
   if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: shape too large");
-  if (reinterpret_cast<uintptr_t>(d_qs) & 15) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: activations misaligned");
-  if (interleave == 4 && (reinterpret_cast<uintptr_t>(d_w) & 7))
-    return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: weights misaligned");
-  GemmArgs a{d_qs, d_d, static_cast<const uint8_t*>(d_w), d_y, (int)m, (int)n, (int)k};
-  hipStream_t st = qstream(ctx, stream);
+  for (int i = nseg; i < kGemmSegs; i++) {
+    a.w[i] = a.w[0];
+    a.y[i] = a.y[0];
+    a.seg_end[i] = (int)n;
+  }
+  a.nseg = nseg;
+  a.accumulate = accumulate ? 1 : 0;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
   // 64-row tiles unless they would not give every CU three workgroups
   const size_t tiles64 = ((n + kBN - 1) / kBN) * ((m + 63) / 64);
   if (tiles64 >= (size_t)3 * gemm_cu_count()) {
@@ -405,4 +449,13 @@ extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const ui
     else launch_gemm<Q8_0, 1, 32>(a, st);
   }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
+}
+
+extern "C" zg_status zg_gemm_q8act_dev(zg_ctx* ctx, const int8_t* d_qs, const uint16_t* d_d, const void* d_w,
+                                      float* d_y, size_t m, size_t n, size_t k, uint32_t w_type, uint32_t interleave,
+                                      void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_qs || !d_d || !d_w || !d_y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: null pointer");
+  const GemmSegDev seg{static_cast<const uint8_t*>(d_w), d_y, n};
+  return run_gemm(ctx, d_qs, d_d, &seg, 1, m, k, w_type, interleave, false, qstream(ctx, stream));
 }

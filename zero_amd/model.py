@@ -90,14 +90,29 @@ class GpuModel:
         self._raise(rc, int(tok.value))
         return int(tok.value), float(mv.value), hid, lg
 
-    def generate(self, prompt: np.ndarray, n_gen: int):
-        """Prefill `prompt` token by token, then n_gen greedy tokens.
+    def prefill(self, tokens: np.ndarray, pos0: int = 0, want_hidden: bool = False):
+        """Batched prefill (zg_model_prefill): tokens at positions
+        pos0..pos0+n-1 through Q8_0-activation GEMMs, then the LM head on the
+        last row.  Returns (next_token, max_logit, last hidden or None)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        hid = np.empty(self.cfg.hidden, np.float32) if want_hidden else None
+        tok = C.c_uint32()
+        mv = C.c_float()
+        rc = self.ctx.lib.zg_model_prefill(self.h, t.ctypes.data, t.size, pos0,
+                                           hid.ctypes.data if hid is not None else None, C.byref(tok), C.byref(mv))
+        self._raise(rc, int(tok.value))
+        return int(tok.value), float(mv.value), hid
+
+    def generate(self, prompt: np.ndarray, n_gen: int, batched_prefill: bool = False):
+        """Prefill `prompt` (token by token, or batched with Q8_0-activation
+        GEMMs), then n_gen greedy tokens.
         Returns (tokens, prefill_seconds, generation_seconds)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(n_gen, np.uint32)
         t_pre = C.c_double()
         t_gen = C.c_double()
-        rc = self.ctx.lib.zg_model_generate(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data, C.byref(t_pre),
-                                            C.byref(t_gen))
+        flags = _lib.ZG_GEN_BATCHED_PREFILL if batched_prefill else 0
+        rc = self.ctx.lib.zg_model_generate_ex(self.h, p.ctypes.data, p.size, n_gen, flags, out.ctypes.data,
+                                               C.byref(t_pre), C.byref(t_gen))
         self._raise(rc, -1)
         return out, float(t_pre.value), float(t_gen.value)
