@@ -7,7 +7,8 @@ Cache cannot hold the set).  A step is one GEMV launch; steps are replayed
 from a HIP graph so that host launch cost is not timed.
 
 Also reported: batch-1 greedy decode tok/s of a random-init
-Qwen3-1.7B-shaped model (128-token prompt, then 256 tokens), and the CPU
+Qwen3-1.7B-shaped model (128-token prompt, then 256 tokens), the same prompt
+through the batched int8-MFMA prefill (Q8_0 activations), and the CPU
 baseline (the oracle's AVX-512 restatement of the reference kernels on the
 host cores, pinned threads, same rotating working set).
 
@@ -226,13 +227,20 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
     gm.generate(prompt, 8)  # warm-up (first graph launches)
     toks, t_pre, t_gen = gm.generate(prompt, n_gen)
     tok_s = (n_gen - 1) / t_gen
+    # the same prompt through the batched int8-MFMA prefill (Q8_0 activations)
+    gm.generate(prompt, 8, batched_prefill=True)  # warm-up (row buffers, first launches)
+    toks_b, t_pre_b, t_gen_b = gm.generate(prompt, n_gen, batched_prefill=True)
+    agree = int(np.argmin(np.concatenate([toks_b == toks, [False]])))
     # mean algorithmic bytes per decode step over contexts t = n_prompt+1 .. n_prompt+n_gen-1
     kv_per_pos = 2 * cfg.n_layers * cfg.kv_dim * 4
     norms = (2 * cfg.n_layers * cfg.hidden + 2 * cfg.n_layers * cfg.head_dim + cfg.hidden) * 4
     ctxs = np.arange(n_prompt + 1, n_prompt + n_gen)
     per_tok = cfg.weight_bytes_per_token() + norms + float(np.mean(ctxs)) * kv_per_pos + kv_per_pos
     gm.close()
-    return {"tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "prefill_tok_s": n_prompt / t_pre, "n_prompt": n_prompt,
+    return {"tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "prefill_tok_s": n_prompt / t_pre,
+            "batched_prefill": {"prefill_tok_s": n_prompt / t_pre_b, "prefill_ms": t_pre_b * 1e3,
+                                "decode_tok_s": (n_gen - 1) / t_gen_b, "tokens_equal_to_token_by_token": agree},
+            "n_prompt": n_prompt,
             "n_gen": n_gen, "bytes_per_token": int(per_tok), "gbs": per_tok * tok_s / 1e9,
             "first_tokens": [int(t) for t in toks[:8]], "model": model, "prompt": prompt}
 
@@ -341,8 +349,13 @@ def main():
     if not args.no_decode:
         dec = bench_decode(ctx)
         log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['gbs']:.0f} GB/s effective)")
+        bp = dec["batched_prefill"]
+        log(f"batched prefill: {bp['prefill_ms']:.2f} ms for {dec['n_prompt']} tokens "
+            f"({bp['prefill_tok_s']:.0f} tok/s; token by token {dec['prefill_tok_s']:.0f} tok/s)")
         out["decode"] = {"tok_s": round(dec["tok_s"], 2), "ms_per_token": dec["ms_per_token"],
                          "prefill_tok_s": round(dec["prefill_tok_s"], 2),
+                         "batched_prefill": {k: (round(v, 2) if isinstance(v, float) else v)
+                                             for k, v in dec["batched_prefill"].items()},
                          "workload": "random-init Qwen3-1.7B shape, Q4_0X4 linears, Q8_0X4 LM head, "
                                      f"{dec['n_prompt']}-token prompt then {dec['n_gen']} greedy tokens",
                          "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,

@@ -171,4 +171,88 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
   return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - idx);
 }
 
+// binary64 -> binary16, round to nearest even, for finite |v| <= 65504
+// (the packer clamps to that range first, silicatepack.py:854-861).
+__device__ __forceinline__ uint32_t f64_to_f16_rne(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t sign = (uint32_t)(u >> 48) & 0x8000u;
+  const uint64_t a = u & 0x7FFFFFFFFFFFFFFFull;
+  if (a == 0) return sign;
+  const int e = (int)(a >> 52) - 1023;
+  const uint64_t mant = (a & ((1ull << 52) - 1)) | (1ull << 52);
+  if (e < -14) {
+    // subnormal half: count units of 2^-24
+    const int s = 28 - e;
+    if (s >= 64) return sign;
+    const uint64_t q = mant >> s;
+    const uint64_t rem = mant & ((1ull << s) - 1);
+    const uint64_t half = 1ull << (s - 1);
+    const uint64_t r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+    return sign | (uint32_t)r;  // r == 1024 encodes the smallest normal
+  }
+  uint64_t q = mant >> 42;
+  const uint64_t rem = mant & ((1ull << 42) - 1);
+  const uint64_t half = 1ull << 41;
+  if (rem > half || (rem == half && (q & 1))) q++;
+  int eb = e + 15;
+  if (q == 2048) {
+    q = 1024;
+    eb++;
+  }
+  return sign | ((uint32_t)eb << 10) | ((uint32_t)q & 0x3FFu);
+}
+
+// The packer's Q8_0 block encoder (tools/silicatepack.py:893-907) on 32
+// values: amax, d = amax/127, 1/d and v/d in double as Python computes them,
+// round-half-even, clamp to +-127, d stored as the RNE binary16 of the
+// double d.  A block holding a non-finite value (the packer raises
+// ValueError there, :877-887) gets q = 0 and d = NaN (0x7E00) so that it
+// cannot pass unnoticed.  Returns the fp16 bits of d.
+__device__ __forceinline__ uint32_t q8_0_encode(const float v[32], int8_t q[32]) {
+  bool finite = true;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    finite = finite && isfinite(v[i]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  if (!finite || amax == 0.0f) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) q[i] = 0;
+    return finite ? 0u : 0x7E00u;
+  }
+  const double dd = (double)amax / 127.0;
+  const double inv = 1.0 / dd;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    double r = rint((double)v[i] * inv);
+    r = fmin(127.0, fmax(-127.0, r));
+    q[i] = (int8_t)(int)r;
+  }
+  return f64_to_f16_rne(fmin(dd, 65504.0));
+}
+
+// The same encoder with one value per lane: each aligned 32-lane segment of
+// the wave is one block (every lane of the segment must be active).  Returns
+// this lane's q; *dbits gets the block's fp16 d bits.
+__device__ __forceinline__ int8_t q8_0_encode_lane(float v, uint32_t* dbits) {
+  float amax = fabsf(v);
+  float bad = isfinite(v) ? 0.0f : 1.0f;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    bad += __shfl_xor(bad, o, 64);
+  }
+  if (bad != 0.0f || amax == 0.0f) {
+    *dbits = bad != 0.0f ? 0x7E00u : 0u;
+    return 0;
+  }
+  const double dd = (double)amax / 127.0;
+  const double inv = 1.0 / dd;
+  double r = rint((double)v * inv);
+  r = fmin(127.0, fmax(-127.0, r));
+  *dbits = f64_to_f16_rne(fmin(dd, 65504.0));
+  return (int8_t)(int)r;
+}
+
 }  // namespace zg

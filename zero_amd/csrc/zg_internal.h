@@ -79,7 +79,6 @@ zg_status run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int
 zg_status stage_in(zg_ctx* ctx, const void* src, size_t bytes, DevBuf& dst);
 zg_status lm_head_status(zg_ctx* ctx, uint64_t packed, size_t vocab_real, uint32_t* token, float* max_val);
 
-zg_status run_quant_split(zg_ctx* ctx, const float* x, int8_t* qs, uint16_t* d, size_t rows, size_t k, hipStream_t st);
 zg_status run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const GemmSegDev* segs, int nseg, size_t m,
                    size_t k, uint32_t w_type, uint32_t interleave, bool accumulate, hipStream_t st);
 

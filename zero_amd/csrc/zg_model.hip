@@ -98,10 +98,13 @@ struct AttnArgs {
   int nkv, g, nsplit, split_len;
   float eps, scale;
   // batched prefill: query row z of the chunk sits at position pos0 + z,
-  // its (already normalised and rotated) query at q + z * row_stride and
-  // its output at out + z * row_stride
+  // its (already normalised and rotated) query at q + z * row_stride; its
+  // output is Q8_0-encoded into qs + z * row_stride (int8) and
+  // qsd + z * row_stride / 32 (fp16 d bits)
   int pos0;
   int row_stride;
+  int8_t* qs;
+  uint16_t* qsd;
 };
 
 constexpr int kAttnWaves = 4;
@@ -132,7 +135,9 @@ constexpr int kAttnWaves = 4;
 // Prefill form (PF): grid (query heads, 1, chunk rows), one split; query row
 // z attends to cache rows 0..pos0+z, all of which are in the cache already
 // (qk_rope_store_kernel ran first), and its query is already normalised and
-// rotated.  Everything else is the decode kernel's arithmetic.
+// rotated.  The output row goes out Q8_0-encoded for the O GEMM (each 32-lane
+// segment of the output waves is one block).  Everything else is the decode
+// kernel's arithmetic.
 template <int HD, bool PF>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
   constexpr int F4 = HD / 4;            // float4 per head row
@@ -151,7 +156,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int pos = PF ? a.pos0 + (int)blockIdx.z : (int)a.st->pos;
   if (PF) {
     a.q += (size_t)blockIdx.z * a.row_stride;
-    a.out += (size_t)blockIdx.z * a.row_stride;
+    a.qs += (size_t)blockIdx.z * a.row_stride;
+    a.qsd += (size_t)blockIdx.z * a.row_stride / 32;
   }
   const int c0 = sp * a.split_len;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -324,7 +330,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       o = fmaf(f, wo[w][tid], o);
     }
     if (tid == 0 && !isfinite(M)) atomicOr(&a.st->err, 4u);
-    if (a.nsplit == 1) {
+    if (PF) {
+      uint32_t dbits;
+      const int8_t qv = q8_0_encode_lane(o * (1.0f / L), &dbits);
+      a.qs[qh * HD + tid] = qv;
+      if ((tid & 31) == 0) a.qsd[(qh * HD + tid) / 32] = (uint16_t)dbits;
+    } else if (a.nsplit == 1) {
       a.out[qh * HD + tid] = o * (1.0f / L);
     } else {
       a.out[((size_t)sp * nq + qh) * HD + tid] = o;
@@ -476,14 +487,76 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(QkStoreArgs a) {
   }
 }
 
-// out[i] = silu(g[i]) * u[i] with the decode epilogue's operand order
-// (activation.rs:115-148: g / (1 + exp(-g)), then * up).
-__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out,
-                              size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float gv = g[i];
-  out[i] = (gv / (1.0f + expf(-gv))) * u[i];
+// One row of n per workgroup: rmsnorm (rmsnorm_kernel's arithmetic) and the
+// Q8_0 encoding of the normalised row, 32 values per thread at a time.
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            int8_t* __restrict__ qs, uint16_t* __restrict__ qd, int n,
+                                                            float eps) {
+  __shared__ float red[4];
+  const size_t row = blockIdx.x;
+  x += row * n;
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) ssq += x[i] * x[i];
+  ssq = seg_sum<64>(ssq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ssq;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rinv = 1.0f / sqrtf(tot / (float)n + eps);
+  for (int b = threadIdx.x; b < n / 32; b += 256) {
+    const float4* x4 = reinterpret_cast<const float4*>(x + b * 32);
+    const float4* w4 = reinterpret_cast<const float4*>(w + b * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 xv = x4[i], wv = w4[i];
+      v[4 * i] = xv.x * rinv * wv.x;
+      v[4 * i + 1] = xv.y * rinv * wv.y;
+      v[4 * i + 2] = xv.z * rinv * wv.z;
+      v[4 * i + 3] = xv.w * rinv * wv.w;
+    }
+    int8_t q[32];
+    const uint32_t dbits = q8_0_encode(v, q);
+    u32x4* dst = reinterpret_cast<u32x4*>(qs + row * n + b * 32);
+    uint32_t wq[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      wq[i] = (uint32_t)(uint8_t)q[4 * i] | ((uint32_t)(uint8_t)q[4 * i + 1] << 8) |
+              ((uint32_t)(uint8_t)q[4 * i + 2] << 16) | ((uint32_t)(uint8_t)q[4 * i + 3] << 24);
+    dst[0] = u32x4{wq[0], wq[1], wq[2], wq[3]};
+    dst[1] = u32x4{wq[4], wq[5], wq[6], wq[7]};
+    qd[row * (n / 32) + b] = (uint16_t)dbits;
+  }
+}
+
+// One row of n per workgroup: silu(g) * u with the decode epilogue's operand
+// order (activation.rs:115-148: g / (1 + exp(-g)), then * up), Q8_0-encoded.
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                           int8_t* __restrict__ qs, uint16_t* __restrict__ qd, int n) {
+  const size_t row = blockIdx.x;
+  for (int b = threadIdx.x; b < n / 32; b += 256) {
+    const float4* g4 = reinterpret_cast<const float4*>(g + row * n + b * 32);
+    const float4* u4 = reinterpret_cast<const float4*>(u + row * n + b * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 gv = g4[i], uv = u4[i];
+      v[4 * i] = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
+      v[4 * i + 1] = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
+      v[4 * i + 2] = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
+      v[4 * i + 3] = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+    }
+    int8_t q[32];
+    const uint32_t dbits = q8_0_encode(v, q);
+    u32x4* dst = reinterpret_cast<u32x4*>(qs + row * n + b * 32);
+    uint32_t wq[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      wq[i] = (uint32_t)(uint8_t)q[4 * i] | ((uint32_t)(uint8_t)q[4 * i + 1] << 8) |
+              ((uint32_t)(uint8_t)q[4 * i + 2] << 16) | ((uint32_t)(uint8_t)q[4 * i + 3] << 24);
+    dst[0] = u32x4{wq[0], wq[1], wq[2], wq[3]};
+    dst[1] = u32x4{wq[4], wq[5], wq[6], wq[7]};
+    qd[row * (n / 32) + b] = (uint16_t)dbits;
+  }
 }
 
 }  // namespace zg
@@ -531,8 +604,8 @@ struct zg_model {
   // batched prefill: row buffers for chunks of up to pf_cap tokens,
   // allocated on first use
   size_t pf_cap = 0;
-  float *pf_x = nullptr, *pf_t = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
-  float *pf_a = nullptr, *pf_g = nullptr, *pf_u = nullptr;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+  float *pf_g = nullptr, *pf_u = nullptr;
   int8_t* pf_qs = nullptr;
   uint16_t* pf_qd = nullptr;
 };
@@ -678,11 +751,9 @@ static zg_status prefill_alloc(zg_model* m) {
     if (!s) s = model_alloc(m, reinterpret_cast<void**>(p), bytes);
   };
   al(&m->pf_x, C * H * 4);
-  al(&m->pf_t, C * std::max(H, qd) * 4);
   al(&m->pf_q, C * qd * 4);
   al(&m->pf_k, C * kvd * 4);
   al(&m->pf_v, C * kvd * 4);
-  al(&m->pf_a, C * qd * 4);
   al(&m->pf_g, C * F * 4);
   al(&m->pf_u, C * F * 4);
   al(&m->pf_qs, C * kmax);
@@ -693,10 +764,11 @@ static zg_status prefill_alloc(zg_model* m) {
 
 // One chunk of n <= pf_cap prompt rows (device tokens) at positions
 // pos0..pos0+n-1 through every layer, leaving the final hidden states in
-// pf_x.  Per layer: rmsnorm rows -> Q8_0 -> Q|K|V GEMM -> QK-norm + RoPE +
-// cache store -> causal attention -> Q8_0 -> O GEMM (+= residual) ->
-// rmsnorm rows -> Q8_0 -> gate|up GEMM -> SwiGLU -> Q8_0 -> down GEMM
-// (+= residual).
+// pf_x.  Per layer: rmsnorm + Q8_0 rows -> Q|K|V GEMM -> QK-norm + RoPE +
+// cache store -> causal attention + Q8_0 -> O GEMM (+= residual) ->
+// rmsnorm + Q8_0 rows -> gate|up GEMM -> SwiGLU + Q8_0 -> down GEMM
+// (+= residual).  Each fused encode gives the bits the separate quantizer
+// would give for the same fp32 row.
 static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, uint32_t pos0, hipStream_t st) {
   const zg_model_desc& d = m->d;
   zg_ctx* ctx = m->ctx;
@@ -712,10 +784,9 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     const ZLayer& L = m->layers[l];
     float* kc = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
     float* vc = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.attn_norm, m->pf_t, H,
-                       d.rms_eps);
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.attn_norm, m->pf_qs,
+                       m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
-    if ((s = run_quant_split(ctx, m->pf_t, m->pf_qs, m->pf_qd, n, H, st))) break;
     const GemmSegDev qkv[3] = {{L.q, m->pf_q, qd}, {L.k, m->pf_k, kvd}, {L.v, m->pf_v, kvd}};
     if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, qkv, 3, n, H, lt, 4, false, st))) break;
     QkStoreArgs qa{m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm, m->inv_freq, kc, vc, nq, nkv, (int)pos0, d.rms_eps};
@@ -727,7 +798,8 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     aa.q = m->pf_q;
     aa.kcache = kc;
     aa.vcache = vc;
-    aa.out = m->pf_a;
+    aa.qs = m->pf_qs;
+    aa.qsd = m->pf_qd;
     aa.part_ml = m->part_ml;
     aa.st = m->st;
     aa.nkv = nkv;
@@ -742,19 +814,16 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, true>), ag, ab, 0, st, aa);
     else hipLaunchKernelGGL((attn_split_kernel<64, true>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill attention launch"))) break;
-    if ((s = run_quant_split(ctx, m->pf_a, m->pf_qs, m->pf_qd, n, qd, st))) break;
     const GemmSegDev o{L.o, m->pf_x, (size_t)H};
     if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &o, 1, n, qd, lt, 4, true, st))) break;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_t, H, d.rms_eps);
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_qs,
+                       m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
-    if ((s = run_quant_split(ctx, m->pf_t, m->pf_qs, m->pf_qd, n, H, st))) break;
     const GemmSegDev gu[2] = {{L.gate, m->pf_g, (size_t)F}, {L.up, m->pf_u, (size_t)F}};
     if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, gu, 2, n, H, lt, 4, false, st))) break;
-    const size_t ne = n * (size_t)F;
-    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_g,
-                       ne);
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_qs, m->pf_qd,
+                       F);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill swiglu launch"))) break;
-    if ((s = run_quant_split(ctx, m->pf_g, m->pf_qs, m->pf_qd, n, F, st))) break;
     const GemmSegDev dn{L.down, m->pf_x, (size_t)H};
     if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &dn, 1, n, F, lt, 4, true, st))) break;
   }

@@ -18,37 +18,6 @@ using namespace zg;
 
 namespace zg {
 
-// binary64 -> binary16, round to nearest even, for finite |v| <= 65504
-// (the packer clamps to that range first, silicatepack.py:854-861).
-__device__ __forceinline__ uint32_t f64_to_f16_rne(double v) {
-  const uint64_t u = (uint64_t)__double_as_longlong(v);
-  const uint32_t sign = (uint32_t)(u >> 48) & 0x8000u;
-  const uint64_t a = u & 0x7FFFFFFFFFFFFFFFull;
-  if (a == 0) return sign;
-  const int e = (int)(a >> 52) - 1023;
-  const uint64_t mant = (a & ((1ull << 52) - 1)) | (1ull << 52);
-  if (e < -14) {
-    // subnormal half: count units of 2^-24
-    const int s = 28 - e;
-    if (s >= 64) return sign;
-    const uint64_t q = mant >> s;
-    const uint64_t rem = mant & ((1ull << s) - 1);
-    const uint64_t half = 1ull << (s - 1);
-    const uint64_t r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
-    return sign | (uint32_t)r;  // r == 1024 encodes the smallest normal
-  }
-  uint64_t q = mant >> 42;
-  const uint64_t rem = mant & ((1ull << 42) - 1);
-  const uint64_t half = 1ull << 41;
-  if (rem > half || (rem == half && (q & 1))) q++;
-  int eb = e + 15;
-  if (q == 2048) {
-    q = 1024;
-    eb++;
-  }
-  return sign | ((uint32_t)eb << 10) | ((uint32_t)q & 0x3FFu);
-}
-
 struct QuantArgs {
   const float* x;   // [rows][k]
   uint8_t* blocks;  // optional: [rows][k/32] x 34-byte Q8_0 blocks
@@ -75,33 +44,8 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(QuantArgs a) {
     v[4 * i + 2] = f.z;
     v[4 * i + 3] = f.w;
   }
-  bool finite = true;
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    finite = finite && isfinite(v[i]);
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
-  uint32_t dbits = 0;
   int8_t q[32];
-  if (!finite) {
-    dbits = 0x7E00u;
-#pragma unroll
-    for (int i = 0; i < 32; i++) q[i] = 0;
-  } else if (amax == 0.0f) {
-#pragma unroll
-    for (int i = 0; i < 32; i++) q[i] = 0;
-  } else {
-    const double dd = (double)amax / 127.0;
-    const double inv = 1.0 / dd;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      double r = rint((double)v[i] * inv);
-      r = fmin(127.0, fmax(-127.0, r));
-      q[i] = (int8_t)(int)r;
-    }
-    dbits = f64_to_f16_rne(fmin(dd, 65504.0));
-  }
+  const uint32_t dbits = q8_0_encode(v, q);
   if (a.qs) {
     uint32_t w[8];
 #pragma unroll
@@ -152,44 +96,52 @@ struct GemmArgs {
   int m, n, k;     // n: total columns
 };
 
-constexpr int kBN = 64, kBK = 4;  // tile columns; kBK blocks of 32 per stage (tile rows BM: 64 or 32)
-constexpr int kRow = kBK * 32 + 16;         // LDS row stride in bytes (padded, 16-B aligned)
+constexpr int kBN = 64;  // tile columns (tile rows BM: 64 or 32)
+// LDS row stride in bytes for BK blocks of 32 per stage (padded, 16-B aligned)
+template <int BK>
+constexpr int lds_row() { return BK * 32 + 16; }
 
 // One stage's global operands held in registers between the load and the
 // LDS store (so that the next stage's loads fly while the current stage is
-// multiplied): BM/32 16-byte activation chunks and one activation scale, one
-// weight block row (raw quants + scale) per thread.
-template <uint32_t WT, int BM>
+// multiplied).  Per thread: NA 16-byte activation chunks, ND activation
+// scales, NW weight block rows (raw quants + scale).
+template <uint32_t WT, int BM, int BK>
 struct GemmStage {
-  u32x4 a[BM / 32];
-  uint32_t ad;
-  uint32_t q[WT == Q4_0 ? 4 : 8];
-  uint32_t wd;
+  static constexpr int NA = BM * BK * 2 / 256;
+  static constexpr int ND = (BM * BK + 255) / 256;
+  static constexpr int NW = kBN * BK / 256;
+  static constexpr int QW = WT == Q4_0 ? 4 : 8;
+  u32x4 a[NA];
+  uint32_t ad[ND];
+  uint32_t q[NW][QW];
+  uint32_t wd[NW];
 };
 
-template <uint32_t WT, int IL, int BM>
-__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const GemmArgs& a, const uint8_t* w, int ns,
+template <uint32_t WT, int IL, int BM, int BK>
+__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const GemmArgs& a, const uint8_t* w, int ns,
                                                 int m0, int n0, int b0, int tid) {
+  using St = GemmStage<WT, BM, BK>;
   const int nb = a.k / 32;
 #pragma unroll
-  for (int i = 0; i < BM / 32; i++) {
-    const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
+  for (int i = 0; i < St::NA; i++) {
+    const int c = tid + 256 * i, row = c / (BK * 2), ch = c % (BK * 2);
     const int gm = m0 + row, kb = b0 + ch / 2;
     S.a[i] = u32x4{0, 0, 0, 0};
     if (gm < a.m && kb < nb) S.a[i] = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
   }
-  {
-    const int row = tid / kBK, kk = tid % kBK;
-    const int gm = m0 + row, kb = b0 + kk;
-    S.ad = (row < BM && gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
-  }
-  {
-    const int row = tid / kBK, kk = tid % kBK;
-    const int gn = n0 + row, kb = b0 + kk;
-    constexpr int QW = WT == Q4_0 ? 4 : 8;
 #pragma unroll
-    for (int i = 0; i < QW; i++) S.q[i] = 0;
-    S.wd = 0;
+  for (int i = 0; i < St::ND; i++) {
+    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    const int gm = m0 + row, kb = b0 + kk;
+    S.ad[i] = (row < BM && gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
+  }
+#pragma unroll
+  for (int i = 0; i < St::NW; i++) {
+    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    const int gn = n0 + row, kb = b0 + kk;
+#pragma unroll
+    for (int j = 0; j < St::QW; j++) S.q[i][j] = 0;
+    S.wd[i] = 0;
     if (gn < ns && kb < nb) {
       const uint8_t* dp;
       const uint8_t* qp;
@@ -199,72 +151,87 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM>& S, const Gemm
         dp = g + 2 * (gn & 3);
         qp = g + 8 + (gn & 3) * ((WT == Q4_0) ? 16 : 32);
 #pragma unroll
-        for (int i = 0; i < QW / 2; i++) {
-          const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * i);
-          S.q[2 * i] = v.x;
-          S.q[2 * i + 1] = v.y;
+        for (int j = 0; j < St::QW / 2; j++) {
+          const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * j);
+          S.q[i][2 * j] = v.x;
+          S.q[i][2 * j + 1] = v.y;
         }
       } else {
         const size_t bb = (WT == Q4_0) ? 18 : 34;
         dp = w + ((size_t)gn * nb + kb) * bb;
         qp = dp + 2;
 #pragma unroll
-        for (int i = 0; i < QW; i++)
-          S.q[i] = (uint32_t)qp[4 * i] | ((uint32_t)qp[4 * i + 1] << 8) | ((uint32_t)qp[4 * i + 2] << 16) |
-                   ((uint32_t)qp[4 * i + 3] << 24);
+        for (int j = 0; j < St::QW; j++)
+          S.q[i][j] = (uint32_t)qp[4 * j] | ((uint32_t)qp[4 * j + 1] << 8) | ((uint32_t)qp[4 * j + 2] << 16) |
+                      ((uint32_t)qp[4 * j + 3] << 24);
       }
-      S.wd = (uint32_t)dp[0] | ((uint32_t)dp[1] << 8);
+      S.wd[i] = (uint32_t)dp[0] | ((uint32_t)dp[1] << 8);
     }
   }
 }
 
-template <uint32_t WT, int BM>
-__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM>& S, int8_t* As, int8_t* Bs, float* Ad,
+template <uint32_t WT, int BM, int BK>
+__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S, int8_t* As, int8_t* Bs, float* Ad,
                                                  float* Bd, int tid) {
+  using St = GemmStage<WT, BM, BK>;
+  constexpr int R = lds_row<BK>();
 #pragma unroll
-  for (int i = 0; i < BM / 32; i++) {
-    const int c = tid + 256 * i, row = c / (kBK * 2), ch = c % (kBK * 2);
-    *reinterpret_cast<u32x4*>(As + row * kRow + ch * 16) = S.a[i];
+  for (int i = 0; i < St::NA; i++) {
+    const int c = tid + 256 * i, row = c / (BK * 2), ch = c % (BK * 2);
+    *reinterpret_cast<u32x4*>(As + row * R + ch * 16) = S.a[i];
   }
-  const int row = tid / kBK, kk = tid % kBK;
-  if (row < BM) Ad[kk * BM + row] = half_bits_to_f32(S.ad);
-  uint32_t q[8];
-  if (WT == Q4_0) {
-    // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
-    // bytes is (n + 0x78) ^ 0x80
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t lo = S.q[i] & 0x0F0F0F0Fu;         // elements 4i..4i+3
-      const uint32_t hi = (S.q[i] >> 4) & 0x0F0F0F0Fu;  // elements 16+4i..
-      q[i] = ((lo + 0x78787878u) ^ 0x80808080u);
-      q[4 + i] = ((hi + 0x78787878u) ^ 0x80808080u);
+  for (int i = 0; i < St::ND; i++) {
+    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    if (row < BM) Ad[kk * BM + row] = half_bits_to_f32(S.ad[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < St::NW; i++) {
+    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    uint32_t q[8];
+    if (WT == Q4_0) {
+      // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
+      // bytes is (n + 0x78) ^ 0x80
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t lo = S.q[i][j] & 0x0F0F0F0Fu;         // elements 4j..4j+3
+        const uint32_t hi = (S.q[i][j] >> 4) & 0x0F0F0F0Fu;  // elements 16+4j..
+        q[j] = ((lo + 0x78787878u) ^ 0x80808080u);
+        q[4 + j] = ((hi + 0x78787878u) ^ 0x80808080u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) q[j] = S.q[i][St::QW == 8 ? j : 0];
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = S.q[i];
+    u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * R + kk * 32);
+    dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+    dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+    Bd[kk * kBN + row] = half_bits_to_f32(S.wd[i]);
   }
-  u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * kRow + kk * 32);
-  dst[0] = u32x4{q[0], q[1], q[2], q[3]};
-  dst[1] = u32x4{q[4], q[5], q[6], q[7]};
-  Bd[kk * kBN + row] = half_bits_to_f32(S.wd);
 }
 
 // Workgroup tile BM (m) x 64 (n), 4 waves of BM/2 x 32 (BM/32 x 2 MFMA
-// tiles): BM = 64, or 32 when the 64-row tiles would leave CUs idle.  kBK
-// blocks (128 K) per stage, double-buffered in LDS; the next stage's global
-// loads are issued before the current stage is multiplied.  Per 32-K block:
-// v_mfma_i32_16x16x32_i8 gives the block's integer dots, and every output
-// adds dX*dW*isum with one fma, blocks in ascending order.  The 64-row
-// tile's block loop is not unrolled: that keeps it near 100 VGPRs, four
-// workgroups per CU (M=512 x 6144: all 768 tiles resident at once; 34.7 vs
-// 41-43 us unrolled); the 32-row tile is unrolled (48.7 vs 54.3 us).
-template <uint32_t WT, int IL, int BM>
+// tiles), BK blocks (BK * 32 of K) per stage, double-buffered in LDS; the
+// next stage's global loads are issued before the current stage is
+// multiplied.  Per 32-K block: v_mfma_i32_16x16x32_i8 gives the block's
+// integer dots, and every output adds dX*dW*isum with one fma, blocks in
+// ascending order.  Shapes:
+//   BM 64, BK 4   large M: ~100 VGPRs, four workgroups per CU; the block
+//                 loop is not unrolled (M=512 x 6144: all 768 tiles
+//                 resident at once; 34.7 vs 41-43 us unrolled)
+//   BM 32, BK 8   few tiles per CU (small M, or narrow N): each stage is
+//                 one memory round trip, so 256 K per stage halves the trips
+//                 of a 4-block stage; 58 KB of LDS keeps two workgroups per
+//                 CU (M=512 x 2048x6144: 48.1 us, vs 50.9 with 4 blocks and
+//                 77.4 with 16 at one workgroup per CU).
+template <uint32_t WT, int IL, int BM, int BK>
 __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   constexpr int MI = BM / 32;  // 16-row MFMA tiles per wave
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * kRow];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][kBN * kRow];
-  __shared__ __attribute__((aligned(16))) float Ad[2][kBK * BM];   // [kk][row]
-  __shared__ __attribute__((aligned(16))) float Bd[2][kBK * kBN];  // [kk][col]
+  constexpr int R = lds_row<BK>();
+  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * R];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][kBN * R];
+  __shared__ __attribute__((aligned(16))) float Ad[2][BK * BM];   // [kk][row]
+  __shared__ __attribute__((aligned(16))) float Bd[2][BK * kBN];  // [kk][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.y * BM;
   // this tile's segment (uniform): its weights, output and local columns
@@ -275,7 +242,7 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   const uint8_t* w = a.w[sg];
   float* y = a.y[sg];
   const int nb = a.k / 32;
-  const int nst = (nb + kBK - 1) / kBK;
+  const int nst = (nb + BK - 1) / BK;
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
   const int r16 = lane & 15, kq = (lane >> 4) * 8, rq = (lane >> 4) * 4;
   float acc[MI][2][4];
@@ -286,28 +253,30 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
-  GemmStage<WT, BM> S;
-  gemm_stage_load<WT, IL, BM>(S, a, w, ns, m0, n0, 0, tid);
-  gemm_stage_store<WT, BM>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
+  GemmStage<WT, BM, BK> S;
+  gemm_stage_load<WT, IL, BM, BK>(S, a, w, ns, m0, n0, 0, tid);
+  gemm_stage_store<WT, BM, BK>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
   for (int st = 0; st < nst; st++) {
     const int buf = st & 1;
-    if (st + 1 < nst) gemm_stage_load<WT, IL, BM>(S, a, w, ns, m0, n0, (st + 1) * kBK, tid);
+    if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
-#pragma unroll(BM == 64 ? 1 : kBK)
-    for (int kk = 0; kk < kBK; kk++) {
+    // blocks past k in the last stage hold zero quants: they add 0 * scale
+    const int kend = min(BK, nb - st * BK);
+#pragma unroll(BM == 64 ? 1 : 4)
+    for (int kk = 0; kk < kend; kk++) {
       long av[MI], bv[2];
       float4 da[MI];
       float db[2];
 #pragma unroll
       for (int i = 0; i < MI; i++) {
-        av[i] = *reinterpret_cast<const long*>(A + (wm + 16 * i + r16) * kRow + kk * 32 + kq);
+        av[i] = *reinterpret_cast<const long*>(A + (wm + 16 * i + r16) * R + kk * 32 + kq);
         da[i] = *reinterpret_cast<const float4*>(&Ad[buf][kk * BM + wm + 16 * i + rq]);
       }
 #pragma unroll
       for (int j = 0; j < 2; j++) {
-        bv[j] = *reinterpret_cast<const long*>(B + (wn + 16 * j + r16) * kRow + kk * 32 + kq);
+        bv[j] = *reinterpret_cast<const long*>(B + (wn + 16 * j + r16) * R + kk * 32 + kq);
         db[j] = Bd[buf][kk * kBN + wn + 16 * j + r16];
       }
       v4i c[MI][2];
@@ -324,7 +293,7 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
           for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(__fmul_rn(dai[r], db[j]), (float)c[i][j][r], acc[i][j][r]);
       }
     }
-    if (st + 1 < nst) gemm_stage_store<WT, BM>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
+    if (st + 1 < nst) gemm_stage_store<WT, BM, BK>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
     __syncthreads();
   }
   // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16
@@ -365,11 +334,6 @@ static zg_status launch_quant(zg_ctx* ctx, const float* x, uint8_t* blocks, int8
   return hip_check(ctx, hipGetLastError(), "quantize launch");
 }
 
-zg_status zg::run_quant_split(zg_ctx* ctx, const float* x, int8_t* qs, uint16_t* d, size_t rows, size_t k,
-                             hipStream_t st) {
-  return launch_quant(ctx, x, nullptr, qs, d, rows, k, st);
-}
-
 extern "C" zg_status zg_quantize_q8_0_dev(zg_ctx* ctx, const float* d_x, void* d_q, size_t rows, size_t k,
                                          void* stream) {
   if (!ctx) return ZG_ERR_INVALID_ARG;
@@ -395,10 +359,15 @@ static int gemm_cu_count() {
   return n;
 }
 
-template <uint32_t WT, int IL, int BM>
+#ifndef ZG_GEMM_SMALL_BK
+#define ZG_GEMM_SMALL_BK 8
+#endif
+constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row tile
+
+template <uint32_t WT, int IL, int BM, int BK>
 static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK>), grid, dim3(256), 0, st, a);
 }
 
 // Checks and launches one Q8_0-activation GEMM over 1..3 weight segments.
@@ -438,15 +407,15 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
   // 64-row tiles unless they would not give every CU three workgroups
   const size_t tiles64 = ((n + kBN - 1) / kBN) * ((m + 63) / 64);
   if (tiles64 >= (size_t)3 * gemm_cu_count()) {
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 64>(a, st);
-    else launch_gemm<Q8_0, 1, 64>(a, st);
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64, 4>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64, 4>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 64, 4>(a, st);
+    else launch_gemm<Q8_0, 1, 64, 4>(a, st);
   } else {
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 32>(a, st);
-    else launch_gemm<Q8_0, 1, 32>(a, st);
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32, kSmallBK>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32, kSmallBK>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 32, kSmallBK>(a, st);
+    else launch_gemm<Q8_0, 1, 32, kSmallBK>(a, st);
   }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
 }
