@@ -117,7 +117,8 @@ def _row(name, per_ms, nbytes, n, copies, **extra):
 def bench_rows(ctx, steps: int):
     """The other hot-path workloads, each timed like the headline GEMV:
     fused Q|K|V Q8_0X4, LM head Q8_0X4 + argmax, Q4_K and Q6_K GEMVs at
-    Llama-3-8B FFN shapes, and the M=512 int8-MFMA prefill GEMM."""
+    Llama-3-8B FFN shapes (Q4_K also through the Q8_K integer path), and the
+    M=512 int8-MFMA prefill GEMM."""
     import numpy as np
     import torch
 
@@ -177,6 +178,18 @@ def bench_rows(ctx, steps: int):
         per, n, _ = _graph_time(kq, c, max(40, steps // 10), 20)
         key = "q4_k_14336x4096" if qt == synth.Q4K else "q6_k_4096x14336"
         out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
+        if qt == synth.Q4K:
+            # the same weights through the Q8_K integer path: quantize_row_q8k
+            # of x, then the integer GEMV (two launches per call)
+            q8 = torch.empty(k // 256 * 292, dtype=torch.uint8, device="cuda")
+
+            def kq8(i, st, wd=wd, xk=xk, yk=yk, rows=rows, k=k, q8=q8):
+                ctx.quantize_q8k_dev(xk, q8, k, stream=st)
+                ctx.linear_q4k_q8k_dev(q8, wd[i], yk, k, rows, stream=st)
+
+            per8, n8, _ = _graph_time(kq8, c, max(40, steps // 10), 20)
+            out["q4_k_q8_k_14336x4096"] = _row("Q4_K x Q8_K integer path 14336x4096 (quantize + GEMV)", per8,
+                                               wh.nbytes + 4 * k + k // 256 * 292 + 4 * rows, n8, c)
         del wd
 
     # prefill GEMM, M = 512, both FFN shapes, Q4_0X4 weights, Q8_0 activations

@@ -241,6 +241,25 @@ zg_status zg_model_generate_ex(zg_model *m, const uint32_t *prompt, size_t n_pro
                                double *gen_seconds);
 
 /* ------------------------------------------------------------------ */
+/* Q4_K x Q8_K integer path (kernel/src/arch/x86_64/math/vnni.rs,       */
+/* behind the reference's "vnni-acceleration" feature).  Q8_K blocks    */
+/* are the reference's 292-byte form: f32 d, 256 int8, 16 int16 sums.   */
+/* ------------------------------------------------------------------ */
+
+/* quantize_row_q8k (vnni.rs:78-170) of n device floats (n % 256 == 0) into
+ * n / 256 blocks at d_q8k (4-byte aligned); bit-exact. */
+zg_status zg_quantize_q8k_dev(zg_ctx *ctx, const float *d_x, void *d_q8k, size_t n, void *stream);
+/* linear_q4k_vnni_range (vnni.rs:258-476) over all out_dim rows: d_w is
+ * plain Q4_K (144-byte superblocks), in_dim % 256 == 0, in_dim <= 32768. */
+zg_status zg_linear_q4k_q8k_dev(zg_ctx *ctx, const void *d_q8k, const void *d_w, float *d_out,
+                                size_t in_dim, size_t out_dim, void *stream);
+/* linear_q4k_vnni_dispatch (kernel/src/inference_avx512.rs:519-547): host
+ * x, registered Q4_K w, host out; quantizes x to Q8_K, then the integer
+ * GEMV.  Synchronous. */
+zg_status zg_linear_q4k_vnni(zg_ctx *ctx, const float *x, const void *w, float *out, size_t in_dim,
+                             size_t out_dim);
+
+/* ------------------------------------------------------------------ */
 /* .smodel native container (SilicatePack SILM + SIDX).                 */
 /* ------------------------------------------------------------------ */
 

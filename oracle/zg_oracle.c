@@ -996,6 +996,115 @@ int zo_gemm_q8act(const uint8_t *xq, const uint8_t *w, float *y, size_t m, size_
 }
 
 /* ------------------------------------------------------------------ */
+/* Q4_K x Q8_K integer path (kernel/src/arch/x86_64/math/vnni.rs,       */
+/* feature "vnni-acceleration"): the ggml Q8_K activation quantizer and  */
+/* the integer Q4_K dot.                                                 */
+/* ------------------------------------------------------------------ */
+
+/* quantize_row_q8k (vnni.rs:78-170): per 256 values, the first value of
+ * largest magnitude (max_val), iscale = -127 / max_val in f32, q =
+ * rintf(v * iscale) clamped to [-128, 127], d = 1 / iscale, 16 int16 sums
+ * of 16 q each.  Block: f32 d, 256 int8, 16 int16 (292 bytes). */
+void zo_quantize_row_q8k(const float *x, uint8_t *out, size_t n) {
+    for (size_t b = 0; b < n / 256; b++) {
+        const float *v = x + b * 256;
+        uint8_t *o = out + b * ZO_Q8K_BYTES;
+        float amax = 0.0f, max_val = 0.0f;
+        for (int j = 0; j < 256; j++) {
+            float av = fabsf(v[j]);
+            if (av > amax) {
+                amax = av;
+                max_val = v[j];
+            }
+        }
+        if (amax == 0.0f) {
+            memset(o, 0, ZO_Q8K_BYTES);
+            continue;
+        }
+        float iscale = -127.0f / max_val;
+        int32_t bsums[16] = {0};
+        for (int j = 0; j < 256; j++) {
+            float t = rintf(v[j] * iscale);
+            /* Rust's `as i32`: NaN -> 0, saturating */
+            int32_t q = isnan(t) ? 0 : (t >= 2147483647.0f ? INT32_MAX : (t <= -2147483648.0f ? INT32_MIN : (int32_t)t));
+            if (q > 127) q = 127;
+            if (q < -128) q = -128;
+            o[4 + j] = (uint8_t)(int8_t)q;
+            bsums[j / 16] += q;
+        }
+        float d = 1.0f / iscale;
+        memcpy(o, &d, 4);
+        for (int k = 0; k < 16; k++) {
+            int32_t c = bsums[k] < -32768 ? -32768 : (bsums[k] > 32767 ? 32767 : bsums[k]);
+            int16_t s16 = (int16_t)c;
+            memcpy(o + 260 + 2 * k, &s16, 2);
+        }
+    }
+}
+
+/* unpack_mins_and_scales (vnni.rs:176-205): the 12 scale bytes of a Q4_K
+ * superblock as 8 six-bit scales then 8 six-bit mins (ggml's utmp form). */
+void zo_unpack_mins_and_scales(const uint8_t *s12, uint8_t *out16) {
+    uint32_t u[4];
+    memcpy(u, s12, 12);
+    u[3] = ((u[2] >> 4) & 0x0f0f0f0fu) | (((u[1] >> 6) & 0x03030303u) << 4);
+    uint32_t uaux = u[1] & 0x3f3f3f3fu;
+    u[1] = (u[2] & 0x0f0f0f0fu) | (((u[0] >> 6) & 0x03030303u) << 4);
+    u[2] = uaux;
+    u[0] &= 0x3f3f3f3fu;
+    memcpy(out16, u, 16);
+}
+
+/* linear_q4k_vnni_range (vnni.rs:258-476): per row, per superblock b in
+ * order, int_sum = sum_g sc_g * sum_{i in g} nibble_i * q8_i (exact),
+ * min_sum = sum_g m_g * (bsum[2g] + bsum[2g+1]);
+ * sumf_dot += (d_w * d_q8) * (float)int_sum;
+ * sumf_min += (dmin_w * d_q8) * (float)min_sum;  out = sumf_dot - sumf_min.
+ * Sub-block g covers elements 32g..32g+31: low nibbles of qs[32(g/2)..+32]
+ * for even g, high nibbles for odd g. */
+int zo_linear_q4k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, size_t in_dim, size_t start,
+                            size_t end) {
+    if (in_dim % 256) return -1;
+    size_t nb = in_dim / 256;
+    for (size_t r = start; r < end; r++) {
+        float sumf_dot = 0.0f, sumf_min = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t *wb = w + (r * nb + b) * 144;
+            const uint8_t *xb = q8k + b * ZO_Q8K_BYTES;
+            float dw = rd_fp16(wb), dminw = rd_fp16(wb + 2);
+            uint8_t sm[16];
+            zo_unpack_mins_and_scales(wb + 4, sm);
+            const uint8_t *qs = wb + 16;
+            const int8_t *q8 = (const int8_t *)(xb + 4);
+            float dq8;
+            memcpy(&dq8, xb, 4);
+            int64_t int_sum = 0;
+            for (int g = 0; g < 8; g++) {
+                int32_t sub = 0;
+                for (int i = 0; i < 32; i++) {
+                    uint8_t byte = qs[(g / 2) * 32 + i];
+                    int nib = (g & 1) ? (byte >> 4) : (byte & 15);
+                    sub += nib * (int32_t)q8[g * 32 + i];
+                }
+                int_sum += (int64_t)sub * (int64_t)sm[g];
+            }
+            int32_t min_sum = 0;
+            for (int g = 0; g < 8; g++) {
+                int16_t lo, hi;
+                memcpy(&lo, xb + 260 + 4 * g, 2);
+                memcpy(&hi, xb + 262 + 4 * g, 2);
+                min_sum += (int32_t)sm[8 + g] * ((int32_t)lo + (int32_t)hi);
+            }
+            float dc = dw * dq8, dmc = dminw * dq8;
+            sumf_dot = sumf_dot + dc * (float)int_sum;
+            sumf_min = sumf_min + dmc * (float)min_sum;
+        }
+        out[r] = sumf_dot - sumf_min;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* Full forward pass.  forward_single_token_avx512                      */
 /* (kernel/src/inference_avx512.rs:1826-1987) with the attention block   */
 /* gqa_attention_single_token_avx512 (:1527-1810) and the LM head        */

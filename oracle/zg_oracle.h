@@ -114,6 +114,15 @@ void zo_silu_mul(const float *gate, const float *up, float *out, size_t n);
 int zo_gemm_q8act(const uint8_t *xq, const uint8_t *w, float *y, size_t m, size_t n,
                   size_t k, int w_type, int interleave);
 
+/* ---- Q4_K x Q8_K integer path (vnni.rs, feature "vnni-acceleration"):
+ *      quantize_row_q8k :78-170 (292-byte blocks), unpack_mins_and_scales
+ *      :176-205, linear_q4k_vnni_range :258-476 ---- */
+#define ZO_Q8K_BYTES 292
+void zo_quantize_row_q8k(const float *x, uint8_t *out, size_t n);
+void zo_unpack_mins_and_scales(const uint8_t *s12, uint8_t *out16);
+int zo_linear_q4k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, size_t in_dim, size_t start,
+                            size_t end);
+
 /* ---- full single-token forward pass for a Qwen3-shaped model
  *      (inference_avx512.rs:1826-1987 order; scalar crate ops for norms,
  *      RoPE, softmax, SiLU) ---- */

@@ -75,6 +75,9 @@ _SIG = {
     "zo_model_forward": (_I, [_P, _U32, _S, _P]),
     "zo_model_lm_head": (_I, [_P, _P, C.POINTER(_U32), C.POINTER(_F)]),
     "zo_model_prefill_q8": (_I, [_P, _P, _S, _S, _P]),
+    "zo_quantize_row_q8k": (None, [_P, _P, _S]),
+    "zo_unpack_mins_and_scales": (None, [_P, _P]),
+    "zo_linear_q4k_q8k_range": (_I, [_P, _P, _P, _S, _S, _S]),
 }
 
 _lib = None
@@ -165,6 +168,32 @@ def quantize_q4_0(x) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.size // 32 * 18, np.uint8)
     load().zo_quantize_q4_0_row(_p(x), _p(out), x.size)
+    return out
+
+
+Q8K_BYTES = 292
+
+
+def quantize_q8k(x) -> np.ndarray:
+    """quantize_row_q8k: 292-byte blocks (f32 d, 256 int8, 16 int16 sums)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size // 256 * Q8K_BYTES, np.uint8)
+    load().zo_quantize_row_q8k(_p(x), _p(out), x.size)
+    return out
+
+
+def unpack_mins_and_scales(s12) -> np.ndarray:
+    s = np.ascontiguousarray(s12, np.uint8)
+    out = np.empty(16, np.uint8)
+    load().zo_unpack_mins_and_scales(_p(s), _p(out))
+    return out
+
+
+def linear_q4k_q8k(q8k, w, in_dim, out_dim, start=0, end=None) -> np.ndarray:
+    """linear_q4k_vnni_range over rows [start, end)."""
+    end = out_dim if end is None else end
+    out = np.zeros(out_dim, np.float32)
+    assert load().zo_linear_q4k_q8k_range(_p(q8k), _p(w), _p(out), in_dim, start, end) == 0
     return out
 
 

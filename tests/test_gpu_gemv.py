@@ -110,6 +110,26 @@ GEMV_CASES = [
     (Q8_0, 4, 32768, 512),   # tall Q8_0X4 (LM-head strip path): one strip, four waves per strip
     (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
     (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
+    # DeepSeek2 / Kimi K2 projections through linear_dispatch_avx512
+    # (kernel/src/inference_avx512.rs:2101-2825): MLA kv_a_mqa, q_a, q_b,
+    # the kv_b decompressions, o_proj and the MoE expert FFN, Q4_0 as GGUF
+    # rows (plain) and as .smodel X4 (Kimi K2 dims: hidden 7168, q_lora
+    # 1536, kv_lora 512 + rope 64, 64 heads x (128 + 64), expert FFN 2048)
+    (Q4_0, 4, 576, 7168),
+    (Q4_0, 1, 576, 7168),
+    (Q4_0, 4, 1536, 7168),
+    (Q4_0, 4, 12288, 1536),
+    (Q4_0, 1, 12288, 1536),
+    (Q4_0, 4, 8192, 512),
+    (Q4_0, 4, 7168, 8192),
+    (Q4_0, 1, 7168, 8192),
+    (Q4_0, 4, 2048, 7168),
+    (Q4_0, 4, 7168, 2048),
+    (Q4_0, 1, 2048, 7168),
+    # DeepSeek-V2-Lite: expert FFN 1408 (44 blocks: an in_dim not a multiple of 64 blocks)
+    (Q4_0, 4, 1408, 2048),
+    (Q4_0, 4, 2048, 1408),
+    (Q4_0, 1, 2048, 1408),
 ]
 
 

@@ -9,6 +9,8 @@ path replaces, re-expressed in Python over the C ABI:
 * ``lm_head_argmax``          kernel/src/inference_avx512.rs:1200-1270
 * ``register`` / ``group_of`` / ``rebase`` / ``clear``
                               kernel/src/weight_layout.rs:57-149
+* ``linear_q4k_vnni``         kernel/src/inference_avx512.rs:519-547
+                              (feature "vnni-acceleration")
 
 Weights are numpy uint8 arrays (the ``&[u8]`` block bytes); activations and
 outputs are float32 arrays.  Every call runs on the GPU; there is no CPU
@@ -240,6 +242,26 @@ class Context:
     def gemm_q8act_dev(self, qs, d, w, y, m, n, k, w_type, interleave, stream=None):
         self.check(self.lib.zg_gemm_q8act_dev(self.h, _ptr(qs), _ptr(d), _ptr(w), _ptr(y), m, n, k, int(w_type),
                                               int(interleave), stream))
+
+    # ---- Q4_K x Q8_K integer path (kernel/src/arch/x86_64/math/vnni.rs) ----
+    def linear_q4k_vnni(self, x: np.ndarray, w_blocks: np.ndarray, out: np.ndarray, in_dim: int,
+                        out_dim: int) -> None:
+        """linear_q4k_vnni_dispatch (inference_avx512.rs:519-547): x is
+        quantized to Q8_K and dotted with the registered Q4_K rows in
+        integers; out = W . x up to the activation quantization."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if out.dtype != np.float32 or not out.flags.c_contiguous or out.size < out_dim or x.size < in_dim:
+            raise ValueError("x/out must be float32 and sized in_dim/out_dim")
+        self.check(self.lib.zg_linear_q4k_vnni(self.h, x.ctypes.data, _ptr(w_blocks), out.ctypes.data, in_dim,
+                                               out_dim))
+
+    def quantize_q8k_dev(self, x, q8k, n, stream=None):
+        """quantize_row_q8k (vnni.rs:78-170) into 292-byte blocks."""
+        self.check(self.lib.zg_quantize_q8k_dev(self.h, _ptr(x), _ptr(q8k), n, stream))
+
+    def linear_q4k_q8k_dev(self, q8k, w, out, in_dim, out_dim, stream=None):
+        """linear_q4k_vnni_range (vnni.rs:258-476) over all rows."""
+        self.check(self.lib.zg_linear_q4k_q8k_dev(self.h, _ptr(q8k), _ptr(w), _ptr(out), in_dim, out_dim, stream))
 
     @staticmethod
     def argmax_unpack(packed: int):
