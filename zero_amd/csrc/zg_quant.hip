@@ -219,11 +219,12 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S,
 //   BM 64, BK 4   large M: ~100 VGPRs, four workgroups per CU; the block
 //                 loop is not unrolled (M=512 x 6144: all 768 tiles
 //                 resident at once; 34.7 vs 41-43 us unrolled)
-//   BM 32, BK 8   few tiles per CU (small M, or narrow N): each stage is
-//                 one memory round trip, so 256 K per stage halves the trips
-//                 of a 4-block stage; 58 KB of LDS keeps two workgroups per
-//                 CU (M=512 x 2048x6144: 48.1 us, vs 50.9 with 4 blocks and
-//                 77.4 with 16 at one workgroup per CU).
+//   BM 32, BK 4   few 64-row tiles per CU (M=512 x 2048x6144: 46.5 us)
+//   BM 32, BK 8   at most one 32-row tile per CU (the batched prefill's 128
+//                 rows): each stage is one exposed memory round trip, so
+//                 256 K per stage halves the trips (128-token prefill 3.72
+//                 ms vs 4.24 with 4-block stages; 16-block stages, at one
+//                 workgroup per CU, were slower still)
 template <uint32_t WT, int IL, int BM, int BK>
 __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   constexpr int MI = BM / 32;  // 16-row MFMA tiles per wave
@@ -262,10 +263,11 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
     if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
-    // blocks past k in the last stage hold zero quants: they add 0 * scale
-    const int kend = min(BK, nb - st * BK);
-#pragma unroll(BM == 64 ? 1 : 4)
-    for (int kk = 0; kk < kend; kk++) {
+    // blocks past k in the last stage hold zero quants and scales: they add
+    // fma(0, 0, acc) = acc
+    constexpr int UNR = BM == 64 ? 1 : 4;
+#pragma unroll UNR
+    for (int kk = 0; kk < BK; kk++) {
       long av[MI], bv[2];
       float4 da[MI];
       float db[2];
@@ -411,11 +413,18 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
     else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64, 4>(a, st);
     else if (interleave == 4) launch_gemm<Q8_0, 4, 64, 4>(a, st);
     else launch_gemm<Q8_0, 1, 64, 4>(a, st);
-  } else {
+  } else if (((n + kBN - 1) / kBN) * ((m + 31) / 32) <= (size_t)gemm_cu_count()) {
+    // at most one 32-row tile per CU: each stage's round trip is exposed,
+    // so fewer, larger stages
     if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32, kSmallBK>(a, st);
     else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32, kSmallBK>(a, st);
     else if (interleave == 4) launch_gemm<Q8_0, 4, 32, kSmallBK>(a, st);
     else launch_gemm<Q8_0, 1, 32, kSmallBK>(a, st);
+  } else {
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32, 4>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32, 4>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 32, 4>(a, st);
+    else launch_gemm<Q8_0, 1, 32, 4>(a, st);
   }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
 }
