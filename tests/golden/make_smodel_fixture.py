@@ -1,4 +1,4 @@
-"""Write tests/golden/tiny_qwen3_v2.smodel with the reference packer.
+"""Write tests/golden/tiny_qwen3_v2.smodel (and the _q8 variant) with the reference packer.
 
 Builds a tiny seeded Qwen3-shaped Hugging Face checkpoint (config.json and
 one fp32 SafeTensors file: 2 layers, hidden 128, 2 query heads and 1 KV head
@@ -12,9 +12,10 @@ which emits a `.smodel`-v2 native container: Q4_0X4 layer linears, Q8_0
 token embedding, Q8_0X4 output.weight, F32 norms (silicatepack.py:799-852,
 943-1059, 1097-1161).  The packer's own `inspect` record of that file
 (header and manifest, silicatepack.py:1754-1780) is written next to it as
-tiny_qwen3_v2.inspect.json.
+tiny_qwen3_v2.inspect.json.  The `_q8` variant packs a one-layer model of
+the same shape with `--quant q8_0` (Q8_0X4 layer linears).
 
-The two files are what travels; the reference and the SafeTensors input do
+These files are what travels; the reference and the SafeTensors input do
 not.  Usage: python tests/golden/make_smodel_fixture.py [/path/to/reference]
 """
 from __future__ import annotations
@@ -28,8 +29,8 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-OUT = HERE / "tiny_qwen3_v2.smodel"
-OUT_JSON = HERE / "tiny_qwen3_v2.inspect.json"
+# variant -> (file stem, packer --quant, layers)
+VARIANTS = {"auto": ("tiny_qwen3_v2", "auto", 2), "q8_0": ("tiny_qwen3_v2_q8", "q8_0", 1)}
 
 CONFIG = {
     "model_type": "qwen3",
@@ -48,10 +49,14 @@ CONFIG = {
 }
 
 
-def checkpoint(seed: int = 20241) -> dict[str, np.ndarray]:
+def config(variant: str = "auto") -> dict:
+    return dict(CONFIG, num_hidden_layers=VARIANTS[variant][2])
+
+
+def checkpoint(seed: int = 20241, variant: str = "auto") -> dict[str, np.ndarray]:
     """Seeded fp32 weights with Hugging Face Qwen3 names."""
     rng = np.random.default_rng(seed)
-    c = CONFIG
+    c = config(variant)
     h, f, v = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
     hd = c["head_dim"]
     qd, kvd = c["num_attention_heads"] * hd, c["num_key_value_heads"] * hd
@@ -86,21 +91,23 @@ def main(ref_root: str) -> None:
     sys.path.insert(0, str(Path(ref_root) / "tools"))
     import silicatepack  # noqa: E402  (reference packer, stdlib only)
 
-    with tempfile.TemporaryDirectory() as tmp:
-        src = Path(tmp) / "hf"
-        src.mkdir()
-        (src / "config.json").write_text(json.dumps(CONFIG))
-        save_file(checkpoint(), str(src / "model.safetensors"))
-        out = Path(tmp) / "tiny.smodel"
-        rc = silicatepack.main(["pack-hf", "--input-dir", str(src), "--output", str(out), "--quant", "auto",
-                                "--interleave", "4", "--payload-alignment", "4096", "--force"])
-        if rc not in (0, None):
-            raise SystemExit(f"packer failed: {rc}")
-        record = silicatepack.inspect_path(out, json_output=False)
-        record["file"] = OUT.name
-        shutil.copyfile(out, OUT)
-    OUT_JSON.write_text(json.dumps(record, indent=1, sort_keys=True) + "\n")
-    print(f"wrote {OUT} ({OUT.stat().st_size} bytes) and {OUT_JSON}")
+    for variant, (stem, quant, _) in VARIANTS.items():
+        out_file, out_json = HERE / f"{stem}.smodel", HERE / f"{stem}.inspect.json"
+        with tempfile.TemporaryDirectory() as tmp:
+            src = Path(tmp) / "hf"
+            src.mkdir()
+            (src / "config.json").write_text(json.dumps(config(variant)))
+            save_file(checkpoint(variant=variant), str(src / "model.safetensors"))
+            out = Path(tmp) / "tiny.smodel"
+            rc = silicatepack.main(["pack-hf", "--input-dir", str(src), "--output", str(out), "--quant", quant,
+                                    "--interleave", "4", "--payload-alignment", "4096", "--force"])
+            if rc not in (0, None):
+                raise SystemExit(f"packer failed: {rc}")
+            record = silicatepack.inspect_path(out, json_output=False)
+            record["file"] = out_file.name
+            shutil.copyfile(out, out_file)
+        out_json.write_text(json.dumps(record, indent=1, sort_keys=True) + "\n")
+        print(f"wrote {out_file} ({out_file.stat().st_size} bytes) and {out_json}")
 
 
 if __name__ == "__main__":

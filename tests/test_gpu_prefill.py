@@ -61,6 +61,30 @@ def test_prefill_matches_oracle(ctx, zo, tiny, n):
         ctx.clear()
 
 
+def test_q8_0_linears_and_q4_0_embedding(ctx, zo):
+    """The other layer and embedding types the model takes: Q8_0X4 linears
+    (Q8_0 weight GEMMs) and a plain Q4_0 token embedding."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=1, head_dim=64,
+                            vocab_padded=512, vocab_real=500, max_ctx=96, lin_type=synth.Q8_0,
+                            embd_type=synth.Q4_0)
+    model = synth.random_model(cfg, seed=12)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(13, 40, cfg.vocab_real)
+        tok, _, hid = gm.prefill(prompt, want_hidden=True)
+        assert rel_err(hid, om.prefill_q8(prompt)) <= REL_TOL
+        assert tok == om.lm_head()[1]
+        toks, _, _ = gm.generate(prompt, 30, batched_prefill=True)
+        assert np.array_equal(toks, om.generate_batched(prompt, 30))
+        toks, _, _ = gm.generate(prompt, 30)
+        assert np.array_equal(toks, om.generate(prompt, 30))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def test_generate_batched_matches_oracle(ctx, zo, tiny):
     gm = GpuModel(ctx, tiny)
     om = zo.OracleModel(tiny)

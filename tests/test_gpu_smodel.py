@@ -1,5 +1,6 @@
-"""A packed .smodel-v2 through the GPU path: the tiny Qwen3 artifact that the
-reference packer wrote (tests/golden/tiny_qwen3_v2.smodel) is read by
+"""A packed .smodel-v2 through the GPU path: the tiny Qwen3 artifacts that the
+reference packer wrote (tests/golden/tiny_qwen3_v2*.smodel: Q4_0X4 and
+Q8_0X4 layer linears) are read by
 zg_smodel_open, registered by zg_smodel_register_all with its SIDX
 layouts, and decoded by the HIP model; the oracle decodes the same tensor
 views on the CPU.
@@ -48,8 +49,9 @@ def test_register_all_layouts(ctx, zo):
         ctx.clear()
 
 
-def test_smodel_decode_matches_oracle(ctx, zo):
-    sm = SModel(FIX)
+@pytest.mark.parametrize("stem", ["tiny_qwen3_v2", "tiny_qwen3_v2_q8"])
+def test_smodel_decode_matches_oracle(ctx, zo, stem):
+    sm = SModel(FIX.parent / f"{stem}.smodel")
     gm = GpuModel.from_smodel(ctx, sm, max_ctx=64)
     om = zo.OracleModel(gm.model)
     try:
@@ -68,6 +70,9 @@ def test_smodel_decode_matches_oracle(ctx, zo):
         prompt = synth.prompt(9, 12, gm.cfg.vocab_real)
         toks, _, _ = gm.generate(prompt, 48)
         assert np.array_equal(toks, om.generate(prompt, 48))
+        # the batched prefill on the packed weights (Q4_0X4 or Q8_0X4 GEMMs)
+        toks_b, _, _ = gm.generate(prompt, 40, batched_prefill=True)
+        assert np.array_equal(toks_b, om.generate_batched(prompt, 40))
     finally:
         om.close()
         gm.close()

@@ -1,14 +1,14 @@
 """The .smodel reader (zg_smodel_*, zero_amd.smodel) on the CPU.
 
 Pinned three ways:
-* against the packer's own record of the fixture (tiny_qwen3_v2.inspect.json,
+* against the packer's own record of each fixture (tiny_qwen3_v2*.inspect.json,
   written by tools/silicatepack.py's `inspect` from its manifest, not from
   the SIDX bytes this reader parses): header fields, every tensor's name,
   dtype, shape, payload offset, byte length and sha256;
 * byte for byte against the oracle's quantizers (themselves pinned to the
   packer's golden vectors) applied to the seeded fp32 checkpoint the
-  fixture was packed from: Q4_0X4 linears, Q8_0 embedding, Q8_0X4 LM head,
-  F32 norms;
+  fixture was packed from: Q4_0X4 (or, in the q8 fixture, Q8_0X4) linears,
+  Q8_0 embedding, Q8_0X4 LM head, F32 norms;
 * the reference loader's rejection rules
   (kernel/src/model_loader.rs:380-575, 599-659), one patched field at a
   time, each mapped to its LoadError kind.
@@ -29,25 +29,37 @@ GOLDEN = Path(__file__).parent / "golden"
 FIX = (GOLDEN / "tiny_qwen3_v2.smodel").read_bytes()
 REC = json.loads((GOLDEN / "tiny_qwen3_v2.inspect.json").read_text())
 MAN = REC["manifest"]
+# (fixture stem, make_smodel_fixture variant): the 2-layer --quant auto
+# artifact and the 1-layer --quant q8_0 artifact (Q8_0X4 layer linears)
+FIXTURES = [("tiny_qwen3_v2", "auto"), ("tiny_qwen3_v2_q8", "q8_0")]
+
 DTYPE_ID = {"F32": 0, "Q8_0": 8, "Q4_0": 2, "Q4_0X4": 100, "Q8_0X4": 101}
 P0 = REC["header"]["payload_offset"]  # SIDX header position in the file
 ENTRY0 = P0 + 128
+
+
+def _load(stem):
+    return (GOLDEN / f"{stem}.smodel").read_bytes(), json.loads((GOLDEN / f"{stem}.inspect.json").read_text())
 
 
 def _index(name: str) -> int:
     return [t.name for t in SModel(FIX).tensors].index(name)
 
 
-def test_header_matches_packer_record():
-    s = SModel(FIX)
-    h = REC["header"]
+@pytest.mark.parametrize("stem,variant", FIXTURES)
+def test_header_matches_packer_record(stem, variant):
+    fix, rec = _load(stem)
+    s = SModel(fix)
+    h = rec["header"]
     for f in ("version", "payload_kind", "flags", "manifest_offset", "manifest_len", "payload_offset", "payload_len"):
         assert getattr(s.info, f) == h[f], f
-    assert s.info.tensor_count == MAN["tensor_count"] == 25
+    assert s.info.tensor_count == rec["manifest"]["tensor_count"] == 3 + 11 * fx.VARIANTS[variant][2]
 
 
-def test_model_config_matches_packer_record():
-    i, c = SModel(FIX).info, MAN["model_config"]
+@pytest.mark.parametrize("stem,variant", FIXTURES)
+def test_model_config_matches_packer_record(stem, variant):
+    fix, rec = _load(stem)
+    i, c = SModel(fix).info, rec["manifest"]["model_config"]
     assert i.architecture_id == 1  # qwen3
     assert (i.block_count, i.embedding_length, i.feed_forward_length) == (
         c["num_hidden_layers"], c["hidden_size"], c["intermediate_size"])
@@ -59,11 +71,13 @@ def test_model_config_matches_packer_record():
     assert i.layer_norm_rms_epsilon == np.float32(c["rms_norm_eps"])
 
 
-def test_tensors_match_packer_record():
+@pytest.mark.parametrize("stem,variant", FIXTURES)
+def test_tensors_match_packer_record(stem, variant):
     import hashlib
 
-    s = SModel(FIX)
-    want = {t["name"]: t for t in MAN["tensors"]}
+    fix, rec = _load(stem)
+    s = SModel(fix)
+    want = {t["name"]: t for t in rec["manifest"]["tensors"]}
     assert sorted(t.name for t in s.tensors) == sorted(want)
     for t in s.tensors:
         w = want[t.name]
@@ -72,9 +86,10 @@ def test_tensors_match_packer_record():
         assert (t.payload_offset, t.byte_len) == (w["payload_offset"], w["byte_len"]), t.name
         assert t.interleave == w.get("row_interleave", 1), t.name
         assert hashlib.sha256(t.data.tobytes()).hexdigest() == w["sha256"], t.name
-    # interleaved: the 14 layer linears and the LM head; embedding and norms plain
-    assert sum(t.interleave == 4 for t in s.tensors) == 15
+    # interleaved: the 7 linears per layer and the LM head; embedding and norms plain
+    assert sum(t.interleave == 4 for t in s.tensors) == 7 * fx.VARIANTS[variant][2] + 1
     assert s["token_embd.weight"].interleave == 1 and s["output.weight"].ggml_type == Q8_0
+    assert s["blk.0.attn_q.weight"].ggml_type == (Q4_0 if variant == "auto" else Q8_0)
 
 
 def test_find_uses_exact_names():
@@ -84,12 +99,14 @@ def test_find_uses_exact_names():
         s.find("blk.1.ffn_down")
 
 
-def test_tensor_bytes_rebuild_from_the_checkpoint(zo):
+@pytest.mark.parametrize("stem,variant", FIXTURES)
+def test_tensor_bytes_rebuild_from_the_checkpoint(zo, stem, variant):
     """Every packed tensor equals the oracle's quantization of the seeded
     fp32 source named in the manifest."""
-    src = fx.checkpoint()
-    s = SModel(FIX)
-    for w in MAN["tensors"]:
+    src = fx.checkpoint(variant=variant)
+    fix, rec = _load(stem)
+    s = SModel(fix)
+    for w in rec["manifest"]["tensors"]:
         x = src[w["source"]["name"]]
         rows = x.shape[0]
         cols = x.shape[1] if x.ndim == 2 else 1
