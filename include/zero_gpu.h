@@ -309,7 +309,10 @@ zg_status zg_smodel_get_tensor(const zg_smodel *sm, uint64_t index, zg_smodel_te
 zg_status zg_smodel_find(const zg_smodel *sm, const char *name, zg_smodel_tensor *out);
 /* Register every quantized tensor (Q4_0/Q8_0 plain or X4, Q4_K, Q6_K) with
  * its layout, as smodel_native_tensor_index registers the X4 ones in
- * weight_layout (model_loader.rs:527-552); F32 tensors are skipped. */
+ * weight_layout (model_loader.rs:527-552); F32 tensors are skipped.  The
+ * reference clears its registry before indexing a model; here the context
+ * may hold other weights, so nothing is cleared: on an error the tensors
+ * registered before the failing one stay registered (zg_clear drops all). */
 zg_status zg_smodel_register_all(zg_ctx *ctx, const zg_smodel *sm);
 
 #ifdef __cplusplus

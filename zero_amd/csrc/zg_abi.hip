@@ -7,6 +7,8 @@
 // device copy of the tensor bytes (byte-identical to the host bytes).
 #include <hip/hip_runtime.h>
 
+#include <new>
+
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
@@ -82,7 +84,8 @@ extern "C" zg_status zg_init(int device, zg_ctx** out) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return ZG_ERR_HIP;
   if (hipSetDevice(device) != hipSuccess) return ZG_ERR_HIP;
-  zg_ctx* ctx = new zg_ctx();
+  zg_ctx* ctx = new (std::nothrow) zg_ctx();
+  if (!ctx) return ZG_ERR_OUT_OF_MEMORY;
   ctx->device = device;
   // A blocking stream: work on it is ordered against the legacy null stream,
   // so callers that stage data with null-stream copies need no extra sync.
@@ -154,7 +157,12 @@ static zg_status do_register(zg_ctx* ctx, uintptr_t key, const void* host, const
   }
   auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), key,
                              [](uintptr_t k, const RegEntry& r) { return k < r.key; });
-  ctx->reg.insert(it, e);
+  try {
+    ctx->reg.insert(it, e);
+  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+    if (e.owned) hipFree(e.dev);
+    return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "register: registry growth failed");
+  }
   return ZG_OK;
 }
 

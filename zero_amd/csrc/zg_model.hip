@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstring>
+#include <new>
 #include <vector>
 
 #include "../../include/zero_gpu.h"
@@ -617,7 +618,13 @@ constexpr size_t kPrefillChunk = 512;
 static zg_status model_alloc(zg_model* m, void** p, size_t bytes) {
   hipError_t e = hipMalloc(p, bytes);
   if (e != hipSuccess) return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-  m->owned.push_back(*p);
+  try {
+    m->owned.push_back(*p);
+  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+    hipFree(*p);
+    *p = nullptr;
+    return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
+  }
   e = hipMemset(*p, 0, bytes);
   return hip_check(m->ctx, e, "model: memset");
 }
@@ -870,13 +877,20 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     if (kk % 64 || kk > kMaxPairK) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: in_dim %zu not supported", kk);
   if (qd % 4 || kvd % 4 || d.ffn % 4 || d.hidden % 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: rows % 4");
   hipSetDevice(ctx->device);
-  zg_model* m = new zg_model();
+  zg_model* m = new (std::nothrow) zg_model();
+  if (!m) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
   m->ctx = ctx;
   m->d = d;
   m->d.layers = nullptr;
   zg_status s = ZG_OK;
   const size_t H = d.hidden, F = d.ffn;
-  m->layers.resize(d.n_layers);
+  try {
+    m->layers.resize(d.n_layers);
+    m->owned.reserve(32 + 4 * (size_t)d.n_layers);  // room for every buffer the model allocates
+  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+    delete m;
+    return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
+  }
   for (uint32_t l = 0; l < d.n_layers && !s; l++) {
     const zg_layer_weights& W = d.layers[l];
     ZLayer& L = m->layers[l];
@@ -902,12 +916,12 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = upload_f32(m, &m->out_norm, d.output_norm, H);
   if (!s) {
     // RopeContext::new (ops.rs:79-93): inv_freq[i] = theta^(-2i/head_dim) in f32
-    std::vector<float> inv(d.head_dim / 2);
+    float inv[64];  // head_dim <= 128
     for (uint32_t i = 0; i < d.head_dim / 2; i++) {
       const float ex = -2.0f * (float)i / (float)d.head_dim;
       inv[i] = powf(d.rope_theta, ex);
     }
-    s = upload_f32(m, &m->inv_freq, inv.data(), inv.size());
+    s = upload_f32(m, &m->inv_freq, inv, d.head_dim / 2);
   }
   // up to kAttnSplits workgroups per query head share its context (one CU
   // loads ~150 GB/s, so a head's K/V rows are spread over several CUs);

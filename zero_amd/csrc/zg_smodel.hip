@@ -10,7 +10,7 @@
 #include <stdint.h>
 #include <string.h>
 
-#include <string>
+#include <new>
 #include <vector>
 
 #include "../../include/zero_gpu.h"
@@ -184,8 +184,19 @@ extern "C" zg_status zg_smodel_open(const void* bytes_v, size_t len, zg_smodel**
   info.tensor_count = count;
 
   const uint8_t* names = p + names_offset;
-  std::vector<zg_smodel_tensor> tensors;
-  tensors.reserve(count);
+  zg_smodel* sm = new (std::nothrow) zg_smodel;
+  if (!sm) return ZG_ERR_OUT_OF_MEMORY;
+  std::vector<zg_smodel_tensor>& tensors = sm->tensors;
+  try {
+    tensors.reserve(count);  // count <= kMaxTensors: no growth below
+  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+    delete sm;
+    return ZG_ERR_OUT_OF_MEMORY;
+  }
+  auto fail = [&](zg_status e) {
+    delete sm;
+    return e;
+  };
   for (uint32_t i = 0; i < count; i++) {
     const size_t off = kIndexHeaderSize + (size_t)i * kEntrySize;
     uint32_t name_off = 0, name_len = 0, dtype = 0, rank = 0;
@@ -193,9 +204,9 @@ extern "C" zg_status zg_smodel_open(const void* bytes_v, size_t len, zg_smodel**
     rd32(p, plen, off + 4, name_len);
     rd32(p, plen, off + 8, dtype);
     rd32(p, plen, off + 12, rank);
-    if (rank > 8) return ZG_ERR_INVALID_CONTAINER;
+    if (rank > 8) return fail(ZG_ERR_INVALID_CONTAINER);
     const uint64_t name_end = (uint64_t)name_off + name_len;
-    if (name_end > names_len || !valid_utf8(names + name_off, name_len)) return ZG_ERR_INVALID_CONTAINER;
+    if (name_end > names_len || !valid_utf8(names + name_off, name_len)) return fail(ZG_ERR_INVALID_CONTAINER);
     zg_smodel_tensor t{};
     t.name = reinterpret_cast<const char*>(names + name_off);
     t.name_len = name_len;
@@ -206,18 +217,16 @@ extern "C" zg_status zg_smodel_open(const void* bytes_v, size_t len, zg_smodel**
     rd64(p, plen, off + 80, t.payload_offset);
     rd64(p, plen, off + 88, t.byte_len);
     uint64_t tensor_end;
-    if (!add_ok(t.payload_offset, t.byte_len, tensor_end) || tensor_end > plen) return ZG_ERR_INVALID_CONTAINER;
-    if (!decode_dtype(dtype, t.ggml_type, t.interleave)) return ZG_ERR_UNSUPPORTED_FORMAT;
+    if (!add_ok(t.payload_offset, t.byte_len, tensor_end) || tensor_end > plen) return fail(ZG_ERR_INVALID_CONTAINER);
+    if (!decode_dtype(dtype, t.ggml_type, t.interleave)) return fail(ZG_ERR_UNSUPPORTED_FORMAT);
     // interleaving needs a rank-2 matmul weight with rows % 4 == 0 (:527-544)
-    if (t.interleave > 1 && !(rank == 2 && t.dims[0] % t.interleave == 0)) return ZG_ERR_INVALID_CONTAINER;
+    if (t.interleave > 1 && !(rank == 2 && t.dims[0] % t.interleave == 0)) return fail(ZG_ERR_INVALID_CONTAINER);
     t.data = p + t.payload_offset;
     tensors.push_back(t);
   }
-  zg_smodel* sm = new zg_smodel;
   sm->bytes = b;
   sm->len = len;
   sm->info = info;
-  sm->tensors.swap(tensors);
   *out = sm;
   return ZG_OK;
 }
