@@ -164,6 +164,22 @@ def bench_rows(ctx, steps: int):
     out["lm_head_q8_0x4_argmax"] = _row("LM head Q8_0X4 151936x2048 + argmax", per, wl.nbytes + 4 * H + 4 * V, n, c)
     del wd, wl
 
+    # plain (GGUF, .smodel-v1) row-major Q4_0: the headline shape and a Kimi K2
+    # expert projection (the DeepSeek2 path's bulk layer weights)
+    for name, key, rows, k in (("Q4_0 plain 6144x2048", "q4_0_plain_6144x2048", 6144, 2048),
+                               ("Q4_0 plain 2048x7168 (Kimi K2 expert gate/up)", "q4_0_plain_2048x7168", 2048, 7168)):
+        wh = synth.weight(rng, synth.Q4_0, rows, k, 1)
+        wd, c = rotating(wh)
+        xk = torch.from_numpy(synth.activations(rng, k)).cuda()
+        yk = torch.empty(rows, device="cuda")
+
+        def pl(i, st, wd=wd, xk=xk, yk=yk, rows=rows, k=k):
+            ctx.linear_dev(xk, wd[i], yk, k, rows, synth.Q4_0, 1, stream=st)
+
+        per, n, _ = _graph_time(pl, c, max(200, steps // 4), 40)
+        out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
+        del wd
+
     # k-quants at Llama-3-8B FFN shapes
     for name, qt, rows, k in (("Q4_K 14336x4096 (gate/up)", synth.Q4K, 14336, 4096),
                               ("Q6_K 4096x14336 (down)", synth.Q6K, 4096, 14336)):

@@ -166,7 +166,7 @@ def test_gemv_device_api_matches_host_api(ctx, zo):
     ctx.clear()
 
 
-@pytest.mark.parametrize("quant,il", [(Q4_0, 4), (Q8_0, 4), (Q6K, 1)])
+@pytest.mark.parametrize("quant,il", [(Q4_0, 4), (Q8_0, 4), (Q4_0, 1), (Q8_0, 1), (Q6K, 1)])
 def test_row_ranges(ctx, zo, quant, il):
     rng = np.random.default_rng(2)
     rows, k = 40, 1024
@@ -199,18 +199,20 @@ def test_tall_q8_0_ranges(ctx, zo):
     ctx.clear()
 
 
-def test_fused_qkv_q8_0(ctx, zo):
-    """Config 2: fused Q|K|V Q8_0X4, Qwen3-1.7B attention (2048 + 1024 + 1024) x 2048."""
+@pytest.mark.parametrize("il", [4, 1])
+def test_fused_qkv_q8_0(ctx, zo, il):
+    """Config 2: fused Q|K|V Q8_0, Qwen3-1.7B attention (2048 + 1024 + 1024) x 2048,
+    in the X4 layout and in the plain (GGUF) layout."""
     rng = np.random.default_rng(3)
     k = 2048
-    ws = [synth.weight(rng, Q8_0, n, k, 4) for n in (2048, 1024, 1024)]
+    ws = [synth.weight(rng, Q8_0, n, k, il) for n in (2048, 1024, 1024)]
     x = synth.activations(rng, k)
     outs = [np.empty(w.size // (k // 32 * 34), np.float32) for w in ws]
     for w in ws:
-        ctx.register(w, Q8_0, 4)
+        ctx.register(w, Q8_0, il)
     ctx.linear_fused_dispatch(x, [(w, o, Q8_0) for w, o in zip(ws, outs)], k)
     for w, o in zip(ws, outs):
-        ref = zo.linear_range(x, w, k, o.size, Q8_0, 4)
+        ref = zo.linear_range(x, w, k, o.size, Q8_0, il)
         assert rel_err(o, ref) <= REL_TOL
     ctx.clear()
 
@@ -243,6 +245,23 @@ def test_lm_head_argmax(ctx, zo, lm_head):
     top2 = np.sort(ref)[-2:]
     print(f"LM head: argmax {tok} (oracle {idx}), margin {top2[1] - top2[0]:.4f}, rel err {rel_err(logits, ref):.2e}")
     assert tok == idx and tok == int(np.argmax(logits))
+    ctx.clear()
+
+
+def test_lm_head_argmax_plain_q8_0(ctx, zo, lm_head):
+    """The same LM head in the plain (GGUF) Q8_0 layout."""
+    w4, hidden, norm = lm_head
+    V, H = kats.VOCAB_SIZE_PADDED, 2048
+    w = synth.deinterleave_x4(w4, V, H, Q8_0)
+    ctx.register(w, Q8_0, 1)
+    logits = np.empty(V, np.float32)
+    tok = ctx.lm_head_argmax(hidden, norm, w, Q8_0, 1e-6, H, logits_buf=logits)
+    xn = np.empty(H, np.float32)
+    zo.load().zo_rmsnorm(hidden.ctypes.data, norm.ctypes.data, xn.ctypes.data, H, 1e-6)
+    with zo.Pool(8):
+        ref = zo.linear_parallel(xn, w, H, V, Q8_0, 1)
+    assert rel_err(logits, ref) <= REL_TOL
+    assert tok == zo.argmax(ref)[0]
     ctx.clear()
 
 

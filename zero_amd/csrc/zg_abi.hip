@@ -273,6 +273,28 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
     return hip_check(ctx, launch_gemv_x4(a, qt, pro, epi, st), "gemv_x4 launch");
   }
+  if (plain_strip_ok(qt, il, k, n, w, x) && (pro == PRO_PLAIN || pro == PRO_RMSNORM) &&
+      (epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX) && !(pro == PRO_RMSNORM && epi == EPI_RESID)) {
+    // plain rows in fours: group g is rows 4g..4g+3
+    const size_t rbytes = (k / 32) * (qt == ZG_Q4_0 ? 18 : 34);
+    const size_t g0 = start / 4, g1 = (end + 3) / 4;
+    GemvArgs a{};
+    a.nseg = 1;
+    a.k = (int)k;
+    a.total_groups = (uint32_t)(g1 - g0);
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.best = best;
+    a.flags = gemv_flags;
+    a.seg[0].w = w + 4 * g0 * rbytes;
+    a.seg[0].y = y ? y + 4 * g0 : nullptr;
+    a.seg[0].resid = resid ? resid + 4 * g0 : nullptr;
+    a.seg[0].g_begin = 0;
+    a.seg[0].row_lo = (uint32_t)(start - 4 * g0);
+    a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
+    return hip_check(ctx, launch_gemv_plain(a, qt, pro, epi, st), "gemv plain launch");
+  }
   const float* xin = x;
   if (pro == PRO_RMSNORM) {
     // generic path: normalize into the context's aux buffer first

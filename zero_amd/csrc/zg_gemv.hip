@@ -381,6 +381,27 @@ typedef uint32_t u32x4a8 __attribute__((ext_vector_type(4), aligned(8)));
 // pointee's alignment attribute must reach the load)
 #define ZG_LD_POL(NT, p) ((NT) ? __builtin_nontemporal_load(p) : *(p))
 
+// Plain (GGUF / .smodel-v1) row-major blocks: the lane's block starts at
+// blk (fp16 d, then the quants): 2-byte aligned, so the quant loads use a
+// 2-byte-aligned vector type (still single dwordx4 loads, unaligned access).
+typedef uint32_t u32x4s2 __attribute__((ext_vector_type(4), aligned(2)));
+
+template <uint32_t QT>
+__device__ __forceinline__ void strip_load_plain(LaneW<QT>& L, const uint8_t* blk) {
+  constexpr int QW = StripGeom<QT>::QW;
+  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : ZG_STRIP_NT_Q4;
+  const u32x4s2* p = reinterpret_cast<const u32x4s2*>(blk + 2);
+#pragma unroll
+  for (int i = 0; i < QW / 4; i++) {
+    const u32x4s2 v = ZG_LD_POL(NT, p + i);
+    L.q[4 * i] = v.x;
+    L.q[4 * i + 1] = v.y;
+    L.q[4 * i + 2] = v.z;
+    L.q[4 * i + 3] = v.w;
+  }
+  L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk));
+}
+
 template <uint32_t QT>
 __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int r) {
   constexpr int QW = StripGeom<QT>::QW;
@@ -423,9 +444,12 @@ __device__ __forceinline__ float row_sum4(float v) {
   return v;
 }
 
-template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false>
+// IL 4: X4 group-blocks; IL 1: plain row-major blocks, a "group" being 4
+// consecutive rows (lane (b, r) reads block b of row 4 g + r).
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
 __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   constexpr int GBY = StripGeom<QT>::GB;
+  constexpr int BB = QT == Q4_0 ? 18 : 34;  // plain block bytes
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) float part[];  // [2][NW][GBATCH][PARTS][16]
   __shared__ float red[16];
@@ -467,7 +491,10 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
       for (int p = 0; p < PARTS; p++) {
         uint32_t lg;
         const GemvSeg sg = locate(min(base + j, items - 1), p, lg);
-        strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
+        if (IL == 4)
+          strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
+        else
+          strip_load_plain<QT>(L[j][p], sg.w + ((size_t)(4 * lg + r) * nb + kb) * BB);
       }
     }
   };
@@ -854,7 +881,7 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
-template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false>
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
 static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   const int wps = nw / S;
@@ -868,7 +895,7 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
     static int resident = 0;
     if (resident == 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1>, nw * 64,
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL>, nw * 64,
                                                        shm) !=
               hipSuccess ||
           n <= 0)
@@ -880,20 +907,20 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   const size_t cap = (size_t)cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1>), dim3((unsigned)grid), dim3(nw * 64), shm, st,
-                     a, S);
+  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL>), dim3((unsigned)grid), dim3(nw * 64), shm,
+                     st, a, S);
   return hipGetLastError();
 }
 
-template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024>
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, int IL = 4>
 static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   if constexpr (EPI != EPI_SWIGLU) {
-    if (a.nseg == 1) return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, true>(a, S, nw, items, st);
+    if (a.nseg == 1) return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, true, IL>(a, S, nw, items, st);
   }
-  return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, false>(a, S, nw, items, st);
+  return launch_strip_gb1<QT, PRO, EPI, GBATCH, MAXT, false, IL>(a, S, nw, items, st);
 }
 
-template <uint32_t QT, int PRO, int EPI>
+template <uint32_t QT, int PRO, int EPI, int IL = 4>
 static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   const int S = a.k / 512;
   const int nw = S >= 4 ? S : 4;  // S in {1, 2} -> 4 waves: 4 / S waves per strip
@@ -904,20 +931,20 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   const size_t wps = nw / S;
   if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
     if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
-      return launch_strip_gb<QT, PRO, EPI, 4>(a, S, nw, items, st);
+      return launch_strip_gb<QT, PRO, EPI, 4, 1024, IL>(a, S, nw, items, st);
   }
   if constexpr (QT == Q8_0 && EPI != EPI_SWIGLU && PRO != PRO_ATTN) {
     // tall Q8_0X4 (the LM head): four groups per batch with 16-byte loads
     // need more than 128 registers, so these launches are 256-thread
     // workgroups (in_dim at most 2048)
     if (nw == 4 && items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
-      return launch_strip_gb<QT, PRO, EPI, 4, 256>(a, S, nw, items, st);
+      return launch_strip_gb<QT, PRO, EPI, 4, 256, IL>(a, S, nw, items, st);
   }
   // gate|up (SwiGLU): one item (a gate and an up group) per batch gives
   // 1536 batches at Qwen3-1.7B's FFN, so most workgroups get a second batch
   // to overlap (8.35 vs 8.60 us traced, 2 items per batch)
-  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, 1>(a, S, nw, items, st);
-  return launch_strip_gb<QT, PRO, EPI, 2>(a, S, nw, items, st);
+  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, 1, 1024, IL>(a, S, nw, items, st);
+  return launch_strip_gb<QT, PRO, EPI, 2, 1024, IL>(a, S, nw, items, st);
 }
 
 // Tall single-projection Q8_0X4 launches (the LM head: 37,984 groups) take
@@ -970,6 +997,29 @@ static hipError_t dispatch_x4_qt(const GemvArgs& a, int pro, int epi, hipStream_
   if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
   if (pro == PRO_ATTN && epi == EPI_RESID) return launch_x4_any<QT, PRO_ATTN, EPI_RESID>(a, st);
+  return hipErrorInvalidValue;
+}
+
+// Plain row-major Q4_0 / Q8_0 (GGUF and .smodel-v1 layouts) through the
+// strip kernel: rows in fours, in_dim a multiple of 512 up to 8192.
+bool plain_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
+  return il == 1 && (qt == Q4_0 || qt == Q8_0) && strip_path_ok((int)k) && n % 4 == 0 &&
+         (reinterpret_cast<uintptr_t>(w) & 1u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+template <uint32_t QT>
+static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStream_t st) {
+  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_strip<QT, PRO_PLAIN, EPI_STORE, 1>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_strip<QT, PRO_PLAIN, EPI_RESID, 1>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_strip<QT, PRO_PLAIN, EPI_ARGMAX, 1>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_strip<QT, PRO_RMSNORM, EPI_STORE, 1>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 1>(a, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_plain(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st) {
+  if (qt == Q4_0) return dispatch_plain_qt<Q4_0>(a, pro, epi, st);
+  if (qt == Q8_0) return dispatch_plain_qt<Q8_0>(a, pro, epi, st);
   return hipErrorInvalidValue;
 }
 

@@ -66,6 +66,10 @@ struct DequantArgs {
 };
 
 hipError_t launch_gemv_x4(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
+// Plain row-major Q4_0 / Q8_0 through the strip kernel (groups = 4 rows);
+// prologue none or rmsnorm, epilogue store, residual or argmax.
+bool plain_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
+hipError_t launch_gemv_plain(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
 // LDS bytes the X4 streaming kernel needs for in_dim k.
 size_t gemv_x4_lds_bytes(uint32_t qt, int k);
 hipError_t launch_gemv_generic(const GenericArgs& a, hipStream_t st);
