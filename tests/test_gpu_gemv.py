@@ -265,20 +265,22 @@ def test_lm_head_argmax_plain_q8_0(ctx, zo, lm_head):
     ctx.clear()
 
 
-def test_lm_head_argmax_q6_k(ctx, zo):
-    """LM head in Q6_K (the output.weight type of Q4_K_M GGUF artifacts)."""
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("qt", [Q6K, Q4K])
+def test_lm_head_argmax_kquant(ctx, zo, qt):
+    """LM head in Q6_K (the output.weight type of Q4_K_M GGUF artifacts) and
+    Q4_K (OutputQuant::Q4K, kernel/src/inference.rs:3119-3125)."""
+    rng = np.random.default_rng(5 + qt)
     V, H = 32000, 4096
-    w = synth.weight(rng, Q6K, V, H, 1)
+    w = synth.weight(rng, qt, V, H, 1)
     hidden = synth.activations(rng, H)
     norm = (1 + 0.05 * rng.standard_normal(H)).astype(np.float32)
-    ctx.register(w, Q6K, 1)
+    ctx.register(w, qt, 1)
     logits = np.empty(V, np.float32)
-    tok = ctx.lm_head_argmax(hidden, norm, w, Q6K, 1e-6, H, vocab_padded=V, vocab_real=V, logits_buf=logits)
+    tok = ctx.lm_head_argmax(hidden, norm, w, qt, 1e-6, H, vocab_padded=V, vocab_real=V, logits_buf=logits)
     xn = np.empty(H, np.float32)
     zo.load().zo_rmsnorm(hidden.ctypes.data, norm.ctypes.data, xn.ctypes.data, H, 1e-6)
     with zo.Pool(8):
-        ref = zo.linear_parallel(xn, w, H, V, Q6K, 1)
+        ref = zo.linear_parallel(xn, w, H, V, qt, 1)
     assert rel_err(logits, ref) <= REL_TOL
     idx, _ = zo.argmax(ref)
     assert tok == idx
