@@ -164,6 +164,30 @@ def bench_rows(ctx, steps: int):
     out["lm_head_q8_0x4_argmax"] = _row("LM head Q8_0X4 151936x2048 + argmax", per, wl.nbytes + 4 * H + 4 * V, n, c)
     del wd, wl
 
+    # the headline GEMV with x encoded to Q8_0 first (the integer block dots):
+    # the GEMV alone on a resident Q8_0 row, and quantize + GEMV
+    wh = synth.weight(rng, synth.Q4_0, 6144, H, 4)
+    wd, c = rotating(wh)
+    xf = torch.from_numpy(synth.activations(rng, H)).cuda()
+    xq = torch.empty(H // 32 * 34, dtype=torch.uint8, device="cuda")
+    yq = torch.empty(6144, device="cuda")
+    ctx.quantize_q8_0_dev(xf, xq, 1, H)
+
+    def g8(i, st):
+        ctx.linear_q8act_dev(xq, wd[i], yq, H, 6144, synth.Q4_0, 4, stream=st)
+
+    def g8q(i, st):
+        ctx.quantize_q8_0_dev(xf, xq, 1, H, stream=st)
+        ctx.linear_q8act_dev(xq, wd[i], yq, H, 6144, synth.Q4_0, 4, stream=st)
+
+    nbytes = wh.nbytes + H // 32 * 34 + 4 * 6144
+    per, n, _ = _graph_time(g8, c, max(200, steps // 4), 40)
+    out["q4_0x4_q8act_6144x2048"] = _row("Q4_0X4 6144x2048, x as Q8_0 (integer dots)", per, nbytes, n, c)
+    per, n, _ = _graph_time(g8q, c, max(200, steps // 4), 40)
+    out["q4_0x4_quant_q8act_6144x2048"] = _row("Q4_0X4 6144x2048, quantize x to Q8_0 + GEMV", per,
+                                               nbytes + 4 * H + H // 32 * 34, n, c)
+    del wd
+
     # plain (GGUF, .smodel-v1) row-major Q4_0: the headline shape and a Kimi K2
     # expert projection (the DeepSeek2 path's bulk layer weights)
     for name, key, rows, k in (("Q4_0 plain 6144x2048", "q4_0_plain_6144x2048", 6144, 2048),

@@ -139,6 +139,16 @@ zg_status zg_lm_head_dev(zg_ctx *ctx, const float *d_x, const void *d_w, float *
                          uint64_t *d_best, void *stream);
 /* Decode the packed argmax candidate. Returns 0 when no finite candidate. */
 int zg_argmax_unpack(uint64_t packed, uint32_t *index, float *value);
+/* The GEMV with a Q8_0-quantized activation (variant (ii) of the decode
+ * GEMV: x encoded on the fly with zg_quantize_q8_0_dev, the packer's Q8_0
+ * encoder): out = W . x over in_dim / 32 34-byte Q8_0 blocks at d_xq (2-byte
+ * aligned), integer block dots (v_dot4_i32_i8) scaled by dW * dX, as
+ * zg_gemm_q8act_dev computes one row.  No counterpart in the reference,
+ * whose Q4_0/Q8_0 GEMVs take fp32 x (its only activation-quantized path is
+ * the Q4_K x Q8_K one below).  Q4_0 or Q8_0 weights, X4 or plain;
+ * in_dim a multiple of 512 up to 8192, out_dim % 4 == 0. */
+zg_status zg_linear_q8act_dev(zg_ctx *ctx, const void *d_xq, const void *d_w, float *d_out, size_t in_dim,
+                              size_t out_dim, uint32_t ggml_type, uint32_t interleave, void *stream);
 /* Bit-exact dequantization of a device tensor into fp32 rows (test hook for
  * dequant parity with crates/zero-gguf-parser/src/dequant.rs). */
 zg_status zg_dequant_dev(zg_ctx *ctx, const void *d_w, float *d_out, size_t rows, size_t in_dim,

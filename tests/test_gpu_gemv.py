@@ -152,6 +152,31 @@ def test_gemv_parity_host_api(ctx, zo, quant, il, rows, k):
     ctx.clear()
 
 
+Q8X_CASES = [(Q4_0, 4, 6144, 2048), (Q8_0, 4, 4096, 2048), (Q4_0, 1, 2048, 6144), (Q4_0, 4, 12288, 1536),
+             (Q8_0, 1, 64, 512), (Q8_0, 4, 151936, 2048)]
+
+
+@pytest.mark.parametrize("quant,il,rows,k", Q8X_CASES)
+def test_gemv_q8_0_activation(ctx, zo, quant, il, rows, k):
+    """The GEMV on a Q8_0-encoded x (zg_linear_q8act_dev) against the oracle's
+    Q8_0-activation GEMM at one row: the same per-block integer dots and
+    dW * dX scales, summed in another order."""
+    rng = np.random.default_rng(rows + k + il)
+    w = synth.weight(rng, quant, rows, k, il)
+    x = synth.activations(rng, k)
+    xq = zo.quantize_q8_0(x)
+    # the GPU encoder gives the same blocks
+    qd = torch.empty(xq.size, dtype=torch.uint8, device="cuda")
+    ctx.quantize_q8_0_dev(dev(x), qd, 1, k, stream=torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(qd.cpu().numpy(), xq)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.linear_q8act_dev(qd, dev(w), y, k, rows, quant, il, stream=torch.cuda.current_stream().cuda_stream)
+    ref = zo.gemm_q8act(xq, w, 1, rows, k, quant, il)[0]
+    got = y.cpu().numpy()
+    print(f"Q8_0-activation GEMV quant={quant} il={il} {rows}x{k}: rel err {rel_err(got, ref):.2e}")
+    assert rel_err(got, ref) <= 1e-5
+
+
 def test_gemv_device_api_matches_host_api(ctx, zo):
     rng = np.random.default_rng(1)
     rows, k = 6144, 2048

@@ -136,6 +136,7 @@ SIGNATURES = {
     "zg_model_reset": (None, [_P]),
     "zg_model_prefill": (_ST, [_P, _P, _S, _U32, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),
     "zg_model_generate_ex": (_ST, [_P, _P, _S, _S, _U32, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "zg_linear_q8act_dev": (_ST, [_P, _P, _P, _P, _S, _S, _U32, _U32, _P]),
     "zg_quantize_q8k_dev": (_ST, [_P, _P, _P, _S, _P]),
     "zg_linear_q4k_q8k_dev": (_ST, [_P, _P, _P, _P, _S, _S, _P]),
     "zg_linear_q4k_vnni": (_ST, [_P, _P, _P, _P, _S, _S]),

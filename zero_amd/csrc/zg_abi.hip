@@ -544,6 +544,37 @@ extern "C" zg_status zg_linear_dev(zg_ctx* ctx, const float* d_x, const void* d_
                     end, EPI_STORE, nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, pick_stream(ctx, stream));
 }
 
+extern "C" zg_status zg_linear_q8act_dev(zg_ctx* ctx, const void* d_xq, const void* d_w, float* d_out, size_t in_dim,
+                                         size_t out_dim, uint32_t ggml_type, uint32_t interleave, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_xq || !d_w || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_q8act: null pointer");
+  if (ggml_type != ZG_Q4_0 && ggml_type != ZG_Q8_0)
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "linear_q8act: weights must be Q4_0/Q8_0");
+  zg_status s = check_shape(ctx, ggml_type, interleave, in_dim, out_dim);
+  if (s) return s;
+  if (!strip_path_ok((int)in_dim) || out_dim % 4)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_q8act: in_dim %zu (multiple of 512 up to 8192) / out_dim %zu (%% 4)",
+                     in_dim, out_dim);
+  const uintptr_t wa = reinterpret_cast<uintptr_t>(d_w);
+  if ((reinterpret_cast<uintptr_t>(d_xq) & 1) || (interleave == 4 ? (wa & 7) : (wa & 1)))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_q8act: misaligned buffer");
+  if (out_dim == 0) return ZG_OK;
+  GemvArgs a{};
+  a.nseg = 1;
+  a.k = (int)in_dim;
+  a.total_groups = (uint32_t)(out_dim / 4);
+  a.xq = static_cast<const uint8_t*>(d_xq);
+  a.seg[0].w = static_cast<const uint8_t*>(d_w);
+  a.seg[0].y = d_out;
+  a.seg[0].g_begin = 0;
+  a.seg[0].row_lo = 0;
+  a.seg[0].row_hi = (uint32_t)out_dim;
+  hipStream_t st = pick_stream(ctx, stream);
+  const hipError_t e = interleave == 4 ? launch_gemv_x4(a, ggml_type, PRO_Q8X, EPI_STORE, st)
+                                       : launch_gemv_plain(a, ggml_type, PRO_Q8X, EPI_STORE, st);
+  return hip_check(ctx, e, "linear_q8act launch");
+}
+
 extern "C" zg_status zg_linear_fused_dev(zg_ctx* ctx, const float* d_x, const zg_segment* segs, size_t n_segs,
                                          size_t in_dim, void* stream) {
   if (!ctx) return ZG_ERR_INVALID_ARG;

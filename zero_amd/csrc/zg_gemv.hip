@@ -437,6 +437,27 @@ __device__ __forceinline__ float strip_dot(const LaneW<QT>& L, const float4* xb,
   return d * (q8u_block_dot(L.q, xb) + mterm);
 }
 
+// The same block with a Q8_0 activation block (int8 x8, fp16 scale dx,
+// sx = sum of x8): the integer dot (v_dot4_i32_i8; Q4_0 nibbles enter
+// unsigned and the -8 offset is -8 sx), then (dW dX) * isum, the per-block
+// term of zo_gemm_q8act.
+template <uint32_t QT>
+__device__ __forceinline__ float strip_dot_q8x(const LaneW<QT>& L, const uint32_t* x8, float dx, int sx) {
+  int isum = 0;
+  if (QT == Q4_0) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      isum = __builtin_amdgcn_sdot4((int)(L.q[c] & 0x0F0F0F0Fu), (int)x8[c], isum, false);
+      isum = __builtin_amdgcn_sdot4((int)((L.q[c] >> 4) & 0x0F0F0F0Fu), (int)x8[4 + c], isum, false);
+    }
+    isum -= 8 * sx;
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; c++) isum = __builtin_amdgcn_sdot4((int)L.q[c], (int)x8[c], isum, false);
+  }
+  return (half_bits_to_f32(L.d) * dx) * (float)isum;
+}
+
 // partial sums over the 4 lanes of each DPP row that share lane & 3
 __device__ __forceinline__ float row_sum4(float v) {
   v += dpp_f32<0x124>(v);  // row_ror:4
@@ -503,10 +524,19 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   // loads are issued before any of them is waited for, x first because it
   // is consumed first
   float4 xb[8], gw[8];
+  uint32_t x8[8];  // PRO_Q8X: the lane's Q8_0 activation block
+  float dxq = 0.0f;
   AttnSplitIn am;
   const int e0 = min(8 * (int)threadIdx.x, a.k - 8);  // PRO_ATTN: this thread's 8 merged dims
   if (PRO == PRO_ATTN) {
     attn_split_load(am, a.x, a.attn_ml, a.k, a.attn_hd, a.attn_nsplit, e0);
+  } else if (PRO == PRO_Q8X) {
+    const uint8_t* xbk = a.xq + (size_t)kb * 34;
+    const u32x4s2* p = reinterpret_cast<const u32x4s2*>(xbk + 2);
+    const u32x4s2 v0 = p[0], v1 = p[1];
+    x8[0] = v0.x, x8[1] = v0.y, x8[2] = v0.z, x8[3] = v0.w;
+    x8[4] = v1.x, x8[5] = v1.y, x8[6] = v1.z, x8[7] = v1.w;
+    dxq = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(xbk));
   } else {
     const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
 #pragma unroll
@@ -570,11 +600,19 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
       xb[c].w = xb[c].w * rinv * g.w;
     }
   }
-  float t = 0.0f;
+  float mterm = 0.0f;
+  int sx = 0;
+  if (PRO == PRO_Q8X) {
 #pragma unroll
-  for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
-  float mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
-  asm volatile("" : "+v"(mterm));  // computed here, not sunk below the next load
+    for (int c = 0; c < 8; c++) sx = __builtin_amdgcn_sdot4((int)x8[c], 0x01010101, sx, false);
+    asm volatile("" : "+v"(sx));  // computed here, not sunk below the next load
+  } else {
+    float t = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+    mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
+    asm volatile("" : "+v"(mterm));  // computed here, not sunk below the next load
+  }
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
 
   uint64_t key = 0;
@@ -588,7 +626,8 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
       if (base + j < items) {
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
-          const float v = row_sum4(strip_dot<QT>(L[j][p], xb, mterm));
+          const float v = row_sum4(PRO == PRO_Q8X ? strip_dot_q8x<QT>(L[j][p], x8, dxq, sx)
+                                                  : strip_dot<QT>(L[j][p], xb, mterm));
           if ((lane & 15) < 4) pb[((wave * GBATCH + j) * PARTS + p) * 16 + (lane >> 4) * 4 + r] = v;
         }
       }
@@ -964,7 +1003,11 @@ static bool tall_path_ok(const GemvArgs& a) {
 // Q4_0X4 takes the strip kernel (measured faster at every decode shape).
 template <uint32_t QT, int PRO, int EPI>
 static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
-  if constexpr (PRO == PRO_ATTN) {
+  if constexpr (PRO == PRO_Q8X) {
+    // Q8_0 activations: strip kernel only
+    if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+    return hipErrorInvalidValue;
+  } else if constexpr (PRO == PRO_ATTN) {
     // only the Q4_0 strip kernel merges attention splits
     if constexpr (QT == Q4_0) {
       if (strip_path_ok(a.k) && a.attn_nsplit >= 1 && a.attn_nsplit <= kAttnSplits && a.attn_hd % 8 == 0 &&
@@ -997,6 +1040,7 @@ static hipError_t dispatch_x4_qt(const GemvArgs& a, int pro, int epi, hipStream_
   if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_RMSNORM, EPI_SWIGLU>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_SWIGLU) return launch_x4_any<QT, PRO_PLAIN, EPI_SWIGLU>(a, st);
   if (pro == PRO_ATTN && epi == EPI_RESID) return launch_x4_any<QT, PRO_ATTN, EPI_RESID>(a, st);
+  if (pro == PRO_Q8X && epi == EPI_STORE) return launch_x4_any<QT, PRO_Q8X, EPI_STORE>(a, st);
   return hipErrorInvalidValue;
 }
 
@@ -1014,6 +1058,7 @@ static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStre
   if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_strip<QT, PRO_PLAIN, EPI_ARGMAX, 1>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_strip<QT, PRO_RMSNORM, EPI_STORE, 1>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 1>(a, st);
+  if (pro == PRO_Q8X && epi == EPI_STORE) return launch_strip<QT, PRO_Q8X, EPI_STORE, 1>(a, st);
   return hipErrorInvalidValue;
 }
 

@@ -9,7 +9,9 @@ namespace zg {
 
 // PRO_ATTN: x holds split-context attention outputs and the kernel merges
 // them into the activation vector (strip path only).
-enum Prologue : int { PRO_PLAIN = 0, PRO_RMSNORM = 1, PRO_ATTN = 2 };
+// PRO_Q8X: the activation is a row of Q8_0 blocks (GemvArgs::xq) and the
+// block dots are integer (strip kernel only).
+enum Prologue : int { PRO_PLAIN = 0, PRO_RMSNORM = 1, PRO_ATTN = 2, PRO_Q8X = 3 };
 enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3 };
 
 // One projection of a (possibly fused) X4 GEMV launch.  Groups
@@ -37,6 +39,7 @@ struct GemvArgs {
   const float* attn_ml;
   int attn_nsplit, attn_hd;
   uint32_t flags;  // kGemvStream
+  const uint8_t* xq;  // PRO_Q8X: k / 32 Q8_0 blocks (34 bytes, 2-byte aligned)
 };
 
 // The weights are streamed without allocating in the last-level cache:
@@ -69,6 +72,8 @@ hipError_t launch_gemv_x4(const GemvArgs& a, uint32_t qt, int pro, int epi, hipS
 // Plain row-major Q4_0 / Q8_0 through the strip kernel (groups = 4 rows);
 // prologue none or rmsnorm, epilogue store, residual or argmax.
 bool plain_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
+// in_dim accepted by the strip kernel: a multiple of 512 up to 8192
+bool strip_path_ok(int k);
 hipError_t launch_gemv_plain(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
 // LDS bytes the X4 streaming kernel needs for in_dim k.
 size_t gemv_x4_lds_bytes(uint32_t qt, int k);

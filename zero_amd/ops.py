@@ -239,6 +239,11 @@ class Context:
     def quantize_q8_0_split_dev(self, x, qs, d, rows, k, stream=None):
         self.check(self.lib.zg_quantize_q8_0_split_dev(self.h, _ptr(x), _ptr(qs), _ptr(d), rows, k, stream))
 
+    def linear_q8act_dev(self, xq, w, out, in_dim, out_dim, quant, interleave, stream=None):
+        """GEMV with a Q8_0-encoded activation row (34-byte blocks)."""
+        self.check(self.lib.zg_linear_q8act_dev(self.h, _ptr(xq), _ptr(w), _ptr(out), in_dim, out_dim, int(quant),
+                                                int(interleave), stream))
+
     def gemm_q8act_dev(self, qs, d, w, y, m, n, k, w_type, interleave, stream=None):
         self.check(self.lib.zg_gemm_q8act_dev(self.h, _ptr(qs), _ptr(d), _ptr(w), _ptr(y), m, n, k, int(w_type),
                                               int(interleave), stream))
