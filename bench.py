@@ -265,6 +265,25 @@ def bench_rows(ctx, steps: int):
     return out
 
 
+def _plain_copy(model):
+    """The model with plain row-major layer linears and LM head."""
+    import dataclasses
+
+    from zero_amd import synth
+
+    c = model.cfg
+    shapes = {"attn_q": (c.q_dim, c.hidden), "attn_k": (c.kv_dim, c.hidden), "attn_v": (c.kv_dim, c.hidden),
+              "attn_o": (c.hidden, c.q_dim), "ffn_gate": (c.ffn, c.hidden), "ffn_up": (c.ffn, c.hidden),
+              "ffn_down": (c.hidden, c.ffn)}
+    out = synth.RandomModel(dataclasses.replace(c, lin_interleave=1, head_interleave=1),
+                            token_embd=model.token_embd.copy(), output_norm=model.output_norm,
+                            lm_head=synth.deinterleave_x4(model.lm_head, c.vocab_padded, c.hidden, c.head_type))
+    for L in model.layers:
+        out.layers.append(dataclasses.replace(
+            L, **{k: synth.deinterleave_x4(getattr(L, k), r, kk, c.lin_type) for k, (r, kk) in shapes.items()}))
+    return out
+
+
 def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
     import numpy as np
 
@@ -290,9 +309,19 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
     ctxs = np.arange(n_prompt + 1, n_prompt + n_gen)
     per_tok = cfg.weight_bytes_per_token() + norms + float(np.mean(ctxs)) * kv_per_pos + kv_per_pos
     gm.close()
+    # the same weights in the packer's default v1 layout (plain rows for the
+    # layer linears and the LM head)
+    plain = _plain_copy(model)
+    gp = GpuModel(ctx, plain)
+    gp.generate(prompt, 8)
+    toks_p, _, t_gen_p = gp.generate(prompt, n_gen)
+    agree_p = int(np.argmin(np.concatenate([toks_p == toks, [False]])))
+    gp.close()
+    del plain
     return {"tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "prefill_tok_s": n_prompt / t_pre,
             "batched_prefill": {"prefill_tok_s": n_prompt / t_pre_b, "prefill_ms": t_pre_b * 1e3,
                                 "decode_tok_s": (n_gen - 1) / t_gen_b, "tokens_equal_to_token_by_token": agree},
+            "plain_layout": {"decode_tok_s": (n_gen - 1) / t_gen_p, "tokens_equal_to_x4": agree_p},
             "n_prompt": n_prompt,
             "n_gen": n_gen, "bytes_per_token": int(per_tok), "gbs": per_tok * tok_s / 1e9,
             "first_tokens": [int(t) for t in toks[:8]], "model": model, "prompt": prompt}
@@ -405,10 +434,13 @@ def main():
         bp = dec["batched_prefill"]
         log(f"batched prefill: {bp['prefill_ms']:.2f} ms for {dec['n_prompt']} tokens "
             f"({bp['prefill_tok_s']:.0f} tok/s; token by token {dec['prefill_tok_s']:.0f} tok/s)")
+        log(f"decode, plain v1 layout: {dec['plain_layout']['decode_tok_s']:.1f} tok/s")
         out["decode"] = {"tok_s": round(dec["tok_s"], 2), "ms_per_token": dec["ms_per_token"],
                          "prefill_tok_s": round(dec["prefill_tok_s"], 2),
                          "batched_prefill": {k: (round(v, 2) if isinstance(v, float) else v)
                                              for k, v in dec["batched_prefill"].items()},
+                         "plain_layout": {k: (round(v, 2) if isinstance(v, float) else v)
+                                          for k, v in dec["plain_layout"].items()},
                          "workload": "random-init Qwen3-1.7B shape, Q4_0X4 linears, Q8_0X4 LM head, "
                                      f"{dec['n_prompt']}-token prompt then {dec['n_gen']} greedy tokens",
                          "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,

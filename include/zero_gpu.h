@@ -196,7 +196,8 @@ typedef struct {
     uint32_t n_layers, hidden, ffn, n_q_heads, n_kv_heads, head_dim;
     uint32_t vocab_padded, vocab_real, max_ctx;
     float rms_eps, rope_theta;
-    uint32_t lin_type, lin_interleave;   /* ForwardPassDispatch quants (forward_pass.rs:191-207) */
+    uint32_t lin_type, lin_interleave;   /* ForwardPassDispatch quants (forward_pass.rs:191-207):
+                                            Q4_0 or Q8_0, X4 (4) or plain rows (1) */
     uint32_t embd_type;                  /* token_embd quant (plain layout) */
     uint32_t head_type, head_interleave; /* output.weight quant + layout */
     const void *token_embd;

@@ -247,8 +247,8 @@ class OracleModel:
         d.n_q_heads, d.n_kv_heads, d.head_dim = cfg.n_q_heads, cfg.n_kv_heads, cfg.head_dim
         d.vocab_padded, d.vocab_real, d.max_ctx = cfg.vocab_padded, cfg.vocab_real, cfg.max_ctx
         d.rms_eps, d.rope_theta = cfg.rms_eps, cfg.rope_theta
-        d.lin_type, d.lin_interleave, d.embd_type = cfg.lin_type, 4, cfg.embd_type
-        d.head_type, d.head_interleave = cfg.head_type, 4
+        d.lin_type, d.lin_interleave, d.embd_type = cfg.lin_type, cfg.lin_interleave, cfg.embd_type
+        d.head_type, d.head_interleave = cfg.head_type, cfg.head_interleave
         d.token_embd, d.lm_head, d.output_norm = (model.token_embd.ctypes.data, model.lm_head.ctypes.data,
                                                   model.output_norm.ctypes.data)
         d.layers = self._layers

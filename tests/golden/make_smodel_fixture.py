@@ -1,4 +1,4 @@
-"""Write tests/golden/tiny_qwen3_v2.smodel (and the _q8 variant) with the reference packer.
+"""Write tests/golden/tiny_qwen3_v2.smodel (and the _q8 and v1 variants) with the reference packer.
 
 Builds a tiny seeded Qwen3-shaped Hugging Face checkpoint (config.json and
 one fp32 SafeTensors file: 2 layers, hidden 128, 2 query heads and 1 KV head
@@ -13,10 +13,14 @@ token embedding, Q8_0X4 output.weight, F32 norms (silicatepack.py:799-852,
 943-1059, 1097-1161).  The packer's own `inspect` record of that file
 (header and manifest, silicatepack.py:1754-1780) is written next to it as
 tiny_qwen3_v2.inspect.json.  The `_q8` variant packs a one-layer model of
-the same shape with `--quant q8_0` (Q8_0X4 layer linears).
+the same shape with `--quant q8_0` (Q8_0X4 layer linears); the `v1` variant
+packs a one-layer model with the packer's default layout (no --interleave:
+a `.smodel`-v1 container of plain row-major Q4_0 linears and a plain Q8_0
+output.weight, silicatepack.py:1434-1450).
 
 These files are what travels; the reference and the SafeTensors input do
 not.  Usage: python tests/golden/make_smodel_fixture.py [/path/to/reference]
+[variant ...] (default: every variant)
 """
 from __future__ import annotations
 
@@ -29,8 +33,9 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-# variant -> (file stem, packer --quant, layers)
-VARIANTS = {"auto": ("tiny_qwen3_v2", "auto", 2), "q8_0": ("tiny_qwen3_v2_q8", "q8_0", 1)}
+# variant -> (file stem, packer --quant, layers, packer --interleave)
+VARIANTS = {"auto": ("tiny_qwen3_v2", "auto", 2, 4), "q8_0": ("tiny_qwen3_v2_q8", "q8_0", 1, 4),
+            "v1": ("tiny_qwen3_v1", "auto", 1, 0)}
 
 CONFIG = {
     "model_type": "qwen3",
@@ -85,13 +90,15 @@ def checkpoint(seed: int = 20241, variant: str = "auto") -> dict[str, np.ndarray
     return t
 
 
-def main(ref_root: str) -> None:
+def main(ref_root: str, only: list[str] | None = None) -> None:
     from safetensors.numpy import save_file
 
     sys.path.insert(0, str(Path(ref_root) / "tools"))
     import silicatepack  # noqa: E402  (reference packer, stdlib only)
 
-    for variant, (stem, quant, _) in VARIANTS.items():
+    for variant, (stem, quant, _, il) in VARIANTS.items():
+        if only and variant not in only:
+            continue
         out_file, out_json = HERE / f"{stem}.smodel", HERE / f"{stem}.inspect.json"
         with tempfile.TemporaryDirectory() as tmp:
             src = Path(tmp) / "hf"
@@ -99,8 +106,11 @@ def main(ref_root: str) -> None:
             (src / "config.json").write_text(json.dumps(config(variant)))
             save_file(checkpoint(variant=variant), str(src / "model.safetensors"))
             out = Path(tmp) / "tiny.smodel"
-            rc = silicatepack.main(["pack-hf", "--input-dir", str(src), "--output", str(out), "--quant", quant,
-                                    "--interleave", "4", "--payload-alignment", "4096", "--force"])
+            args = ["pack-hf", "--input-dir", str(src), "--output", str(out), "--quant", quant,
+                    "--payload-alignment", "4096", "--force"]
+            if il:
+                args += ["--interleave", str(il)]
+            rc = silicatepack.main(args)
             if rc not in (0, None):
                 raise SystemExit(f"packer failed: {rc}")
             record = silicatepack.inspect_path(out, json_output=False)
@@ -111,4 +121,4 @@ def main(ref_root: str) -> None:
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", sys.argv[2:])

@@ -8,6 +8,8 @@ Bar: the last row's hidden state and the next token's logits within rel
 1e-3 of the oracle, identical greedy tokens after the prefill; chunked calls
 (pos0 > 0) bit-identical to one call; at the Qwen3-1.7B shape, within the
 activation-quantization distance of the token-by-token pass."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -82,6 +84,81 @@ def test_q8_0_linears_and_q4_0_embedding(ctx, zo):
     finally:
         om.close()
         gm.close()
+        ctx.clear()
+
+
+@pytest.mark.parametrize("lin_type", [synth.Q4_0, synth.Q8_0])
+def test_plain_row_layouts(ctx, zo, lin_type):
+    """Plain row-major layer linears and LM head (.smodel-v1 / GGUF layouts)
+    at strip-sized dims: the rmsnorm and SwiGLU prologue/epilogue and (Q4_0)
+    the attention-split merge run in the plain strip GEMV, the prefill GEMMs
+    read plain rows."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=512, ffn=1024, n_q_heads=8, n_kv_heads=2, head_dim=64,
+                            vocab_padded=1024, vocab_real=1000, max_ctx=160, lin_type=lin_type,
+                            lin_interleave=1, head_interleave=1)
+    model = synth.random_model(cfg, seed=14)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(17, 70, cfg.vocab_real)
+        tok, _, hid = gm.prefill(prompt, want_hidden=True)
+        err = rel_err(hid, om.prefill_q8(prompt))
+        print(f"plain layout type {lin_type}: prefill hidden rel err {err:.2e}")
+        assert err <= REL_TOL and tok == om.lm_head()[1]
+        pos = len(prompt)
+        for _ in range(6):
+            nxt, _, h2, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+            h2_ref = om.forward(tok, pos)
+            rc, t2_ref, _, lg2_ref = om.lm_head()
+            assert rel_err(h2, h2_ref) <= REL_TOL and rel_err(lg, lg2_ref) <= REL_TOL
+            assert nxt == t2_ref, pos
+            tok, pos = nxt, pos + 1
+        toks, _, _ = gm.generate(prompt, 24, batched_prefill=True)
+        assert np.array_equal(toks, om.generate_batched(prompt, 24))
+        toks, _, _ = gm.generate(prompt[:20], 24)
+        assert np.array_equal(toks, om.generate(prompt[:20], 24))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
+def _x4_layers(model):
+    """The same weights with X4 layer linears (copies throughout: a host
+    array is one registry key)."""
+    c = model.cfg
+    x4 = synth.RandomModel(dataclasses.replace(c, lin_interleave=4), token_embd=model.token_embd.copy(),
+                           lm_head=model.lm_head.copy(), output_norm=model.output_norm)
+    shapes = {"attn_q": (c.q_dim, c.hidden), "attn_k": (c.kv_dim, c.hidden), "attn_v": (c.kv_dim, c.hidden),
+              "attn_o": (c.hidden, c.q_dim), "ffn_gate": (c.ffn, c.hidden), "ffn_up": (c.ffn, c.hidden),
+              "ffn_down": (c.hidden, c.ffn)}
+    for L in model.layers:
+        x4.layers.append(dataclasses.replace(
+            L, **{k: synth.interleave_x4(getattr(L, k), r, kk, c.lin_type) for k, (r, kk) in shapes.items()}))
+    return x4
+
+
+def test_qwen3_1_7b_shape_plain_layout_bit_identical(ctx):
+    """At the Qwen3-1.7B shape the plain-row Q4_0 model gives the X4 model's
+    bits: every lane of the strip GEMV reads the same block of the same row
+    in either layout, and the GEMMs are bit-exact with the oracle in both.
+    Checked on a 64-token batched prefill, then 16 decode steps."""
+    cfg = synth.ModelConfig(max_ctx=128, lin_interleave=1)
+    plain = synth.random_model(cfg, seed=3)
+    models = [GpuModel(ctx, plain), GpuModel(ctx, _x4_layers(plain))]
+    try:
+        prompt = synth.prompt(23, 64, cfg.vocab_real)
+        outs = [m.prefill(prompt, want_hidden=True) for m in models]
+        assert outs[0][0] == outs[1][0] and np.array_equal(outs[0][2], outs[1][2])
+        toks = [outs[0][0]] * 2
+        for pos in range(64, 80):
+            r = [m.step(t, pos, want_hidden=True, want_logits=True) for m, t in zip(models, toks)]
+            assert np.array_equal(r[0][2], r[1][2]) and np.array_equal(r[0][3], r[1][3]), pos
+            assert r[0][0] == r[1][0]
+            toks = [r[0][0], r[1][0]]
+    finally:
+        for m in models:
+            m.close()
         ctx.clear()
 
 

@@ -1,6 +1,7 @@
-"""A packed .smodel-v2 through the GPU path: the tiny Qwen3 artifacts that the
+"""A packed .smodel through the GPU path: the tiny Qwen3 artifacts that the
 reference packer wrote (tests/golden/tiny_qwen3_v2*.smodel: Q4_0X4 and
-Q8_0X4 layer linears) are read by
+Q8_0X4 layer linears; tiny_qwen3_v1.smodel: the packer's default v1
+layout, plain Q4_0 rows) are read by
 zg_smodel_open, registered by zg_smodel_register_all with its SIDX
 layouts, and decoded by the HIP model; the oracle decodes the same tensor
 views on the CPU.
@@ -49,7 +50,7 @@ def test_register_all_layouts(ctx, zo):
         ctx.clear()
 
 
-@pytest.mark.parametrize("stem", ["tiny_qwen3_v2", "tiny_qwen3_v2_q8"])
+@pytest.mark.parametrize("stem", ["tiny_qwen3_v2", "tiny_qwen3_v2_q8", "tiny_qwen3_v1"])
 def test_smodel_decode_matches_oracle(ctx, zo, stem):
     sm = SModel(FIX.parent / f"{stem}.smodel")
     gm = GpuModel.from_smodel(ctx, sm, max_ctx=64)

@@ -8,7 +8,8 @@ Pinned three ways:
 * byte for byte against the oracle's quantizers (themselves pinned to the
   packer's golden vectors) applied to the seeded fp32 checkpoint the
   fixture was packed from: Q4_0X4 (or, in the q8 fixture, Q8_0X4) linears,
-  Q8_0 embedding, Q8_0X4 LM head, F32 norms;
+  Q8_0 embedding, Q8_0X4 LM head, F32 norms; in the v1 fixture (the
+  packer's default layout) plain Q4_0 linears and a plain Q8_0 LM head;
 * the reference loader's rejection rules
   (kernel/src/model_loader.rs:380-575, 599-659), one patched field at a
   time, each mapped to its LoadError kind.
@@ -30,8 +31,9 @@ FIX = (GOLDEN / "tiny_qwen3_v2.smodel").read_bytes()
 REC = json.loads((GOLDEN / "tiny_qwen3_v2.inspect.json").read_text())
 MAN = REC["manifest"]
 # (fixture stem, make_smodel_fixture variant): the 2-layer --quant auto
-# artifact and the 1-layer --quant q8_0 artifact (Q8_0X4 layer linears)
-FIXTURES = [("tiny_qwen3_v2", "auto"), ("tiny_qwen3_v2_q8", "q8_0")]
+# artifact, the 1-layer --quant q8_0 artifact (Q8_0X4 layer linears) and the
+# 1-layer v1 artifact (no --interleave: plain rows)
+FIXTURES = [("tiny_qwen3_v2", "auto"), ("tiny_qwen3_v2_q8", "q8_0"), ("tiny_qwen3_v1", "v1")]
 
 DTYPE_ID = {"F32": 0, "Q8_0": 8, "Q4_0": 2, "Q4_0X4": 100, "Q8_0X4": 101}
 P0 = REC["header"]["payload_offset"]  # SIDX header position in the file
@@ -86,10 +88,13 @@ def test_tensors_match_packer_record(stem, variant):
         assert (t.payload_offset, t.byte_len) == (w["payload_offset"], w["byte_len"]), t.name
         assert t.interleave == w.get("row_interleave", 1), t.name
         assert hashlib.sha256(t.data.tobytes()).hexdigest() == w["sha256"], t.name
-    # interleaved: the 7 linears per layer and the LM head; embedding and norms plain
-    assert sum(t.interleave == 4 for t in s.tensors) == 7 * fx.VARIANTS[variant][2] + 1
+    # v2: the 7 linears per layer and the LM head interleaved, embedding and
+    # norms plain; v1: every tensor plain
+    _, _, layers, il = fx.VARIANTS[variant]
+    assert s.info.version == (2 if il else 1)
+    assert sum(t.interleave == 4 for t in s.tensors) == (7 * layers + 1 if il else 0)
     assert s["token_embd.weight"].interleave == 1 and s["output.weight"].ggml_type == Q8_0
-    assert s["blk.0.attn_q.weight"].ggml_type == (Q4_0 if variant == "auto" else Q8_0)
+    assert s["blk.0.attn_q.weight"].ggml_type == (Q8_0 if variant == "q8_0" else Q4_0)
 
 
 def test_find_uses_exact_names():
@@ -119,8 +124,11 @@ def test_tensor_bytes_rebuild_from_the_checkpoint(zo, stem, variant):
                 want = zo.interleave_x4(want, rows, cols, Q8_0)
             want = want.tobytes()
         else:
-            assert dt == "Q4_0X4"
-            want = zo.interleave_x4(zo.quantize_q4_0(x.reshape(-1)), rows, cols, Q4_0).tobytes()
+            assert dt.startswith("Q4_0")
+            want = zo.quantize_q4_0(x.reshape(-1))
+            if dt.endswith("X4"):
+                want = zo.interleave_x4(want, rows, cols, Q4_0)
+            want = want.tobytes()
         assert s[w["name"]].data.tobytes() == want, w["name"]
 
 
@@ -136,6 +144,16 @@ def test_to_model_shapes_and_views():
     assert L.q_norm.dtype == np.float32 and L.q_norm.size == 64
     # zero-copy: the arrays alias the container image
     assert np.shares_memory(m.lm_head, s.image) and np.shares_memory(L.attn_norm, s.image)
+
+
+def test_to_model_plain_layout():
+    """A v1 artifact: the model view keeps the plain row layouts."""
+    m = SModel(GOLDEN / "tiny_qwen3_v1.smodel").to_model()
+    c = m.cfg
+    assert (c.n_layers, c.lin_type, c.lin_interleave, c.head_type, c.head_interleave) == (1, Q4_0, 1, Q8_0, 1)
+    assert m.layers[0].attn_o.nbytes == 128 * 4 * 18 and m.lm_head.nbytes == 256 * 4 * 34
+    v2 = SModel(FIX).to_model().cfg
+    assert (v2.lin_interleave, v2.head_interleave) == (4, 4)
 
 
 def test_path_and_memmap_source(tmp_path):

@@ -11,6 +11,8 @@
   same numpy restatement with each matmul input quantized to Q8_0 (numpy's
   own round-half-even and binary16 rounding), and for chunk invariance.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -70,8 +72,8 @@ def _np_forward(model, tokens, q8_rows=0):
 
     inv = cfg.rope_theta ** (-2.0 * np.arange(hd // 2) / hd)
     emb = deq(model.token_embd, cfg.vocab_padded, H, cfg.embd_type, 1)
-    head = deq(model.lm_head, cfg.vocab_padded, H, cfg.head_type, 4)
-    Ws = [{k: deq(getattr(L, k), *shape, cfg.lin_type, 4) for k, shape in
+    head = deq(model.lm_head, cfg.vocab_padded, H, cfg.head_type, cfg.head_interleave)
+    Ws = [{k: deq(getattr(L, k), *shape, cfg.lin_type, cfg.lin_interleave) for k, shape in
            (("attn_q", (cfg.q_dim, H)), ("attn_k", (cfg.kv_dim, H)), ("attn_v", (cfg.kv_dim, H)),
             ("attn_o", (H, cfg.q_dim)), ("ffn_gate", (cfg.ffn, H)), ("ffn_up", (cfg.ffn, H)),
             ("ffn_down", (H, cfg.ffn)))} for L in model.layers]
@@ -112,9 +114,11 @@ def _np_forward(model, tokens, q8_rows=0):
     return np.array(logits)
 
 
-def test_model_forward_vs_numpy(zo):
+@pytest.mark.parametrize("il", [4, 1])
+def test_model_forward_vs_numpy(zo, il):
+    """X4 (.smodel-v2) and plain-row (v1) layer linears and LM head."""
     cfg = synth.ModelConfig(n_layers=2, hidden=128, ffn=256, n_q_heads=4, n_kv_heads=2, head_dim=32,
-                            vocab_padded=256, vocab_real=250, max_ctx=16)
+                            vocab_padded=256, vocab_real=250, max_ctx=16, lin_interleave=il, head_interleave=il)
     model = synth.random_model(cfg, seed=2)
     toks = [3, 17, 101, 5, 5, 42]
     ref = _np_forward(model, toks)
@@ -139,8 +143,9 @@ def test_np_q8_matches_the_oracle_quantizer(zo):
     assert np.array_equal(_np_q8(x.astype(np.float64)).astype(np.float32), want)
 
 
-def test_prefill_q8_vs_numpy(zo):
-    model = synth.random_model(PREFILL_CFG, seed=4)
+@pytest.mark.parametrize("il", [4, 1])
+def test_prefill_q8_vs_numpy(zo, il):
+    model = synth.random_model(dataclasses.replace(PREFILL_CFG, lin_interleave=il, head_interleave=il), seed=4)
     toks = [3, 17, 101, 5, 5, 42, 9, 200, 7]
     n = 7  # prefill 7 tokens, then decode the last two one by one
     ref = _np_forward(model, toks, q8_rows=n)

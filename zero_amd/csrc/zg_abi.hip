@@ -320,16 +320,39 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
   return hip_check(ctx, launch_gemv_generic(g, st), "gemv_generic launch");
 }
 
-// Fused same-x dispatch: one pair launch over the concatenated group space
-// when every segment qualifies, else one launch per segment.
+// run_fused's one-launch forms: X4 segments through the X4 kernels, plain
+// row-major Q4_0 / Q8_0 segments through the strip kernel (rmsnorm or plain
+// prologue)
+bool zg::fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k) {
+  bool ok = nseg >= 1 && nseg <= 3;
+  for (size_t i = 0; i < nseg && ok; i++)
+    ok = pair_path_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
+  return ok;
+}
+
+bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro) {
+  bool ok = nseg >= 1 && nseg <= 3 && (pro == PRO_PLAIN || pro == PRO_RMSNORM);
+  for (size_t i = 0; i < nseg && ok; i++)
+    ok = plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
+  return ok;
+}
+
+// Whether run_linear takes a rmsnorm prologue inside the GEMV kernel (else
+// it normalizes into the context's aux buffer first).
+bool zg::rmsnorm_fused_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x, int epi) {
+  if (pair_path_ok(qt, il, k, n, w, x)) return true;
+  return plain_strip_ok(qt, il, k, n, w, x) && (epi == EPI_STORE || epi == EPI_ARGMAX);
+}
+
+// Fused same-x dispatch: one launch over the concatenated group space when
+// every segment qualifies, else one launch per segment.
 zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                         const float* norm_w, float eps, int epi, hipStream_t st) {
-  bool pair = nseg >= 1 && nseg <= 3;
-  for (size_t i = 0; i < nseg && pair; i++)
-    pair = pair_path_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
-  if (epi == EPI_SWIGLU && !(pair && nseg == 2 && segs[0].n == segs[1].n))
-    return set_error(ctx, ZG_ERR_INVALID_ARG, "swiglu fusion needs two equal X4 segments");
-  if (pair) {
+  const bool pair = fused_x4_ok(x, segs, nseg, k);
+  const bool plain = !pair && fused_plain_ok(x, segs, nseg, k, pro);
+  if (epi == EPI_SWIGLU && !((pair || plain) && nseg == 2 && segs[0].n == segs[1].n))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "swiglu fusion needs two equal Q4_0/Q8_0 segments on a one-launch path");
+  if (pair || plain) {
     GemvArgs a{};
     a.nseg = (int)nseg;
     a.k = (int)k;
@@ -347,7 +370,8 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
       g += (uint32_t)(segs[i].n / 4);
     }
     a.total_groups = g;
-    return hip_check(ctx, launch_gemv_x4(a, segs[0].qt, pro, epi, st), "fused gemv launch");
+    return hip_check(ctx, pair ? launch_gemv_x4(a, segs[0].qt, pro, epi, st) : launch_gemv_plain(a, segs[0].qt, pro, epi, st),
+                     "fused gemv launch");
   }
   for (size_t i = 0; i < nseg; i++) {
     zg_status s = run_linear(ctx, x, segs[i].w, segs[i].y, k, segs[i].n, segs[i].qt, segs[i].il, 0, segs[i].n,
@@ -361,8 +385,10 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
 // split merge in the strip kernel's prologue.
 zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd,
                          const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st) {
-  if (!attn_merge_gemv_ok(qt, il, k) || !pair_path_ok(qt, il, k, n, w, part_o))
-    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0X4 and a strip-sized in_dim");
+  const bool x4 = il == 4;
+  if (!attn_merge_gemv_ok(qt, il, k) ||
+      !(x4 ? pair_path_ok(qt, il, k, n, w, part_o) : plain_strip_ok(qt, il, k, n, w, part_o)))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0 weights and a strip-sized in_dim");
   GemvArgs a{};
   a.nseg = 1;
   a.k = (int)k;
@@ -377,7 +403,8 @@ zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml,
   a.seg[0].g_begin = 0;
   a.seg[0].row_lo = 0;
   a.seg[0].row_hi = (uint32_t)n;
-  return hip_check(ctx, launch_gemv_x4(a, qt, PRO_ATTN, EPI_RESID, st), "attention-merge gemv launch");
+  return hip_check(ctx, x4 ? launch_gemv_x4(a, qt, PRO_ATTN, EPI_RESID, st) : launch_gemv_plain(a, qt, PRO_ATTN, EPI_RESID, st),
+                   "attention-merge gemv launch");
 }
 
 // ---------------------------------------------------------------------------

@@ -72,6 +72,9 @@ zg_status check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n)
 zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,
                      uint32_t il, size_t start, size_t end, int epi, const float* resid, uint64_t* best, int pro,
                      const float* norm_w, float eps, hipStream_t st, uint32_t gemv_flags = 0);
+bool rmsnorm_fused_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x, int epi);
+bool fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k);
+bool fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro);
 zg_status run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                     const float* norm_w, float eps, int epi, hipStream_t st);
 zg_status run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd, const uint8_t* w,

@@ -531,6 +531,16 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
 
 // One row of n per workgroup: silu(g) * u with the decode epilogue's operand
 // order (activation.rs:115-148: g / (1 + exp(-g)), then * up), Q8_0-encoded.
+// act = silu(act) * up in place (activation.rs:115-148 operand order), for
+// decode steps whose gate and up projections are separate launches
+__global__ __launch_bounds__(256) void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const float gv = g[i];
+    g[i] = (gv / (1.0f + expf(-gv))) * u[i];
+  }
+}
+
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                            int8_t* __restrict__ qs, uint16_t* __restrict__ qd, int n) {
   const size_t row = blockIdx.x;
@@ -587,6 +597,8 @@ struct zg_model {
   float* rope_cs = nullptr;  // this position's RoPE cos/sin table [head_dim]
   float* kv = nullptr;
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
+  float* xn = nullptr;  // rmsnorm output where a GEMV has no rmsnorm prologue [hidden]
+  float* up = nullptr;  // up projection where gate|up is not one launch [ffn]
   float* logits = nullptr;
   float* part_o = nullptr;   // attention split outputs [nsplit][nq*HD]
   float* part_ml = nullptr;  // attention split (max, exp-sum) [nsplit][nq]
@@ -598,6 +610,8 @@ struct zg_model {
   size_t out_cap = 0;
   int nsplit = 1, split_len = 0;
   bool o_merge = false;  // the O GEMV merges the attention splits itself
+  bool qkv_one = false, gu_one = false;  // Q|K|V, gate|up (SwiGLU) as one rmsnorm GEMV launch
+  bool head_norm = false;                // the LM-head GEMV takes the output rmsnorm itself
   std::vector<void*> owned;  // device allocations to free
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
@@ -649,6 +663,27 @@ static zg_status weight_dev(zg_model* m, const void* key, uint32_t qt, uint32_t 
   return ZG_OK;
 }
 
+// rmsnorm of x into m->xn, for GEMVs without a rmsnorm prologue (the
+// model's own buffer: a captured graph must not hold context scratch, which
+// a later call may reallocate)
+static zg_status model_rmsnorm(zg_model* m, const float* x, const float* gain, hipStream_t st) {
+  return hip_check(m->ctx, launch_rmsnorm(x, gain, m->xn, (int)m->d.hidden, m->d.rms_eps, st), "rmsnorm launch");
+}
+
+// Output rmsnorm + LM head + argmax of the hidden state x.
+static zg_status head_argmax(zg_model* m, const float* x, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  const float* xin = x;
+  if (!m->head_norm) {
+    zg_status s = model_rmsnorm(m, x, m->out_norm, st);
+    if (s) return s;
+    xin = m->xn;
+  }
+  return run_linear(m->ctx, xin, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type, d.head_interleave, 0,
+                    d.vocab_padded, EPI_ARGMAX, nullptr, m->best, m->head_norm ? PRO_RMSNORM : PRO_PLAIN, m->out_norm,
+                    d.rms_eps, st, kGemvStream);
+}
+
 // Record the per-token sequence on the context stream.
 static zg_status record_layers(zg_model* m, hipStream_t st) {
   const zg_model_desc& d = m->d;
@@ -662,10 +697,14 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)HD);
   for (uint32_t l = 0; l < d.n_layers; l++) {
     const ZLayer& L = m->layers[l];
-    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, d.lin_type, 4},
-                       {L.k, m->k, (size_t)kvd, d.lin_type, 4},
-                       {L.v, m->v, (size_t)kvd, d.lin_type, 4}};
-    if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
+    const uint32_t lt = d.lin_type, il = d.lin_interleave;
+    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, lt, il}, {L.k, m->k, (size_t)kvd, lt, il}, {L.v, m->v, (size_t)kvd, lt, il}};
+    if (m->qkv_one) {
+      if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
+    } else {
+      if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
+      if ((s = run_fused(ctx, m->xn, qkv, 3, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
+    }
     AttnArgs aa{};
     aa.q = m->q;
     aa.k = m->k;
@@ -689,7 +728,7 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
     if (m->o_merge) {
-      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, d.lin_type, 4, st)))
+      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, lt, il, st)))
         return s;
     } else {
       if (m->nsplit > 1) {
@@ -698,14 +737,22 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
                            qd, HD, m->nsplit, m->attn);
         if ((s = hip_check(ctx, hipGetLastError(), "attention merge launch"))) return s;
       }
-      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
-                          PRO_PLAIN, nullptr, 0.0f, st)))
+      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, lt, il, 0, H, EPI_RESID, m->hidden, nullptr, PRO_PLAIN,
+                          nullptr, 0.0f, st)))
         return s;
     }
-    FusedDev gu[2] = {{L.gate, m->act, (size_t)F, d.lin_type, 4}, {L.up, nullptr, (size_t)F, d.lin_type, 4}};
-    if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
-    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, d.lin_type, 4, 0, H, EPI_RESID, m->hidden, nullptr,
-                        PRO_PLAIN, nullptr, 0.0f, st)))
+    if (m->gu_one) {
+      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, lt, il}, {L.up, nullptr, (size_t)F, lt, il}};
+      if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
+    } else {
+      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, lt, il}, {L.up, m->up, (size_t)F, lt, il}};
+      if ((s = model_rmsnorm(m, m->hidden, L.ffn_norm, st))) return s;
+      if ((s = run_fused(ctx, m->xn, gu, 2, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
+      hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, st, m->act, m->up, F);
+      if ((s = hip_check(ctx, hipGetLastError(), "swiglu launch"))) return s;
+    }
+    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, lt, il, 0, H, EPI_RESID, m->hidden, nullptr, PRO_PLAIN,
+                        nullptr, 0.0f, st)))
       return s;
   }
   return ZG_OK;
@@ -722,9 +769,7 @@ static zg_status record_step(zg_model* m, hipStream_t st) {
   const zg_model_desc& d = m->d;
   zg_status s = record_layers(m, st);
   if (s) return s;
-  s = run_linear(m->ctx, m->hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
-                           d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM,
-                           m->out_norm, d.rms_eps, st, kGemvStream);
+  s = head_argmax(m, m->hidden, st);
   if (s) return s;
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
   return hip_check(m->ctx, hipGetLastError(), "finalize launch");
@@ -782,7 +827,7 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
   const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
   const int nq = (int)d.n_q_heads, nkv = (int)d.n_kv_heads;
   const size_t qd = (size_t)nq * HD, kvd = (size_t)nkv * HD;
-  const uint32_t lt = d.lin_type;
+  const uint32_t lt = d.lin_type, il = d.lin_interleave;
   hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(256), 0, st, m->embd, d.embd_type, H, d_tokens,
                      m->pf_x, m->best);
   zg_status s = hip_check(ctx, hipGetLastError(), "prefill embed launch");
@@ -795,7 +840,7 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
                        m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
     const GemmSegDev qkv[3] = {{L.q, m->pf_q, qd}, {L.k, m->pf_k, kvd}, {L.v, m->pf_v, kvd}};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, qkv, 3, n, H, lt, 4, false, st))) break;
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, qkv, 3, n, H, lt, il, false, st))) break;
     QkStoreArgs qa{m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm, m->inv_freq, kc, vc, nq, nkv, (int)pos0, d.rms_eps};
     const dim3 qg((unsigned)n, (unsigned)(nq + nkv));
     if (HD == 128) hipLaunchKernelGGL(qk_rope_store_kernel<128>, qg, dim3(64), 0, st, qa);
@@ -822,17 +867,17 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     else hipLaunchKernelGGL((attn_split_kernel<64, true>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill attention launch"))) break;
     const GemmSegDev o{L.o, m->pf_x, (size_t)H};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &o, 1, n, qd, lt, 4, true, st))) break;
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &o, 1, n, qd, lt, il, true, st))) break;
     hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_qs,
                        m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
     const GemmSegDev gu[2] = {{L.gate, m->pf_g, (size_t)F}, {L.up, m->pf_u, (size_t)F}};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, gu, 2, n, H, lt, 4, false, st))) break;
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, gu, 2, n, H, lt, il, false, st))) break;
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_qs, m->pf_qd,
                        F);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill swiglu launch"))) break;
     const GemmSegDev dn{L.down, m->pf_x, (size_t)H};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &dn, 1, n, F, lt, 4, true, st))) break;
+    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &dn, 1, n, F, lt, il, true, st))) break;
   }
   return s;
 }
@@ -850,9 +895,7 @@ static zg_status prefill_run(zg_model* m, size_t off, size_t n, uint32_t pos0, s
     s = prefill_chunk(m, m->prompt + off + c, rows, pos0 + (uint32_t)c, st);
   }
   if (s) return s;
-  s = run_linear(m->ctx, m->pf_x + (rows - 1) * d.hidden, m->head, m->logits, d.hidden, d.vocab_padded, d.head_type,
-                 d.head_interleave, 0, d.vocab_padded, EPI_ARGMAX, nullptr, m->best, PRO_RMSNORM, m->out_norm,
-                 d.rms_eps, st, kGemvStream);
+  s = head_argmax(m, m->pf_x + (rows - 1) * d.hidden, st);
   if (s) return s;
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
   *last_rows = rows;
@@ -868,8 +911,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       d.n_q_heads / d.n_kv_heads > (uint32_t)kMaxG || (d.head_dim != 128 && d.head_dim != 64) || d.max_ctx == 0 ||
       d.vocab_real > d.vocab_padded || d.vocab_padded == 0)
     return set_error(ctx, ZG_ERR_INVALID_ARG, "model: unsupported dimensions");
-  if (d.lin_interleave != 4 || (d.lin_type != ZG_Q4_0 && d.lin_type != ZG_Q8_0))
-    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: layer linears must be Q4_0X4 or Q8_0X4");
+  if ((d.lin_interleave != 4 && d.lin_interleave != 1) || (d.lin_type != ZG_Q4_0 && d.lin_type != ZG_Q8_0))
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: layer linears must be Q4_0 or Q8_0, plain or X4");
   if (d.embd_type != ZG_Q4_0 && d.embd_type != ZG_Q8_0)
     return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: token_embd must be plain Q4_0 or Q8_0");
   const size_t qd = (size_t)d.n_q_heads * d.head_dim, kvd = (size_t)d.n_kv_heads * d.head_dim;
@@ -898,13 +941,13 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null norm weight");
       break;
     }
-    if ((s = weight_dev(m, W.attn_q, d.lin_type, 4, qd, H, &L.q))) break;
-    if ((s = weight_dev(m, W.attn_k, d.lin_type, 4, kvd, H, &L.k))) break;
-    if ((s = weight_dev(m, W.attn_v, d.lin_type, 4, kvd, H, &L.v))) break;
-    if ((s = weight_dev(m, W.attn_o, d.lin_type, 4, H, qd, &L.o))) break;
-    if ((s = weight_dev(m, W.ffn_gate, d.lin_type, 4, F, H, &L.gate))) break;
-    if ((s = weight_dev(m, W.ffn_up, d.lin_type, 4, F, H, &L.up))) break;
-    if ((s = weight_dev(m, W.ffn_down, d.lin_type, 4, H, F, &L.down))) break;
+    if ((s = weight_dev(m, W.attn_q, d.lin_type, d.lin_interleave, qd, H, &L.q))) break;
+    if ((s = weight_dev(m, W.attn_k, d.lin_type, d.lin_interleave, kvd, H, &L.k))) break;
+    if ((s = weight_dev(m, W.attn_v, d.lin_type, d.lin_interleave, kvd, H, &L.v))) break;
+    if ((s = weight_dev(m, W.attn_o, d.lin_type, d.lin_interleave, H, qd, &L.o))) break;
+    if ((s = weight_dev(m, W.ffn_gate, d.lin_type, d.lin_interleave, F, H, &L.gate))) break;
+    if ((s = weight_dev(m, W.ffn_up, d.lin_type, d.lin_interleave, F, H, &L.up))) break;
+    if ((s = weight_dev(m, W.ffn_down, d.lin_type, d.lin_interleave, H, F, &L.down))) break;
     if ((s = upload_f32(m, &L.attn_norm, W.attn_norm, H))) break;
     if ((s = upload_f32(m, &L.ffn_norm, W.ffn_norm, H))) break;
     if ((s = upload_f32(m, &L.q_norm, W.q_norm, d.head_dim))) break;
@@ -930,7 +973,6 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     const uint32_t per = (d.max_ctx + kAttnSplits - 1) / kAttnSplits;
     m->split_len = (int)(per < 32 ? 32 : (per + 31) / 32 * 32);
     m->nsplit = (int)((d.max_ctx + m->split_len - 1) / m->split_len);
-    m->o_merge = m->nsplit > 1 && attn_merge_gemv_ok(d.lin_type, 4, qd);
   }
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->kv), (size_t)d.n_layers * 2 * d.max_ctx * kvd * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->rope_cs), d.head_dim * sizeof(float));
@@ -949,9 +991,26 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   m->out_cap = d.max_ctx;
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->prompt), m->prompt_cap * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->out_tokens), m->out_cap * sizeof(uint32_t));
-  // the generic LM-head path normalizes into the context's aux buffer;
-  // allocate it before capture (no allocation inside a captured stream)
-  if (!s) s = ensure_buf(ctx, ctx->d_aux, H * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->xn), H * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->up), F * sizeof(float));
+  if (!s) {
+    // which GEMVs are one launch with the rmsnorm (or attention-merge)
+    // prologue: X4 weights, or plain Q4_0 / Q8_0 at a strip-sized in_dim;
+    // one choice for every layer, so every layer's pointers must qualify
+    const uint32_t lt = d.lin_type, il = d.lin_interleave;
+    bool qkv = true, gu = true, om = m->nsplit > 1 && attn_merge_gemv_ok(lt, il, qd);
+    for (const ZLayer& Li : m->layers) {
+      const FusedDev q3[3] = {{Li.q, m->q, qd, lt, il}, {Li.k, m->k, kvd, lt, il}, {Li.v, m->v, kvd, lt, il}};
+      const FusedDev g2[2] = {{Li.gate, m->act, F, lt, il}, {Li.up, nullptr, F, lt, il}};
+      qkv = qkv && (fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM));
+      gu = gu && (fused_x4_ok(m->hidden, g2, 2, H) || fused_plain_ok(m->hidden, g2, 2, H, PRO_RMSNORM));
+      om = om && (il == 4 ? pair_path_ok(lt, il, qd, H, Li.o, m->part_o) : plain_strip_ok(lt, il, qd, H, Li.o, m->part_o));
+    }
+    m->qkv_one = qkv;
+    m->gu_one = gu;
+    m->o_merge = om;
+    m->head_norm = rmsnorm_fused_ok(d.head_type, d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
+  }
   if (!s) s = capture(m, record_prefill, &m->g_prefill);
   if (!s) s = capture(m, record_step, &m->g_step);
   if (s) {

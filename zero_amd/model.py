@@ -27,9 +27,9 @@ class GpuModel:
         if register:
             for L in model.layers:
                 for w in (L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down):
-                    ctx.register(w, cfg.lin_type, 4)
+                    ctx.register(w, cfg.lin_type, cfg.lin_interleave)
             ctx.register(model.token_embd, cfg.embd_type, 1)
-            ctx.register(model.lm_head, cfg.head_type, 4)
+            ctx.register(model.lm_head, cfg.head_type, cfg.head_interleave)
         self._layers = (_lib.zg_layer_weights * cfg.n_layers)()
         for i, L in enumerate(model.layers):
             self._layers[i] = _lib.zg_layer_weights(
@@ -41,9 +41,9 @@ class GpuModel:
         d.n_q_heads, d.n_kv_heads, d.head_dim = cfg.n_q_heads, cfg.n_kv_heads, cfg.head_dim
         d.vocab_padded, d.vocab_real, d.max_ctx = cfg.vocab_padded, cfg.vocab_real, cfg.max_ctx
         d.rms_eps, d.rope_theta = cfg.rms_eps, cfg.rope_theta
-        d.lin_type, d.lin_interleave = cfg.lin_type, 4
+        d.lin_type, d.lin_interleave = cfg.lin_type, cfg.lin_interleave
         d.embd_type = cfg.embd_type
-        d.head_type, d.head_interleave = cfg.head_type, 4
+        d.head_type, d.head_interleave = cfg.head_type, cfg.head_interleave
         d.token_embd = model.token_embd.ctypes.data
         d.lm_head = model.lm_head.ctypes.data
         d.output_norm = model.output_norm.ctypes.data

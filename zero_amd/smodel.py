@@ -171,7 +171,8 @@ class SModel:
             max_ctx=min(ctx_len, max_ctx) if max_ctx else ctx_len,
             rms_eps=float(i.layer_norm_rms_epsilon), rope_theta=float(i.rope_freq_base),
             lin_type=self["blk.0.attn_q.weight"].ggml_type, embd_type=self["token_embd.weight"].ggml_type,
-            head_type=head.ggml_type)
+            head_type=head.ggml_type, lin_interleave=self["blk.0.attn_q.weight"].interleave,
+            head_interleave=head.interleave)
 
     def _quant(self, name: str, rows: int, cols: int, qtype: int, interleave: int) -> np.ndarray:
         if name not in self:
@@ -196,26 +197,27 @@ class SModel:
 
     def to_model(self, max_ctx: int | None = None) -> RandomModel:
         """The dense Qwen3 tensors as the model object GpuModel and the
-        oracle take: X4 layer linears of one quant type, plain token
-        embedding, X4 LM head, F32 norms.  Arrays are views of the file."""
+        oracle take: layer linears of one quant type and one layout (X4 in a
+        v2 artifact, plain rows in v1), plain token embedding, the LM head in
+        its own layout, F32 norms.  Arrays are views of the file."""
         cfg = self.config(max_ctx)
         H, F, qd, kvd, hd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim, cfg.head_dim
-        lt = cfg.lin_type
+        lt, il = cfg.lin_type, cfg.lin_interleave
         m = RandomModel(cfg)
         for b in range(cfg.n_layers):
             p = f"blk.{b}."
             m.layers.append(Layer(
-                attn_q=self._quant(p + "attn_q.weight", qd, H, lt, 4),
-                attn_k=self._quant(p + "attn_k.weight", kvd, H, lt, 4),
-                attn_v=self._quant(p + "attn_v.weight", kvd, H, lt, 4),
-                attn_o=self._quant(p + "attn_output.weight", H, qd, lt, 4),
-                ffn_gate=self._quant(p + "ffn_gate.weight", F, H, lt, 4),
-                ffn_up=self._quant(p + "ffn_up.weight", F, H, lt, 4),
-                ffn_down=self._quant(p + "ffn_down.weight", H, F, lt, 4),
+                attn_q=self._quant(p + "attn_q.weight", qd, H, lt, il),
+                attn_k=self._quant(p + "attn_k.weight", kvd, H, lt, il),
+                attn_v=self._quant(p + "attn_v.weight", kvd, H, lt, il),
+                attn_o=self._quant(p + "attn_output.weight", H, qd, lt, il),
+                ffn_gate=self._quant(p + "ffn_gate.weight", F, H, lt, il),
+                ffn_up=self._quant(p + "ffn_up.weight", F, H, lt, il),
+                ffn_down=self._quant(p + "ffn_down.weight", H, F, lt, il),
                 attn_norm=self._f32(p + "attn_norm.weight", H), ffn_norm=self._f32(p + "ffn_norm.weight", H),
                 q_norm=self._f32(p + "attn_q_norm.weight", hd), k_norm=self._f32(p + "attn_k_norm.weight", hd)))
         # one row per token id the LM head can emit
         m.token_embd = self._quant("token_embd.weight", cfg.vocab_padded, H, cfg.embd_type, 1)
-        m.lm_head = self._quant("output.weight", cfg.vocab_padded, H, cfg.head_type, 4)
+        m.lm_head = self._quant("output.weight", cfg.vocab_padded, H, cfg.head_type, cfg.head_interleave)
         m.output_norm = self._f32("output_norm.weight", H)
         return m

@@ -115,6 +115,8 @@ class ModelConfig:
     lin_type: int = Q4_0
     embd_type: int = Q8_0
     head_type: int = Q8_0
+    lin_interleave: int = 4   # 4: Q4_0X4/Q8_0X4 layer linears (.smodel-v2); 1: plain rows (v1, GGUF)
+    head_interleave: int = 4
 
     @property
     def q_dim(self):
@@ -163,13 +165,13 @@ class RandomModel:
 
 
 def random_model(cfg: ModelConfig, seed: int = 0) -> RandomModel:
-    """Random-init weights of the given shape: X4 layer linears, plain
-    token_embd, X4 LM head with the padding rows (vocab_real..vocab_padded)
-    zeroed so that an argmax can never land there, fp32 norm gains
-    1 + 0.05 N(0,1)."""
+    """Random-init weights of the given shape: layer linears and LM head in
+    the configured layouts (X4 by default), plain token_embd, the LM head's
+    padding rows (vocab_real..vocab_padded) zeroed so that an argmax can
+    never land there, fp32 norm gains 1 + 0.05 N(0,1)."""
     rng = np.random.default_rng(seed)
     H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
-    lt = cfg.lin_type
+    lt, il = cfg.lin_type, cfg.lin_interleave
 
     def gain(n):
         return (1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32)
@@ -177,15 +179,15 @@ def random_model(cfg: ModelConfig, seed: int = 0) -> RandomModel:
     m = RandomModel(cfg)
     for _ in range(cfg.n_layers):
         m.layers.append(Layer(
-            attn_q=weight(rng, lt, qd, H, 4), attn_k=weight(rng, lt, kvd, H, 4), attn_v=weight(rng, lt, kvd, H, 4),
-            attn_o=weight(rng, lt, H, qd, 4), ffn_gate=weight(rng, lt, F, H, 4), ffn_up=weight(rng, lt, F, H, 4),
-            ffn_down=weight(rng, lt, H, F, 4), attn_norm=gain(H), ffn_norm=gain(H), q_norm=gain(cfg.head_dim),
+            attn_q=weight(rng, lt, qd, H, il), attn_k=weight(rng, lt, kvd, H, il), attn_v=weight(rng, lt, kvd, H, il),
+            attn_o=weight(rng, lt, H, qd, il), ffn_gate=weight(rng, lt, F, H, il), ffn_up=weight(rng, lt, F, H, il),
+            ffn_down=weight(rng, lt, H, F, il), attn_norm=gain(H), ffn_norm=gain(H), q_norm=gain(cfg.head_dim),
             k_norm=gain(cfg.head_dim)))
     m.token_embd = weight(rng, cfg.embd_type, cfg.vocab_padded, H, 1)
     head_plain = weight(rng, cfg.head_type, cfg.vocab_padded, H, 1)
     bb, nb = BLOCK_BYTES[cfg.head_type], H // 32
     head_plain.reshape(cfg.vocab_padded, nb * bb)[cfg.vocab_real:] = 0
-    m.lm_head = interleave_x4(head_plain, cfg.vocab_padded, H, cfg.head_type)
+    m.lm_head = interleave_x4(head_plain, cfg.vocab_padded, H, cfg.head_type) if cfg.head_interleave == 4 else head_plain
     m.output_norm = gain(H)
     return m
 
