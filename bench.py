@@ -204,6 +204,21 @@ def bench_rows(ctx, steps: int):
         out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
         del wd
 
+    # the headline kernel on taller Q4_0X4 matrices (8x the headline rows, and
+    # the LM head's height): the same strip GEMV with more bytes per launch
+    for name, key, rows in (("Q4_0X4 49152x2048 (8x the headline rows)", "q4_0x4_49152x2048", 49152),
+                            ("Q4_0X4 151936x2048 (LM-head height)", "q4_0x4_151936x2048", 151_936)):
+        wh = synth.weight(rng, synth.Q4_0, rows, H, 4)
+        wd, c = rotating(wh)
+        yk = torch.empty(rows, device="cuda")
+
+        def tall(i, st, wd=wd, yk=yk, rows=rows):
+            ctx.linear_dev(x, wd[i], yk, H, rows, synth.Q4_0, 4, stream=st)
+
+        per, n, _ = _graph_time(tall, c, max(40, steps // 20), 8)
+        out[key] = _row(name, per, wh.nbytes + 4 * H + 4 * rows, n, c)
+        del wd, wh
+
     # k-quants at Llama-3-8B FFN shapes
     for name, qt, rows, k in (("Q4_K 14336x4096 (gate/up)", synth.Q4K, 14336, 4096),
                               ("Q6_K 4096x14336 (down)", synth.Q6K, 4096, 14336)):

@@ -110,6 +110,7 @@ GEMV_CASES = [
     (Q8_0, 4, 32768, 512),   # tall Q8_0X4 (LM-head strip path): one strip, four waves per strip
     (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
     (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
+    (Q4_0, 4, 151936, 2048), # tall Q4_0X4: four groups per batch, batches looped over
     # DeepSeek2 / Kimi K2 projections through linear_dispatch_avx512
     # (kernel/src/inference_avx512.rs:2101-2825): MLA kv_a_mqa, q_a, q_b,
     # the kv_b decompressions, o_proj and the MoE expert FFN, Q4_0 as GGUF

@@ -117,7 +117,9 @@ struct GemmStage {
   uint32_t wd[NW];
 };
 
-template <uint32_t WT, int IL, int BM, int BK>
+// FULL: the whole tile lies inside the matrix and k is a whole number of
+// stages, so every load is in bounds and none is guarded
+template <uint32_t WT, int IL, int BM, int BK, bool FULL>
 __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const GemmArgs& a, const uint8_t* w, int ns,
                                                 int m0, int n0, int b0, int tid) {
   using St = GemmStage<WT, BM, BK>;
@@ -127,13 +129,14 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
     const int c = tid + 256 * i, row = c / (BK * 2), ch = c % (BK * 2);
     const int gm = m0 + row, kb = b0 + ch / 2;
     S.a[i] = u32x4{0, 0, 0, 0};
-    if (gm < a.m && kb < nb) S.a[i] = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
+    if (FULL || (gm < a.m && kb < nb))
+      S.a[i] = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
   }
 #pragma unroll
   for (int i = 0; i < St::ND; i++) {
     const int c = tid + 256 * i, row = c / BK, kk = c % BK;
     const int gm = m0 + row, kb = b0 + kk;
-    S.ad[i] = (row < BM && gm < a.m && kb < nb) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
+    S.ad[i] = (row < BM && (FULL || (gm < a.m && kb < nb))) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
   }
 #pragma unroll
   for (int i = 0; i < St::NW; i++) {
@@ -142,7 +145,7 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
 #pragma unroll
     for (int j = 0; j < St::QW; j++) S.q[i][j] = 0;
     S.wd[i] = 0;
-    if (gn < ns && kb < nb) {
+    if (FULL || (gn < ns && kb < nb)) {
       const uint8_t* dp;
       const uint8_t* qp;
       if (IL == 4) {
@@ -225,7 +228,7 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S,
 //                 256 K per stage halves the trips (128-token prefill 3.72
 //                 ms vs 4.24 with 4-block stages; 16-block stages, at one
 //                 workgroup per CU, were slower still)
-template <uint32_t WT, int IL, int BM, int BK>
+template <uint32_t WT, int IL, int BM, int BK, bool FULL>
 __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   constexpr int MI = BM / 32;  // 16-row MFMA tiles per wave
   constexpr int R = lds_row<BK>();
@@ -255,12 +258,12 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
   GemmStage<WT, BM, BK> S;
-  gemm_stage_load<WT, IL, BM, BK>(S, a, w, ns, m0, n0, 0, tid);
+  gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, 0, tid);
   gemm_stage_store<WT, BM, BK>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
   for (int st = 0; st < nst; st++) {
     const int buf = st & 1;
-    if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
+    if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
     // blocks past k in the last stage hold zero quants and scales: they add
@@ -366,10 +369,16 @@ static int gemm_cu_count() {
 #endif
 constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row tile
 
+// Every tile full (m a multiple of the tile rows, each segment's width a
+// multiple of 64, k a whole number of stages): the kernel form with
+// unguarded loads.
 template <uint32_t WT, int IL, int BM, int BK>
 static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK>), grid, dim3(256), 0, st, a);
+  bool full = a.m % BM == 0 && (a.k / 32) % BK == 0;
+  for (int i = 0, lo = 0; i < a.nseg; lo = a.seg_end[i], i++) full = full && (a.seg_end[i] - lo) % kBN == 0;
+  if (full) hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, true>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, false>), grid, dim3(256), 0, st, a);
 }
 
 // Checks and launches one Q8_0-activation GEMM over 1..3 weight segments.
