@@ -109,6 +109,47 @@ def test_attention_split_geometries(ctx, zo, n_q, n_kv, hd, max_ctx, n_gen):
     ctx.clear()
 
 
+@pytest.mark.parametrize("head_type", [synth.Q6K, synth.Q4K])
+def test_kquant_lm_head(ctx, zo, head_type):
+    """A K-quant output.weight (GGUF Q4_K_M checkpoints carry a Q6_K one):
+    the model normalizes into its own buffer, then the K-quant GEMV with the
+    argmax epilogue.  Midway an op-level LM head 4096 wide goes through the
+    context's rmsnorm buffer and reallocates it; the captured decode graph
+    does not use that buffer."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=1024, vocab_real=1000, max_ctx=64, head_type=head_type, head_interleave=1)
+    model = synth.random_model(cfg, seed=21 + head_type)
+    rng = np.random.default_rng(head_type)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        tok = 3
+        for pos in range(24):
+            if pos == 12:
+                k, rows = 4096, 64
+                w = synth.weight(rng, head_type, rows, k, 1)
+                ctx.register(w, head_type, 1)
+                h = synth.activations(rng, k)
+                g = (1.0 + 0.05 * rng.standard_normal(k)).astype(np.float32)
+                lg_op = np.empty(rows, np.float32)
+                t_op = ctx.lm_head_argmax(h, g, w, head_type, 1e-6, k, lg_op, vocab_padded=rows, vocab_real=rows)
+                assert t_op == int(np.argmax(lg_op))
+            nxt, _, hid, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+            h_ref = om.forward(tok, pos)
+            rc, t_ref, _, lg_ref = om.lm_head()
+            assert rc == 0
+            assert rel_err(hid, h_ref) <= REL_TOL and rel_err(lg, lg_ref) <= REL_TOL, pos
+            assert nxt == t_ref, pos
+            tok = nxt
+        prompt = synth.prompt(head_type, 20, cfg.vocab_real)
+        toks, _, _ = gm.generate(prompt, 30, batched_prefill=True)
+        assert np.array_equal(toks, om.generate_batched(prompt, 30))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def test_tiny_model_generate_matches_oracle(ctx, zo, tiny):
     gm = GpuModel(ctx, tiny)
     om = zo.OracleModel(tiny)

@@ -114,11 +114,14 @@ def _np_forward(model, tokens, q8_rows=0):
     return np.array(logits)
 
 
-@pytest.mark.parametrize("il", [4, 1])
-def test_model_forward_vs_numpy(zo, il):
-    """X4 (.smodel-v2) and plain-row (v1) layer linears and LM head."""
-    cfg = synth.ModelConfig(n_layers=2, hidden=128, ffn=256, n_q_heads=4, n_kv_heads=2, head_dim=32,
-                            vocab_padded=256, vocab_real=250, max_ctx=16, lin_interleave=il, head_interleave=il)
+@pytest.mark.parametrize("il,head", [(4, synth.Q8_0), (1, synth.Q8_0), (4, synth.Q6K)])
+def test_model_forward_vs_numpy(zo, il, head):
+    """X4 (.smodel-v2) and plain-row (v1) layer linears and LM head, and a
+    Q6_K LM head."""
+    hil = il if head == synth.Q8_0 else 1
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=256, n_q_heads=4, n_kv_heads=2, head_dim=32,
+                            vocab_padded=256, vocab_real=250, max_ctx=16, lin_interleave=il, head_type=head,
+                            head_interleave=hil)
     model = synth.random_model(cfg, seed=2)
     toks = [3, 17, 101, 5, 5, 42]
     ref = _np_forward(model, toks)

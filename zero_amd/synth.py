@@ -185,7 +185,7 @@ def random_model(cfg: ModelConfig, seed: int = 0) -> RandomModel:
             k_norm=gain(cfg.head_dim)))
     m.token_embd = weight(rng, cfg.embd_type, cfg.vocab_padded, H, 1)
     head_plain = weight(rng, cfg.head_type, cfg.vocab_padded, H, 1)
-    bb, nb = BLOCK_BYTES[cfg.head_type], H // 32
+    bb, nb = BLOCK_BYTES[cfg.head_type], H // BLOCK_ELEMS[cfg.head_type]
     head_plain.reshape(cfg.vocab_padded, nb * bb)[cfg.vocab_real:] = 0
     m.lm_head = interleave_x4(head_plain, cfg.vocab_padded, H, cfg.head_type) if cfg.head_interleave == 4 else head_plain
     m.output_norm = gain(H)
