@@ -333,10 +333,24 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
     agree_p = int(np.argmin(np.concatenate([toks_p == toks, [False]])))
     gp.close()
     del plain
+    # the reference's default dispatch (GGUF Q4_K_M pattern): Q4_K
+    # projections with Q6_K attn_v / ffn_down on 14 of the 28 layers, Q4_K
+    # token embedding, Q6_K LM head
+    kcfg = synth.ModelConfig(max_ctx=n_prompt + n_gen, embd_type=synth.Q4K, head_type=synth.Q6K, head_interleave=1,
+                             layer_quants=synth.q4_k_m_layers(cfg.n_layers))
+    kmodel = synth.random_model(kcfg, seed)
+    gk = GpuModel(ctx, kmodel)
+    gk.generate(prompt, 8)
+    _, _, t_gen_k = gk.generate(prompt, n_gen)
+    gk.close()
+    k_bytes = kcfg.weight_bytes_per_token() + norms + float(np.mean(ctxs)) * kv_per_pos + kv_per_pos
+    del kmodel
     return {"tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "prefill_tok_s": n_prompt / t_pre,
             "batched_prefill": {"prefill_tok_s": n_prompt / t_pre_b, "prefill_ms": t_pre_b * 1e3,
                                 "decode_tok_s": (n_gen - 1) / t_gen_b, "tokens_equal_to_token_by_token": agree},
             "plain_layout": {"decode_tok_s": (n_gen - 1) / t_gen_p, "tokens_equal_to_x4": agree_p},
+            "q4_k_m": {"decode_tok_s": (n_gen - 1) / t_gen_k, "bytes_per_token": int(k_bytes),
+                       "gbs": k_bytes * (n_gen - 1) / t_gen_k / 1e9},
             "n_prompt": n_prompt,
             "n_gen": n_gen, "bytes_per_token": int(per_tok), "gbs": per_tok * tok_s / 1e9,
             "first_tokens": [int(t) for t in toks[:8]], "model": model, "prompt": prompt}
@@ -450,12 +464,15 @@ def main():
         log(f"batched prefill: {bp['prefill_ms']:.2f} ms for {dec['n_prompt']} tokens "
             f"({bp['prefill_tok_s']:.0f} tok/s; token by token {dec['prefill_tok_s']:.0f} tok/s)")
         log(f"decode, plain v1 layout: {dec['plain_layout']['decode_tok_s']:.1f} tok/s")
+        log(f"decode, Q4_K_M pattern: {dec['q4_k_m']['decode_tok_s']:.1f} tok/s ({dec['q4_k_m']['gbs']:.0f} GB/s)")
         out["decode"] = {"tok_s": round(dec["tok_s"], 2), "ms_per_token": dec["ms_per_token"],
                          "prefill_tok_s": round(dec["prefill_tok_s"], 2),
                          "batched_prefill": {k: (round(v, 2) if isinstance(v, float) else v)
                                              for k, v in dec["batched_prefill"].items()},
                          "plain_layout": {k: (round(v, 2) if isinstance(v, float) else v)
                                           for k, v in dec["plain_layout"].items()},
+                         "q4_k_m": {k: (round(v, 2) if isinstance(v, float) else v)
+                                    for k, v in dec["q4_k_m"].items()},
                          "workload": "random-init Qwen3-1.7B shape, Q4_0X4 linears, Q8_0X4 LM head, "
                                      f"{dec['n_prompt']}-token prompt then {dec['n_gen']} greedy tokens",
                          "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,

@@ -192,19 +192,32 @@ typedef struct {
     const float *attn_norm, *ffn_norm, *q_norm, *k_norm; /* host fp32 arrays */
 } zg_layer_weights;
 
+/* ForwardPassDispatch's per-layer quant pathways
+ * (crates/zero-llm-inference/src/forward_pass.rs:191-207): the ggml type
+ * (Q4_0, Q8_0, Q4_K, Q6_K) and layout (1 plain rows, 4 X4; X4 only for
+ * Q4_0/Q8_0) of each projection of one layer, indexed by ZG_PROJ_*. */
+enum { ZG_PROJ_Q = 0, ZG_PROJ_K, ZG_PROJ_V, ZG_PROJ_O, ZG_PROJ_GATE, ZG_PROJ_UP, ZG_PROJ_DOWN, ZG_N_PROJ };
+typedef struct {
+    uint32_t type[ZG_N_PROJ];
+    uint32_t interleave[ZG_N_PROJ];
+} zg_layer_quants;
+
 typedef struct {
     uint32_t n_layers, hidden, ffn, n_q_heads, n_kv_heads, head_dim;
     uint32_t vocab_padded, vocab_real, max_ctx;
     float rms_eps, rope_theta;
-    uint32_t lin_type, lin_interleave;   /* ForwardPassDispatch quants (forward_pass.rs:191-207):
-                                            Q4_0 or Q8_0, X4 (4) or plain rows (1) */
-    uint32_t embd_type;                  /* token_embd quant (plain layout) */
+    uint32_t lin_type, lin_interleave;   /* every layer projection's quant and layout when
+                                            layer_quants is NULL: Q4_0 or Q8_0 X4 (4), or any
+                                            of Q4_0 / Q8_0 / Q4_K / Q6_K as plain rows (1) */
+    uint32_t embd_type;                  /* token_embd quant (plain layout; token_embd_quant) */
     uint32_t head_type, head_interleave; /* output.weight quant + layout */
     const void *token_embd;
     const void *lm_head;
     const float *output_norm;
     const zg_layer_weights *layers;
     uint32_t device_pointers;            /* weights are device pointers, not keys */
+    const zg_layer_quants *layer_quants; /* n_layers entries (the per-layer arrays of
+                                            ForwardPassDispatch), or NULL */
 } zg_model_desc;
 
 typedef struct zg_model zg_model;
@@ -241,7 +254,10 @@ void zg_model_reset(zg_model *m);
  * before them), then runs the LM head on the last row.  Leaves the model
  * ready to decode at position pos0 + n.  hidden_out (optional): the final
  * hidden state of the last row.  Activations are quantized to 8 bits, so
- * results differ from token-by-token prefill by that quantization. */
+ * results differ from token-by-token prefill by that quantization.  The
+ * GEMMs take Q4_0 / Q8_0 weights: a model with a Q4_K or Q6_K layer
+ * projection returns ZG_ERR_UNSUPPORTED_QUANT here (it decodes, and
+ * prefills token by token). */
 zg_status zg_model_prefill(zg_model *m, const uint32_t *tokens, size_t n, uint32_t pos0,
                            float *hidden_out, uint32_t *next_token, float *max_logit);
 #define ZG_GEN_BATCHED_PREFILL 1u

@@ -1115,6 +1115,7 @@ int zo_linear_q4k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, si
 struct zo_model {
     zo_model_desc d;
     zo_layer *layers;
+    zo_layer_quants *quants;  /* per layer, always filled */
     float *kv;
     float *hidden, *norm, *q, *k, *v, *attn, *proj, *gate, *up, *act, *scores, *logits;
     float *inv_freqs;
@@ -1125,8 +1126,21 @@ zo_model *zo_model_create(const zo_model_desc *desc) {
     if (!m) return NULL;
     m->d = *desc;
     m->layers = (zo_layer *)malloc(sizeof(zo_layer) * (size_t)desc->n_layers);
+    m->quants = (zo_layer_quants *)malloc(sizeof(zo_layer_quants) * (size_t)desc->n_layers);
+    if (!m->layers || !m->quants) {
+        free(m->layers);
+        free(m->quants);
+        free(m);
+        return NULL;
+    }
     memcpy(m->layers, desc->layers, sizeof(zo_layer) * (size_t)desc->n_layers);
+    for (int l = 0; l < desc->n_layers; l++)
+        for (int p = 0; p < 7; p++) {
+            m->quants[l].type[p] = desc->layer_quants ? desc->layer_quants[l].type[p] : desc->lin_type;
+            m->quants[l].interleave[p] = desc->layer_quants ? desc->layer_quants[l].interleave[p] : desc->lin_interleave;
+        }
     m->d.layers = m->layers;
+    m->d.layer_quants = m->quants;
     size_t H = (size_t)desc->hidden, F = (size_t)desc->ffn;
     size_t qd = (size_t)desc->n_q_heads * desc->head_dim, kvd = (size_t)desc->n_kv_heads * desc->head_dim;
     m->kv = (float *)calloc((size_t)desc->n_layers * 2 * desc->max_ctx * kvd, sizeof(float));
@@ -1154,6 +1168,7 @@ zo_model *zo_model_create(const zo_model_desc *desc) {
 void zo_model_destroy(zo_model *m) {
     if (!m) return;
     free(m->layers);
+    free(m->quants);
     free(m->kv);
     free(m->hidden); free(m->norm); free(m->q); free(m->k); free(m->v); free(m->attn);
     free(m->proj); free(m->gate); free(m->up); free(m->act); free(m->scores); free(m->logits);
@@ -1198,11 +1213,12 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
     size_t T = pos + 1;
     for (int l = 0; l < d->n_layers; l++) {
         const zo_layer *L = &m->layers[l];
+        const int *qt = m->quants[l].type, *il = m->quants[l].interleave;
         zo_rmsnorm(m->hidden, L->attn_norm, m->norm, H, d->rms_eps);
         zo_segment qkv[3] = {
-            {L->attn_q, m->q, qd, d->lin_type, d->lin_interleave},
-            {L->attn_k, m->k, kvd, d->lin_type, d->lin_interleave},
-            {L->attn_v, m->v, kvd, d->lin_type, d->lin_interleave},
+            {L->attn_q, m->q, qd, qt[0], il[0]},
+            {L->attn_k, m->k, kvd, qt[1], il[1]},
+            {L->attn_v, m->v, kvd, qt[2], il[2]},
         };
         zo_linear_fused_parallel(m->norm, qkv, 3, H);
         float tmp[512];
@@ -1221,16 +1237,16 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
         memcpy(kc + pos * kvd, m->k, kvd * 4);
         memcpy(vc + pos * kvd, m->v, kvd * 4);
         if (attend(d, kc, vc, m->q, T, scale, m->scores, m->attn)) return -4;
-        zo_linear_parallel(m->attn, L->attn_o, m->proj, qd, H, d->lin_type, d->lin_interleave);
+        zo_linear_parallel(m->attn, L->attn_o, m->proj, qd, H, qt[3], il[3]);
         for (size_t i = 0; i < H; i++) m->hidden[i] = m->hidden[i] + m->proj[i];
         zo_rmsnorm(m->hidden, L->ffn_norm, m->norm, H, d->rms_eps);
         zo_segment gu[2] = {
-            {L->ffn_gate, m->gate, F, d->lin_type, d->lin_interleave},
-            {L->ffn_up, m->up, F, d->lin_type, d->lin_interleave},
+            {L->ffn_gate, m->gate, F, qt[4], il[4]},
+            {L->ffn_up, m->up, F, qt[5], il[5]},
         };
         zo_linear_fused_parallel(m->norm, gu, 2, H);
         zo_silu_mul(m->gate, m->up, m->act, F);
-        zo_linear_parallel(m->act, L->ffn_down, m->proj, F, H, d->lin_type, d->lin_interleave);
+        zo_linear_parallel(m->act, L->ffn_down, m->proj, F, H, qt[6], il[6]);
         for (size_t i = 0; i < H; i++) m->hidden[i] = m->hidden[i] + m->proj[i];
     }
     if (hidden_out) memcpy(hidden_out, m->hidden, H * 4);
@@ -1252,6 +1268,9 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
     if (n == 0 || pos0 + n > d->max_ctx) return -3;
     for (size_t i = 0; i < n; i++)
         if (tokens[i] >= d->vocab_padded) return -3;
+    for (int l = 0; l < d->n_layers; l++)
+        for (int p = 0; p < 7; p++)
+            if (m->quants[l].type[p] != 2 && m->quants[l].type[p] != 8) return -3;
     size_t be, bb;
     if (type_geom(d->embd_type, &be, &bb) || H % be) return -3;
     size_t km = H > qd ? H : qd;
@@ -1270,13 +1289,14 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
     float tmp[512];
     for (int l = 0; l < d->n_layers && !rc; l++) {
         const zo_layer *L = &m->layers[l];
+        const int *qt = m->quants[l].type, *il = m->quants[l].interleave;
         float *kc = m->kv + ((size_t)l * 2 + 0) * d->max_ctx * kvd;
         float *vc = m->kv + ((size_t)l * 2 + 1) * d->max_ctx * kvd;
         for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->attn_norm, T + i * H, H, d->rms_eps);
         zo_quantize_q8_0_row(T, xq, n * H);
-        if (zo_gemm_q8act(xq, L->attn_q, Q, n, qd, H, d->lin_type, d->lin_interleave) ||
-            zo_gemm_q8act(xq, L->attn_k, K, n, kvd, H, d->lin_type, d->lin_interleave) ||
-            zo_gemm_q8act(xq, L->attn_v, V, n, kvd, H, d->lin_type, d->lin_interleave)) {
+        if (zo_gemm_q8act(xq, L->attn_q, Q, n, qd, H, qt[0], il[0]) ||
+            zo_gemm_q8act(xq, L->attn_k, K, n, kvd, H, qt[1], il[1]) ||
+            zo_gemm_q8act(xq, L->attn_v, V, n, kvd, H, qt[2], il[2])) {
             rc = -3;
             break;
         }
@@ -1301,15 +1321,15 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
             if (attend(d, kc, vc, Q + i * qd, pos0 + i + 1, scale, scores, A + i * qd)) rc = -4;
         if (rc) break;
         zo_quantize_q8_0_row(A, xq, n * qd);
-        zo_gemm_q8act(xq, L->attn_o, P, n, H, qd, d->lin_type, d->lin_interleave);
+        zo_gemm_q8act(xq, L->attn_o, P, n, H, qd, qt[3], il[3]);
         for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
         for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->ffn_norm, T + i * H, H, d->rms_eps);
         zo_quantize_q8_0_row(T, xq, n * H);
-        zo_gemm_q8act(xq, L->ffn_gate, G, n, F, H, d->lin_type, d->lin_interleave);
-        zo_gemm_q8act(xq, L->ffn_up, U, n, F, H, d->lin_type, d->lin_interleave);
+        zo_gemm_q8act(xq, L->ffn_gate, G, n, F, H, qt[4], il[4]);
+        zo_gemm_q8act(xq, L->ffn_up, U, n, F, H, qt[5], il[5]);
         zo_silu_mul(G, U, T, n * F);
         zo_quantize_q8_0_row(T, xq, n * F);
-        zo_gemm_q8act(xq, L->ffn_down, P, n, H, F, d->lin_type, d->lin_interleave);
+        zo_gemm_q8act(xq, L->ffn_down, P, n, H, F, qt[6], il[6]);
         for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
     }
     if (!rc) {

@@ -132,17 +132,25 @@ typedef struct {
     const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
 } zo_layer;
 
+/* ForwardPassDispatch's per-layer quants (forward_pass.rs:191-207): type and
+ * layout of the projections Q, K, V, O, gate, up, down, in that order. */
+typedef struct {
+    int type[7];
+    int interleave[7];
+} zo_layer_quants;
+
 typedef struct {
     int n_layers, hidden, ffn, n_q_heads, n_kv_heads, head_dim;
     size_t vocab_padded, vocab_real, max_ctx;
     float rms_eps, rope_theta;
-    int lin_type, lin_interleave;    /* layer linears */
+    int lin_type, lin_interleave;    /* layer linears, when layer_quants is NULL */
     int embd_type;                   /* token_embd (plain) */
     int head_type, head_interleave;  /* LM head */
     const uint8_t *token_embd;
     const uint8_t *lm_head;
     const float *output_norm;
     const zo_layer *layers;          /* n_layers entries */
+    const zo_layer_quants *layer_quants; /* n_layers entries, or NULL */
 } zo_model_desc;
 
 typedef struct zo_model zo_model;
@@ -154,7 +162,8 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
 /* Batched prefill with Q8_0-quantized activations (the GPU's int8-MFMA
  * prefill; no reference counterpart): n tokens at positions
  * pos0..pos0+n-1, KV rows stored; the last row's final hidden state is left
- * in the model for zo_model_lm_head and copied to hidden_out if non-NULL. */
+ * in the model for zo_model_lm_head and copied to hidden_out if non-NULL.
+ * Returns -3 when a layer projection is not Q4_0 / Q8_0. */
 int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t pos0, float *hidden_out);
 /* final rmsnorm + LM head + argmax; returns 0 / -1 non-finite / -2 padding */
 int zo_model_lm_head(zo_model *m, float *logits_out, uint32_t *token, float *max_val);

@@ -27,6 +27,10 @@ class zo_layer(C.Structure):
                                   "attn_norm", "ffn_norm", "q_norm", "k_norm")]
 
 
+class zo_layer_quants(C.Structure):
+    _fields_ = [("type", _I * 7), ("interleave", _I * 7)]
+
+
 class zo_model_desc(C.Structure):
     _fields_ = [
         ("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_q_heads", _I), ("n_kv_heads", _I), ("head_dim", _I),
@@ -34,6 +38,7 @@ class zo_model_desc(C.Structure):
         ("rms_eps", _F), ("rope_theta", _F),
         ("lin_type", _I), ("lin_interleave", _I), ("embd_type", _I), ("head_type", _I), ("head_interleave", _I),
         ("token_embd", _P), ("lm_head", _P), ("output_norm", _P), ("layers", C.POINTER(zo_layer)),
+        ("layer_quants", C.POINTER(zo_layer_quants)),
     ]
 
 
@@ -252,6 +257,12 @@ class OracleModel:
         d.token_embd, d.lm_head, d.output_norm = (model.token_embd.ctypes.data, model.lm_head.ctypes.data,
                                                   model.output_norm.ctypes.data)
         d.layers = self._layers
+        if cfg.layer_quants is not None:
+            self._quants = (zo_layer_quants * cfg.n_layers)()
+            for i, lq in enumerate(cfg.layer_quants):
+                for p, (t, il) in enumerate(lq):
+                    self._quants[i].type[p], self._quants[i].interleave[p] = t, il
+            d.layer_quants = self._quants
         self._desc = d
         self.h = load().zo_model_create(C.byref(d))
         assert self.h

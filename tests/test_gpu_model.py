@@ -150,6 +150,76 @@ def test_kquant_lm_head(ctx, zo, head_type):
         ctx.clear()
 
 
+MIXED = ((synth.Q4K, 1), (synth.Q6K, 1), (synth.Q4_0, 4), (synth.Q8_0, 1), (synth.Q4K, 1), (synth.Q4K, 1),
+         (synth.Q6K, 1))
+
+
+def test_mixed_projection_quants(ctx, zo):
+    """ForwardPassDispatch's per-layer, per-projection quants: a layer of
+    mixed Q4_K / Q6_K / Q4_0X4 / plain Q8_0 projections and a layer of the
+    Q4_K_M pattern, Q4_K token embedding, Q6_K LM head.  The batched
+    prefill (Q4_0 / Q8_0 GEMMs) refuses such a model."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=1024, vocab_real=1000, max_ctx=80, embd_type=synth.Q4K,
+                            head_type=synth.Q6K, head_interleave=1, layer_quants=(MIXED, synth.q4_k_m_layers(8)[0]))
+    model = synth.random_model(cfg, seed=17)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        tok = 11
+        for pos in range(40):
+            nxt, _, hid, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+            h_ref = om.forward(tok, pos)
+            rc, t_ref, _, lg_ref = om.lm_head()
+            assert rc == 0
+            assert rel_err(hid, h_ref) <= REL_TOL and rel_err(lg, lg_ref) <= REL_TOL, pos
+            assert nxt == t_ref, pos
+            tok = nxt
+        prompt = synth.prompt(4, 12, cfg.vocab_real)
+        toks, _, _ = gm.generate(prompt, 30)
+        assert np.array_equal(toks, om.generate(prompt, 30))
+        import zero_amd
+        from zero_amd import _lib
+        with pytest.raises(zero_amd.ZgError) as e:
+            gm.generate(prompt, 4, batched_prefill=True)
+        assert e.value.code == _lib.ZG_ERR_UNSUPPORTED_QUANT
+        with pytest.raises(zero_amd.ZgError) as e:
+            gm.prefill(prompt)
+        assert e.value.code == _lib.ZG_ERR_UNSUPPORTED_QUANT
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
+def test_qwen3_1_7b_shape_q4_k_m(ctx, zo):
+    """The reference's default dispatch at the Qwen3-1.7B shape: Q4_K layer
+    projections with the Q4_K_M pattern's Q6_K attn_v / ffn_down, Q4_K token
+    embedding, Q6_K LM head.  8-token prompt, then 24 greedy tokens against
+    the oracle; logits compared at the last 4 prompt positions."""
+    cfg = synth.ModelConfig(max_ctx=64, embd_type=synth.Q4K, head_type=synth.Q6K, head_interleave=1,
+                            layer_quants=synth.q4_k_m_layers(28))
+    model = synth.random_model(cfg, seed=6)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(8, 8, cfg.vocab_real)
+        for i, t in enumerate(prompt):
+            nxt, _, _, lg = gm.step(int(t), i, want_logits=i >= 4)
+            om.forward(int(t), i)
+            if i >= 4:
+                rc, t_ref, _, lg_ref = om.lm_head()
+                err = rel_err(lg, lg_ref)
+                print(f"Q4_K_M-pattern Qwen3-1.7B shape, pos {i}: logits rel err {err:.2e}")
+                assert err <= REL_TOL and nxt == t_ref
+        toks, _, _ = gm.generate(prompt, 24)
+        assert np.array_equal(toks, om.generate(prompt, 24))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def test_tiny_model_generate_matches_oracle(ctx, zo, tiny):
     gm = GpuModel(ctx, tiny)
     om = zo.OracleModel(tiny)

@@ -123,6 +123,47 @@ def test_plain_row_layouts(ctx, zo, lin_type):
         ctx.clear()
 
 
+def test_mixed_q4_0_q8_0_projections(ctx, zo):
+    """Per-projection Q4_0 / Q8_0 types and layouts: the prefill runs one
+    GEMM per projection where a fused group's types differ.
+
+    The synthetic Q8_0 weights are ~16x the Q4_0 ones, and in this mix one
+    Q8_0 rounding flip of an activation moves the hidden state by 1e-3..5e-3
+    (on the CPU a 1e-6 relative perturbation of the quantizer inputs already
+    does; the oracle's f32 prefill and an f64 numpy restatement differ by
+    1.7e-3).  The device expf and the host's can differ in the last bit on a
+    SwiGLU input, so the prefill is held to 2e-2 here (a wrong GEMM type or
+    layout gives errors of order 1); the token-by-token decode, which has no
+    quantization step, to the usual 1e-3 and identical tokens."""
+    lq = ((synth.Q4_0, 4), (synth.Q4_0, 4), (synth.Q8_0, 4), (synth.Q4_0, 1), (synth.Q8_0, 1), (synth.Q8_0, 1),
+          (synth.Q4_0, 4))
+    cfg = synth.ModelConfig(n_layers=2, hidden=512, ffn=1024, n_q_heads=8, n_kv_heads=2, head_dim=64,
+                            vocab_padded=1024, vocab_real=1000, max_ctx=128, layer_quants=(lq, lq[::-1]))
+    model = synth.random_model(cfg, seed=19)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(29, 50, cfg.vocab_real)
+        tok, _, hid = gm.prefill(prompt, want_hidden=True)
+        err = rel_err(hid, om.prefill_q8(prompt))
+        print(f"mixed Q4_0/Q8_0 projections: prefill hidden rel err vs oracle {err:.2e}")
+        assert err <= 2e-2
+        toks, _, _ = gm.generate(prompt, 8, batched_prefill=True)
+        assert toks[0] == tok
+        for pos in range(12):
+            t = int(prompt[pos])
+            _, _, h2, lg = gm.step(t, pos, want_hidden=True, want_logits=True)
+            h2_ref = om.forward(t, pos)
+            lg_ref = om.lm_head()[3]
+            assert rel_err(h2, h2_ref) <= REL_TOL and rel_err(lg, lg_ref) <= REL_TOL, pos
+        toks, _, _ = gm.generate(prompt[:10], 30)
+        assert np.array_equal(toks, om.generate(prompt[:10], 30))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def _x4_layers(model):
     """The same weights with X4 layer linears (copies throughout: a host
     array is one registry key)."""

@@ -14,7 +14,7 @@ from zero_amd import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "zero_gpu.h"
-STRUCTS = [_lib.zg_segment, _lib.zg_layer_weights, _lib.zg_model_desc, _lib.zg_smodel_info, _lib.zg_smodel_tensor]
+STRUCTS = [_lib.zg_segment, _lib.zg_layer_weights, _lib.zg_layer_quants, _lib.zg_model_desc, _lib.zg_smodel_info, _lib.zg_smodel_tensor]
 
 
 def _declared_functions() -> list[str]:

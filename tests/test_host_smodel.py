@@ -288,8 +288,14 @@ def test_model_view_rejections():
     with pytest.raises(UnsupportedFormat):
         s.to_model()
     q = _index("blk.1.attn_q.weight")
-    s = SModel(_patched(("<I", _entry(q, 8), 101)))  # one layer Q8_0X4, the rest Q4_0X4
-    with pytest.raises(UnsupportedFormat):
+    # per-projection types are taken from the file (ForwardPassDispatch's
+    # per-layer table), so relabelling one Q4_0X4 tensor Q8_0X4 is caught by
+    # its byte length, not its type
+    s = SModel(_patched(("<I", _entry(q, 8), 101)))
+    with pytest.raises(InvalidContainer):
+        s.to_model()
+    s = SModel(_patched(("<I", _entry(q, 8), 12)))  # Q4_K in place of Q4_0X4: same check
+    with pytest.raises(InvalidContainer):
         s.to_model()
     n = _index("blk.0.attn_q_norm.weight")
     s = SModel(_patched(("<Q", _entry(n, 16), 32)))  # q_norm of the wrong length

@@ -73,10 +73,9 @@ def _np_forward(model, tokens, q8_rows=0):
     inv = cfg.rope_theta ** (-2.0 * np.arange(hd // 2) / hd)
     emb = deq(model.token_embd, cfg.vocab_padded, H, cfg.embd_type, 1)
     head = deq(model.lm_head, cfg.vocab_padded, H, cfg.head_type, cfg.head_interleave)
-    Ws = [{k: deq(getattr(L, k), *shape, cfg.lin_type, cfg.lin_interleave) for k, shape in
-           (("attn_q", (cfg.q_dim, H)), ("attn_k", (cfg.kv_dim, H)), ("attn_v", (cfg.kv_dim, H)),
-            ("attn_o", (H, cfg.q_dim)), ("ffn_gate", (cfg.ffn, H)), ("ffn_up", (cfg.ffn, H)),
-            ("ffn_down", (H, cfg.ffn)))} for L in model.layers]
+    names = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down")
+    Ws = [{k: deq(getattr(L, k), *shape, *cfg.proj_quant(li, p))
+           for p, (k, shape) in enumerate(zip(names, cfg.proj_shapes()))} for li, L in enumerate(model.layers)]
     kc = [[] for _ in model.layers]
     vc = [[] for _ in model.layers]
     logits = []
@@ -133,6 +132,34 @@ def test_model_forward_vs_numpy(zo, il, head):
         err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
         assert err < 1e-4, (pos, err)
         assert tok == int(np.argmax(ref[pos][:cfg.vocab_real]))
+    om.close()
+
+
+MIXED = ((synth.Q4K, 1), (synth.Q6K, 1), (synth.Q4_0, 4), (synth.Q8_0, 1), (synth.Q4K, 1), (synth.Q4K, 1),
+         (synth.Q6K, 1))
+
+
+def test_model_forward_mixed_quants_vs_numpy(zo):
+    """Per-layer, per-projection quants (ForwardPassDispatch): one layer of
+    mixed K-quant / Q4_0X4 / plain Q8_0 projections and one of the Q4_K_M
+    pattern, with a Q4_K token embedding and a Q6_K LM head."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=256, vocab_real=250, max_ctx=16, embd_type=synth.Q4K, head_type=synth.Q6K,
+                            head_interleave=1, layer_quants=(MIXED, synth.q4_k_m_layers(8)[0]))
+    model = synth.random_model(cfg, seed=5)
+    assert model.layers[0].attn_k.nbytes == cfg.kv_dim * 210 and model.layers[1].attn_v.nbytes == cfg.kv_dim * 210
+    toks = [3, 17, 101, 5, 42]
+    ref = _np_forward(model, toks)
+    om = zo.OracleModel(model)
+    for pos, t in enumerate(toks):
+        om.forward(t, pos)
+        rc, tok, mv, lg = om.lm_head()
+        assert rc == 0
+        err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
+        assert err < 1e-4, (pos, err)
+    # the batched prefill's GEMMs take Q4_0 / Q8_0 projections only
+    with pytest.raises(AssertionError):
+        om.prefill_q8(np.array(toks, np.uint32))
     om.close()
 
 

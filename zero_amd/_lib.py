@@ -57,6 +57,13 @@ class zg_layer_weights(C.Structure):
     ]
 
 
+N_PROJ = 7  # ZG_PROJ_Q .. ZG_PROJ_DOWN: Q, K, V, O, gate, up, down
+
+
+class zg_layer_quants(C.Structure):
+    _fields_ = [("type", C.c_uint32 * N_PROJ), ("interleave", C.c_uint32 * N_PROJ)]
+
+
 class zg_model_desc(C.Structure):
     _fields_ = [
         ("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("ffn", C.c_uint32),
@@ -69,6 +76,7 @@ class zg_model_desc(C.Structure):
         ("token_embd", C.c_void_p), ("lm_head", C.c_void_p), ("output_norm", C.c_void_p),
         ("layers", C.POINTER(zg_layer_weights)),
         ("device_pointers", C.c_uint32),
+        ("layer_quants", C.POINTER(zg_layer_quants)),
     ]
 
 

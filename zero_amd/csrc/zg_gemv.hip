@@ -703,92 +703,6 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
 // each element with the reference's operation order (bit-exact weights) and
 // accumulates x*w with fmaf.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float rd_half(const uint8_t* p) {
-  return half_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
-}
-
-// Dequantize element e (0..blk_elems-1) of the block at blk (plain-layout
-// block bytes, or for X4 the (d, qs) pointers).  Operation order follows
-// dequant.rs: Q4_0 (q-8)*d; Q8_0 q*d; Q4_K d1*q - m1; Q6_K (d*sc)*q.
-__device__ __forceinline__ float deq_q4_0(float d, const uint8_t* qs, int e) {
-  const int q = (e < 16) ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
-  return (float)(q - 8) * d;
-}
-__device__ __forceinline__ float deq_q8_0(float d, const uint8_t* qs, int e) {
-  return (float)(int8_t)qs[e] * d;
-}
-__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& sc, int& mn) {
-  if (j < 4) {
-    sc = s[j] & 0x3F;
-    mn = s[j + 4] & 0x3F;
-  } else {
-    sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
-    mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-  }
-}
-__device__ __forceinline__ float deq_q4k(const uint8_t* blk, int e) {
-  const float d = rd_half(blk), dmin = rd_half(blk + 2);
-  const int g = e >> 6, w = e & 63;
-  int sc, mn;
-  q4k_scale_min(blk + 4, 2 * g + (w >= 32 ? 1 : 0), sc, mn);
-  const uint8_t byte = blk[16 + 32 * g + (w & 31)];
-  const int q = (w < 32) ? (byte & 0xF) : (byte >> 4);
-  const float dd = d * (float)sc, m = dmin * (float)mn;
-  return dd * (float)q - m;
-}
-__device__ __forceinline__ float deq_q6k(const uint8_t* blk, int e) {
-  const float d = rd_half(blk + 208);
-  const int h = e >> 7, w = e & 127, quarter = w >> 5, l = w & 31;
-  const uint8_t* ql = blk + 64 * h;
-  const uint8_t* qh = blk + 128 + 32 * h;
-  const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * h);
-  const int is = l >> 4;
-  int q;
-  switch (quarter) {
-    case 0: q = (ql[l] & 0xF) | ((qh[l] & 3) << 4); break;
-    case 1: q = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4); break;
-    case 2: q = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4); break;
-    default: q = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4); break;
-  }
-  return d * (float)sc[is + 2 * quarter] * (float)(q - 32);
-}
-
-struct BlockRef {
-  const uint8_t* d;   // scale location (Q4_0/Q8_0) or block start (k-quants)
-  const uint8_t* qs;  // quant bytes (Q4_0/Q8_0)
-};
-
-__device__ __forceinline__ BlockRef block_ref(const uint8_t* w, uint32_t qt, int il, size_t row,
-                                              size_t b, size_t nb) {
-  BlockRef br;
-  if (qt == Q4_0 || qt == Q8_0) {
-    const size_t bb = (qt == Q4_0) ? 18 : 34;
-    if (il == 4) {
-      const size_t gb = 4 * bb;
-      const uint8_t* g = w + (row >> 2) * nb * gb + b * gb;
-      br.d = g + 2 * (row & 3);
-      br.qs = g + 8 + (row & 3) * (bb - 2);
-    } else {
-      br.d = w + (row * nb + b) * bb;
-      br.qs = br.d + 2;
-    }
-  } else {
-    const size_t bb = (qt == Q4K) ? 144 : 210;
-    br.d = w + (row * nb + b) * bb;
-    br.qs = br.d;
-  }
-  return br;
-}
-
-__device__ __forceinline__ float deq_elem(const BlockRef& br, uint32_t qt, float d, int e) {
-  switch (qt) {
-    case Q4_0: return deq_q4_0(d, br.qs, e);
-    case Q8_0: return deq_q8_0(d, br.qs, e);
-    case Q4K: return deq_q4k(br.d, e);
-    default: return deq_q6k(br.d, e);
-  }
-}
-
 __global__ __launch_bounds__(256) void gemv_generic_kernel(GenericArgs a) {
   const int lane = threadIdx.x & 63;
   const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6) + a.row_lo;

@@ -50,11 +50,25 @@ struct DevState {
   uint64_t best;     // last packed argmax (copy of the LM head slot)
 };
 
-// embed_lookup_dispatch (forward_pass.rs:311-370) for plain Q4_0/Q8_0 rows;
-// also clears the LM-head argmax slot for this step.
-// It also fills this position's RoPE table once for all layers, as the
-// reference builds its sin/cos table once per token (trig.rs:148-216):
-// cs[i] = cos(pos * inv_freq[i]), cs[half + i] = sin(pos * inv_freq[i]).
+// embed_lookup_dispatch (forward_pass.rs:311-370): row tok of a plain
+// token_embd (Q4_0, Q8_0, Q4_K or Q6_K), each element dequantized in the
+// reference's operation order
+__device__ __forceinline__ void embed_row(const uint8_t* __restrict__ embd, uint32_t qt, int hidden, uint32_t tok,
+                                          float* __restrict__ out) {
+  const int be = (qt == Q4_0 || qt == Q8_0) ? 32 : 256;
+  const size_t nb = (size_t)(hidden / be);
+  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
+    const BlockRef br = block_ref(embd, qt, 1, tok, (size_t)(e / be), nb);
+    const float d = (qt == Q4_0 || qt == Q8_0) ? rd_half(br.d) : 0.0f;
+    out[e] = deq_elem(br, qt, d, e % be);
+  }
+}
+
+// The decode step's embedding lookup; also clears the LM-head argmax slot
+// for this step, and fills this position's RoPE table once for all layers,
+// as the reference builds its sin/cos table once per token
+// (trig.rs:148-216): cs[i] = cos(pos * inv_freq[i]), cs[half + i] =
+// sin(pos * inv_freq[i]).
 __global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
                              DevState* __restrict__ st, uint64_t* __restrict__ best,
                              float* __restrict__ out, const float* __restrict__ inv_freq, int half,
@@ -65,22 +79,7 @@ __global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int 
     rope_cs[threadIdx.x] = cosf(th);
     rope_cs[half + threadIdx.x] = sinf(th);
   }
-  const int nb = hidden / 32;
-  const int bb = (qt == Q4_0) ? 18 : 34;
-  const uint8_t* row = embd + (size_t)tok * nb * bb;
-  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
-    const uint8_t* blk = row + (e / 32) * bb;
-    const float d = half_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    const int j = e & 31;
-    float v;
-    if (qt == Q4_0) {
-      const int q = (j < 16) ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
-      v = (float)(q - 8) * d;
-    } else {
-      v = (float)(int8_t)blk[2 + j] * d;
-    }
-    out[e] = v;
-  }
+  embed_row(embd, qt, hidden, tok, out);
   if (threadIdx.x == 0) *best = 0;
 }
 
@@ -418,24 +417,7 @@ __global__ void advance_kernel(DevState* st, const uint32_t* prompt) {
 __global__ void embed_rows_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
                                   const uint32_t* __restrict__ tokens, float* __restrict__ out,
                                   uint64_t* __restrict__ best) {
-  const uint32_t tok = tokens[blockIdx.x];
-  out += (size_t)blockIdx.x * hidden;
-  const int nb = hidden / 32;
-  const int bb = (qt == Q4_0) ? 18 : 34;
-  const uint8_t* row = embd + (size_t)tok * nb * bb;
-  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
-    const uint8_t* blk = row + (e / 32) * bb;
-    const float d = half_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    const int j = e & 31;
-    float v;
-    if (qt == Q4_0) {
-      const int q = (j < 16) ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
-      v = (float)(q - 8) * d;
-    } else {
-      v = (float)(int8_t)blk[2 + j] * d;
-    }
-    out[e] = v;
-  }
+  embed_row(embd, qt, hidden, tokens[blockIdx.x], out + (size_t)blockIdx.x * hidden);
   if (blockIdx.x == 0 && threadIdx.x == 0) *best = 0;
 }
 
@@ -584,6 +566,9 @@ hipError_t zg::launch_rmsnorm(const float* x, const float* w, float* out, int n,
 struct ZLayer {
   const uint8_t *q, *k, *v, *o, *gate, *up, *down;
   float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+  uint32_t qt[ZG_N_PROJ], il[ZG_N_PROJ];  // ggml type and layout per projection (ZG_PROJ_*)
+  bool qkv_one = false, gu_one = false;    // Q|K|V, gate|up (SwiGLU) as one rmsnorm GEMV launch
+  bool o_merge = false;                    // the O GEMV merges the attention splits itself
 };
 
 struct zg_model {
@@ -609,9 +594,8 @@ struct zg_model {
   uint32_t* out_tokens = nullptr;
   size_t out_cap = 0;
   int nsplit = 1, split_len = 0;
-  bool o_merge = false;  // the O GEMV merges the attention splits itself
-  bool qkv_one = false, gu_one = false;  // Q|K|V, gate|up (SwiGLU) as one rmsnorm GEMV launch
-  bool head_norm = false;                // the LM-head GEMV takes the output rmsnorm itself
+  bool head_norm = false;  // the LM-head GEMV takes the output rmsnorm itself
+  bool pf_ok = false;      // every layer projection Q4_0 / Q8_0 (the batched prefill's GEMMs)
   std::vector<void*> owned;  // device allocations to free
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
@@ -697,9 +681,11 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)HD);
   for (uint32_t l = 0; l < d.n_layers; l++) {
     const ZLayer& L = m->layers[l];
-    const uint32_t lt = d.lin_type, il = d.lin_interleave;
-    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, lt, il}, {L.k, m->k, (size_t)kvd, lt, il}, {L.v, m->v, (size_t)kvd, lt, il}};
-    if (m->qkv_one) {
+    const uint32_t *qt = L.qt, *il = L.il;
+    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, qt[ZG_PROJ_Q], il[ZG_PROJ_Q]},
+                       {L.k, m->k, (size_t)kvd, qt[ZG_PROJ_K], il[ZG_PROJ_K]},
+                       {L.v, m->v, (size_t)kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
+    if (L.qkv_one) {
       if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
     } else {
       if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
@@ -727,8 +713,9 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), ag, ab, 0, st, aa);
     else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
-    if (m->o_merge) {
-      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, lt, il, st)))
+    if (L.o_merge) {
+      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, qt[ZG_PROJ_O],
+                          il[ZG_PROJ_O], st)))
         return s;
     } else {
       if (m->nsplit > 1) {
@@ -737,22 +724,24 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
                            qd, HD, m->nsplit, m->attn);
         if ((s = hip_check(ctx, hipGetLastError(), "attention merge launch"))) return s;
       }
-      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, lt, il, 0, H, EPI_RESID, m->hidden, nullptr, PRO_PLAIN,
-                          nullptr, 0.0f, st)))
+      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, qt[ZG_PROJ_O], il[ZG_PROJ_O], 0, H, EPI_RESID,
+                          m->hidden, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
         return s;
     }
-    if (m->gu_one) {
-      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, lt, il}, {L.up, nullptr, (size_t)F, lt, il}};
+    if (L.gu_one) {
+      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
+                        {L.up, nullptr, (size_t)F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
       if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
     } else {
-      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, lt, il}, {L.up, m->up, (size_t)F, lt, il}};
+      FusedDev gu[2] = {{L.gate, m->act, (size_t)F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
+                        {L.up, m->up, (size_t)F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
       if ((s = model_rmsnorm(m, m->hidden, L.ffn_norm, st))) return s;
       if ((s = run_fused(ctx, m->xn, gu, 2, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
       hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, st, m->act, m->up, F);
       if ((s = hip_check(ctx, hipGetLastError(), "swiglu launch"))) return s;
     }
-    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, lt, il, 0, H, EPI_RESID, m->hidden, nullptr, PRO_PLAIN,
-                        nullptr, 0.0f, st)))
+    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, qt[ZG_PROJ_DOWN], il[ZG_PROJ_DOWN], 0, H, EPI_RESID,
+                        m->hidden, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
       return s;
   }
   return ZG_OK;
@@ -821,13 +810,26 @@ static zg_status prefill_alloc(zg_model* m) {
 // rmsnorm + Q8_0 rows -> gate|up GEMM -> SwiGLU + Q8_0 -> down GEMM
 // (+= residual).  Each fused encode gives the bits the separate quantizer
 // would give for the same fp32 row.
+// GEMMs of layer projections p0..p0+nseg-1 on the chunk's Q8_0 rows: one
+// segmented launch when they share a type and layout, else one each.
+static zg_status layer_gemm(zg_model* m, const ZLayer& L, int p0, const GemmSegDev* segs, int nseg, size_t n,
+                            size_t k, bool accumulate, hipStream_t st) {
+  bool same = true;
+  for (int i = 1; i < nseg; i++) same = same && L.qt[p0 + i] == L.qt[p0] && L.il[p0 + i] == L.il[p0];
+  if (same) return run_gemm(m->ctx, m->pf_qs, m->pf_qd, segs, nseg, n, k, L.qt[p0], L.il[p0], accumulate, st);
+  for (int i = 0; i < nseg; i++) {
+    zg_status s = run_gemm(m->ctx, m->pf_qs, m->pf_qd, segs + i, 1, n, k, L.qt[p0 + i], L.il[p0 + i], accumulate, st);
+    if (s) return s;
+  }
+  return ZG_OK;
+}
+
 static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, uint32_t pos0, hipStream_t st) {
   const zg_model_desc& d = m->d;
   zg_ctx* ctx = m->ctx;
   const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
   const int nq = (int)d.n_q_heads, nkv = (int)d.n_kv_heads;
   const size_t qd = (size_t)nq * HD, kvd = (size_t)nkv * HD;
-  const uint32_t lt = d.lin_type, il = d.lin_interleave;
   hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(256), 0, st, m->embd, d.embd_type, H, d_tokens,
                      m->pf_x, m->best);
   zg_status s = hip_check(ctx, hipGetLastError(), "prefill embed launch");
@@ -840,7 +842,7 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
                        m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
     const GemmSegDev qkv[3] = {{L.q, m->pf_q, qd}, {L.k, m->pf_k, kvd}, {L.v, m->pf_v, kvd}};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, qkv, 3, n, H, lt, il, false, st))) break;
+    if ((s = layer_gemm(m, L, ZG_PROJ_Q, qkv, 3, n, H, false, st))) break;
     QkStoreArgs qa{m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm, m->inv_freq, kc, vc, nq, nkv, (int)pos0, d.rms_eps};
     const dim3 qg((unsigned)n, (unsigned)(nq + nkv));
     if (HD == 128) hipLaunchKernelGGL(qk_rope_store_kernel<128>, qg, dim3(64), 0, st, qa);
@@ -867,17 +869,17 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     else hipLaunchKernelGGL((attn_split_kernel<64, true>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill attention launch"))) break;
     const GemmSegDev o{L.o, m->pf_x, (size_t)H};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &o, 1, n, qd, lt, il, true, st))) break;
+    if ((s = layer_gemm(m, L, ZG_PROJ_O, &o, 1, n, qd, true, st))) break;
     hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_qs,
                        m->pf_qd, H, d.rms_eps);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
     const GemmSegDev gu[2] = {{L.gate, m->pf_g, (size_t)F}, {L.up, m->pf_u, (size_t)F}};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, gu, 2, n, H, lt, il, false, st))) break;
+    if ((s = layer_gemm(m, L, ZG_PROJ_GATE, gu, 2, n, H, false, st))) break;
     hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_qs, m->pf_qd,
                        F);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill swiglu launch"))) break;
     const GemmSegDev dn{L.down, m->pf_x, (size_t)H};
-    if ((s = run_gemm(ctx, m->pf_qs, m->pf_qd, &dn, 1, n, F, lt, il, true, st))) break;
+    if ((s = layer_gemm(m, L, ZG_PROJ_DOWN, &dn, 1, n, F, true, st))) break;
   }
   return s;
 }
@@ -911,11 +913,25 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       d.n_q_heads / d.n_kv_heads > (uint32_t)kMaxG || (d.head_dim != 128 && d.head_dim != 64) || d.max_ctx == 0 ||
       d.vocab_real > d.vocab_padded || d.vocab_padded == 0)
     return set_error(ctx, ZG_ERR_INVALID_ARG, "model: unsupported dimensions");
-  if ((d.lin_interleave != 4 && d.lin_interleave != 1) || (d.lin_type != ZG_Q4_0 && d.lin_type != ZG_Q8_0))
-    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: layer linears must be Q4_0 or Q8_0, plain or X4");
-  if (d.embd_type != ZG_Q4_0 && d.embd_type != ZG_Q8_0)
-    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: token_embd must be plain Q4_0 or Q8_0");
   const size_t qd = (size_t)d.n_q_heads * d.head_dim, kvd = (size_t)d.n_kv_heads * d.head_dim;
+  // ForwardPassDispatch quants: each projection Q4_0 / Q8_0 (plain or X4) or
+  // Q4_K / Q6_K (plain, in_dim a multiple of 256); token_embd any of the four
+  const size_t proj_k[ZG_N_PROJ] = {d.hidden, d.hidden, d.hidden, qd, d.hidden, d.hidden, d.ffn};
+  for (uint32_t l = 0; l < d.n_layers; l++)
+    for (int p = 0; p < ZG_N_PROJ; p++) {
+      const uint32_t qt = d.layer_quants ? d.layer_quants[l].type[p] : d.lin_type;
+      const uint32_t il = d.layer_quants ? d.layer_quants[l].interleave[p] : d.lin_interleave;
+      const bool q40 = qt == ZG_Q4_0 || qt == ZG_Q8_0, kq = qt == ZG_Q4K || qt == ZG_Q6K;
+      if (!(q40 && (il == 1 || il == 4)) && !(kq && il == 1))
+        return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: layer %u projection %d: type %u layout %u", l, p, qt, il);
+      if (kq && proj_k[p] % 256)
+        return set_error(ctx, ZG_ERR_INVALID_ARG, "model: layer %u projection %d: K-quant in_dim %zu %% 256", l, p,
+                         proj_k[p]);
+    }
+  if (d.embd_type != ZG_Q4_0 && d.embd_type != ZG_Q8_0 && d.embd_type != ZG_Q4K && d.embd_type != ZG_Q6K)
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "model: token_embd type %u", d.embd_type);
+  if ((d.embd_type == ZG_Q4K || d.embd_type == ZG_Q6K) && d.hidden % 256)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "model: K-quant token_embd needs hidden %% 256 == 0");
   for (size_t kk : {(size_t)d.hidden, qd, (size_t)d.ffn})
     if (kk % 64 || kk > kMaxPairK) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: in_dim %zu not supported", kk);
   if (qd % 4 || kvd % 4 || d.ffn % 4 || d.hidden % 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "model: rows % 4");
@@ -925,6 +941,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   m->ctx = ctx;
   m->d = d;
   m->d.layers = nullptr;
+  m->d.layer_quants = nullptr;
   zg_status s = ZG_OK;
   const size_t H = d.hidden, F = d.ffn;
   try {
@@ -941,13 +958,18 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null norm weight");
       break;
     }
-    if ((s = weight_dev(m, W.attn_q, d.lin_type, d.lin_interleave, qd, H, &L.q))) break;
-    if ((s = weight_dev(m, W.attn_k, d.lin_type, d.lin_interleave, kvd, H, &L.k))) break;
-    if ((s = weight_dev(m, W.attn_v, d.lin_type, d.lin_interleave, kvd, H, &L.v))) break;
-    if ((s = weight_dev(m, W.attn_o, d.lin_type, d.lin_interleave, H, qd, &L.o))) break;
-    if ((s = weight_dev(m, W.ffn_gate, d.lin_type, d.lin_interleave, F, H, &L.gate))) break;
-    if ((s = weight_dev(m, W.ffn_up, d.lin_type, d.lin_interleave, F, H, &L.up))) break;
-    if ((s = weight_dev(m, W.ffn_down, d.lin_type, d.lin_interleave, H, F, &L.down))) break;
+    for (int p = 0; p < ZG_N_PROJ; p++) {
+      L.qt[p] = d.layer_quants ? d.layer_quants[l].type[p] : d.lin_type;
+      L.il[p] = d.layer_quants ? d.layer_quants[l].interleave[p] : d.lin_interleave;
+    }
+    const uint32_t *qt = L.qt, *il = L.il;
+    if ((s = weight_dev(m, W.attn_q, qt[ZG_PROJ_Q], il[ZG_PROJ_Q], qd, H, &L.q))) break;
+    if ((s = weight_dev(m, W.attn_k, qt[ZG_PROJ_K], il[ZG_PROJ_K], kvd, H, &L.k))) break;
+    if ((s = weight_dev(m, W.attn_v, qt[ZG_PROJ_V], il[ZG_PROJ_V], kvd, H, &L.v))) break;
+    if ((s = weight_dev(m, W.attn_o, qt[ZG_PROJ_O], il[ZG_PROJ_O], H, qd, &L.o))) break;
+    if ((s = weight_dev(m, W.ffn_gate, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE], F, H, &L.gate))) break;
+    if ((s = weight_dev(m, W.ffn_up, qt[ZG_PROJ_UP], il[ZG_PROJ_UP], F, H, &L.up))) break;
+    if ((s = weight_dev(m, W.ffn_down, qt[ZG_PROJ_DOWN], il[ZG_PROJ_DOWN], H, F, &L.down))) break;
     if ((s = upload_f32(m, &L.attn_norm, W.attn_norm, H))) break;
     if ((s = upload_f32(m, &L.ffn_norm, W.ffn_norm, H))) break;
     if ((s = upload_f32(m, &L.q_norm, W.q_norm, d.head_dim))) break;
@@ -994,21 +1016,24 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->xn), H * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->up), F * sizeof(float));
   if (!s) {
-    // which GEMVs are one launch with the rmsnorm (or attention-merge)
-    // prologue: X4 weights, or plain Q4_0 / Q8_0 at a strip-sized in_dim;
-    // one choice for every layer, so every layer's pointers must qualify
-    const uint32_t lt = d.lin_type, il = d.lin_interleave;
-    bool qkv = true, gu = true, om = m->nsplit > 1 && attn_merge_gemv_ok(lt, il, qd);
-    for (const ZLayer& Li : m->layers) {
-      const FusedDev q3[3] = {{Li.q, m->q, qd, lt, il}, {Li.k, m->k, kvd, lt, il}, {Li.v, m->v, kvd, lt, il}};
-      const FusedDev g2[2] = {{Li.gate, m->act, F, lt, il}, {Li.up, nullptr, F, lt, il}};
-      qkv = qkv && (fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM));
-      gu = gu && (fused_x4_ok(m->hidden, g2, 2, H) || fused_plain_ok(m->hidden, g2, 2, H, PRO_RMSNORM));
-      om = om && (il == 4 ? pair_path_ok(lt, il, qd, H, Li.o, m->part_o) : plain_strip_ok(lt, il, qd, H, Li.o, m->part_o));
+    // per layer, which GEMVs are one launch with the rmsnorm (or
+    // attention-merge) prologue: X4 weights, or plain Q4_0 / Q8_0 at a
+    // strip-sized in_dim, of one type across the fused projections
+    m->pf_ok = true;
+    for (ZLayer& L : m->layers) {
+      const uint32_t *qt = L.qt, *il = L.il;
+      const FusedDev q3[3] = {{L.q, m->q, qd, qt[ZG_PROJ_Q], il[ZG_PROJ_Q]},
+                              {L.k, m->k, kvd, qt[ZG_PROJ_K], il[ZG_PROJ_K]},
+                              {L.v, m->v, kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
+      const FusedDev g2[2] = {{L.gate, m->act, F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
+                              {L.up, nullptr, F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
+      L.qkv_one = fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM);
+      L.gu_one = fused_x4_ok(m->hidden, g2, 2, H) || fused_plain_ok(m->hidden, g2, 2, H, PRO_RMSNORM);
+      const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
+      L.o_merge = m->nsplit > 1 && attn_merge_gemv_ok(ot, oil, qd) &&
+                  (oil == 4 ? pair_path_ok(ot, oil, qd, H, L.o, m->part_o) : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o));
+      for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
     }
-    m->qkv_one = qkv;
-    m->gu_one = gu;
-    m->o_merge = om;
     m->head_norm = rmsnorm_fused_ok(d.head_type, d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
   }
   if (!s) s = capture(m, record_prefill, &m->g_prefill);
@@ -1086,6 +1111,7 @@ extern "C" zg_status zg_model_prefill(zg_model* m, const uint32_t* tokens, size_
   if (!m) return ZG_ERR_INVALID_ARG;
   zg_ctx* ctx = m->ctx;
   if (!tokens || n == 0) return set_error(ctx, ZG_ERR_INVALID_ARG, "prefill: no tokens");
+  if (!m->pf_ok) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "prefill: the GEMMs take Q4_0 / Q8_0 projections");
   if ((size_t)pos0 + n > m->d.max_ctx)
     return set_error(ctx, ZG_ERR_CONTEXT_FULL, "prefill: positions %u..%zu exceed max_ctx %u", pos0, pos0 + n - 1,
                      m->d.max_ctx);
@@ -1130,6 +1156,8 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
                           "prompt upload");
   if (s) return s;
   const bool batched = (flags & ZG_GEN_BATCHED_PREFILL) != 0;
+  if (batched && !m->pf_ok)
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "generate: the batched prefill's GEMMs take Q4_0 / Q8_0 projections");
   if (batched && (s = prefill_alloc(m))) return s;
   if ((s = set_state(m, prompt[0], batched ? (uint32_t)n_prompt - 1 : 0, (uint32_t)n_prompt, (uint32_t)n_gen)))
     return s;

@@ -25,9 +25,9 @@ class GpuModel:
         self.cfg = cfg = model.cfg
         self.model = model
         if register:
-            for L in model.layers:
-                for w in (L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down):
-                    ctx.register(w, cfg.lin_type, cfg.lin_interleave)
+            for li, L in enumerate(model.layers):
+                for p, w in enumerate((L.attn_q, L.attn_k, L.attn_v, L.attn_o, L.ffn_gate, L.ffn_up, L.ffn_down)):
+                    ctx.register(w, *cfg.proj_quant(li, p))
             ctx.register(model.token_embd, cfg.embd_type, 1)
             ctx.register(model.lm_head, cfg.head_type, cfg.head_interleave)
         self._layers = (_lib.zg_layer_weights * cfg.n_layers)()
@@ -49,6 +49,12 @@ class GpuModel:
         d.output_norm = model.output_norm.ctypes.data
         d.layers = self._layers
         d.device_pointers = 0
+        if cfg.layer_quants is not None:
+            self._quants = (_lib.zg_layer_quants * cfg.n_layers)()
+            for i, lq in enumerate(cfg.layer_quants):
+                for p, (t, il) in enumerate(lq):
+                    self._quants[i].type[p], self._quants[i].interleave[p] = t, il
+            d.layer_quants = self._quants
         self._desc = d
         h = C.c_void_p()
         ctx.check(ctx.lib.zg_model_create(ctx.h, C.byref(d), C.byref(h)))

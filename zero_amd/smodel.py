@@ -12,6 +12,7 @@ shape checks (kernel/src/inference.rs:985-1050, main.rs:2745-2760).
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 import os
 from dataclasses import dataclass
 
@@ -20,6 +21,11 @@ import numpy as np
 from . import _lib
 from .ops import ZgError
 from .synth import BLOCK_BYTES, BLOCK_ELEMS, Layer, ModelConfig, RandomModel
+
+# the seven layer projections in ZG_PROJ_* order: runtime tensor names and
+# the model object's fields
+PROJ_NAMES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+LAYER_FIELDS = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down")
 
 NONE_U32 = 0xFFFF_FFFF  # SMODEL_NONE_U32 (model_loader.rs:76)
 ARCH_QWEN3 = 1
@@ -197,24 +203,32 @@ class SModel:
 
     def to_model(self, max_ctx: int | None = None) -> RandomModel:
         """The dense Qwen3 tensors as the model object GpuModel and the
-        oracle take: layer linears of one quant type and one layout (X4 in a
-        v2 artifact, plain rows in v1), plain token embedding, the LM head in
-        its own layout, F32 norms.  Arrays are views of the file."""
+        oracle take: each layer projection in its own quant type and layout
+        (X4 in a v2 artifact, plain rows in v1), plain token embedding, the
+        LM head in its own layout, F32 norms.  Arrays are views of the
+        file."""
         cfg = self.config(max_ctx)
-        H, F, qd, kvd, hd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim, cfg.head_dim
-        lt, il = cfg.lin_type, cfg.lin_interleave
+        H, hd = cfg.hidden, cfg.head_dim
+        # ForwardPassDispatch's per-layer quants: each projection's own type
+        # and layout from the file (a per-layer table only when they differ)
+        quants = []
+        for b in range(cfg.n_layers):
+            row = []
+            for name in PROJ_NAMES:
+                key = f"blk.{b}.{name}.weight"
+                if key not in self:
+                    raise InvalidContainer(_lib.ZG_ERR_INVALID_CONTAINER, f"{key} missing")
+                row.append((self[key].ggml_type, self[key].interleave))
+            quants.append(tuple(row))
+        if any(q != (cfg.lin_type, cfg.lin_interleave) for row in quants for q in row):
+            cfg = dataclasses.replace(cfg, layer_quants=tuple(quants))
         m = RandomModel(cfg)
         for b in range(cfg.n_layers):
             p = f"blk.{b}."
+            w = {field: self._quant(p + name + ".weight", rows, k, *cfg.proj_quant(b, i))
+                 for i, (field, name, (rows, k)) in enumerate(zip(LAYER_FIELDS, PROJ_NAMES, cfg.proj_shapes()))}
             m.layers.append(Layer(
-                attn_q=self._quant(p + "attn_q.weight", qd, H, lt, il),
-                attn_k=self._quant(p + "attn_k.weight", kvd, H, lt, il),
-                attn_v=self._quant(p + "attn_v.weight", kvd, H, lt, il),
-                attn_o=self._quant(p + "attn_output.weight", H, qd, lt, il),
-                ffn_gate=self._quant(p + "ffn_gate.weight", F, H, lt, il),
-                ffn_up=self._quant(p + "ffn_up.weight", F, H, lt, il),
-                ffn_down=self._quant(p + "ffn_down.weight", H, F, lt, il),
-                attn_norm=self._f32(p + "attn_norm.weight", H), ffn_norm=self._f32(p + "ffn_norm.weight", H),
+                **w, attn_norm=self._f32(p + "attn_norm.weight", H), ffn_norm=self._f32(p + "ffn_norm.weight", H),
                 q_norm=self._f32(p + "attn_q_norm.weight", hd), k_norm=self._f32(p + "attn_k_norm.weight", hd)))
         # one row per token id the LM head can emit
         m.token_embd = self._quant("token_embd.weight", cfg.vocab_padded, H, cfg.embd_type, 1)

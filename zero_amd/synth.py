@@ -117,6 +117,19 @@ class ModelConfig:
     head_type: int = Q8_0
     lin_interleave: int = 4   # 4: Q4_0X4/Q8_0X4 layer linears (.smodel-v2); 1: plain rows (v1, GGUF)
     head_interleave: int = 4
+    # per layer, (type, interleave) of Q, K, V, O, gate, up, down (the
+    # per-layer arrays of ForwardPassDispatch); None: lin_type / lin_interleave
+    layer_quants: tuple = None
+
+    def proj_quant(self, layer: int, p: int) -> tuple:
+        if self.layer_quants is None:
+            return self.lin_type, self.lin_interleave
+        return tuple(self.layer_quants[layer][p])
+
+    def proj_shapes(self) -> tuple:
+        """(rows, in_dim) of Q, K, V, O, gate, up, down."""
+        H, F = self.hidden, self.ffn
+        return ((self.q_dim, H), (self.kv_dim, H), (self.kv_dim, H), (H, self.q_dim), (F, H), (F, H), (H, F))
 
     @property
     def q_dim(self):
@@ -129,12 +142,14 @@ class ModelConfig:
     def weight_bytes_per_token(self) -> int:
         """Weight bytes one decode step streams (layers + LM head + one
         embedding row)."""
-        lin = (self.q_dim * self.hidden + 2 * self.kv_dim * self.hidden + self.hidden * self.q_dim
-               + 3 * self.ffn * self.hidden)
-        per = BLOCK_BYTES[self.lin_type] / 32
-        head = self.vocab_padded * self.hidden * BLOCK_BYTES[self.head_type] / 32
-        embd_row = self.hidden * BLOCK_BYTES[self.embd_type] / 32
-        return int(self.n_layers * lin * per + head + embd_row)
+        lin = 0.0
+        for layer in range(self.n_layers):
+            for p, (rows, k) in enumerate(self.proj_shapes()):
+                t = self.proj_quant(layer, p)[0]
+                lin += rows * k * BLOCK_BYTES[t] / BLOCK_ELEMS[t]
+        head = self.vocab_padded * self.hidden * BLOCK_BYTES[self.head_type] / BLOCK_ELEMS[self.head_type]
+        embd_row = self.hidden * BLOCK_BYTES[self.embd_type] / BLOCK_ELEMS[self.embd_type]
+        return int(lin + head + embd_row)
 
 
 QWEN3_1_7B = ModelConfig()
@@ -170,19 +185,20 @@ def random_model(cfg: ModelConfig, seed: int = 0) -> RandomModel:
     padding rows (vocab_real..vocab_padded) zeroed so that an argmax can
     never land there, fp32 norm gains 1 + 0.05 N(0,1)."""
     rng = np.random.default_rng(seed)
-    H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
-    lt, il = cfg.lin_type, cfg.lin_interleave
+    H = cfg.hidden
 
     def gain(n):
         return (1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32)
 
     m = RandomModel(cfg)
-    for _ in range(cfg.n_layers):
-        m.layers.append(Layer(
-            attn_q=weight(rng, lt, qd, H, il), attn_k=weight(rng, lt, kvd, H, il), attn_v=weight(rng, lt, kvd, H, il),
-            attn_o=weight(rng, lt, H, qd, il), ffn_gate=weight(rng, lt, F, H, il), ffn_up=weight(rng, lt, F, H, il),
-            ffn_down=weight(rng, lt, H, F, il), attn_norm=gain(H), ffn_norm=gain(H), q_norm=gain(cfg.head_dim),
-            k_norm=gain(cfg.head_dim)))
+    names = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down")
+    for layer in range(cfg.n_layers):
+        ws = {}
+        for p, (name, (rows, k)) in enumerate(zip(names, cfg.proj_shapes())):
+            qt, il = cfg.proj_quant(layer, p)
+            ws[name] = weight(rng, qt, rows, k, il)
+        m.layers.append(Layer(**ws, attn_norm=gain(H), ffn_norm=gain(H), q_norm=gain(cfg.head_dim),
+                              k_norm=gain(cfg.head_dim)))
     m.token_embd = weight(rng, cfg.embd_type, cfg.vocab_padded, H, 1)
     head_plain = weight(rng, cfg.head_type, cfg.vocab_padded, H, 1)
     bb, nb = BLOCK_BYTES[cfg.head_type], H // BLOCK_ELEMS[cfg.head_type]
@@ -190,6 +206,21 @@ def random_model(cfg: ModelConfig, seed: int = 0) -> RandomModel:
     m.lm_head = interleave_x4(head_plain, cfg.vocab_padded, H, cfg.head_type) if cfg.head_interleave == 4 else head_plain
     m.output_norm = gain(H)
     return m
+
+
+def q4_k_m_layers(n_layers: int) -> tuple:
+    """Per-layer projection quants in the pattern of a GGUF Q4_K_M
+    checkpoint (the reference's default dispatch, forward_pass.rs:209-224,
+    is Q4_K everywhere; such files carry Q6_K attn_v and ffn_down on the
+    first and last eighth of the layers and every third layer between)."""
+    out = []
+    for i in range(n_layers):
+        more = i < n_layers // 8 or i >= 7 * n_layers // 8 or (i - n_layers // 8) % 3 == 2
+        t = [Q4K] * 7
+        if more:
+            t[2] = t[6] = Q6K
+        out.append(tuple((q, 1) for q in t))
+    return tuple(out)
 
 
 def prompt(seed: int, n: int, vocab_real: int) -> np.ndarray:
