@@ -374,6 +374,43 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
   for (int i = threadIdx.x; i < n; i += 256) out[i] = x[i] * rinv * w[i];
 }
 
+// The same for one row of up to 16,384 floats (16-byte aligned, n % 4 == 0):
+// 1024 threads, every x and w load issued before the first is used (the
+// loop above pays one memory round trip per step: 7.8 us for 2048 floats).
+constexpr int kRmsV = 4;  // float4 per thread
+__global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          float* __restrict__ out, int n, float eps) {
+  __shared__ float red[16];
+  const int n4 = n >> 2;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  float4 xv[kRmsV], wv[kRmsV];
+#pragma unroll
+  for (int j = 0; j < kRmsV; j++) {
+    const int i = threadIdx.x + 1024 * j;
+    xv[j] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    wv[j] = i < n4 ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float ssq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRmsV; j++) ssq += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+  ssq = seg_sum<64>(ssq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ssq;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) tot += red[i];
+  const float rinv = 1.0f / sqrtf(tot / (float)n + eps);
+  float4* o4 = reinterpret_cast<float4*>(out);
+#pragma unroll
+  for (int j = 0; j < kRmsV; j++) {
+    const int i = threadIdx.x + 1024 * j;
+    if (i < n4)
+      o4[i] = make_float4(xv[j].x * rinv * wv[j].x, xv[j].y * rinv * wv[j].y, xv[j].z * rinv * wv[j].z,
+                          xv[j].w * rinv * wv[j].w);
+  }
+}
+
 // After the LM head: argmax -> next token, error bits, output record, then
 // move to the next position.
 __global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t vocab_real, uint32_t* out_tokens) {
@@ -555,7 +592,10 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
 }  // namespace zg
 
 hipError_t zg::launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t st) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, n, eps);
+  const bool row = n % 4 == 0 && n <= 4096 * kRmsV && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                                       reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+  if (row) hipLaunchKernelGGL(rmsnorm_row_kernel, dim3(1), dim3(1024), 0, st, x, w, out, n, eps);
+  else hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, n, eps);
   return hipGetLastError();
 }
 
