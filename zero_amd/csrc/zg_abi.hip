@@ -295,6 +295,25 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
     return hip_check(ctx, launch_gemv_plain(a, qt, pro, epi, st), "gemv plain launch");
   }
+  if (pro == PRO_RMSNORM && (epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX) && aligned16(norm_w) &&
+      kq_fused_ok(qt, il, k, w, x)) {
+    // Q4_K strip kernel with the rmsnorm prologue
+    GenericArgs g{};
+    g.w = w;
+    g.x = x;
+    g.y = y;
+    g.resid = resid;
+    g.best = best;
+    g.k = k;
+    g.row_lo = start;
+    g.row_hi = end;
+    g.qt = qt;
+    g.il = (int)il;
+    g.epi = epi;
+    g.norm_w = norm_w;
+    g.eps = eps;
+    return hip_check(ctx, launch_kq_fused(g, true, st), "gemv_kq rmsnorm launch");
+  }
   const float* xin = x;
   if (pro == PRO_RMSNORM) {
     // generic path: normalize into the context's aux buffer first
@@ -341,7 +360,34 @@ bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_
 // it normalizes into the context's aux buffer first).
 bool zg::rmsnorm_fused_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x, int epi) {
   if (pair_path_ok(qt, il, k, n, w, x)) return true;
+  if (kq_fused_ok(qt, il, k, w, x)) return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX;
   return plain_strip_ok(qt, il, k, n, w, x) && (epi == EPI_STORE || epi == EPI_ARGMAX);
+}
+
+// Q4_K gate|up in one launch: y[r] = silu(gate_r . x') * (up_r . x'), x' the
+// rmsnorm of x (norm_w non-null) or x itself.
+bool zg::kq_swiglu_ok(uint32_t qt_gate, uint32_t qt_up, uint32_t il_gate, uint32_t il_up, size_t k, const void* gate,
+                      const void* up, const void* x, const float* norm_w) {
+  return qt_gate == ZG_Q4K && qt_up == ZG_Q4K && kq_fused_ok(qt_gate, il_gate, k, gate, x) &&
+         kq_fused_ok(qt_up, il_up, k, up, x) && (!norm_w || aligned16(norm_w));
+}
+
+zg_status zg::run_kq_swiglu(zg_ctx* ctx, const float* x, const uint8_t* gate, const uint8_t* up, float* y, size_t k,
+                            size_t n, const float* norm_w, float eps, hipStream_t st) {
+  GenericArgs g{};
+  g.w = gate;
+  g.w_up = up;
+  g.x = x;
+  g.y = y;
+  g.k = k;
+  g.row_lo = 0;
+  g.row_hi = n;
+  g.qt = ZG_Q4K;
+  g.il = 1;
+  g.epi = EPI_SWIGLU;
+  g.norm_w = norm_w;
+  g.eps = eps;
+  return hip_check(ctx, launch_kq_fused(g, norm_w != nullptr, st), "gemv_kq swiglu launch");
 }
 
 // Fused same-x dispatch: one launch over the concatenated group space when

@@ -73,6 +73,10 @@ zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, si
                      uint32_t il, size_t start, size_t end, int epi, const float* resid, uint64_t* best, int pro,
                      const float* norm_w, float eps, hipStream_t st, uint32_t gemv_flags = 0);
 bool rmsnorm_fused_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x, int epi);
+bool kq_swiglu_ok(uint32_t qt_gate, uint32_t qt_up, uint32_t il_gate, uint32_t il_up, size_t k, const void* gate,
+                  const void* up, const void* x, const float* norm_w);
+zg_status run_kq_swiglu(zg_ctx* ctx, const float* x, const uint8_t* gate, const uint8_t* up, float* y, size_t k,
+                        size_t n, const float* norm_w, float eps, hipStream_t st);
 bool fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k);
 bool fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro);
 zg_status run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,

@@ -58,6 +58,12 @@ struct GenericArgs {
   uint32_t qt;
   int il;
   int epi;
+  // Q4_K strip kernel only: rmsnorm prologue (norm_w non-null) and, with
+  // EPI_SWIGLU, the up projection paired row for row with w (gate):
+  // y[r] = silu(gate . x) * (up . x)
+  const float* norm_w;
+  float eps;
+  const uint8_t* w_up;
 };
 
 struct DequantArgs {
@@ -85,6 +91,8 @@ constexpr size_t kMaxKqK = 15360;
 bool kq_path_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x);
 size_t kq_lds_bytes(int k);
 hipError_t launch_gemv_kq(const GenericArgs& a, hipStream_t st);
+bool kq_fused_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x);
+hipError_t launch_kq_fused(const GenericArgs& a, bool rmsnorm, hipStream_t st);
 // The strip GEMV can merge attention splits in its prologue (PRO_ATTN).
 bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);

@@ -280,10 +280,18 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
 // strips) and walks batches of rows; two batches of loads are in flight
 // (clamped unconditional loads), a row's partials are summed over the wave
 // (DPP) and then over strips through LDS in a fixed order.
-template <uint32_t QT, int EPI, int RB>
+// PRO 1: rmsnorm prologue (ops.rs:29-52): the sum of squares over the whole
+// vector (the strip waves of sub 0, each lane's 32 values), then each lane
+// scales its activations by rinv * gain before the run sums.  EPI_SWIGLU: a
+// wave's two rows are gate row r and up row r (RB 2), and the epilogue
+// writes silu(gate) * up (activation.rs:115-148 operand order).
+template <uint32_t QT, int EPI, int RB, int PRO = 0>
 __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   constexpr int BB = KqGeom<QT>::BB;
+  constexpr int RPU = EPI == EPI_SWIGLU ? 1 : RB;  // output rows per wave per batch
+  static_assert(EPI != EPI_SWIGLU || RB == 2, "SwiGLU pairs a gate and an up row");
   __shared__ float part[2][32][RB];  // [buffer][wave][row of the batch]
+  __shared__ float red[32];
   const int NW = blockDim.x >> 6;
   const int WPS = NW / S;
   const int lane = threadIdx.x & 63;
@@ -293,14 +301,19 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   const int sb = strip * 8 + (lane >> 3);  // this lane's superblock
   const size_t rowbytes = (size_t)nsb * BB;
   const int nrows = (int)(a.row_hi - a.row_lo);
-  const int per_batch = WPS * RB;
+  const int per_batch = WPS * RPU;
   const int nbatch = (nrows + per_batch - 1) / per_batch;
   auto load_batch = [&](KqLane<QT> (&L)[RB], int batch) {
-    const int base = batch * per_batch + sub * RB;
+    const int base = batch * per_batch + sub * RPU;
 #pragma unroll
     for (int j = 0; j < RB; j++) {
-      const size_t row = a.row_lo + (size_t)min(base + j, nrows - 1);
-      kq_load(L[j], a.w + row * rowbytes + (size_t)sb * BB, lane);
+      if (EPI == EPI_SWIGLU) {
+        const size_t row = a.row_lo + (size_t)min(base, nrows - 1);
+        kq_load(L[j], (j == 0 ? a.w : a.w_up) + row * rowbytes + (size_t)sb * BB, lane);
+      } else {
+        const size_t row = a.row_lo + (size_t)min(base + j, nrows - 1);
+        kq_load(L[j], a.w + row * rowbytes + (size_t)sb * BB, lane);
+      }
     }
   };
   // x first, then the first batch (unconditional: the grid never exceeds
@@ -309,12 +322,41 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   KqLane<QT> LA[RB], LB[RB];
   const int b0 = blockIdx.x, bstep = gridDim.x;
   KqX x = kq_x<QT>(a.x, sb, lane);
+  KqX g;
+  if (PRO == 1) g = kq_x<QT>(a.norm_w, sb, lane);
   load_batch(LA, b0);
+  if (PRO == 1) {
+    float ssq = 0.0f;
+    if (sub == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        ssq += (x.a[c].x * x.a[c].x + x.a[c].y * x.a[c].y + x.a[c].z * x.a[c].z + x.a[c].w * x.a[c].w) +
+               (x.b[c].x * x.b[c].x + x.b[c].y * x.b[c].y + x.b[c].z * x.b[c].z + x.b[c].w * x.b[c].w);
+    }
+    ssq = wave_sum(ssq);
+    if (lane == 0) red[wave] = ssq;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < S; i++) tot += red[i];
+    const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+    float sa = 0.0f, sbs = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      x.a[c] = make_float4(x.a[c].x * rinv * g.a[c].x, x.a[c].y * rinv * g.a[c].y, x.a[c].z * rinv * g.a[c].z,
+                           x.a[c].w * rinv * g.a[c].w);
+      x.b[c] = make_float4(x.b[c].x * rinv * g.b[c].x, x.b[c].y * rinv * g.b[c].y, x.b[c].z * rinv * g.b[c].z,
+                           x.b[c].w * rinv * g.b[c].w);
+      sa += (x.a[c].x + x.a[c].y) + (x.a[c].z + x.a[c].w);
+      sbs += (x.b[c].x + x.b[c].y) + (x.b[c].z + x.b[c].w);
+    }
+    x.sa = sa;
+    x.sb = sbs;
+  }
   asm volatile("" : "+v"(x.sa), "+v"(x.sb));
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
   uint64_t key = 0;
   auto process = [&](const KqLane<QT> (&L)[RB], int batch, int buf) {
-    const int base = batch * per_batch + sub * RB;
+    const int base = batch * per_batch + sub * RPU;
 #pragma unroll
     for (int j = 0; j < RB; j++) {
       const float v = wave_sum(kq_dot(L[j], x, lane));
@@ -322,7 +364,19 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
     }
     __syncthreads();
     const int tt = threadIdx.x;
-    if (tt < per_batch) {
+    if (EPI == EPI_SWIGLU) {
+      if (tt < per_batch) {
+        const int ri = batch * per_batch + tt;
+        if (ri < nrows) {
+          float gv = 0.0f, uv = 0.0f;
+          for (int st = 0; st < S; st++) {
+            gv += part[buf][tt * S + st][0];
+            uv += part[buf][tt * S + st][1];
+          }
+          a.y[a.row_lo + ri] = (gv / (1.0f + expf(-gv))) * uv;
+        }
+      }
+    } else if (tt < per_batch) {
       const int su = tt / RB, j = tt % RB;
       const int ri = batch * per_batch + su * RB + j;
       if (ri < nrows) {
@@ -536,7 +590,7 @@ static int kq_cu_count() {
 #endif
 
 
-template <uint32_t QT, int EPI>
+template <uint32_t QT, int EPI, int PRO = 0>
 static hipError_t launch_kq_strip(const GenericArgs& a, hipStream_t st) {
   // Q4_K: 32-element lanes, two rows per wave per batch.  Q6_K: 64-element
   // lanes (half a wave per row), one row pair per wave per batch.  Measured
@@ -547,13 +601,14 @@ static hipError_t launch_kq_strip(const GenericArgs& a, hipStream_t st) {
   const int nw = S >= 4 ? S : (S == 3 ? 6 : 4);
   const int wps = nw / S;
   const size_t rows = a.row_hi - a.row_lo;
-  const size_t nbatch = (rows + (size_t)wps * RPW - 1) / ((size_t)wps * RPW);
+  const size_t rpw = EPI == EPI_SWIGLU ? 1 : RPW;  // output rows per wave per batch
+  const size_t nbatch = (rows + (size_t)wps * rpw - 1) / ((size_t)wps * rpw);
   const size_t per_cu = nw >= ZG_KQ_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_KQ_STRIP_WAVES_PER_CU / nw);
   const size_t cap = (size_t)kq_cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
   if constexpr (QT == Q4K)
-    hipLaunchKernelGGL((kq_strip_kernel<QT, EPI, 2>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
+    hipLaunchKernelGGL((kq_strip_kernel<QT, EPI, 2, PRO>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
   else
     hipLaunchKernelGGL((kq2_strip_kernel<QT, EPI, 1>), dim3((unsigned)grid), dim3(nw * 64), 0, st, a, S);
   return hipGetLastError();
@@ -574,6 +629,26 @@ static hipError_t launch_kq(const GenericArgs& a, hipStream_t st) {
   if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL((kq_gemv_kernel<QT, EPI>), dim3((unsigned)grid), dim3(kKqWaves * 64), shm, st, a);
   return hipGetLastError();
+}
+
+// Q4_K through the strip kernel with the rmsnorm prologue (EPI_STORE,
+// EPI_RESID, EPI_ARGMAX), or gate|up with the SwiGLU epilogue (EPI_SWIGLU,
+// with or without the prologue): in_dim a multiple of 2048 up to 32768.
+bool kq_fused_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x) {
+  return qt == Q4K && il == 1 && k % 2048 == 0 && k / 2048 <= 16 && kq_path_ok(qt, il, k, w, x);
+}
+
+hipError_t launch_kq_fused(const GenericArgs& a, bool rmsnorm, hipStream_t st) {
+  if (a.qt != Q4K || a.k % 2048 || a.k / 2048 > 16) return hipErrorInvalidValue;
+  if (rmsnorm) {
+    if (a.epi == EPI_STORE) return launch_kq_strip<Q4K, EPI_STORE, 1>(a, st);
+    if (a.epi == EPI_RESID) return launch_kq_strip<Q4K, EPI_RESID, 1>(a, st);
+    if (a.epi == EPI_ARGMAX) return launch_kq_strip<Q4K, EPI_ARGMAX, 1>(a, st);
+    if (a.epi == EPI_SWIGLU) return launch_kq_strip<Q4K, EPI_SWIGLU, 1>(a, st);
+  } else if (a.epi == EPI_SWIGLU) {
+    return launch_kq_strip<Q4K, EPI_SWIGLU, 0>(a, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 bool kq_path_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x) {

@@ -608,6 +608,8 @@ struct ZLayer {
   float *attn_norm, *ffn_norm, *q_norm, *k_norm;
   uint32_t qt[ZG_N_PROJ], il[ZG_N_PROJ];  // ggml type and layout per projection (ZG_PROJ_*)
   bool qkv_one = false, gu_one = false;    // Q|K|V, gate|up (SwiGLU) as one rmsnorm GEMV launch
+  bool qkv_norm_each = false;              // else Q, K, V each with the rmsnorm prologue
+  bool gu_kq = false;                      // else Q4_K gate|up with rmsnorm and SwiGLU in one launch
   bool o_merge = false;                    // the O GEMV merges the attention splits itself
 };
 
@@ -727,6 +729,11 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
                        {L.v, m->v, (size_t)kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
     if (L.qkv_one) {
       if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
+    } else if (L.qkv_norm_each) {
+      for (const FusedDev& f : qkv)
+        if ((s = run_linear(ctx, m->hidden, f.w, f.y, H, f.n, f.qt, f.il, 0, f.n, EPI_STORE, nullptr, nullptr,
+                            PRO_RMSNORM, L.attn_norm, d.rms_eps, st)))
+          return s;
     } else {
       if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
       if ((s = run_fused(ctx, m->xn, qkv, 3, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
@@ -772,6 +779,8 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
       FusedDev gu[2] = {{L.gate, m->act, (size_t)F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
                         {L.up, nullptr, (size_t)F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
       if ((s = run_fused(ctx, m->hidden, gu, 2, H, PRO_RMSNORM, L.ffn_norm, d.rms_eps, EPI_SWIGLU, st))) return s;
+    } else if (L.gu_kq) {
+      if ((s = run_kq_swiglu(ctx, m->hidden, L.gate, L.up, m->act, H, F, L.ffn_norm, d.rms_eps, st))) return s;
     } else {
       FusedDev gu[2] = {{L.gate, m->act, (size_t)F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
                         {L.up, m->up, (size_t)F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
@@ -1069,6 +1078,11 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
                               {L.up, nullptr, F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
       L.qkv_one = fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM);
       L.gu_one = fused_x4_ok(m->hidden, g2, 2, H) || fused_plain_ok(m->hidden, g2, 2, H, PRO_RMSNORM);
+      L.qkv_norm_each = !L.qkv_one;
+      for (const FusedDev& f : q3)
+        L.qkv_norm_each = L.qkv_norm_each && rmsnorm_fused_ok(f.qt, f.il, H, f.n, f.w, m->hidden, EPI_STORE);
+      L.gu_kq = !L.gu_one && kq_swiglu_ok(qt[ZG_PROJ_GATE], qt[ZG_PROJ_UP], il[ZG_PROJ_GATE], il[ZG_PROJ_UP], H,
+                                          L.gate, L.up, m->hidden, L.ffn_norm);
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
       L.o_merge = m->nsplit > 1 && attn_merge_gemv_ok(ot, oil, qd) &&
                   (oil == 4 ? pair_path_ok(ot, oil, qd, H, L.o, m->part_o) : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o));
