@@ -243,6 +243,25 @@ def test_fused_qkv_q8_0(ctx, zo, il):
     ctx.clear()
 
 
+@pytest.mark.parametrize("types", [(Q4K, Q4K, Q4K), (Q4K, Q4K, Q6K), (Q6K, Q4K, Q4K)])
+def test_fused_qkv_kquants(ctx, zo, types):
+    """Q|K|V in K-quants (the Q4_K_M pattern): Q4_K segments share one
+    segmented strip launch (a leading run of two when V is Q6_K); the rest
+    go one by one."""
+    rng = np.random.default_rng(sum(types))
+    k = 2048
+    ws = [synth.weight(rng, t, n, k, 1) for t, n in zip(types, (2048, 1024, 1024))]
+    x = synth.activations(rng, k)
+    outs = [np.empty(n, np.float32) for n in (2048, 1024, 1024)]
+    for w, t in zip(ws, types):
+        ctx.register(w, t, 1)
+    ctx.linear_fused_dispatch(x, [(w, o, t) for w, o, t in zip(ws, outs, types)], k)
+    for w, o, t in zip(ws, outs, types):
+        ref = zo.linear_range(x, w, k, o.size, t, 1)
+        assert rel_err(o, ref) <= REL_TOL
+    ctx.clear()
+
+
 @pytest.fixture(scope="module")
 def lm_head():
     rng = np.random.default_rng(4)

@@ -390,8 +390,42 @@ zg_status zg::run_kq_swiglu(zg_ctx* ctx, const float* x, const uint8_t* gate, co
   return hip_check(ctx, launch_kq_fused(g, norm_w != nullptr, st), "gemv_kq swiglu launch");
 }
 
+// Q4_K segments through the segmented K-quant strip form (EPI_STORE).
+bool zg::fused_kq_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro, const float* norm_w) {
+  bool ok = nseg >= 1 && nseg <= 3 && (pro == PRO_PLAIN || (pro == PRO_RMSNORM && aligned16(norm_w)));
+  for (size_t i = 0; i < nseg && ok; i++) ok = segs[i].qt == ZG_Q4K && kq_fused_ok(segs[i].qt, segs[i].il, k, segs[i].w, x);
+  return ok;
+}
+
+static zg_status run_kq_segs(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
+                             const float* norm_w, float eps, hipStream_t st) {
+  GenericArgs g{};
+  g.x = x;
+  g.k = k;
+  g.qt = ZG_Q4K;
+  g.il = 1;
+  g.epi = EPI_STORE;
+  g.norm_w = pro == PRO_RMSNORM ? norm_w : nullptr;
+  g.eps = eps;
+  g.nseg = (int)nseg;
+  uint32_t end = 0;
+  for (size_t i = 0; i < 3; i++) {
+    const size_t j = i < nseg ? i : nseg - 1;
+    if (i < nseg) end += (uint32_t)segs[i].n;
+    g.seg_w[i] = segs[j].w;
+    g.seg_y[i] = segs[j].y;
+    g.seg_end[i] = end;
+  }
+  g.w = segs[0].w;
+  g.y = segs[0].y;
+  g.row_lo = 0;
+  g.row_hi = end;
+  return hip_check(ctx, launch_kq_fused(g, pro == PRO_RMSNORM, st), "gemv_kq segmented launch");
+}
+
 // Fused same-x dispatch: one launch over the concatenated group space when
-// every segment qualifies, else one launch per segment.
+// every segment qualifies, else one launch per segment (a leading run of
+// two or more Q4_K segments still shares one launch).
 zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                         const float* norm_w, float eps, int epi, hipStream_t st) {
   const bool pair = fused_x4_ok(x, segs, nseg, k);
@@ -419,7 +453,17 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
     return hip_check(ctx, pair ? launch_gemv_x4(a, segs[0].qt, pro, epi, st) : launch_gemv_plain(a, segs[0].qt, pro, epi, st),
                      "fused gemv launch");
   }
-  for (size_t i = 0; i < nseg; i++) {
+  size_t first = 0;
+  if (epi == EPI_STORE) {
+    size_t run = 0;
+    while (run < nseg && fused_kq_ok(x, segs, run + 1, k, pro, norm_w)) run++;
+    if (run == nseg || run >= 2) {
+      zg_status s = run_kq_segs(ctx, x, segs, run, k, pro, norm_w, eps, st);
+      if (s) return s;
+      first = run;
+    }
+  }
+  for (size_t i = first; i < nseg; i++) {
     zg_status s = run_linear(ctx, x, segs[i].w, segs[i].y, k, segs[i].n, segs[i].qt, segs[i].il, 0, segs[i].n,
                              EPI_STORE, nullptr, nullptr, pro, norm_w, eps, st);
     if (s) return s;

@@ -64,6 +64,13 @@ struct GenericArgs {
   const float* norm_w;
   float eps;
   const uint8_t* w_up;
+  // Q4_K strip kernel, EPI_STORE: nseg > 1 concatenates up to 3 projections
+  // of the same x (rows [seg_end[i-1], seg_end[i]) are segment i's rows 0..,
+  // weights seg_w[i], outputs seg_y[i]); w / y / row range are then unused
+  int nseg;
+  const uint8_t* seg_w[3];
+  float* seg_y[3];
+  uint32_t seg_end[3];
 };
 
 struct DequantArgs {

@@ -280,6 +280,11 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
 // strips) and walks batches of rows; two batches of loads are in flight
 // (clamped unconditional loads), a row's partials are summed over the wave
 // (DPP) and then over strips through LDS in a fixed order.
+// Row r of a segmented launch: its weights and output slot.
+__device__ __forceinline__ int kq_seg(const GenericArgs& a, int r) {
+  return r < (int)a.seg_end[0] ? 0 : (r < (int)a.seg_end[1] ? 1 : 2);
+}
+
 // PRO 1: rmsnorm prologue (ops.rs:29-52): the sum of squares over the whole
 // vector (the strip waves of sub 0, each lane's 32 values), then each lane
 // scales its activations by rinv * gain before the run sums.  EPI_SWIGLU: a
@@ -310,6 +315,10 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
       if (EPI == EPI_SWIGLU) {
         const size_t row = a.row_lo + (size_t)min(base, nrows - 1);
         kq_load(L[j], (j == 0 ? a.w : a.w_up) + row * rowbytes + (size_t)sb * BB, lane);
+      } else if (a.nseg > 1) {
+        const int r = min(base + j, nrows - 1), sg = kq_seg(a, r);
+        const size_t local = (size_t)(r - (sg == 0 ? 0 : (int)a.seg_end[sg - 1]));
+        kq_load(L[j], a.seg_w[sg] + local * rowbytes + (size_t)sb * BB, lane);
       } else {
         const size_t row = a.row_lo + (size_t)min(base + j, nrows - 1);
         kq_load(L[j], a.w + row * rowbytes + (size_t)sb * BB, lane);
@@ -383,7 +392,10 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
         float v = 0.0f;
         for (int st = 0; st < S; st++) v += part[buf][su * S + st][j];
         const size_t row = a.row_lo + ri;
-        if (EPI == EPI_RESID)
+        if (EPI == EPI_STORE && a.nseg > 1) {
+          const int sg = kq_seg(a, ri);
+          a.seg_y[sg][ri - (sg == 0 ? 0 : (int)a.seg_end[sg - 1])] = v;
+        } else if (EPI == EPI_RESID)
           a.y[row] = a.resid[row] + v;
         else if (a.y)
           a.y[row] = v;
@@ -632,14 +644,18 @@ static hipError_t launch_kq(const GenericArgs& a, hipStream_t st) {
 }
 
 // Q4_K through the strip kernel with the rmsnorm prologue (EPI_STORE,
-// EPI_RESID, EPI_ARGMAX), or gate|up with the SwiGLU epilogue (EPI_SWIGLU,
-// with or without the prologue): in_dim a multiple of 2048 up to 32768.
+// EPI_RESID, EPI_ARGMAX), gate|up with the SwiGLU epilogue (EPI_SWIGLU, with
+// or without the prologue), or up to 3 segments of one x (EPI_STORE, with or
+// without the prologue): in_dim a multiple of 2048 up to 32768.
 bool kq_fused_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x) {
   return qt == Q4K && il == 1 && k % 2048 == 0 && k / 2048 <= 16 && kq_path_ok(qt, il, k, w, x);
 }
 
 hipError_t launch_kq_fused(const GenericArgs& a, bool rmsnorm, hipStream_t st) {
   if (a.qt != Q4K || a.k % 2048 || a.k / 2048 > 16) return hipErrorInvalidValue;
+  if (a.nseg > 1 && (a.epi != EPI_STORE || a.nseg > 3 || a.row_lo != 0 || a.row_hi != a.seg_end[a.nseg - 1]))
+    return hipErrorInvalidValue;
+  if (!rmsnorm && a.epi == EPI_STORE) return launch_kq_strip<Q4K, EPI_STORE, 0>(a, st);
   if (rmsnorm) {
     if (a.epi == EPI_STORE) return launch_kq_strip<Q4K, EPI_STORE, 1>(a, st);
     if (a.epi == EPI_RESID) return launch_kq_strip<Q4K, EPI_RESID, 1>(a, st);

@@ -1076,7 +1076,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
                               {L.v, m->v, kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
       const FusedDev g2[2] = {{L.gate, m->act, F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
                               {L.up, nullptr, F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
-      L.qkv_one = fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM);
+      L.qkv_one = fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM) ||
+                  fused_kq_ok(m->hidden, q3, 3, H, PRO_RMSNORM, L.attn_norm);
       L.gu_one = fused_x4_ok(m->hidden, g2, 2, H) || fused_plain_ok(m->hidden, g2, 2, H, PRO_RMSNORM);
       L.qkv_norm_each = !L.qkv_one;
       for (const FusedDev& f : q3)
