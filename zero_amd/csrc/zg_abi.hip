@@ -475,6 +475,25 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
 // split merge in the strip kernel's prologue.
 zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd,
                          const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st) {
+  if (qt == ZG_Q4K) {
+    if (!kq_attn_o_ok(qt, il, k, nsplit, hd, w, part_o))
+      return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge Q4_K GEMV: in_dim %zu not supported", k);
+    GenericArgs g{};
+    g.w = w;
+    g.x = part_o;
+    g.y = y;
+    g.resid = y;
+    g.k = k;
+    g.row_lo = 0;
+    g.row_hi = n;
+    g.qt = qt;
+    g.il = (int)il;
+    g.epi = EPI_RESID;
+    g.attn_ml = part_ml;
+    g.attn_nsplit = nsplit;
+    g.attn_hd = hd;
+    return hip_check(ctx, launch_kq_attn_o(g, st), "attention-merge gemv_kq launch");
+  }
   const bool x4 = il == 4;
   if (!attn_merge_gemv_ok(qt, il, k) ||
       !(x4 ? pair_path_ok(qt, il, k, n, w, part_o) : plain_strip_ok(qt, il, k, n, w, part_o)))

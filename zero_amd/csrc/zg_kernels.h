@@ -71,6 +71,10 @@ struct GenericArgs {
   const uint8_t* seg_w[3];
   float* seg_y[3];
   uint32_t seg_end[3];
+  // Q4_K strip kernel, attention-merge prologue: x holds the attention
+  // splits [attn_nsplit][k], attn_ml their (max, exp-sum) per head of attn_hd
+  const float* attn_ml;
+  int attn_nsplit, attn_hd;
 };
 
 struct DequantArgs {
@@ -100,6 +104,8 @@ size_t kq_lds_bytes(int k);
 hipError_t launch_gemv_kq(const GenericArgs& a, hipStream_t st);
 bool kq_fused_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x);
 hipError_t launch_kq_fused(const GenericArgs& a, bool rmsnorm, hipStream_t st);
+bool kq_attn_o_ok(uint32_t qt, uint32_t il, size_t k, int nsplit, int hd, const void* w, const void* x);
+hipError_t launch_kq_attn_o(const GenericArgs& a, hipStream_t st);
 // The strip GEMV can merge attention splits in its prologue (PRO_ATTN).
 bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);

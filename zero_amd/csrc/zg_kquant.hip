@@ -287,7 +287,9 @@ __device__ __forceinline__ int kq_seg(const GenericArgs& a, int r) {
 
 // PRO 1: rmsnorm prologue (ops.rs:29-52): the sum of squares over the whole
 // vector (the strip waves of sub 0, each lane's 32 values), then each lane
-// scales its activations by rinv * gain before the run sums.  EPI_SWIGLU: a
+// scales its activations by rinv * gain before the run sums.  PRO 2: x is
+// the decode attention's split outputs; the workgroup merges them into LDS
+// (8 dims per thread, attn_split_merge) and the lanes read their runs there.  EPI_SWIGLU: a
 // wave's two rows are gate row r and up row r (RB 2), and the epilogue
 // writes silu(gate) * up (activation.rs:115-148 operand order).
 template <uint32_t QT, int EPI, int RB, int PRO = 0>
@@ -297,6 +299,7 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   static_assert(EPI != EPI_SWIGLU || RB == 2, "SwiGLU pairs a gate and an up row");
   __shared__ float part[2][32][RB];  // [buffer][wave][row of the batch]
   __shared__ float red[32];
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // PRO 2: merged x [k]
   const int NW = blockDim.x >> 6;
   const int WPS = NW / S;
   const int lane = threadIdx.x & 63;
@@ -330,10 +333,29 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
   // so that their wait leaves the first batch's loads in flight
   KqLane<QT> LA[RB], LB[RB];
   const int b0 = blockIdx.x, bstep = gridDim.x;
-  KqX x = kq_x<QT>(a.x, sb, lane);
-  KqX g;
+  KqX x, g;
+  AttnSplitIn am;
+  const int k = (int)a.k;
+  if (PRO == 2) {
+    // the first 8 merged dims' inputs ahead of the weights (the wait for
+    // them then leaves the weight loads in flight)
+    if (8 * (int)threadIdx.x < k) attn_split_load(am, a.x, a.attn_ml, k, a.attn_hd, a.attn_nsplit, 8 * threadIdx.x);
+  } else {
+    x = kq_x<QT>(a.x, sb, lane);
+  }
   if (PRO == 1) g = kq_x<QT>(a.norm_w, sb, lane);
   load_batch(LA, b0);
+  if (PRO == 2) {
+    for (int e0 = 8 * threadIdx.x; e0 < k; e0 += 8 * blockDim.x) {
+      if (e0 != 8 * (int)threadIdx.x) attn_split_load(am, a.x, a.attn_ml, k, a.attn_hd, a.attn_nsplit, e0);
+      float4 m0, m1;
+      attn_split_merge(am, a.attn_nsplit, m0, m1);
+      reinterpret_cast<float4*>(xs + e0)[0] = m0;
+      reinterpret_cast<float4*>(xs + e0)[1] = m1;
+    }
+    __syncthreads();
+    x = kq_x<QT>(xs, sb, lane);
+  }
   if (PRO == 1) {
     float ssq = 0.0f;
     if (sub == 0) {
@@ -665,6 +687,31 @@ hipError_t launch_kq_fused(const GenericArgs& a, bool rmsnorm, hipStream_t st) {
     return launch_kq_strip<Q4K, EPI_SWIGLU, 0>(a, st);
   }
   return hipErrorInvalidValue;
+}
+
+// Q4_K O projection with the attention-merge prologue and the residual
+// epilogue; the merged x (k floats) sits in LDS.
+bool kq_attn_o_ok(uint32_t qt, uint32_t il, size_t k, int nsplit, int hd, const void* w, const void* x) {
+  return kq_fused_ok(qt, il, k, w, x) && k <= 8192 && nsplit >= 1 && nsplit <= kAttnSplits && hd % 8 == 0 &&
+         k % hd == 0;
+}
+
+hipError_t launch_kq_attn_o(const GenericArgs& a, hipStream_t st) {
+  if (!kq_attn_o_ok(a.qt, a.il, a.k, a.attn_nsplit, a.attn_hd, a.w, a.x) || a.epi != EPI_RESID || a.nseg > 1)
+    return hipErrorInvalidValue;
+  constexpr int RPW = 2;
+  const int S = (int)(a.k / 2048);
+  const int nw = S >= 4 ? S : (S == 3 ? 6 : 4);
+  const int wps = nw / S;
+  const size_t rows = a.row_hi - a.row_lo;
+  const size_t nbatch = (rows + (size_t)wps * RPW - 1) / ((size_t)wps * RPW);
+  const size_t per_cu = nw >= ZG_KQ_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_KQ_STRIP_WAVES_PER_CU / nw);
+  const size_t cap = (size_t)kq_cu_count() * per_cu;
+  const size_t grid = nbatch < cap ? nbatch : cap;
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((kq_strip_kernel<Q4K, EPI_RESID, 2, 2>), dim3((unsigned)grid), dim3(nw * 64), a.k * sizeof(float),
+                     st, a, S);
+  return hipGetLastError();
 }
 
 bool kq_path_ok(uint32_t qt, uint32_t il, size_t k, const void* w, const void* x) {

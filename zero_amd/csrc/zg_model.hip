@@ -1085,8 +1085,10 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       L.gu_kq = !L.gu_one && kq_swiglu_ok(qt[ZG_PROJ_GATE], qt[ZG_PROJ_UP], il[ZG_PROJ_GATE], il[ZG_PROJ_UP], H,
                                           L.gate, L.up, m->hidden, L.ffn_norm);
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
-      L.o_merge = m->nsplit > 1 && attn_merge_gemv_ok(ot, oil, qd) &&
-                  (oil == 4 ? pair_path_ok(ot, oil, qd, H, L.o, m->part_o) : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o));
+      L.o_merge = m->nsplit > 1 &&
+                  ((attn_merge_gemv_ok(ot, oil, qd) && (oil == 4 ? pair_path_ok(ot, oil, qd, H, L.o, m->part_o)
+                                                                 : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o))) ||
+                   kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
       for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
     }
     m->head_norm = rmsnorm_fused_ok(d.head_type, d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
