@@ -1,7 +1,7 @@
 /*
  * zg_oracle.h -- CPU oracle for the quantized-matmul hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the GPU
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the GPU
  * kernels are compared against, and the CPU baseline that bench.py times
  * beside them.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it.  The product path (zero_amd/) never links,

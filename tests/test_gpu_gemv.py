@@ -16,7 +16,7 @@ from zero_amd import synth
 pytestmark = pytest.mark.gpu
 
 Q4_0, Q8_0, Q4K, Q6K = 2, 8, 12, 14
-REL_TOL = 1e-3  # north-star bar for dot products / logits
+REL_TOL = 1e-3  # parity bar for dot products / logits (rel 1e-3)
 
 
 def dev(a):

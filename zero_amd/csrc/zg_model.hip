@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       }
     }
   };
-  // prologue operands, then round 0's K/V loads
+  // prologue operands, then the first step's K/V loads
   const int hl = lane % HALF;
   const float qx0 = a.q[qh * HD + hl], qx1 = a.q[qh * HD + hl + HALF];
   float kx0 = 0.0f, kx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f, cs0 = 0.0f, cs1 = 0.0f;
