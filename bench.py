@@ -38,7 +38,7 @@ ROTATE_BYTES = 512 << 20
 # (3,527.5 KiB x 2.00) and WRITE_SIZE (24.0 KiB x 1.00); the factors come from
 # the same counters read on an elementwise kernel that reads and writes 256 MiB
 # (--pmc-calib).  1.02 x GEMV_BYTES: the weights are read exactly once.
-GEMV_TRAFFIC_BYTES = 7_248_896
+GEMV_TRAFFIC_BYTES = 7_254_016
 
 
 def log(*a):
