@@ -35,7 +35,7 @@ ROWS, K = 6144, 2048
 GEMV_BYTES = ROWS * (K // 32) * 18 + 4 * K + 4 * ROWS
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the GEMV kernel, from rocprofv3 --pmc FETCH_SIZE
-# (3,527.5 KiB x 2.00) and WRITE_SIZE (24.0 KiB x 1.00); the factors come from
+# (3,530.0 KiB x 2.00) and WRITE_SIZE (24.0 KiB x 1.00); the factors come from
 # the same counters read on an elementwise kernel that reads and writes 256 MiB
 # (--pmc-calib).  1.02 x GEMV_BYTES: the weights are read exactly once.
 GEMV_TRAFFIC_BYTES = 7_254_016
