@@ -386,10 +386,12 @@ typedef uint32_t u32x4a8 __attribute__((ext_vector_type(4), aligned(8)));
 // 2-byte-aligned vector type (still single dwordx4 loads, unaligned access).
 typedef uint32_t u32x4s2 __attribute__((ext_vector_type(4), aligned(2)));
 
-template <uint32_t QT>
+// STREAM: nontemporal loads whatever the type's default (a decode-step LM
+// head, whose cache-allocating read would evict the KV cache).
+template <uint32_t QT, bool STREAM = false>
 __device__ __forceinline__ void strip_load_plain(LaneW<QT>& L, const uint8_t* blk) {
   constexpr int QW = StripGeom<QT>::QW;
-  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : ZG_STRIP_NT_Q4;
+  constexpr bool NT = STREAM || (QT == Q8_0 ? ZG_STRIP_NT_Q8 : ZG_STRIP_NT_Q4);
   const u32x4s2* p = reinterpret_cast<const u32x4s2*>(blk + 2);
 #pragma unroll
   for (int i = 0; i < QW / 4; i++) {
@@ -469,7 +471,8 @@ __device__ __forceinline__ float row_sum4(float v) {
   return v;
 }
 
-// IL 4: X4 group-blocks; IL 1: plain row-major blocks, a "group" being 4
+// IL 4: X4 group-blocks; IL 1: plain row-major blocks (IL 2: the same with
+// nontemporal loads), a "group" being 4
 // consecutive rows (lane (b, r) reads block b of row 4 g + r, b = lane >> 2,
 // r = lane & 3 in either layout, so both give the same bits).  A plain
 // mapping with 16 lanes per row (b = lane & 15, r = lane >> 4: one row's 16
@@ -523,7 +526,7 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
         if (IL == 4)
           strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
         else
-          strip_load_plain<QT>(L[j][p], sg.w + ((size_t)(4 * lg + r) * nb + kb) * BB);
+          strip_load_plain<QT, IL == 2>(L[j][p], sg.w + ((size_t)(4 * lg + r) * nb + kb) * BB);
       }
     }
   };
@@ -980,7 +983,12 @@ static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStre
   if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_strip<QT, PRO_PLAIN, EPI_RESID, 1>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_strip<QT, PRO_PLAIN, EPI_ARGMAX, 1>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_strip<QT, PRO_RMSNORM, EPI_STORE, 1>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 1>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) {
+    // a streamed LM head (the decode step's): 1,032 vs 1,005 tok/s for the
+    // plain-layout Qwen3-1.7B-shape decode
+    if (a.flags & kGemvStream) return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 2>(a, st);
+    return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 1>(a, st);
+  }
   if (pro == PRO_Q8X && epi == EPI_STORE) return launch_strip<QT, PRO_Q8X, EPI_STORE, 1>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_strip<QT, PRO_RMSNORM, EPI_SWIGLU, 1>(a, st);
   if constexpr (QT == Q4_0) {
