@@ -397,9 +397,11 @@ bool zg::fused_kq_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k
   return ok;
 }
 
-static zg_status run_kq_segs(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
-                             const float* norm_w, float eps, hipStream_t st) {
+// xn_out (rmsnorm prologue only): also store the normalized x there.
+zg_status zg::run_kq_segs(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
+                          const float* norm_w, float eps, hipStream_t st, float* xn_out) {
   GenericArgs g{};
+  g.xn_out = pro == PRO_RMSNORM ? xn_out : nullptr;
   g.x = x;
   g.k = k;
   g.qt = ZG_Q4K;

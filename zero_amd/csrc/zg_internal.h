@@ -80,6 +80,8 @@ zg_status run_kq_swiglu(zg_ctx* ctx, const float* x, const uint8_t* gate, const 
 bool fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k);
 bool fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro);
 bool fused_kq_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro, const float* norm_w);
+zg_status run_kq_segs(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
+                      const float* norm_w, float eps, hipStream_t st, float* xn_out = nullptr);
 zg_status run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                     const float* norm_w, float eps, int epi, hipStream_t st);
 zg_status run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd, const uint8_t* w,

@@ -75,6 +75,9 @@ struct GenericArgs {
   // splits [attn_nsplit][k], attn_ml their (max, exp-sum) per head of attn_hd
   const float* attn_ml;
   int attn_nsplit, attn_hd;
+  // rmsnorm prologue: workgroup 0 also stores the normalized x here (k
+  // floats) when non-null, for a following GEMV without the prologue
+  float* xn_out;
 };
 
 struct DequantArgs {

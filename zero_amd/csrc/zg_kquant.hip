@@ -382,6 +382,15 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
     }
     x.sa = sa;
     x.sb = sbs;
+    if (a.xn_out && blockIdx.x == 0 && sub == 0) {
+      // the sub-0 waves' lanes hold every element once
+      float4* o = reinterpret_cast<float4*>(a.xn_out + sb * 256 + kq_lane_elem<QT>(lane));
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        o[c] = x.a[c];
+        o[8 + c] = x.b[c];
+      }
+    }
   }
   asm volatile("" : "+v"(x.sa), "+v"(x.sb));
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);

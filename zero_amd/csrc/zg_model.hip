@@ -609,6 +609,7 @@ struct ZLayer {
   uint32_t qt[ZG_N_PROJ], il[ZG_N_PROJ];  // ggml type and layout per projection (ZG_PROJ_*)
   bool qkv_one = false, gu_one = false;    // Q|K|V, gate|up (SwiGLU) as one rmsnorm GEMV launch
   bool qkv_norm_each = false;              // else Q, K, V each with the rmsnorm prologue
+  bool qk_norm_v = false;                  // else Q4_K Q|K with the prologue, which leaves x' for V
   bool gu_kq = false;                      // else Q4_K gate|up with rmsnorm and SwiGLU in one launch
   bool o_merge = false;                    // the O GEMV merges the attention splits itself
 };
@@ -734,6 +735,11 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
         if ((s = run_linear(ctx, m->hidden, f.w, f.y, H, f.n, f.qt, f.il, 0, f.n, EPI_STORE, nullptr, nullptr,
                             PRO_RMSNORM, L.attn_norm, d.rms_eps, st)))
           return s;
+    } else if (L.qk_norm_v) {
+      if ((s = run_kq_segs(ctx, m->hidden, qkv, 2, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, st, m->xn))) return s;
+      if ((s = run_linear(ctx, m->xn, qkv[2].w, qkv[2].y, H, qkv[2].n, qkv[2].qt, qkv[2].il, 0, qkv[2].n, EPI_STORE,
+                          nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
+        return s;
     } else {
       if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
       if ((s = run_fused(ctx, m->xn, qkv, 3, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
@@ -1082,6 +1088,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       L.qkv_norm_each = !L.qkv_one;
       for (const FusedDev& f : q3)
         L.qkv_norm_each = L.qkv_norm_each && rmsnorm_fused_ok(f.qt, f.il, H, f.n, f.w, m->hidden, EPI_STORE);
+      L.qk_norm_v = !L.qkv_one && !L.qkv_norm_each && fused_kq_ok(m->hidden, q3, 2, H, PRO_RMSNORM, L.attn_norm);
       L.gu_kq = !L.gu_one && kq_swiglu_ok(qt[ZG_PROJ_GATE], qt[ZG_PROJ_UP], il[ZG_PROJ_GATE], il[ZG_PROJ_UP], H,
                                           L.gate, L.up, m->hidden, L.ffn_norm);
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
