@@ -52,6 +52,9 @@ typedef struct zg_ctx zg_ctx;
  * the SMP bring-up that the reference performs before its first dispatch
  * (kernel/src/main.rs:979-1113, smp::set_active_cores). */
 zg_status zg_init(int device, zg_ctx **out);
+/* Releases the context.  A context that still has models (zg_model_create)
+ * is released by the last zg_model_destroy instead; the caller makes no
+ * other call on it after zg_destroy. */
 void zg_destroy(zg_ctx *ctx);
 /* Human-readable message of the last failing call on this context. */
 const char *zg_last_error(const zg_ctx *ctx);
@@ -68,7 +71,10 @@ void *zg_stream(zg_ctx *ctx);
  * the SIDX dtype decode 100/101 -> (Q4_0|Q8_0, 4)
  * (kernel/src/model_loader.rs:82-90).  Lookups are by exact start address
  * or by an address inside a plain tensor (weight_layout.rs:133 semantics:
- * an interior pointer is never interleaved). */
+ * an interior pointer is never interleaved).  The bytes are copied once, at
+ * registration: later changes to the host bytes are not seen, and the host
+ * memory may be freed.  Byte ranges [host_ptr, host_ptr + bytes) of
+ * registered tensors must not overlap (ZG_ERR_INVALID_ARG). */
 zg_status zg_register_weight(zg_ctx *ctx, const void *host_ptr, size_t bytes, uint32_t ggml_type,
                              uint32_t interleave);
 /* Same, but the bytes are already on the device at `dev_ptr` (borrowed,
@@ -80,7 +86,11 @@ zg_status zg_register_weight_device(zg_ctx *ctx, const void *key, const void *de
 uint32_t zg_group_of(const zg_ctx *ctx, const void *host_ptr);
 /* weight_layout::rebase (weight_layout.rs:76): shift every key by delta. */
 void zg_rebase(zg_ctx *ctx, int64_t delta);
-/* weight_layout::clear (weight_layout.rs:57); frees owned uploads. */
+/* weight_layout::clear (weight_layout.rs:57): drops every registration.
+ * Uploaded copies are freed, except those a live model reads: a model keeps
+ * its weights until zg_model_destroy, so it stays valid after a clear (the
+ * reference clears its registry before indexing the next model,
+ * model_loader.rs:488). */
 void zg_clear(zg_ctx *ctx);
 /* Number of registered tensors (weight_layout::count). */
 size_t zg_registered_count(const zg_ctx *ctx);

@@ -11,7 +11,9 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
+#include <iterator>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -38,9 +40,18 @@ zg_status zg::set_error(zg_ctx* ctx, zg_status code, const char* fmt, ...) {
   return code;
 }
 
+// A failing HIP call also leaves its code in the runtime's per-thread
+// last-error slot, which the next hipGetLastError() after an unrelated
+// launch would report: every error path reads that slot once to clear it.
 zg_status zg::hip_check(zg_ctx* ctx, hipError_t e, const char* what) {
   if (e == hipSuccess) return ZG_OK;
+  (void)hipGetLastError();
   return set_error(ctx, ZG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+zg_status zg::alloc_failed(zg_ctx* ctx, hipError_t e, const char* what, size_t bytes) {
+  (void)hipGetLastError();
+  return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "%s: hipMalloc(%zu): %s", what, bytes, hipGetErrorString(e));
 }
 
 static bool type_geom(uint32_t qt, size_t* be, size_t* bb) {
@@ -65,7 +76,7 @@ zg_status zg::ensure_buf(zg_ctx* ctx, DevBuf& b, size_t bytes) {
   b.ptr = nullptr;
   b.bytes = 0;
   hipError_t e = hipMalloc(&b.ptr, bytes);
-  if (e != hipSuccess) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  if (e != hipSuccess) return alloc_failed(ctx, e, "scratch", bytes);
   b.bytes = bytes;
   return ZG_OK;
 }
@@ -94,6 +105,7 @@ extern "C" zg_status zg_init(int device, zg_ctx** out) {
     return ZG_ERR_HIP;
   }
   if (hipMalloc(&ctx->d_best, sizeof(uint64_t) * 4) != hipSuccess) {
+    (void)hipGetLastError();
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return ZG_ERR_OUT_OF_MEMORY;
@@ -102,8 +114,7 @@ extern "C" zg_status zg_init(int device, zg_ctx** out) {
   return ZG_OK;
 }
 
-extern "C" void zg_destroy(zg_ctx* ctx) {
-  if (!ctx) return;
+void zg::destroy_context(zg_ctx* ctx) {
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
   zg_clear(ctx);
@@ -114,6 +125,17 @@ extern "C" void zg_destroy(zg_ctx* ctx) {
   if (ctx->d_best) hipFree(ctx->d_best);
   hipStreamDestroy(ctx->stream);
   delete ctx;
+}
+
+// A model keeps using its context's stream and error slot, so a context
+// with live models is released by the last zg_model_destroy instead.
+extern "C" void zg_destroy(zg_ctx* ctx) {
+  if (!ctx) return;
+  if (ctx->live_models > 0) {
+    ctx->destroy_pending = true;
+    return;
+  }
+  destroy_context(ctx);
 }
 
 extern "C" const char* zg_last_error(const zg_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
@@ -134,8 +156,16 @@ static zg_status do_register(zg_ctx* ctx, uintptr_t key, const void* host, const
   if (il == 4 && qt != ZG_Q4_0 && qt != ZG_Q8_0)
     return set_error(ctx, ZG_ERR_INVALID_ARG, "register: interleave 4 needs Q4_0 or Q8_0");
   if (ctx->reg.size() >= kMaxEntries) return set_error(ctx, ZG_ERR_REGISTRY_FULL, "register: registry full");
-  for (const RegEntry& e : ctx->reg)
-    if (e.key == key) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: key already registered");
+  if (key > UINTPTR_MAX - bytes) return set_error(ctx, ZG_ERR_INVALID_ARG, "register: key range wraps");
+  // Registered byte ranges are disjoint: an interior address resolves to
+  // exactly one tensor.  The table is sorted, so only the neighbours of the
+  // insertion point can overlap [key, key + bytes).
+  auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), key,
+                             [](uintptr_t k, const RegEntry& r) { return k < r.key; });
+  if (it != ctx->reg.begin() && std::prev(it)->key + std::prev(it)->bytes > key)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "register: [%#zx, +%zu) overlaps a registered tensor", (size_t)key, bytes);
+  if (it != ctx->reg.end() && key + bytes > it->key)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "register: [%#zx, +%zu) overlaps a registered tensor", (size_t)key, bytes);
   hipSetDevice(ctx->device);
   RegEntry e;
   e.key = key;
@@ -144,23 +174,27 @@ static zg_status do_register(zg_ctx* ctx, uintptr_t key, const void* host, const
   e.il = il;
   if (dev) {
     e.dev = const_cast<void*>(dev);
-    e.owned = false;
   } else {
     hipError_t he = hipMalloc(&e.dev, bytes);
-    if (he != hipSuccess) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "register: hipMalloc(%zu): %s", bytes, hipGetErrorString(he));
+    if (he != hipSuccess) return alloc_failed(ctx, he, "register", bytes);
     he = hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice);
     if (he != hipSuccess) {
       hipFree(e.dev);
       return hip_check(ctx, he, "register: upload");
     }
-    e.owned = true;
+    const int device = ctx->device;
+    try {
+      e.hold = std::shared_ptr<void>(e.dev, [device](void* p) {
+        hipSetDevice(device);
+        hipFree(p);
+      });
+    } catch (const std::bad_alloc&) {  // the deleter has already run
+      return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "register: host allocation");
+    }
   }
-  auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), key,
-                             [](uintptr_t k, const RegEntry& r) { return k < r.key; });
   try {
     ctx->reg.insert(it, e);
-  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
-    if (e.owned) hipFree(e.dev);
+  } catch (const std::bad_alloc&) {  // no exception crosses the C ABI; e.hold frees the copy
     return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "register: registry growth failed");
   }
   return ZG_OK;
@@ -192,12 +226,13 @@ extern "C" void zg_rebase(zg_ctx* ctx, int64_t delta) {
   for (RegEntry& e : ctx->reg) e.key = (uintptr_t)((int64_t)e.key + delta);
 }
 
+// Drops every registration.  Uploaded copies that a live model resolved
+// stay allocated (the model holds a reference) until that model is
+// destroyed; the others are freed here.
 extern "C" void zg_clear(zg_ctx* ctx) {
   if (!ctx) return;
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
-  for (RegEntry& e : ctx->reg)
-    if (e.owned && e.dev) hipFree(e.dev);
   ctx->reg.clear();
 }
 
@@ -207,7 +242,8 @@ extern "C" size_t zg_registered_count(const zg_ctx* ctx) { return ctx ? ctx->reg
 // gives the tensor and its layout; an interior pointer resolves only inside
 // a plain (interleave 1) tensor, as weight_layout::group_of treats interior
 // pointers as plain (weight_layout.rs:13-19).
-zg_status zg::resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il) {
+zg_status zg::resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il,
+                      std::shared_ptr<void>* hold) {
   const uintptr_t k = reinterpret_cast<uintptr_t>(w);
   auto it = std::upper_bound(ctx->reg.begin(), ctx->reg.end(), k,
                              [](uintptr_t key, const RegEntry& r) { return key < r.key; });
@@ -223,6 +259,7 @@ zg_status zg::resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, cons
     return set_error(ctx, ZG_ERR_INVALID_ARG, "weight %p: %zu bytes needed, %zu registered", w, need, it->bytes - off);
   *dev = static_cast<const uint8_t*>(it->dev) + off;
   *il = off ? 1u : it->il;
+  if (hold) *hold = it->hold;
   return ZG_OK;
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -30,7 +31,11 @@ struct RegEntry {
   uint32_t qt = 0;
   uint32_t il = 1;    // weight_layout.rs GROUPS
   void* dev = nullptr;
-  bool owned = false;
+  // Owner of an uploaded copy (null for borrowed device bytes).  A model
+  // that resolved this tensor holds a second reference, so zg_clear drops
+  // the registry entry while the bytes live until the last model using
+  // them is destroyed.
+  std::shared_ptr<void> hold;
 };
 
 // One weight segment of a prefill GEMM: n output columns into y [m][n].
@@ -58,15 +63,24 @@ struct zg_ctx {
   void* h_pinned = nullptr;
   uint64_t* d_best = nullptr;
   std::string last_error;
+  // models created on this context and not yet destroyed; zg_destroy of a
+  // context with live models is deferred to the last zg_model_destroy
+  int live_models = 0;
+  bool destroy_pending = false;
 };
 
 namespace zg {
 
 zg_status set_error(zg_ctx* ctx, zg_status code, const char* fmt, ...);
 zg_status hip_check(zg_ctx* ctx, hipError_t e, const char* what);
+// ZG_ERR_OUT_OF_MEMORY for a failed hipMalloc, with the runtime's error slot cleared
+zg_status alloc_failed(zg_ctx* ctx, hipError_t e, const char* what, size_t bytes);
 size_t tensor_bytes(uint32_t qt, size_t rows, size_t k);
 zg_status ensure_buf(zg_ctx* ctx, DevBuf& b, size_t bytes);
-zg_status resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il);
+zg_status resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const uint8_t** dev, uint32_t* il,
+                  std::shared_ptr<void>* hold = nullptr);
+// releases the context's own device resources and the context itself
+void destroy_context(zg_ctx* ctx);
 bool pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
 zg_status check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n);
 zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,

@@ -640,6 +640,9 @@ struct zg_model {
   bool head_norm = false;  // the LM-head GEMV takes the output rmsnorm itself
   bool pf_ok = false;      // every layer projection Q4_0 / Q8_0 (the batched prefill's GEMMs)
   std::vector<void*> owned;  // device allocations to free
+  // references to the registry's uploaded weight copies this model reads:
+  // they outlive a zg_clear of the context until the model is destroyed
+  std::vector<std::shared_ptr<void>> weight_refs;
   // g_prefill: embed + layers + advance (prompt tokens before the last);
   // g_step: embed + layers + LM head + finalize (every step that emits a token)
   hipGraphExec_t g_prefill = nullptr, g_step = nullptr;
@@ -658,7 +661,7 @@ constexpr size_t kPrefillChunk = 512;
 
 static zg_status model_alloc(zg_model* m, void** p, size_t bytes) {
   hipError_t e = hipMalloc(p, bytes);
-  if (e != hipSuccess) return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  if (e != hipSuccess) return alloc_failed(m->ctx, e, "model", bytes);
   try {
     m->owned.push_back(*p);
   } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
@@ -684,9 +687,17 @@ static zg_status weight_dev(zg_model* m, const void* key, uint32_t qt, uint32_t 
     return ZG_OK;
   }
   uint32_t got_il;
-  zg_status s = resolve(m->ctx, key, tensor_bytes(qt, rows, k), qt, out, &got_il);
+  std::shared_ptr<void> hold;
+  zg_status s = resolve(m->ctx, key, tensor_bytes(qt, rows, k), qt, out, &got_il, &hold);
   if (s) return s;
   if (got_il != il) return set_error(m->ctx, ZG_ERR_INVALID_ARG, "model: weight %p layout %u, expected %u", key, got_il, il);
+  if (hold) {
+    try {
+      m->weight_refs.push_back(std::move(hold));
+    } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+      return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
+    }
+  }
   return ZG_OK;
 }
 
@@ -994,6 +1005,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   zg_model* m = new (std::nothrow) zg_model();
   if (!m) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
   m->ctx = ctx;
+  ctx->live_models++;  // released by zg_model_destroy (also on the error path below)
   m->d = d;
   m->d.layers = nullptr;
   m->d.layer_quants = nullptr;
@@ -1112,12 +1124,14 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
 
 extern "C" void zg_model_destroy(zg_model* m) {
   if (!m) return;
-  hipSetDevice(m->ctx->device);
-  hipStreamSynchronize(m->ctx->stream);
+  zg_ctx* ctx = m->ctx;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
   for (hipGraphExec_t g : {m->g_prefill, m->g_step})
     if (g) hipGraphExecDestroy(g);
   for (void* p : m->owned) hipFree(p);
-  delete m;
+  delete m;  // drops the weight references: copies cleared from the registry are freed here
+  if (--ctx->live_models == 0 && ctx->destroy_pending) destroy_context(ctx);
 }
 
 static zg_status set_state(zg_model* m, uint32_t token, uint32_t pos, uint32_t n_prompt, uint32_t gen_cap) {
