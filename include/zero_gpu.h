@@ -295,6 +295,17 @@ zg_status zg_linear_q4k_q8k_dev(zg_ctx *ctx, const void *d_q8k, const void *d_w,
  * GEMV.  Synchronous. */
 zg_status zg_linear_q4k_vnni(zg_ctx *ctx, const float *x, const void *w, float *out, size_t in_dim,
                              size_t out_dim);
+/* No counterpart in the reference.  For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops): zg_linear_q4k_vnni on device
+ * pointers (d_x fp32, 16-byte aligned; d_w plain Q4_K, 16-byte aligned;
+ * d_out fp32), asynchronous on `stream` (NULL = the context's stream), with
+ * no hipMalloc or hipFree.  The Q8_K blocks of x go to a fixed device array
+ * of the library: in_dim <= 32768 (37,376 bytes per GPU, held until the
+ * process ends); a larger in_dim is ZG_ERR_INVALID_ARG.  Every call on one
+ * GPU shares that array: calls that may overlap on the same GPU (streams
+ * not ordered against each other) race. */
+zg_status zg_linear_q4k_vnni_noalloc(zg_ctx *ctx, const float *d_x, const void *d_w, float *d_out,
+                                     size_t in_dim, size_t out_dim, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* .smodel native container (SilicatePack SILM + SIDX).                 */

@@ -148,6 +148,7 @@ SIGNATURES = {
     "zg_quantize_q8k_dev": (_ST, [_P, _P, _P, _S, _P]),
     "zg_linear_q4k_q8k_dev": (_ST, [_P, _P, _P, _P, _S, _S, _P]),
     "zg_linear_q4k_vnni": (_ST, [_P, _P, _P, _P, _S, _S]),
+    "zg_linear_q4k_vnni_noalloc": (_ST, [_P, _P, _P, _P, _S, _S, _P]),
     "zg_smodel_open": (_ST, [_P, _S, C.POINTER(_P)]),
     "zg_smodel_close": (None, [_P]),
     "zg_smodel_get_info": (_ST, [_P, C.POINTER(zg_smodel_info)]),

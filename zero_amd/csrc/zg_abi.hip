@@ -110,6 +110,13 @@ extern "C" zg_status zg_init(int device, zg_ctx** out) {
     delete ctx;
     return ZG_ERR_OUT_OF_MEMORY;
   }
+  // the no-allocation entry point's scratch address on this device
+  if (noalloc_scratch_setup(ctx) != ZG_OK) {
+    hipFree(ctx->d_best);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ZG_ERR_HIP;
+  }
   *out = ctx;
   return ZG_OK;
 }

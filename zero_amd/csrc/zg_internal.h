@@ -67,6 +67,9 @@ struct zg_ctx {
   // context with live models is deferred to the last zg_model_destroy
   int live_models = 0;
   bool destroy_pending = false;
+  // this device's copy of the fixed Q8_K scratch array of
+  // zg_linear_q4k_vnni_noalloc (resolved by zg_init)
+  uint8_t* noalloc_scratch = nullptr;
 };
 
 namespace zg {
@@ -81,6 +84,8 @@ zg_status resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, const ui
                   std::shared_ptr<void>* hold = nullptr);
 // releases the context's own device resources and the context itself
 void destroy_context(zg_ctx* ctx);
+// looks up this device's address of the fixed no-allocation scratch array
+zg_status noalloc_scratch_setup(zg_ctx* ctx);
 bool pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
 zg_status check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n);
 zg_status run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt,

@@ -18,6 +18,8 @@
 // in which the superblock terms are added differs (wave and strip sums).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "../../include/zero_gpu.h"
 #include "zg_device.h"
 #include "zg_internal.h"
@@ -294,6 +296,40 @@ static zg_status run_q4k_q8k(zg_ctx* ctx, const uint8_t* q8k, const uint8_t* w, 
   return hip_check(ctx, hipGetLastError(), "q4k x q8k launch");
 }
 
+// ---------------------------------------------------------------------------
+// No-allocation variant of zg_linear_q4k_vnni.  Its Q8_K activation blocks
+// go to a fixed device array of this library instead of a context buffer
+// grown with hipMalloc: in_dim <= 32768 gives at most 128 blocks, 37,376
+// bytes, held by every GPU the library runs on until the process ends.
+// On the host, `scratch` names a host-side stand-in, not device memory:
+// zg_init looks up each device's address of the array once
+// (noalloc_scratch_setup) and host code only ever passes that address.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocMaxK = (size_t)kQ8kMaxStrips * 2048;
+constexpr size_t kNoAllocScratchBytes = kNoAllocMaxK / 256 * kQ8kBytes;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_addr[kMaxDevices];  // per device, filled once
+}  // namespace
+
+// Called by zg_init with ctx->device current.
+zg_status noalloc_scratch_setup(zg_ctx* ctx) {
+  if (ctx->device < 0 || ctx->device >= kMaxDevices)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "noalloc scratch: device %d above %d", ctx->device, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[ctx->device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_check(ctx, e != hipSuccess ? e : hipErrorInvalidSymbol, "noalloc scratch lookup");
+    g_scratch_addr[ctx->device] = static_cast<uint8_t*>(p);
+  }
+  ctx->noalloc_scratch = g_scratch_addr[ctx->device];
+  return ZG_OK;
+}
+
 }  // namespace zg
 
 extern "C" zg_status zg_quantize_q8k_dev(zg_ctx* ctx, const float* d_x, void* d_q8k, size_t n, void* stream) {
@@ -339,4 +375,24 @@ extern "C" zg_status zg_linear_q4k_vnni(zg_ctx* ctx, const float* x, const void*
                                                     ctx->stream), "download")))
     return s;
   return hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync");
+}
+
+// Device pointers, asynchronous on `stream`; no hipMalloc / hipFree.  The
+// quantizer writes every byte of the blocks the GEMV then reads, so the
+// array needs no clearing between calls.  Calls on one GPU share its array:
+// calls that may overlap on that GPU (unordered streams) race.
+extern "C" zg_status zg_linear_q4k_vnni_noalloc(zg_ctx* ctx, const float* d_x, const void* d_w, float* d_out,
+                                               size_t in_dim, size_t out_dim, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_x || !d_w || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "q8k noalloc: null pointer");
+  if (in_dim > kNoAllocMaxK)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "q8k noalloc: in_dim %zu above the %zu values the fixed scratch holds",
+                     in_dim, kNoAllocMaxK);
+  zg_status s = q8k_check(ctx, in_dim, out_dim);
+  if (s) return s;
+  if (!ctx->noalloc_scratch) return set_error(ctx, ZG_ERR_HIP, "q8k noalloc: scratch address not resolved");
+  hipSetDevice(ctx->device);
+  const hipStream_t st = stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+  if ((s = run_q8k_quant(ctx, d_x, ctx->noalloc_scratch, in_dim, st))) return s;
+  return run_q4k_q8k(ctx, ctx->noalloc_scratch, static_cast<const uint8_t*>(d_w), d_out, in_dim, out_dim, st);
 }

@@ -260,6 +260,13 @@ class Context:
         self.check(self.lib.zg_linear_q4k_vnni(self.h, x.ctypes.data, _ptr(w_blocks), out.ctypes.data, in_dim,
                                                out_dim))
 
+    def linear_q4k_vnni_noalloc(self, x, w, out, in_dim, out_dim, stream=None):
+        """linear_q4k_vnni_dispatch on device pointers with no allocation:
+        the Q8_K blocks of x live in the library's fixed device array
+        (in_dim <= 32768)."""
+        self.check(self.lib.zg_linear_q4k_vnni_noalloc(self.h, _ptr(x), _ptr(w), _ptr(out), in_dim, out_dim,
+                                                       stream))
+
     def quantize_q8k_dev(self, x, q8k, n, stream=None):
         """quantize_row_q8k (vnni.rs:78-170) into 292-byte blocks."""
         self.check(self.lib.zg_quantize_q8k_dev(self.h, _ptr(x), _ptr(q8k), n, stream))
