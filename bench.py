@@ -114,11 +114,12 @@ def _row(name, per_ms, nbytes, n, copies, **extra):
     return d
 
 
-def bench_rows(ctx, steps: int):
+def bench_rows(ctx, steps: int, cpu=None):
     """The other hot-path workloads, each timed like the headline GEMV:
     fused Q|K|V Q8_0X4, LM head Q8_0X4 + argmax, Q4_K and Q6_K GEMVs at
     Llama-3-8B FFN shapes (Q4_K also through the Q8_K integer path), and the
-    M=512 int8-MFMA prefill GEMM."""
+    M=512 int8-MFMA prefill GEMM.  With `cpu`, every row also carries the
+    same workload on the host cores (cpu_baseline)."""
     import numpy as np
     import torch
 
@@ -140,7 +141,8 @@ def bench_rows(ctx, steps: int):
     c = _copies(per_copy)
     sd = [[torch.from_numpy(w).cuda() for _, w in segs]]
     sd += [[t.clone() for t in sd[0]] for _ in range(c - 1)]
-    x = torch.from_numpy(synth.activations(rng, H)).cuda()
+    x_host = synth.activations(rng, H)
+    x = torch.from_numpy(x_host).cuda()
     ys = [torch.empty(n, device="cuda") for n, _ in segs]
 
     def qkv(i, st):
@@ -149,6 +151,10 @@ def bench_rows(ctx, steps: int):
     per, n, _ = _graph_time(qkv, c, steps, steps // 10)
     out["fused_qkv_q8_0x4"] = _row("fused Q|K|V Q8_0X4 (2048+1024+1024)x2048", per, per_copy + 4 * H + 4 * 4096, n, c)
     del sd
+    if cpu:
+        out["fused_qkv_q8_0x4"]["cpu_baseline"] = cpu.fused(
+            "Q|K|V Q8_0X4 (2048+1024+1024)x2048", [(r, w, synth.Q8_0, 4) for r, w in segs], x_host, H,
+            per_copy + 4 * H + 4 * 4096)
 
     # LM head Q8_0X4 151936 x 2048 + argmax, logits written
     V = 151_936
@@ -162,7 +168,11 @@ def bench_rows(ctx, steps: int):
 
     per, n, _ = _graph_time(head, c, max(20, steps // 40), 4)
     out["lm_head_q8_0x4_argmax"] = _row("LM head Q8_0X4 151936x2048 + argmax", per, wl.nbytes + 4 * H + 4 * V, n, c)
-    del wd, wl
+    del wd
+    if cpu:
+        out["lm_head_q8_0x4_argmax"]["cpu_baseline"] = cpu.lm_head("LM head Q8_0X4 151936x2048", wl, x_host, H, V,
+                                                                   synth.Q8_0, 4, wl.nbytes + 4 * H + 4 * V)
+    del wl
 
     # the headline GEMV with x encoded to Q8_0 first (the integer block dots):
     # the GEMV alone on a resident Q8_0 row, and quantize + GEMV
@@ -187,6 +197,13 @@ def bench_rows(ctx, steps: int):
     out["q4_0x4_quant_q8act_6144x2048"] = _row("Q4_0X4 6144x2048, quantize x to Q8_0 + GEMV", per,
                                                nbytes + 4 * H + H // 32 * 34, n, c)
     del wd
+    if cpu:
+        # the reference has no Q8_0-activation GEMV: its CPU path for these
+        # weights is the fp32-x Q4_0X4 kernel
+        cb = cpu.gemv("Q4_0X4 6144x2048 (fp32 x: the reference's kernel for these weights)", wh,
+                      xf.cpu().numpy(), H, 6144, synth.Q4_0, 4, wh.nbytes + 4 * H + 4 * 6144)
+        out["q4_0x4_q8act_6144x2048"]["cpu_baseline"] = cb
+        out["q4_0x4_quant_q8act_6144x2048"]["cpu_baseline"] = cb
 
     # plain (GGUF, .smodel-v1) row-major Q4_0: the headline shape and a Kimi K2
     # expert projection (the DeepSeek2 path's bulk layer weights)
@@ -194,7 +211,8 @@ def bench_rows(ctx, steps: int):
                                ("Q4_0 plain 2048x7168 (Kimi K2 expert gate/up)", "q4_0_plain_2048x7168", 2048, 7168)):
         wh = synth.weight(rng, synth.Q4_0, rows, k, 1)
         wd, c = rotating(wh)
-        xk = torch.from_numpy(synth.activations(rng, k)).cuda()
+        xk_host = synth.activations(rng, k)
+        xk = torch.from_numpy(xk_host).cuda()
         yk = torch.empty(rows, device="cuda")
 
         def pl(i, st, wd=wd, xk=xk, yk=yk, rows=rows, k=k):
@@ -203,6 +221,9 @@ def bench_rows(ctx, steps: int):
         per, n, _ = _graph_time(pl, c, max(200, steps // 4), 40)
         out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
         del wd
+        if cpu:
+            out[key]["cpu_baseline"] = cpu.gemv(name, wh, xk_host, k, rows, synth.Q4_0, 1,
+                                                wh.nbytes + 4 * k + 4 * rows)
 
     # the headline kernel on taller Q4_0X4 matrices (8x the headline rows, and
     # the LM head's height): the same strip GEMV with more bytes per launch
@@ -217,14 +238,18 @@ def bench_rows(ctx, steps: int):
 
         per, n, _ = _graph_time(tall, c, max(40, steps // 20), 8)
         out[key] = _row(name, per, wh.nbytes + 4 * H + 4 * rows, n, c)
-        del wd, wh
+        del wd
+        if cpu:
+            out[key]["cpu_baseline"] = cpu.gemv(name, wh, x_host, H, rows, synth.Q4_0, 4, wh.nbytes + 4 * H + 4 * rows)
+        del wh
 
     # k-quants at Llama-3-8B FFN shapes
     for name, qt, rows, k in (("Q4_K 14336x4096 (gate/up)", synth.Q4K, 14336, 4096),
                               ("Q6_K 4096x14336 (down)", synth.Q6K, 4096, 14336)):
         wh = synth.weight(rng, qt, rows, k, 1)
         wd, c = rotating(wh)
-        xk = torch.from_numpy(synth.activations(rng, k)).cuda()
+        xk_host = synth.activations(rng, k)
+        xk = torch.from_numpy(xk_host).cuda()
         yk = torch.empty(rows, device="cuda")
 
         def kq(i, st, wd=wd, xk=xk, yk=yk, qt=qt, rows=rows, k=k):
@@ -233,6 +258,8 @@ def bench_rows(ctx, steps: int):
         per, n, _ = _graph_time(kq, c, max(40, steps // 10), 20)
         key = "q4_k_14336x4096" if qt == synth.Q4K else "q6_k_4096x14336"
         out[key] = _row(name, per, wh.nbytes + 4 * k + 4 * rows, n, c)
+        if cpu:
+            out[key]["cpu_baseline"] = cpu.gemv(name, wh, xk_host, k, rows, qt, 1, wh.nbytes + 4 * k + 4 * rows)
         if qt == synth.Q4K:
             # the same weights through the Q8_K integer path: quantize_row_q8k
             # of x, then the integer GEMV (two launches per call)
@@ -245,6 +272,10 @@ def bench_rows(ctx, steps: int):
             per8, n8, _ = _graph_time(kq8, c, max(40, steps // 10), 20)
             out["q4_k_q8_k_14336x4096"] = _row("Q4_K x Q8_K integer path 14336x4096 (quantize + GEMV)", per8,
                                                wh.nbytes + 4 * k + k // 256 * 292 + 4 * rows, n8, c)
+            if cpu:
+                # the reference's default Q4_K kernel (its VNNI path is
+                # feature-gated off by default)
+                out["q4_k_q8_k_14336x4096"]["cpu_baseline"] = out[key]["cpu_baseline"]
         del wd
 
     # prefill GEMM, M = 512, both FFN shapes, Q4_0X4 weights, Q8_0 activations
@@ -252,7 +283,8 @@ def bench_rows(ctx, steps: int):
     for name, n_out, k in (("up", 6144, 2048), ("down", 2048, 6144)):
         wh = synth.weight(rng, synth.Q4_0, n_out, k, 4)
         wd = torch.from_numpy(wh).cuda()
-        xm = torch.from_numpy(synth.activations(rng, M, k)).cuda()
+        xm_host = synth.activations(rng, M, k)
+        xm = torch.from_numpy(xm_host).cuda()
         qs = torch.empty((M, k), dtype=torch.int8, device="cuda")
         dd = torch.empty((M, k // 32), dtype=torch.int16, device="cuda")
         ym = torch.empty((M, n_out), device="cuda")
@@ -277,7 +309,122 @@ def bench_rows(ctx, steps: int):
             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "ops_per_launch": ops, "bytes_per_launch": nbytes,
             "quantize_us": round(perq * 1e3, 2)}
         log(f"prefill GEMM {name}: {per * 1e3:.1f} us, {tops:.0f} TOPS; quantize {perq * 1e3:.1f} us")
+        if cpu:
+            out[f"prefill_gemm_{name}"]["cpu_baseline"] = cpu.prefill(f"{n_out}x{k} Q4_0X4 (fp32 x rows)", wh,
+                                                                      xm_host, k, n_out, synth.Q4_0, 4, M)
     return out
+
+
+def bench_read_floor(ctx, steps: int):
+    """The floor the GEMVs are measured against: one launch that streams the
+    same number of weight bytes and computes nothing (zg_read_floor_dev),
+    graph-replayed over rotating copies like the headline.  Each size is
+    timed with 1, 2, 4 and 8 128-bit loads per thread; the fastest is the
+    floor."""
+    import torch
+
+    out = {}
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for key, nbytes, what in (("read_floor_7077888B", 7_077_888, "the C1 Q4_0X4 6144x2048 weights"),
+                              ("read_floor_175646208B", 175_646_208, "Q4_0X4 151936x2048 weights")):
+        c = _copies(nbytes)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 0x7F) for i in range(c)]
+        per_u = {}
+        for u in (1, 2, 4, 8):
+            def rd(i, st, u=u):
+                ctx.read_floor_dev(bufs[i], nbytes, u, sink, stream=st)
+
+            per, n, _ = _graph_time(rd, c, max(40, steps // (4 if nbytes < 1 << 24 else 40)), c)
+            per_u[u] = per
+        best_u = min(per_u, key=per_u.get)
+        out[key] = _row(f"read floor: {nbytes} B ({what}), best of 1/2/4/8 loads per thread", per_u[best_u],
+                        nbytes, n, c, loads_per_thread=best_u,
+                        us_by_loads_per_thread={u: round(v * 1e3, 3) for u, v in per_u.items()})
+        del bufs
+    return out
+
+
+def _profile_workloads(ctx, names, reps: int):
+    """Eager launches (no graph) of named workloads, for rocprofv3 counter
+    passes: each dispatch of a kernel gets its own counters.  Weights rotate
+    over copies larger than the Infinity Cache, as in the timed rows."""
+    import numpy as np
+    import torch
+
+    from zero_amd import synth
+
+    rng = np.random.default_rng(11)
+    H = 2048
+    x = torch.from_numpy(synth.activations(rng, 16384)).cuda()
+
+    def rotating(w_host):
+        c = _copies(w_host.nbytes)
+        w0 = torch.from_numpy(w_host).cuda()
+        return [w0] + [w0.clone() for _ in range(c - 1)]
+
+    def run(name, launch, n_rot):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(reps):
+            launch(i % n_rot)
+        torch.cuda.synchronize()
+        log(f"profile {name}: {reps} eager launches, {(time.perf_counter() - t0) / reps * 1e6:.1f} us wall each")
+
+    for name in names:
+        if name == "copy":  # known-size reference for FETCH_SIZE / WRITE_SIZE: 256 MiB read, 256 MiB written
+            src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+            dst = torch.empty_like(src)
+            run(name, lambda i: torch.add(src, 1, out=dst), 1)
+            del src, dst
+        elif name in ("c1", "tall"):
+            rows = 6144 if name == "c1" else 151_936
+            wd = rotating(synth.weight(rng, synth.Q4_0, rows, H, 4))
+            y = torch.empty(rows, device="cuda")
+            run(name, lambda i: ctx.linear_dev(x, wd[i], y, H, rows, synth.Q4_0, 4), len(wd))
+            del wd
+        elif name in ("floor_c1", "floor_tall"):
+            nbytes = 7_077_888 if name == "floor_c1" else 175_646_208
+            bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 0x7F)
+                    for i in range(_copies(nbytes))]
+            sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+            for u in (1, 2, 4, 8):
+                run(f"{name} x{u}", lambda i, u=u: ctx.read_floor_dev(bufs[i], nbytes, u, sink), len(bufs))
+            del bufs
+        elif name == "lmhead":
+            V = 151_936
+            wd = rotating(synth.weight(rng, synth.Q8_0, V, H, 4))
+            logits = torch.empty(V, device="cuda")
+            best = torch.zeros(1, dtype=torch.int64, device="cuda")
+            run(name, lambda i: ctx.lm_head_dev(x, wd[i], logits, H, V, synth.Q8_0, 4, best), len(wd))
+            del wd
+        elif name == "qkv":
+            segs = [(2048, synth.weight(rng, synth.Q8_0, 2048, H, 4)), (1024, synth.weight(rng, synth.Q8_0, 1024, H, 4)),
+                    (1024, synth.weight(rng, synth.Q8_0, 1024, H, 4))]
+            c = _copies(sum(w.nbytes for _, w in segs))
+            sd = [[torch.from_numpy(w).cuda() for _, w in segs]]
+            sd += [[t.clone() for t in sd[0]] for _ in range(c - 1)]
+            ys = [torch.empty(n, device="cuda") for n, _ in segs]
+            run(name, lambda i: ctx.linear_fused_dev(
+                x, [(sd[i][j], ys[j], segs[j][0], synth.Q8_0, 4) for j in range(3)], H), c)
+            del sd
+        elif name in ("q4k", "q6k"):
+            qt, rows, k = (synth.Q4K, 14336, 4096) if name == "q4k" else (synth.Q6K, 4096, 14336)
+            wd = rotating(synth.weight(rng, qt, rows, k, 1))
+            y = torch.empty(rows, device="cuda")
+            run(name, lambda i: ctx.linear_dev(x, wd[i], y, k, rows, qt, 1), len(wd))
+            del wd
+        elif name in ("gemm_up", "gemm_down"):
+            M = 512
+            n_out, k = (6144, 2048) if name == "gemm_up" else (2048, 6144)
+            wd = torch.from_numpy(synth.weight(rng, synth.Q4_0, n_out, k, 4)).cuda()
+            xm = torch.from_numpy(synth.activations(rng, M, k)).cuda()
+            qs = torch.empty((M, k), dtype=torch.int8, device="cuda")
+            dd = torch.empty((M, k // 32), dtype=torch.int16, device="cuda")
+            ym = torch.empty((M, n_out), device="cuda")
+            ctx.quantize_q8_0_split_dev(xm, qs, dd, M, k)
+            run(name, lambda i: ctx.gemm_q8act_dev(qs, dd, wd, ym, M, n_out, k, synth.Q4_0, 4), 1)
+        else:
+            raise SystemExit(f"unknown profile workload {name!r}")
 
 
 def _plain_copy(model):
@@ -356,52 +503,142 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
             "first_tokens": [int(t) for t in toks[:8]], "model": model, "prompt": prompt}
 
 
-def cpu_gemv(w_host, x, seconds=5.0):
-    import numpy as np
+CPU_ROTATE_BYTES = 1 << 30  # host copies per CPU leg: above any host last-level cache
 
-    from oracle import zo
 
-    copies = math.ceil(ROTATE_BYTES / w_host.nbytes) + 1
-    ws = [w_host.copy() for _ in range(copies)]
-    threads = min(16, os.cpu_count() or 1)
-    n = 0
-    with zo.Pool(threads) as pool:
-        zo.linear_parallel(x, ws[0], K, ROWS, 2, 4)
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+class CpuBaseline:
+    """The reference's CPU path on this host: the AVX-512 intrinsics
+    restatement of its range kernels (oracle/zg_avx512.c), split with
+    row_range_for(align = interleave) over one pinned worker per core of the
+    process's CPU share, as the reference's SMP dispatch splits rows over
+    every active core (smp.rs:1282-1296, 1567-1712).  The share is the
+    affinity mask, capped by OMP_NUM_THREADS where the host sets it (the GPU
+    host grants 16 cores per GPU).  Each leg rotates over host copies of its
+    weights totalling >= 1 GiB, so every call streams from DRAM."""
+
+    def __init__(self, seconds: float = 2.0):
+        from oracle import zo
+
+        self.zo = zo
+        self.seconds = seconds
+        aff = len(os.sched_getaffinity(0))
+        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        self.affinity = aff
+        self.threads = min(aff, share) if share > 0 else aff
+        self.model = _cpu_model()
+        self.pool = zo.Pool(self.threads)
+        self.simd = zo.set_simd(True)
+        self.kind = "port"
+
+    def close(self):
+        self.zo.set_simd(False)
+        self.zo.load().zo_pool_stop()
+
+    def _desc(self):
+        kern = "AVX-512 intrinsics" if self.simd else "scalar lane-order C (no AVX-512F on this host)"
+        return (f"{kern} restatement of the reference range kernels, row_range_for split over {self.pool.n} "
+                f"pinned threads of a {self.affinity}-CPU affinity mask, {self.model}")
+
+    def _result(self, value, unit, sample):
+        return {"value": value, "unit": unit, "cores": self.pool.n, "kind": self.kind,
+                "cpu_model": self.model, "sample": f"{sample}; {self._desc()}"}
+
+    def _timed(self, call, n_copies):
+        call(0)  # first touch of the pool and the first copy
+        n = 0
         t0 = time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            zo.linear_parallel(x, ws[n % copies], K, ROWS, 2, 4)
+        while time.perf_counter() - t0 < self.seconds:
+            call(n % n_copies)
             n += 1
-        dt = time.perf_counter() - t0
-        used = pool.n
-    return {"value": GEMV_BYTES * n / dt / 1e9, "unit": "GB/s", "cores": used, "kind": "port",
-            "sample": f"{n} Q4_0X4 6144x2048 GEMVs over {copies} rotating copies ({copies * w_host.nbytes >> 20} MiB), "
-                      f"{dt:.1f}s wall, row_range_for split align 4 over {used} pinned threads"}
+        return n, time.perf_counter() - t0
 
+    @staticmethod
+    def _copies(w_host):
+        c = max(2, math.ceil(CPU_ROTATE_BYTES / w_host.nbytes))
+        return [w_host] + [w_host.copy() for _ in range(c - 1)]
 
-def cpu_decode(model, n_prompt=16, n_gen=32):
-    from oracle import zo
+    def gemv(self, name, w_host, x, k, rows, quant, il, nbytes):
+        """GB/s of algorithmic bytes for the same GEMV as a GPU row."""
+        import numpy as np
 
-    threads = min(16, os.cpu_count() or 1)
-    with zo.Pool(threads) as pool:
+        ws = self._copies(w_host)
+        out = np.empty(rows, np.float32)
+        n, dt = self._timed(lambda i: self.zo.linear_parallel(x, ws[i], k, rows, quant, il, out=out), len(ws))
+        return self._result(nbytes * n / dt / 1e9, "GB/s",
+                            f"{n} {name} GEMVs over {len(ws)} rotating copies "
+                            f"({len(ws) * w_host.nbytes >> 20} MiB) in {dt:.1f}s")
+
+    def fused(self, name, segs, x, k, nbytes):
+        import numpy as np
+
+        n_c = max(2, math.ceil(CPU_ROTATE_BYTES / sum(w.nbytes for _, w, _, _ in segs)))
+        sets = [[(w if c == 0 else w.copy(), r, q, il) for r, w, q, il in segs] for c in range(n_c)]
+        outs = [np.empty(r, np.float32) for r, _, _, _ in segs]
+        n, dt = self._timed(lambda i: self.zo.linear_fused_parallel(
+            x, [(w, r, q, il) for w, r, q, il in sets[i]], k, outs), n_c)
+        return self._result(nbytes * n / dt / 1e9, "GB/s",
+                            f"{n} {name} fused dispatches over {n_c} rotating copies in {dt:.1f}s")
+
+    def lm_head(self, name, w_host, x, k, rows, quant, il, nbytes):
+        import numpy as np
+
+        ws = self._copies(w_host)
+        logits = np.empty(rows, np.float32)
+        n, dt = self._timed(lambda i: self.zo.lm_head_parallel(x, ws[i], k, rows, quant, il, logits), len(ws))
+        return self._result(nbytes * n / dt / 1e9, "GB/s",
+                            f"{n} {name} GEMV + argmax calls over {len(ws)} rotating copies in {dt:.1f}s")
+
+    def prefill(self, name, w_host, xm, k, rows, quant, il, m):
+        """The reference prefills token by token: one GEMV per prompt row.
+        Rate = 2*m*rows*k ops over the time of m GEMVs (fp32 FMAs, in the
+        GPU GEMM's unit), on a bounded sample of rows."""
+        import numpy as np
+
+        ws = self._copies(w_host)
+        out = np.empty(rows, np.float32)
+        n, dt = self._timed(lambda i: self.zo.linear_parallel(xm[i % m], ws[i], k, rows, quant, il, out=out),
+                            len(ws))
+        per_gemv = dt / n
+        tops = 2.0 * rows * k / per_gemv / 1e12
+        return self._result(tops, "TOPS (2*M*N*K fp32 ops)",
+                            f"{n} of the M={m} per-row GEMVs {name} in {dt:.1f}s over {len(ws)} rotating copies "
+                            f"(M GEMVs per GEMM: {m * per_gemv * 1e3:.1f} ms)")
+
+    def decode(self, model, prompt, n_gen, max_gen_seconds=20.0):
+        """forward_single_token over the same random-init model: the prompt
+        token by token (as the reference prefills), then greedy tokens until
+        n_gen or the time bound; tok/s over the generated steps."""
+        zo = self.zo
         om = zo.OracleModel(model)
-        prompt = model_prompt = list(range(1, n_prompt + 1))
         t0 = time.perf_counter()
         for i, t in enumerate(prompt):
-            om.forward(t, i)
+            om.forward(int(t), i)
         rc, tok, _, _ = om.lm_head()
         t1 = time.perf_counter()
-        pos = n_prompt
-        for _ in range(n_gen - 1):
+        pos, steps = len(prompt), 0
+        while steps < n_gen - 1 and time.perf_counter() - t1 < max_gen_seconds:
             om.forward(tok, pos)
             pos += 1
+            steps += 1
             rc, tok, _, _ = om.lm_head()
         t2 = time.perf_counter()
         om.close()
-        used = pool.n
-    del model_prompt
-    return {"value": (n_gen - 1) / (t2 - t1), "unit": "tok/s", "cores": used, "kind": "port",
-            "sample": f"{n_prompt}-token prompt ({t1 - t0:.1f}s) then {n_gen} greedy tokens, tok/s over the "
-                      f"{n_gen - 1} decode steps ({t2 - t1:.1f}s), same random-init Qwen3-1.7B-shape model"}
+        return self._result(steps / (t2 - t1), "tok/s",
+                            f"{len(prompt)}-token prompt token by token ({len(prompt) / (t1 - t0):.1f} tok/s, "
+                            f"{t1 - t0:.1f}s), then {steps} greedy steps in {t2 - t1:.1f}s "
+                            f"(cap {n_gen - 1} steps or {max_gen_seconds:.0f}s), same random-init Qwen3-1.7B-shape "
+                            f"model")
 
 
 def main():
@@ -412,6 +649,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rows", action="store_true", help="skip the fused-QKV, LM-head, k-quant and GEMM lines")
+    ap.add_argument("--profile", default="",
+                    help="comma list of workloads to launch eagerly (no graph) for rocprofv3 counter passes, "
+                         "then exit: c1, tall, floor_c1, floor_tall, lmhead, qkv, q4k, q6k, gemm_up, gemm_down, copy")
+    ap.add_argument("--profile-reps", type=int, default=30)
     ap.add_argument("--pmc-calib", action="store_true",
                     help="first run one elementwise kernel that reads 256 MiB and writes 256 MiB, the "
                          "known-size reference for FETCH_SIZE/WRITE_SIZE counter scaling")
@@ -428,6 +669,10 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     ctx = zero_amd.Context(0)
     torch.cuda.synchronize()
+    if args.profile:
+        _profile_workloads(ctx, [n for n in args.profile.split(",") if n], args.profile_reps)
+        ctx.close()
+        return
     if args.pmc_calib:
         src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -454,8 +699,13 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES},
     }
+    cpu = None if args.no_cpu else CpuBaseline()
+    if cpu:
+        out["cpu_baseline"] = cpu.gemv("Q4_0X4 6144x2048", g["w_host"], g["x_host"], K, ROWS, 2, 4, GEMV_BYTES)
+        log(f"cpu: {out['cpu_baseline']['value']:.1f} GB/s on {cpu.pool.n} threads ({cpu.model})")
     if not args.no_rows:
-        out["rows"] = bench_rows(ctx, args.steps)
+        out["rows"] = bench_rows(ctx, args.steps, cpu)
+        out["rows"].update(bench_read_floor(ctx, args.steps))
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx)
@@ -478,14 +728,12 @@ def main():
                          "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,
                                       "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                                       "bytes_per_token": dec["bytes_per_token"]}}
-    if not args.no_cpu:
-        cb = cpu_gemv(g["w_host"], g["x_host"])
-        log(f"cpu: {cb['value']:.1f} GB/s on {cb['cores']} threads")
-        out["cpu_baseline"] = cb
-        if dec is not None:
-            cd = cpu_decode(dec["model"])
+        if cpu:
+            cd = cpu.decode(dec["model"], dec["prompt"], dec["n_gen"])
             log(f"cpu decode: {cd['value']:.1f} tok/s")
             out["decode"]["cpu_baseline"] = cd
+    if cpu:
+        cpu.close()
     ctx.close()
     print(json.dumps(out))
 

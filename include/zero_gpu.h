@@ -166,6 +166,14 @@ zg_status zg_dequant_dev(zg_ctx *ctx, const void *d_w, float *d_out, size_t rows
 /* fp16 bits -> f32 on the device (dequant.rs:28-61), n values. */
 zg_status zg_fp16_to_f32_dev(zg_ctx *ctx, const uint16_t *d_in, float *d_out, size_t n,
                              void *stream);
+/* Measurement hook, no reference counterpart: one launch that streams
+ * `bytes` (a multiple of 16, 16-byte aligned source) with the GEMV's
+ * nontemporal 128-bit loads and computes nothing, loads_per_thread
+ * (1, 2, 4 or 8) loads per thread of 256-thread workgroups.  The floor a
+ * GEMV of the same weight bytes is measured against.  d_sink: one uint32
+ * that real data never writes. */
+zg_status zg_read_floor_dev(zg_ctx *ctx, const void *d_src, size_t bytes, uint32_t loads_per_thread,
+                            uint32_t *d_sink, void *stream);
 
 /* On-the-fly Q8_0 activation quantization of rows x k values (k % 32 == 0):
  * the packer's quantize_q8_0_block (tools/silicatepack.py:893-907) bit for

@@ -763,6 +763,21 @@ static void pool_run(zo_work_fn fn, void *ctx) {
     while (atomic_load_explicit(&g_pool.done, memory_order_acquire) < n - 1) ZO_PAUSE();
 }
 
+/* The range kernel the pool's slices run: the scalar restatement, or its
+ * AVX-512 intrinsics form (zg_avx512.c) for the CPU baseline. */
+static int g_use_avx512;
+
+int zo_set_simd(int on) {
+    g_use_avx512 = on && zo_avx512_available();
+    return g_use_avx512;
+}
+
+static void run_range(const float *x, const uint8_t *w, float *out, size_t in_dim, size_t out_dim, int t,
+                      int il, size_t s, size_t e) {
+    if (g_use_avx512) zo_linear_range_avx512(x, w, out, in_dim, out_dim, t, il, s, e);
+    else zo_linear_range(x, w, out, in_dim, out_dim, t, il, s, e);
+}
+
 /* for_active_cores_for_rows (smp.rs:1430-1457): at most rows/16 cores. */
 static int cores_for_rows(size_t rows) {
     size_t n = (size_t)zo_pool_size(), cap = rows / 16;
@@ -784,7 +799,7 @@ static void lin_work(void *p, int idx, int n) {
     if (idx >= j->n_eff) return;
     size_t s, e;
     zo_row_range_for(j->out_dim, (uint32_t)j->n_eff, (size_t)idx, (size_t)j->il, &s, &e);
-    if (s < e) zo_linear_range(j->x, j->w, j->out, j->in_dim, j->out_dim, j->t, j->il, s, e);
+    if (s < e) run_range(j->x, j->w, j->out, j->in_dim, j->out_dim, j->t, j->il, s, e);
 }
 
 int zo_linear_parallel(const float *x, const uint8_t *w, float *out, size_t in_dim,
@@ -817,8 +832,8 @@ static void fused_work(void *p, int idx, int n) {
         size_t ss = j->base[k], se = ss + j->segs[k].out_dim;
         size_t lo = s > ss ? s : ss, hi = e < se ? e : se;
         if (lo < hi)
-            zo_linear_range(j->x, j->segs[k].w, j->segs[k].out, j->in_dim, j->segs[k].out_dim,
-                            j->segs[k].ggml_type, j->segs[k].interleave, lo - ss, hi - ss);
+            run_range(j->x, j->segs[k].w, j->segs[k].out, j->in_dim, j->segs[k].out_dim,
+                      j->segs[k].ggml_type, j->segs[k].interleave, lo - ss, hi - ss);
     }
 }
 
@@ -855,8 +870,7 @@ static void lm_work(void *p, int idx, int n) {
     size_t s, e;
     zo_row_range_for(j->lin.out_dim, (uint32_t)j->lin.n_eff, (size_t)idx, (size_t)j->lin.il, &s, &e);
     if (s >= e) return;
-    zo_linear_range(j->lin.x, j->lin.w, j->lin.out, j->lin.in_dim, j->lin.out_dim, j->lin.t,
-                    j->lin.il, s, e);
+    run_range(j->lin.x, j->lin.w, j->lin.out, j->lin.in_dim, j->lin.out_dim, j->lin.t, j->lin.il, s, e);
     float mv;
     size_t li = zo_argmax(j->lin.out + s, e - s, &mv);
     uint32_t gi = (uint32_t)(s + li);
@@ -1154,7 +1168,7 @@ zo_model *zo_model_create(const zo_model_desc *desc) {
     m->gate = (float *)calloc(F, 4);
     m->up = (float *)calloc(F, 4);
     m->act = (float *)calloc(F, 4);
-    m->scores = (float *)calloc(desc->max_ctx, 4);
+    m->scores = (float *)calloc((size_t)desc->n_q_heads * desc->max_ctx, 4);  /* one stripe per head */
     m->logits = (float *)calloc(desc->vocab_padded, 4);
     m->inv_freqs = (float *)calloc((size_t)desc->head_dim / 2, 4);
     if (!m->kv || !m->logits) {
@@ -1176,13 +1190,53 @@ void zo_model_destroy(zo_model *m) {
     free(m);
 }
 
+typedef struct {
+    const float *q, *kc, *vc;
+    size_t T, kvd, hd, gqa, nq, stride;
+    float scale;
+    float *scores, *out;
+    int n_eff;
+    _Atomic int err;
+} attn_job;
+
+/* One participant's heads: row_range_for over the query heads, align 1
+ * (ParallelMatmulContext::for_work_units, smp.rs:1460-1480). */
+static void attn_work(void *p, int idx, int n) {
+    (void)n;
+    attn_job *j = (attn_job *)p;
+    if (idx >= j->n_eff) return;
+    size_t s, e;
+    zo_row_range_for(j->nq, (uint32_t)j->n_eff, (size_t)idx, 1, &s, &e);
+    if (s < e && zo_attn_heads_avx512(j->q, j->kc, j->vc, j->T, j->kvd, j->hd, j->gqa, j->scale, j->scores,
+                                      j->stride, j->out, s, e))
+        atomic_store_explicit(&j->err, 1, memory_order_relaxed);
+}
+
+/* ATTN_PARALLEL_MIN_TOKENS default (inference_avx512.rs:1383). */
+#define ZO_ATTN_PARALLEL_MIN_TOKENS 64
+
 /* All query heads of one token over cache rows 0..T-1
  * (gqa_attention_single_token_avx512, inference_avx512.rs:1744-1800):
- * scores q.k * scale, softmax, weighted sum of V rows in row order. */
+ * scores q.k * scale, softmax, weighted sum of V rows in row order.  With
+ * the AVX-512 kernels in force (the CPU baseline) the heads run in
+ * intrinsics, spread over the pool from 64 cached rows on, one head per
+ * participant at most (inference_avx512.rs:1676-1730); every head's
+ * arithmetic is the same either way.  `scores` holds one stripe of
+ * d->max_ctx floats per query head. */
 static int attend(const zo_model_desc *d, const float *kc, const float *vc, const float *q, size_t T,
                   float scale, float *scores, float *out) {
     size_t hd = (size_t)d->head_dim, nq = (size_t)d->n_q_heads, nkv = (size_t)d->n_kv_heads;
     size_t kvd = nkv * hd, gqa = nq / nkv;
+    if (g_use_avx512) {
+        int n = zo_pool_size();
+        if (T >= ZO_ATTN_PARALLEL_MIN_TOKENS && nq >= 2 && n > 1) {
+            attn_job j = {q, kc, vc, T, kvd, hd, gqa, nq, (size_t)d->max_ctx, scale, scores, out,
+                          (int)(nq < (size_t)n ? nq : (size_t)n), 0};
+            pool_run(attn_work, &j);
+            return atomic_load(&j.err) ? -4 : 0;
+        }
+        return zo_attn_heads_avx512(q, kc, vc, T, kvd, hd, gqa, scale, scores, d->max_ctx, out, 0, nq) ? -4 : 0;
+    }
     for (size_t h = 0; h < nq; h++) {
         size_t kh = h / gqa;
         const float *qv = q + h * hd;

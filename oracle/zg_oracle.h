@@ -54,6 +54,23 @@ int zo_linear_range(const float *x, const uint8_t *w, float *out,
                     size_t in_dim, size_t out_dim, int ggml_type, int interleave,
                     size_t start, size_t end);
 
+/* ---- the same range kernels in AVX-512 intrinsics (zg_avx512.c): the
+ *      CPU baseline; bit-identical to zo_linear_range.  -2 without AVX-512F ---- */
+int zo_avx512_available(void);
+int zo_linear_range_avx512(const float *x, const uint8_t *w, float *out,
+                           size_t in_dim, size_t out_dim, int ggml_type, int interleave,
+                           size_t start, size_t end);
+/* Which range kernels the pool dispatches (zo_linear_parallel, the fused and
+ * LM-head dispatches, the model forward): 1 = the intrinsics, when the CPU
+ * has AVX-512F; 0 = the scalar restatement.  Returns the setting in force. */
+int zo_set_simd(int on);
+/* attn_heads_kernel (inference_avx512.rs:1459-1512) over query heads
+ * [h0, h1) in AVX-512 intrinsics: per-head score stripes of `stride`
+ * floats.  1 on a softmax failure, -2 without AVX-512F. */
+int zo_attn_heads_avx512(const float *q, const float *kc, const float *vc, size_t T, size_t kvd, size_t hd,
+                         size_t gqa, float scale, float *scores, size_t stride, float *out, size_t h0,
+                         size_t h1);
+
 /* ---- f64 brute force (no reference counterpart; exact-ish checker) ---- */
 int zo_linear_f64(const float *x, const uint8_t *w, double *out,
                   size_t in_dim, size_t out_dim, int ggml_type, int interleave);

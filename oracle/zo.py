@@ -53,6 +53,9 @@ _SIG = {
     "zo_dequant_tensor": (_I, [_P, _P, _S, _S, _I, _I]),
     "zo_linear_scalar": (_I, [_P, _P, _P, _S, _S, _I]),
     "zo_linear_range": (_I, [_P, _P, _P, _S, _S, _I, _I, _S, _S]),
+    "zo_avx512_available": (_I, []),
+    "zo_linear_range_avx512": (_I, [_P, _P, _P, _S, _S, _I, _I, _S, _S]),
+    "zo_set_simd": (_I, [_I]),
     "zo_linear_f64": (_I, [_P, _P, _P, _S, _S, _I, _I]),
     "zo_interleave_x4": (_I, [_P, _P, _S, _S, _I]),
     "zo_deinterleave_x4": (_I, [_P, _P, _S, _S, _I]),
@@ -142,6 +145,27 @@ def linear_range(x, w, in_dim, out_dim, quant, interleave=1, start=0, end=None, 
     return out
 
 
+def avx512_available() -> bool:
+    return bool(load().zo_avx512_available())
+
+
+def linear_range_avx512(x, w, in_dim, out_dim, quant, interleave=1, start=0, end=None, out=None) -> np.ndarray:
+    """The AVX-512 intrinsics form of linear_range (zg_avx512.c)."""
+    x = np.ascontiguousarray(x, np.float32)
+    end = out_dim if end is None else end
+    if out is None:
+        out = np.zeros(out_dim, np.float32)
+    rc = load().zo_linear_range_avx512(_p(x), _p(w), _p(out), in_dim, out_dim, quant, interleave, start, end)
+    assert rc == 0, rc
+    return out
+
+
+def set_simd(on: bool) -> bool:
+    """Route the pool's range kernels through the AVX-512 intrinsics (when
+    the CPU has AVX-512F); returns whether they are in force."""
+    return bool(load().zo_set_simd(1 if on else 0))
+
+
 def linear_f64(x, w, in_dim, out_dim, quant, interleave=1) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(out_dim, np.float64)
@@ -149,11 +173,37 @@ def linear_f64(x, w, in_dim, out_dim, quant, interleave=1) -> np.ndarray:
     return out
 
 
-def linear_parallel(x, w, in_dim, out_dim, quant, interleave=1) -> np.ndarray:
+def linear_parallel(x, w, in_dim, out_dim, quant, interleave=1, out=None) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
-    out = np.empty(out_dim, np.float32)
+    if out is None:
+        out = np.empty(out_dim, np.float32)
     assert load().zo_linear_parallel(_p(x), _p(w), _p(out), in_dim, out_dim, quant, interleave) == 0
     return out
+
+
+def linear_fused_parallel(x, segs, in_dim, outs=None):
+    """linear_fused_dispatch over the pool: segs = [(w, out_dim, quant,
+    interleave)], one row split over the concatenated rows."""
+    x = np.ascontiguousarray(x, np.float32)
+    if outs is None:
+        outs = [np.empty(n, np.float32) for _, n, _, _ in segs]
+    arr = (zo_segment * len(segs))()
+    for i, ((w, n, q, il), o) in enumerate(zip(segs, outs)):
+        arr[i] = zo_segment(_p(w), _p(o), n, q, il)
+    assert load().zo_linear_fused_parallel(_p(x), arr, len(segs), in_dim) == 0
+    return outs
+
+
+def lm_head_parallel(x, w, in_dim, out_dim, quant, interleave, logits=None) -> tuple[int, float, np.ndarray]:
+    """lm_head_linear_argmax_dispatch over the pool: logits and the merged
+    first-max argmax."""
+    x = np.ascontiguousarray(x, np.float32)
+    if logits is None:
+        logits = np.empty(out_dim, np.float32)
+    mv = C.c_float()
+    idx = load().zo_lm_head_linear_argmax_parallel(_p(x), _p(w), _p(logits), in_dim, out_dim, quant, interleave,
+                                                   C.byref(mv))
+    return int(idx), float(mv.value), logits
 
 
 def interleave_x4(plain, rows, in_dim, quant) -> np.ndarray:

@@ -804,3 +804,15 @@ extern "C" zg_status zg_fp16_to_f32_dev(zg_ctx* ctx, const uint16_t* d_in, float
   if (!d_in || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "fp16_dev: null pointer");
   return hip_check(ctx, launch_fp16(d_in, d_out, n, pick_stream(ctx, stream)), "fp16 launch");
 }
+
+extern "C" zg_status zg_read_floor_dev(zg_ctx* ctx, const void* d_src, size_t bytes, uint32_t loads_per_thread,
+                                       uint32_t* d_sink, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_src || !d_sink) return set_error(ctx, ZG_ERR_INVALID_ARG, "read_floor: null pointer");
+  if (bytes % 16 || (reinterpret_cast<uintptr_t>(d_src) & 15))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "read_floor: bytes and source must be 16-byte multiples");
+  if (loads_per_thread != 1 && loads_per_thread != 2 && loads_per_thread != 4 && loads_per_thread != 8)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "read_floor: loads_per_thread %u not in {1,2,4,8}", loads_per_thread);
+  return hip_check(ctx, launch_read_floor(d_src, bytes, (int)loads_per_thread, d_sink, pick_stream(ctx, stream)),
+                   "read_floor launch");
+}

@@ -233,6 +233,11 @@ class Context:
     def fp16_to_f32_dev(self, src, out, n, stream=None):
         self.check(self.lib.zg_fp16_to_f32_dev(self.h, _ptr(src), _ptr(out), n, stream))
 
+    def read_floor_dev(self, src, nbytes, loads_per_thread, sink, stream=None):
+        """One streaming read of nbytes (zg_read_floor_dev): the per-launch
+        floor that a GEMV of the same weight bytes is measured against."""
+        self.check(self.lib.zg_read_floor_dev(self.h, _ptr(src), nbytes, loads_per_thread, _ptr(sink), stream))
+
     def quantize_q8_0_dev(self, x, q_blocks, rows, k, stream=None):
         self.check(self.lib.zg_quantize_q8_0_dev(self.h, _ptr(x), _ptr(q_blocks), rows, k, stream))
 
