@@ -432,9 +432,17 @@ __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int
   L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk + 2 * r));
 }
 
+// The block scale through the hardware fp16 conversion: exact for every
+// finite value, subnormals and infinities; a NaN scale gives a NaN row
+// either way (only a signalling NaN's payload would differ from
+// half_bits_to_f32, and the scale only ever feeds a multiply).
+__device__ __forceinline__ float scale_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+}
+
 template <uint32_t QT>
 __device__ __forceinline__ float strip_dot(const LaneW<QT>& L, const float4* xb, float mterm) {
-  const float d = half_bits_to_f32(L.d);
+  const float d = scale_f32(L.d);
   if (QT == Q4_0) return d * (q4_block_dot(L.q, xb) + mterm);
   return d * (q8u_block_dot(L.q, xb) + mterm);
 }
@@ -471,6 +479,40 @@ __device__ __forceinline__ float row_sum4(float v) {
   return v;
 }
 
+// Broadcast of lane S of every quad (DPP quad_perm [S,S,S,S]).
+template <int S>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), S | (S << 2) | (S << 4) | (S << 6), 0xF, 0xF, false));
+}
+template <int S>
+__device__ __forceinline__ float4 quad_bcast4(float4 v) {
+  return make_float4(quad_bcast<S>(v.x), quad_bcast<S>(v.y), quad_bcast<S>(v.z), quad_bcast<S>(v.w));
+}
+
+// The four lanes of a quad (the four rows of one K-block) each hold a
+// quarter of the block's 32 activations: lo = x[4r .. 4r+4), hi =
+// x[16+4r .. 16+4r+4) for quad lane r.  Every lane gets the whole block,
+// xb[c] = lane c's lo and xb[4+c] = lane c's hi, with 32 DPP moves instead
+// of four redundant 128-byte loads per block.
+__device__ __forceinline__ void quad_gather_block(float4 lo, float4 hi, float4 (&xb)[8]) {
+  xb[0] = quad_bcast4<0>(lo);
+  xb[1] = quad_bcast4<1>(lo);
+  xb[2] = quad_bcast4<2>(lo);
+  xb[3] = quad_bcast4<3>(lo);
+  xb[4] = quad_bcast4<0>(hi);
+  xb[5] = quad_bcast4<1>(hi);
+  xb[6] = quad_bcast4<2>(hi);
+  xb[7] = quad_bcast4<3>(hi);
+}
+
+// Sum over a quad: every lane gets ((a + b) + (c + d)), bitwise the same
+// in all four lanes.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+  return v;
+}
+
 // IL 4: X4 group-blocks; IL 1: plain row-major blocks (IL 2: the same with
 // nontemporal loads), a "group" being 4
 // consecutive rows (lane (b, r) reads block b of row 4 g + r, b = lane >> 2,
@@ -478,18 +520,25 @@ __device__ __forceinline__ float row_sum4(float v) {
 // mapping with 16 lanes per row (b = lane & 15, r = lane >> 4: one row's 16
 // blocks contiguous per 16 lanes) measured slower: 5.80 vs 5.22 us at
 // 6144x2048.
-template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
+// ONEB: the grid is the batch count (every workgroup runs exactly one
+// batch), so there is no second register set and no batch loop.
+template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4,
+          bool ONEB = false>
 __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   constexpr int GBY = StripGeom<QT>::GB;
   constexpr int BB = QT == Q4_0 ? 18 : 34;  // plain block bytes
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) float part[];  // [2][NW][GBATCH][PARTS][16]
   __shared__ float red[16];
-  const int NW = blockDim.x >> 6;
-  const int WPS = NW / S;
+  // S >= 3 strips: one wave per strip; S in {1, 2}: four waves, 4 / S per
+  // strip (the launch's block size; no integer division on the way to the
+  // first load)
+  const int WPS = S >= 3 ? 1 : (S == 2 ? 2 : 4);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int strip = wave % S, sub = wave / S;
+  const int strip = S >= 3 ? wave : (S == 2 ? (wave & 1) : 0);
+  const int sub = S >= 3 ? 0 : (S == 2 ? (wave >> 1) : wave);
+  const int NW = S >= 3 ? S : 4;
   const int b = lane >> 2, r = lane & 3;
   const int nb = a.k >> 5;
   const int kb = strip * 16 + b;  // this lane's K-block
@@ -523,10 +572,13 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
       for (int p = 0; p < PARTS; p++) {
         uint32_t lg;
         const GemvSeg sg = locate(min(base + j, items - 1), p, lg);
+        // the group's start is wave-uniform (scalar registers), the lane's
+        // byte offset inside it a 32-bit vector offset
         if (IL == 4)
-          strip_load<QT>(L[j][p], sg.w + ((size_t)lg * nb + kb) * GBY, r);
+          strip_load<QT>(L[j][p], sg.w + (size_t)lg * (size_t)(nb * GBY) + (uint32_t)(kb * GBY), r);
         else
-          strip_load_plain<QT, IL == 2>(L[j][p], sg.w + ((size_t)(4 * lg + r) * nb + kb) * BB);
+          strip_load_plain<QT, IL == 2>(L[j][p], sg.w + (size_t)lg * (size_t)(4 * nb * BB) +
+                                                     (uint32_t)((r * nb + kb) * BB));
       }
     }
   };
@@ -549,15 +601,16 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
     x8[4] = v1.x, x8[5] = v1.y, x8[6] = v1.z, x8[7] = v1.w;
     dxq = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(xbk));
   } else {
+    // this lane's quarter of the x-block (and of the rmsnorm gain, loaded
+    // with x ahead of the barrier that waits for the sum of squares); the
+    // quad shares its quarters through DPP below
     const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
-#pragma unroll
-    for (int c = 0; c < 8; c++) xb[c] = x4[c];
+    xb[0] = x4[r];
+    xb[1] = x4[4 + r];
     if (PRO == PRO_RMSNORM) {
-      // the gain is loaded with x, ahead of the barrier that waits for the
-      // sum of squares
       const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
-#pragma unroll
-      for (int c = 0; c < 8; c++) gw[c] = g4[c];
+      gw[0] = g4[r];
+      gw[1] = g4[4 + r];
     }
   }
   // two batches in flight: this workgroup's first and second
@@ -589,12 +642,12 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
   }
   if (PRO == PRO_RMSNORM) {
     // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w, sum of squares over
-    // the whole vector (each wave's strip blocks, 4 lanes per block: lane
-    // r < 1 of each block contributes)
+    // the whole vector (the first wave of each strip: its 64 lanes hold
+    // the strip's 512 values once)
     float ssq = 0.0f;
-    if (sub == 0 && r == 0) {
+    if (sub == 0) {
 #pragma unroll
-      for (int c = 0; c < 8; c++) ssq += xb[c].x * xb[c].x + xb[c].y * xb[c].y + xb[c].z * xb[c].z + xb[c].w * xb[c].w;
+      for (int c = 0; c < 2; c++) ssq += xb[c].x * xb[c].x + xb[c].y * xb[c].y + xb[c].z * xb[c].z + xb[c].w * xb[c].w;
     }
     ssq = wave_sum(ssq);
     if (lane == 0) red[wave] = ssq;
@@ -603,7 +656,7 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
     for (int i = 0; i < S; i++) tot += red[i];
     const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
+    for (int c = 0; c < 2; c++) {
       const float4 g = gw[c];
       xb[c].x = xb[c].x * rinv * g.x;
       xb[c].y = xb[c].y * rinv * g.y;
@@ -618,13 +671,21 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
     for (int c = 0; c < 8; c++) sx = __builtin_amdgcn_sdot4((int)x8[c], 0x01010101, sx, false);
     asm volatile("" : "+v"(sx));  // computed here, not sunk below the next load
   } else {
-    float t = 0.0f;
+    float t;
+    if (PRO == PRO_ATTN) {
+      t = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+      for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+    } else {
+      // the quad's four quarters: block sum, then the whole block in every lane
+      t = quad_sum(((xb[0].x + xb[0].y) + (xb[0].z + xb[0].w)) + ((xb[1].x + xb[1].y) + (xb[1].z + xb[1].w)));
+      const float4 lo = xb[0], hi = xb[1];
+      quad_gather_block(lo, hi, xb);
+    }
     mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
     asm volatile("" : "+v"(mterm));  // computed here, not sunk below the next load
   }
-  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
+  if (!ONEB && b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
 
   uint64_t key = 0;
   // one batch: partials -> LDS, barrier, per-row totals over strips and
@@ -681,14 +742,18 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
       }
     }
   };
-  // batches b0, b0 + bstep, ... alternate between the two register sets;
-  // a set is refilled with the batch two steps ahead as soon as it is used
-  for (int batch = b0; batch < nbatch; batch += 2 * bstep) {
-    process(LA, batch, 0);
-    if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
-    if (batch + bstep < nbatch) {
-      process(LB, batch + bstep, 1);
-      if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+  if (ONEB) {
+    process(LA, b0, 0);
+  } else {
+    // batches b0, b0 + bstep, ... alternate between the two register sets;
+    // a set is refilled with the batch two steps ahead as soon as it is used
+    for (int batch = b0; batch < nbatch; batch += 2 * bstep) {
+      process(LA, batch, 0);
+      if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
+      if (batch + bstep < nbatch) {
+        process(LB, batch + bstep, 1);
+        if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+      }
     }
   }
   if (EPI == EPI_ARGMAX) {
@@ -870,6 +935,12 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
   const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
+  if (MAXT == 1024 && nbatch <= (size_t)cu_count() * 4) {
+    // one batch per workgroup (every decode-sized launch): no batch loop
+    hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true>), dim3((unsigned)nbatch),
+                       dim3(nw * 64), shm, st, a, S);
+    return hipGetLastError();
+  }
   // about 16 resident waves per CU; the remaining batches are looped over.
   // A 256-thread bound lets the compiler use more registers: the grid is
   // then what the occupancy query says fits.
@@ -906,15 +977,22 @@ static hipError_t launch_strip_gb(const GemvArgs& a, int S, int nw, size_t items
 template <uint32_t QT, int PRO, int EPI, int IL = 4>
 static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   const int S = a.k / 512;
-  const int nw = S >= 4 ? S : 4;  // S in {1, 2} -> 4 waves: 4 / S waves per strip
+  const int nw = S >= 3 ? S : 4;  // S in {1, 2} -> 4 waves: 4 / S waves per strip
   const size_t items = EPI == EPI_SWIGLU ? a.total_groups / 2 : a.total_groups;
   // small launches use short batches so that more workgroups share the
   // work; with argmax epilogues two batches in flight only fit the
   // 1024-thread register budget at two groups per batch
   const size_t wps = nw / S;
-  if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID)) {
+  if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID) && PRO != PRO_ATTN) {
     if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
       return launch_strip_gb<QT, PRO, EPI, 4, 1024, IL>(a, S, nw, items, st);
+    // one-batch launches: groups per wave ~ items / (2 CUs), 1 to 3, so
+    // that every CU gets about two workgroups (C1 6144x2048: three groups
+    // per wave, 512 workgroups of four waves, 3.47 vs 3.56 us at two in a
+    // probe)
+    const size_t per = items / ((size_t)cu_count() * 2 * wps);
+    if (per >= 3) return launch_strip_gb<QT, PRO, EPI, 3, 1024, IL>(a, S, nw, items, st);
+    if (per < 2) return launch_strip_gb<QT, PRO, EPI, 1, 1024, IL>(a, S, nw, items, st);
   }
   if constexpr (QT == Q8_0 && EPI != EPI_SWIGLU && PRO != PRO_ATTN) {
     // tall Q8_0X4 (the LM head): four groups per batch with 16-byte loads
