@@ -522,9 +522,12 @@ __device__ __forceinline__ float quad_sum(float v) {
 // 6144x2048.
 // ONEB: the grid is the batch count (every workgroup runs exactly one
 // batch), so there is no second register set and no batch loop.
+// SC: the strip count as a compile-time constant (0: the argument S_rt),
+// for the common one-batch shapes (in_dim 2048 and 6144).
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4,
-          bool ONEB = false>
-__global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S) {
+          bool ONEB = false, int SC = 0>
+__global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) {
+  const int S = SC ? SC : S_rt;
   constexpr int GBY = StripGeom<QT>::GB;
   constexpr int BB = QT == Q4_0 ? 18 : 34;  // plain block bytes
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -927,6 +930,7 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 #define ZG_STRIP_ENABLE 1
 #endif
 
+
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
@@ -937,8 +941,15 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
   if (MAXT == 1024 && nbatch <= (size_t)cu_count() * 4) {
     // one batch per workgroup (every decode-sized launch): no batch loop
-    hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true>), dim3((unsigned)nbatch),
-                       dim3(nw * 64), shm, st, a, S);
+    if (S == 4)
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 4>), dim3((unsigned)nbatch),
+                         dim3(nw * 64), shm, st, a, S);
+    else if (S == 12)
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 12>), dim3((unsigned)nbatch),
+                         dim3(nw * 64), shm, st, a, S);
+    else
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true>), dim3((unsigned)nbatch),
+                         dim3(nw * 64), shm, st, a, S);
     return hipGetLastError();
   }
   // about 16 resident waves per CU; the remaining batches are looped over.
@@ -1001,10 +1012,10 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
     if (nw == 4 && items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
       return launch_strip_gb<QT, PRO, EPI, 4, 256, IL>(a, S, nw, items, st);
   }
-  // gate|up (SwiGLU): one item (a gate and an up group) per batch gives
-  // 1536 batches at Qwen3-1.7B's FFN, so most workgroups get a second batch
-  // to overlap (8.35 vs 8.60 us traced, 2 items per batch)
-  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, 1, 1024, IL>(a, S, nw, items, st);
+  // gate|up (SwiGLU): two items (a gate and an up group each) per batch,
+  // 768 one-batch workgroups at Qwen3-1.7B's FFN (decode 1,326 vs 1,297
+  // tok/s with one item per batch and a batch loop)
+  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, 2, 1024, IL>(a, S, nw, items, st);
   return launch_strip_gb<QT, PRO, EPI, 2, 1024, IL>(a, S, nw, items, st);
 }
 
@@ -1043,6 +1054,13 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
     }
     if constexpr (QT == Q4_0) {
       if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
+    }
+    if constexpr (QT == Q8_0) {
+      // decode-sized Q8_0X4 launches (fused Q|K|V): the one-batch strip
+      // form; streamed ones (the decode step's LM head) keep the segment
+      // kernel's nontemporal loads
+      if (strip_path_ok(a.k) && !(a.flags & kGemvStream) && a.total_groups <= (uint32_t)cu_count() * 8)
+        return launch_strip<QT, PRO, EPI>(a, st);
     }
     return launch_x4<QT, PRO, EPI>(a, st);
   }

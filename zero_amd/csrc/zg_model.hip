@@ -107,7 +107,13 @@ struct AttnArgs {
   uint16_t* qsd;
 };
 
-constexpr int kAttnWaves = 4;
+#ifndef ZG_ATTN_WAVES
+#define ZG_ATTN_WAVES 4
+#endif
+#ifndef ZG_ATTN_PASSES
+#define ZG_ATTN_PASSES 4
+#endif
+constexpr int kAttnWaves = ZG_ATTN_WAVES;
 
 // Decode attention, flash-decoding over splits: grid (query heads, splits),
 // one 4-wave workgroup per (head, split of split_len context rows).  Rows
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   constexpr int RPW = 64 / LPR;         // rows per wave per pass
   constexpr int NWV = kAttnWaves;
   constexpr int PASS = RPW * NWV;       // rows per pass
-  constexpr int NP = 4;                 // passes per round
+  constexpr int NP = ZG_ATTN_PASSES;    // passes per round
   constexpr int ROUND = NP * PASS;      // rows per round
   constexpr int VPL = HD / 64;          // V dims per lane
   constexpr int HALF = HD / 2;
