@@ -268,6 +268,40 @@ def test_prefill_bounds(ctx, tiny):
         ctx.clear()
 
 
+def test_qwen3_1_7b_shape_batched_prefill_matches_oracle(ctx, zo):
+    """12-row batched prefill through all 28 layers of the Qwen3-1.7B shape
+    against the oracle's zo_model_prefill_q8 on the same prompt: last hidden
+    state and logits within rel 1e-3, the same next token, then 8 decode
+    steps from the prefilled cache token for token."""
+    cfg = synth.ModelConfig(max_ctx=64)
+    model = synth.random_model(cfg, seed=21)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(31, 12, cfg.vocab_real)
+        tok, mv, hid = gm.prefill(prompt, want_hidden=True)
+        h_ref = om.prefill_q8(prompt)
+        rc, t_ref, m_ref, _ = om.lm_head()
+        assert rc == 0
+        err = rel_err(hid, h_ref)
+        print(f"Qwen3-1.7B shape, 12-row prefill: hidden rel err {err:.2e}")
+        assert err <= REL_TOL
+        assert tok == t_ref and abs(mv - m_ref) <= REL_TOL * abs(m_ref)
+        pos = len(prompt)
+        with zo.Pool(16):
+            for _ in range(8):
+                nxt, _, h2, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+                h2_ref = om.forward(tok, pos)
+                rc, t2_ref, _, lg2_ref = om.lm_head()
+                assert rel_err(h2, h2_ref) <= REL_TOL and rel_err(lg, lg2_ref) <= REL_TOL
+                assert nxt == t2_ref, pos
+                tok, pos = nxt, pos + 1
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def test_qwen3_1_7b_shape_batched_prefill(ctx):
     """128-token prefill at the Qwen3-1.7B shape: the last hidden state is
     within the Q8_0 activation-quantization distance of the token-by-token

@@ -92,10 +92,10 @@ def test_gemm_bit_exact_with_oracle(ctx, zo, m, n, k, wt, il):
     x = synth.activations(rng, m, k)
     y = _gemm(ctx, x, w, n, k, wt, il)
     xq = zo.quantize_q8_0(x.reshape(-1))
-    rows = sorted({int(r) for r in [0, 1, m - 1, *rng.integers(0, m, 6)] if r < m})
-    for r in rows:
-        ref = zo.gemm_q8act(xq[r * (k // 32) * 34:(r + 1) * (k // 32) * 34], w, 1, n, k, wt, il)[0]
-        assert np.array_equal(y[r].view(np.uint32), ref.view(np.uint32)), r
+    # every row (the oracle takes ~6 s per 512-row prefill shape)
+    ref = zo.gemm_q8act(xq, w, m, n, k, wt, il)
+    bad = np.flatnonzero(np.any(y.view(np.uint32) != ref.view(np.uint32), axis=1))
+    assert bad.size == 0, f"{bad.size} of {m} rows differ, first {bad[:8]}"
     # report the Q8_0-activation error against the fp32-activation GEMV
     f = zo.linear_range(x[0], w, k, n, wt, il)
     err = float(np.max(np.abs(y[0] - f)) / np.max(np.abs(f)))
