@@ -35,10 +35,11 @@ ROWS, K = 6144, 2048
 GEMV_BYTES = ROWS * (K // 32) * 18 + 4 * K + 4 * ROWS
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the GEMV kernel, from rocprofv3 --pmc FETCH_SIZE
-# (3,530.0 KiB x 2.00) and WRITE_SIZE (24.0 KiB x 1.00); the factors come from
-# the same counters read on an elementwise kernel that reads and writes 256 MiB
-# (--pmc-calib).  1.02 x GEMV_BYTES: the weights are read exactly once.
-GEMV_TRAFFIC_BYTES = 7_254_016
+# (3,516 KiB x 2.00) and WRITE_SIZE (32 KiB x 1.00) over the eager `--profile
+# c1` launches; the factors come from the same counters read on an
+# elementwise kernel that reads and writes 256 MiB (`--profile copy`).
+# 1.02 x GEMV_BYTES: the weights are read exactly once.
+GEMV_TRAFFIC_BYTES = 7_233_432
 
 
 def log(*a):
@@ -423,6 +424,21 @@ def _profile_workloads(ctx, names, reps: int):
             ym = torch.empty((M, n_out), device="cuda")
             ctx.quantize_q8_0_split_dev(xm, qs, dd, M, k)
             run(name, lambda i: ctx.gemm_q8act_dev(qs, dd, wd, ym, M, n_out, k, synth.Q4_0, 4), 1)
+        elif name == "decode":
+            # the decode bench's model and lengths, with the step's kernels
+            # launched directly (no graph replay under the profiler); reps
+            # does not apply
+            from zero_amd.model import GpuModel
+            n_prompt, n_gen = 128, 256
+            cfg = synth.ModelConfig(max_ctx=n_prompt + n_gen)
+            model = synth.random_model(cfg, seed=0)
+            gm = GpuModel(ctx, model)
+            prompt = synth.prompt(1, n_prompt, cfg.vocab_real)
+            t0 = time.perf_counter()
+            gm.generate(prompt, n_gen, eager=True)
+            log(f"profile decode: {n_prompt}-token prompt + {n_gen} tokens eager in {time.perf_counter() - t0:.1f} s")
+            gm.close()
+            ctx.clear()
         else:
             raise SystemExit(f"unknown profile workload {name!r}")
 

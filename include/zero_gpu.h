@@ -279,8 +279,14 @@ void zg_model_reset(zg_model *m);
 zg_status zg_model_prefill(zg_model *m, const uint32_t *tokens, size_t n, uint32_t pos0,
                            float *hidden_out, uint32_t *next_token, float *max_logit);
 #define ZG_GEN_BATCHED_PREFILL 1u
+#define ZG_GEN_EAGER 2u
 /* zg_model_generate with flags: ZG_GEN_BATCHED_PREFILL runs the prompt
- * through zg_model_prefill's batched path instead of token by token. */
+ * through zg_model_prefill's batched path instead of token by token.
+ * ZG_GEN_EAGER (not with ZG_GEN_BATCHED_PREFILL) issues each token's
+ * kernels directly on the stream instead of replaying the captured step
+ * graph: the same launches in the same order and the same tokens, slower;
+ * for profilers that collect counters per dispatch.  Other flag bits are
+ * ZG_ERR_INVALID_ARG. */
 zg_status zg_model_generate_ex(zg_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                                uint32_t flags, uint32_t *out_tokens, double *prefill_seconds,
                                double *gen_seconds);

@@ -235,6 +235,30 @@ def test_tiny_model_generate_matches_oracle(ctx, zo, tiny):
     ctx.clear()
 
 
+def test_eager_generate_matches_graph(ctx, tiny):
+    """ZG_GEN_EAGER issues the step's launches directly: same tokens as the
+    graph replay; combined with the batched prefill, or an unknown flag bit,
+    it is an argument error."""
+    gm = GpuModel(ctx, tiny)
+    try:
+        prompt = synth.prompt(9, 12, TINY.vocab_real)
+        toks_g, _, _ = gm.generate(prompt, 20)
+        toks_e, _, _ = gm.generate(prompt, 20, eager=True)
+        assert np.array_equal(toks_g, toks_e)
+        import zero_amd
+        from zero_amd import _lib
+        with pytest.raises(zero_amd.ZgError) as e:
+            gm.generate(prompt, 4, batched_prefill=True, eager=True)
+        assert e.value.code == _lib.ZG_ERR_INVALID_ARG
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(4, np.uint32)
+        assert ctx.lib.zg_model_generate_ex(gm.h, p.ctypes.data, p.size, 4, 8, out.ctypes.data, None,
+                                            None) == _lib.ZG_ERR_INVALID_ARG
+    finally:
+        gm.close()
+        ctx.clear()
+
+
 def test_generate_bounds(ctx, tiny):
     gm = GpuModel(ctx, tiny)
     import zero_amd

@@ -52,6 +52,10 @@ def test_status_codes_match_header():
     assert codes["ZG_OK"] == 0 and len(codes) >= 14
     for k, v in codes.items():
         assert getattr(_lib, k) == v, k
+    flags = {k: int(v) for k, v in re.findall(r"#define\s+(ZG_GEN_\w+)\s+(\d+)u", HEADER.read_text())}
+    assert set(flags) == {"ZG_GEN_BATCHED_PREFILL", "ZG_GEN_EAGER"}
+    for k, v in flags.items():
+        assert getattr(_lib, k) == v, k
 
 
 def test_struct_layouts_match_gcc(tmp_path):

@@ -37,6 +37,7 @@ ZG_ERR_UNSUPPORTED_FORMAT = -12
 ZG_ERR_INVALID_CONTAINER = -13
 
 ZG_GEN_BATCHED_PREFILL = 1
+ZG_GEN_EAGER = 2
 
 
 class zg_segment(C.Structure):

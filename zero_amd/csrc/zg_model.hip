@@ -1240,6 +1240,16 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
                           "prompt upload");
   if (s) return s;
   const bool batched = (flags & ZG_GEN_BATCHED_PREFILL) != 0;
+  const bool eager = (flags & ZG_GEN_EAGER) != 0;
+  if (flags & ~(ZG_GEN_BATCHED_PREFILL | ZG_GEN_EAGER))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "generate: unknown flags 0x%x", flags);
+  if (batched && eager) return set_error(ctx, ZG_ERR_INVALID_ARG, "generate: ZG_GEN_EAGER is for token-by-token steps");
+  // one token through the layers (and the LM head): the captured graph, or
+  // the same launches issued directly
+  auto run_one = [&](bool head) -> zg_status {
+    if (eager) return head ? record_step(m, ctx->stream) : record_prefill(m, ctx->stream);
+    return hip_check(ctx, hipGraphLaunch(head ? m->g_step : m->g_prefill, ctx->stream), "graph launch");
+  };
   if (batched && !m->pf_ok)
     return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "generate: the batched prefill's GEMMs take Q4_0 / Q8_0 projections");
   if (batched && (s = prefill_alloc(m))) return s;
@@ -1256,14 +1266,14 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
     // prompt tokens 0..n-2 through the layers one by one; the last one also
     // through the LM head, producing generated token 0
     for (size_t i = 0; i + 1 < n_prompt; i++)
-      if ((s = hip_check(ctx, hipGraphLaunch(m->g_prefill, ctx->stream), "graph launch"))) return s;
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
+      if ((s = run_one(false))) return s;
+    if ((s = run_one(true))) return s;
   }
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t1 = std::chrono::steady_clock::now();
   // greedy decode: each generated token goes back through the layers
   for (size_t j = 1; j < n_gen; j++)
-    if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
+    if ((s = run_one(true))) return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
   auto t2 = std::chrono::steady_clock::now();
   if (prefill_seconds) *prefill_seconds = std::chrono::duration<double>(t1 - t0).count();

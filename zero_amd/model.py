@@ -109,15 +109,16 @@ class GpuModel:
         self._raise(rc, int(tok.value))
         return int(tok.value), float(mv.value), hid
 
-    def generate(self, prompt: np.ndarray, n_gen: int, batched_prefill: bool = False):
+    def generate(self, prompt: np.ndarray, n_gen: int, batched_prefill: bool = False, eager: bool = False):
         """Prefill `prompt` (token by token, or batched with Q8_0-activation
-        GEMMs), then n_gen greedy tokens.
+        GEMMs), then n_gen greedy tokens.  eager: launch each token's kernels
+        directly instead of replaying the step graph (per-dispatch profiling).
         Returns (tokens, prefill_seconds, generation_seconds)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(n_gen, np.uint32)
         t_pre = C.c_double()
         t_gen = C.c_double()
-        flags = _lib.ZG_GEN_BATCHED_PREFILL if batched_prefill else 0
+        flags = (_lib.ZG_GEN_BATCHED_PREFILL if batched_prefill else 0) | (_lib.ZG_GEN_EAGER if eager else 0)
         rc = self.ctx.lib.zg_model_generate_ex(self.h, p.ctypes.data, p.size, n_gen, flags, out.ctypes.data,
                                                C.byref(t_pre), C.byref(t_gen))
         self._raise(rc, -1)
