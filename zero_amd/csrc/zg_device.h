@@ -110,7 +110,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // is sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s)
 // (attention.rs:48-84 softmax, regrouped by split).  One thread merges 8
 // consecutive dims of one head.
-constexpr int kAttnSplits = 4;  // max splits per query head
+constexpr int kAttnSplits = 8;  // max splits per query head
 
 struct AttnSplitIn {
   float4 o[kAttnSplits][2];

@@ -95,7 +95,8 @@ struct AttnArgs {
   float* out;          // one split: attention output [nq*HD]; else split outputs [nsplit][nq*HD]
   float* part_ml;      // split (max, exp-sum) pairs [nsplit][nq] (nsplit > 1)
   DevState* st;
-  int nkv, g, nsplit, split_len;
+  int nkv, g, nsplit;
+  int split_len;       // prefill form (one split): max_ctx; decode splits follow attn_split_rows
   float eps, scale;
   // batched prefill: query row z of the chunk sits at position pos0 + z,
   // its (already normalised and rotated) query at q + z * row_stride; its
@@ -114,13 +115,19 @@ struct AttnArgs {
 #define ZG_ATTN_PASSES 4
 #endif
 constexpr int kAttnWaves = ZG_ATTN_WAVES;
+#ifndef ZG_ATTN_SPLITS
+#define ZG_ATTN_SPLITS 4
+#endif
+constexpr int kAttnDecodeSplits = ZG_ATTN_SPLITS;
+static_assert(kAttnDecodeSplits >= 1 && kAttnDecodeSplits <= kAttnSplits, "decode splits within the merge's capacity");
 
 // Decode attention, flash-decoding over splits: grid (query heads, splits),
-// one 4-wave workgroup per (head, split of split_len context rows).  Rows
-// are visited in rounds of 128 (4 passes of 32 rows, 8 rows per wave per
-// pass) whose K/V loads are all issued before any is used, so a split of up
-// to 128 rows costs one memory round trip; the splits spread a head's rows
-// over several CUs.
+// one 4-wave workgroup per (head, split).  The live context (rows 0..pos)
+// is cut evenly over the splits, in multiples of 8 rows
+// (attn_split_rows), so every position spreads its rows over all the
+// splits' CUs.  Rows are visited in rounds of 128 (4 passes of 32 rows, 8
+// rows per wave per pass) whose K/V loads are all issued before any is
+// used, so a split of up to 128 rows costs one memory round trip.
 //   prologue  every wave normalises and rotates the query head and the new
 //             key itself (QK-norm, ops.rs:29-52; NeoX RoPE, ops.rs:111-132)
 //             and parks them in its own LDS rows: no workgroup barrier
@@ -144,6 +151,12 @@ constexpr int kAttnWaves = ZG_ATTN_WAVES;
 // rotated.  The output row goes out Q8_0-encoded for the O GEMM (each 32-lane
 // segment of the output waves is one block).  Everything else is the decode
 // kernel's arithmetic.
+// Rows per split for position pos: ceil((pos + 1) / nsplit) rounded up to a
+// multiple of 8; splits starting past pos hold no row.
+__device__ __forceinline__ int attn_split_rows(int pos, int nsplit) {
+  return (pos + 8 * nsplit) / (8 * nsplit) * 8;
+}
+
 template <int HD, bool PF>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
   constexpr int F4 = HD / 4;            // float4 per head row
@@ -165,7 +178,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     a.qs += (size_t)blockIdx.z * a.row_stride;
     a.qsd += (size_t)blockIdx.z * a.row_stride / 32;
   }
-  const int c0 = sp * a.split_len;
+  const int slen = PF ? a.split_len : attn_split_rows(pos, a.nsplit);
+  const int c0 = sp * slen;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (c0 > pos) {
@@ -174,8 +188,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(-INFINITY, 0.0f);
     return;
   }
-  const int n_t = min(a.split_len, pos + 1 - c0);
-  const bool has_pos = !PF && pos - c0 < a.split_len;  // this split holds the current row (decode)
+  const int n_t = min(slen, pos + 1 - c0);
+  const bool has_pos = !PF && pos - c0 < slen;  // this split holds the current row (decode)
   const size_t rowf4 = (size_t)a.nkv * F4;
   const size_t rowv = (size_t)a.nkv * (HD / VPL);
   const int r = lane / LPR, sl = lane % LPR;
@@ -642,7 +656,7 @@ struct zg_model {
   size_t prompt_cap = 0;
   uint32_t* out_tokens = nullptr;
   size_t out_cap = 0;
-  int nsplit = 1, split_len = 0;
+  int nsplit = 1;
   bool head_norm = false;  // the LM-head GEMV takes the output rmsnorm itself
   bool pf_ok = false;      // every layer projection Q4_0 / Q8_0 (the batched prefill's GEMMs)
   std::vector<void*> owned;  // device allocations to free
@@ -776,7 +790,6 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     aa.nkv = (int)d.n_kv_heads;
     aa.g = (int)(d.n_q_heads / d.n_kv_heads);
     aa.nsplit = m->nsplit;
-    aa.split_len = m->split_len;
     aa.eps = d.rms_eps;
     aa.scale = scale;
     const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnWaves * 64);
@@ -1061,13 +1074,16 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     }
     s = upload_f32(m, &m->inv_freq, inv, d.head_dim / 2);
   }
-  // up to kAttnSplits workgroups per query head share its context (one CU
-  // loads ~150 GB/s, so a head's K/V rows are spread over several CUs);
-  // splits are multiples of 32 rows
+  // kAttnDecodeSplits workgroups per query head share its live context (one
+  // CU loads ~150 GB/s, so a head's K/V rows are spread over several CUs);
+  // fewer when max_ctx has fewer than 8 rows per split.  More splits make
+  // attention faster but the merge in the O projection's prologue slower:
+  // every O workgroup reads nsplit x 8 KB of split outputs (Qwen3-1.7B,
+  // eager trace: 8 splits 4.42 + 4.78 us, 4 splits 5.26 + 4.04 us with the
+  // splits cut by max_ctx)
   {
-    const uint32_t per = (d.max_ctx + kAttnSplits - 1) / kAttnSplits;
-    m->split_len = (int)(per < 32 ? 32 : (per + 31) / 32 * 32);
-    m->nsplit = (int)((d.max_ctx + m->split_len - 1) / m->split_len);
+    const uint32_t ns = (d.max_ctx + 7) / 8;
+    m->nsplit = (int)(ns < (uint32_t)kAttnDecodeSplits ? ns : (uint32_t)kAttnDecodeSplits);
   }
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->kv), (size_t)d.n_layers * 2 * d.max_ctx * kvd * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->rope_cs), d.head_dim * sizeof(float));
