@@ -27,20 +27,6 @@ constexpr int kKqWaves = 8;  // waves per workgroup
 
 __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xFFu; }
 
-// get_scale_min_k4 (dequant.rs:75-85) over the 12 packed scale bytes.
-__device__ __forceinline__ void scale_min_k4(const uint32_t* s, int j, float& sc, float& mn) {
-  uint32_t a, b;
-  if (j < 4) {
-    a = byte_of(s, j) & 63u;
-    b = byte_of(s, j + 4) & 63u;
-  } else {
-    a = (byte_of(s, j + 4) & 0xFu) | ((byte_of(s, j - 4) >> 6) << 4);
-    b = (byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4);
-  }
-  sc = (float)a;
-  mn = (float)b;
-}
-
 // sum_i q_i x_i over 4 dwords of unsigned bytes (q in 0..255) against
 // 16 consecutive x values.
 __device__ __forceinline__ float u8_dot16(const uint32_t* q, const float4* x) {
@@ -148,26 +134,52 @@ struct KqX {
   float sa, sb;
 };
 
+// get_scale_min_k4 (dequant.rs:75-85) for the lane's sub-blocks 2j and 2j+1,
+// branch-free over the wave (j differs between lanes): for j < 2 the low six
+// bits of bytes 2j, 2j+1 of w0 (scales) and w1 (mins); for j >= 2 the low /
+// high nibbles of bytes 2j-4, 2j-3 of w2, with the top two bits of the same
+// bytes of w0 / w1 above them.
+__device__ __forceinline__ void q4k_lane_scales(uint32_t w0, uint32_t w1, uint32_t w2, int j, uint32_t& sA,
+                                                uint32_t& sB, uint32_t& nA, uint32_t& nB) {
+  const uint32_t sh = 16u * (uint32_t)(j & 1);
+  const bool lowj = j < 2;
+  const uint32_t a = w0 >> sh, b = w1 >> sh, c = w2 >> sh;
+  const uint32_t wid = lowj ? 6u : 4u;
+  const uint32_t hmask = lowj ? 0u : ~0u;
+  const uint32_t ls = lowj ? a : c, lm = lowj ? b : (c >> 4);
+  const uint32_t hs = a & hmask, hm = b & hmask;
+  sA = __builtin_amdgcn_ubfe(ls, 0, wid) | (__builtin_amdgcn_ubfe(hs, 6, 2) << 4);
+  sB = __builtin_amdgcn_ubfe(ls, 8, wid) | (__builtin_amdgcn_ubfe(hs, 14, 2) << 4);
+  nA = __builtin_amdgcn_ubfe(lm, 0, wid) | (__builtin_amdgcn_ubfe(hm, 6, 2) << 4);
+  nB = __builtin_amdgcn_ubfe(lm, 8, wid) | (__builtin_amdgcn_ubfe(hm, 14, 2) << 4);
+}
+
+// The superblock's d and dmin through the hardware fp16 conversion: exact
+// for every finite value; a NaN scale gives a NaN row either way.
+__device__ __forceinline__ float kq_half(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+}
+
 __device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const KqX& x, int lane) {
   const int j = (lane >> 1) & 3;
-  const float d = half_bits_to_f32(L.hdr.x), dmin = half_bits_to_f32(L.hdr.x >> 16);
-  const uint32_t sb[3] = {L.hdr.y, L.hdr.z, L.hdr.w};
-  float scA, mA, scB, mB;
-  scale_min_k4(sb, 2 * j, scA, mA);
-  scale_min_k4(sb, 2 * j + 1, scB, mB);
+  const float d = kq_half(L.hdr.x), dmin = kq_half(L.hdr.x >> 16);
+  uint32_t iA, iB, nA, nB;
+  q4k_lane_scales(L.hdr.y, L.hdr.z, L.hdr.w, j, iA, iB, nA, nB);
+  // high nibbles stay in place (16 x the value): the 1/16 goes into the
+  // sub-block scale (exact)
   const uint32_t q[4] = {L.q.x, L.q.y, L.q.z, L.q.w};
   uint32_t lo[4], hi[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     lo[c] = opaque_u32(q[c] & 0x0F0F0F0Fu);
-    hi[c] = opaque_u32((q[c] >> 4) & 0x0F0F0F0Fu);
+    hi[c] = opaque_u32(q[c] & 0xF0F0F0F0u);
   }
   const float sA = u8_dot16(lo, x.a);
   const float sB = u8_dot16(hi, x.b);
-  float acc = (d * scA) * sA;
-  acc = fmaf(-(dmin * mA), x.sa, acc);
-  acc = fmaf(d * scB, sB, acc);
-  return fmaf(-(dmin * mB), x.sb, acc);
+  float acc = (d * (float)iA) * sA;
+  acc = fmaf(-(dmin * (float)nA), x.sa, acc);
+  acc = fmaf((d * 0.0625f) * (float)iB, sB, acc);
+  return fmaf(-(dmin * (float)nB), x.sb, acc);
 }
 
 __device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const KqX& x, int lane) {
