@@ -98,6 +98,9 @@ struct GemmArgs {
 
 constexpr int kBN = 64;  // tile columns (tile rows BM: 64 or 32)
 // LDS row stride in bytes for BK blocks of 32 per stage (padded, 16-B aligned)
+// (36 dwords for 4-block stages: the 16 rows of an MFMA operand read start
+// on 16 distinct 4-bank groups of the 64 banks, so the per-block 8-byte
+// operand reads are conflict-free)
 template <int BK>
 constexpr int lds_row() { return BK * 32 + 16; }
 
@@ -132,15 +135,18 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
     if (FULL || (gm < a.m && kb < nb))
       S.a[i] = *reinterpret_cast<const u32x4*>(a.xq + (size_t)gm * a.k + (size_t)kb * 32 + (ch & 1) * 16);
   }
+  // scales and weight blocks: consecutive threads take consecutive rows
+  // (columns) of one block, so that their LDS stores are conflict-free (the
+  // 64-row tile had 0.59 M conflict cycles with the block index fastest)
 #pragma unroll
   for (int i = 0; i < St::ND; i++) {
-    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    const int c = tid + 256 * i, row = c % BM, kk = c / BM;
     const int gm = m0 + row, kb = b0 + kk;
-    S.ad[i] = (row < BM && (FULL || (gm < a.m && kb < nb))) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
+    S.ad[i] = (kk < BK && (FULL || (gm < a.m && kb < nb))) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
   }
 #pragma unroll
   for (int i = 0; i < St::NW; i++) {
-    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    const int c = tid + 256 * i, row = c % kBN, kk = c / kBN;
     const int gn = n0 + row, kb = b0 + kk;
 #pragma unroll
     for (int j = 0; j < St::QW; j++) S.q[i][j] = 0;
@@ -185,12 +191,12 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S,
   }
 #pragma unroll
   for (int i = 0; i < St::ND; i++) {
-    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
-    if (row < BM) Ad[kk * BM + row] = half_bits_to_f32(S.ad[i]);
+    const int c = tid + 256 * i, row = c % BM, kk = c / BM;
+    if (kk < BK) Ad[kk * BM + row] = half_bits_to_f32(S.ad[i]);
   }
 #pragma unroll
   for (int i = 0; i < St::NW; i++) {
-    const int c = tid + 256 * i, row = c / BK, kk = c % BK;
+    const int c = tid + 256 * i, row = c % kBN, kk = c / kBN;
     uint32_t q[8];
     if (WT == Q4_0) {
       // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
@@ -268,6 +274,11 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
     const int8_t* B = Bs[buf];
     // blocks past k in the last stage hold zero quants and scales: they add
     // fma(0, 0, acc) = acc
+    // the 32-row tile's unrolled block loop lets the compiler pair the
+    // operand reads of blocks kk and kk + 1 (ds_read2_b64, 32 bytes apart),
+    // which conflict (4.7 M conflict cycles for M=512 x 2048x6144); the
+    // rolled loop has none but 13 % more VALU work and is slower (55 vs
+    // 48 us)
     constexpr int UNR = BM == 64 ? 1 : 4;
 #pragma unroll UNR
     for (int kk = 0; kk < BK; kk++) {
