@@ -644,9 +644,12 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
     for (int c = 0; c < 8; c++) xb[c] = x4[c];
   }
   if (PRO == PRO_RMSNORM) {
-    // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w, sum of squares over
-    // the whole vector (the first wave of each strip: its 64 lanes hold
-    // the strip's 512 values once)
+    // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w.  The scalar
+    // 1/sqrt(...) factors out of every row's dot product, so the decode runs
+    // on x * w and the row totals are scaled in the epilogue: the sum of
+    // squares (the first wave of each strip: its 64 lanes hold the strip's
+    // 512 values once) goes to LDS here and is read after the batch's
+    // barrier, off the path between the loads and the decode
     float ssq = 0.0f;
     if (sub == 0) {
 #pragma unroll
@@ -654,17 +657,13 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
     }
     ssq = wave_sum(ssq);
     if (lane == 0) red[wave] = ssq;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < S; i++) tot += red[i];
-    const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const float4 g = gw[c];
-      xb[c].x = xb[c].x * rinv * g.x;
-      xb[c].y = xb[c].y * rinv * g.y;
-      xb[c].z = xb[c].z * rinv * g.z;
-      xb[c].w = xb[c].w * rinv * g.w;
+      xb[c].x = xb[c].x * g.x;
+      xb[c].y = xb[c].y * g.y;
+      xb[c].z = xb[c].z * g.z;
+      xb[c].w = xb[c].w * g.w;
     }
   }
   float mterm = 0.0f;
@@ -713,6 +712,12 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
       const int su = tt / (GBATCH * 4), j = (tt >> 2) % GBATCH, rr = tt & 3;
       const int item = batch * per_batch + su * GBATCH + j;
       if (item < items) {
+        float rinv = 1.0f;
+        if (PRO == PRO_RMSNORM) {
+          float ss = 0.0f;
+          for (int i = 0; i < S; i++) ss += red[i];
+          rinv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+        }
         float tot[PARTS];
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
@@ -721,7 +726,7 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
             const float* q = pb + (((su * S + st) * GBATCH + j) * PARTS + p) * 16 + rr;
             acc += (q[0] + q[4]) + (q[8] + q[12]);
           }
-          tot[p] = acc;
+          tot[p] = PRO == PRO_RMSNORM ? acc * rinv : acc;
         }
         uint32_t lg;
         const GemvSeg sg = locate(item, 0, lg);
