@@ -69,39 +69,38 @@ constexpr int kXBlk = 36;  // LDS floats per 32-float x-block (padded: lane stri
 __device__ __forceinline__ int x_off(int e) { return (e >> 5) * kXBlk + (e & 31); }
 
 // Stage x (K floats) into LDS, applying the prologue.  rmsnorm follows
-// ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w.
+// ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w; the scalar 1/sqrt(...)
+// factors out of every row's dot product, so x * w is staged and the
+// per-wave sums of squares go to red[]: the caller scales the row totals by
+// stage_rinv() after the barrier that follows.
 template <int PRO>
 __device__ __forceinline__ void stage_x(float* xs, float* red, const GemvArgs& a) {
   constexpr int NT = kNW * 64;
   const int tid = threadIdx.x;
   const int K = a.k;
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
   float ssq = 0.0f;
   for (int i = tid; i < K / 4; i += NT) {
-    const float4 v = x4[i];
+    float4 v = x4[i];
+    if (PRO == PRO_RMSNORM) {
+      const float4 g = w4[i];
+      ssq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      v = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+    }
     *reinterpret_cast<float4*>(xs + x_off(4 * i)) = v;
-    if (PRO == PRO_RMSNORM) ssq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
   if (PRO == PRO_RMSNORM) {
     ssq = seg_sum<64>(ssq);
     if ((tid & 63) == 0) red[tid >> 6] = ssq;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kNW; i++) tot += red[i];
-    const float rinv = 1.0f / sqrtf(tot / (float)K + a.eps);
-    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
-    for (int i = tid; i < K / 4; i += NT) {
-      float4* p = reinterpret_cast<float4*>(xs + x_off(4 * i));
-      float4 v = *p;
-      const float4 g = w4[i];
-      v.x = v.x * rinv * g.x;
-      v.y = v.y * rinv * g.y;
-      v.z = v.z * rinv * g.z;
-      v.w = v.w * rinv * g.w;
-      *p = v;
-    }
   }
+}
+
+__device__ __forceinline__ float stage_rinv(const float* red, const GemvArgs& a) {
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNW; i++) tot += red[i];
+  return 1.0f / sqrtf(tot / (float)a.k + a.eps);
 }
 
 // Sum over one Q4_0 block of one row: sum_j q_j * x_j with q the raw nibble
@@ -245,6 +244,7 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
   }
   stage_x<PRO>(xs, red, a);
   __syncthreads();
+  const float rinv = PRO == PRO_RMSNORM ? stage_rinv(red, a) : 1.0f;
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float gate[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
     if (cu.seg != nseg - 1) continue;
     // group finished: reduce and write
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) acc[rr] = wave_sum(acc[rr]);
+    for (int rr = 0; rr < 4; rr++) acc[rr] = PRO == PRO_RMSNORM ? wave_sum(acc[rr]) * rinv : wave_sum(acc[rr]);
     uint32_t lg;
     const GemvSeg sg = locate(cu.item, cu.part, lg);
     if (EPI == EPI_SWIGLU && cu.part == 0) {

@@ -376,34 +376,29 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
         ssq += (x.a[c].x * x.a[c].x + x.a[c].y * x.a[c].y + x.a[c].z * x.a[c].z + x.a[c].w * x.a[c].w) +
                (x.b[c].x * x.b[c].x + x.b[c].y * x.b[c].y + x.b[c].z * x.b[c].z + x.b[c].w * x.b[c].w);
     }
+    // the scalar 1/sqrt(mean + eps) factors out of every row's dot
+    // product: the decode runs on x * w, and the row totals (and the
+    // normalised copy of x) are scaled once the sum of squares has crossed
+    // the batch's barrier
     ssq = wave_sum(ssq);
     if (lane == 0) red[wave] = ssq;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < S; i++) tot += red[i];
-    const float rinv = 1.0f / sqrtf(tot / (float)a.k + a.eps);
     float sa = 0.0f, sbs = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      x.a[c] = make_float4(x.a[c].x * rinv * g.a[c].x, x.a[c].y * rinv * g.a[c].y, x.a[c].z * rinv * g.a[c].z,
-                           x.a[c].w * rinv * g.a[c].w);
-      x.b[c] = make_float4(x.b[c].x * rinv * g.b[c].x, x.b[c].y * rinv * g.b[c].y, x.b[c].z * rinv * g.b[c].z,
-                           x.b[c].w * rinv * g.b[c].w);
+      x.a[c] = make_float4(x.a[c].x * g.a[c].x, x.a[c].y * g.a[c].y, x.a[c].z * g.a[c].z, x.a[c].w * g.a[c].w);
+      x.b[c] = make_float4(x.b[c].x * g.b[c].x, x.b[c].y * g.b[c].y, x.b[c].z * g.b[c].z, x.b[c].w * g.b[c].w);
       sa += (x.a[c].x + x.a[c].y) + (x.a[c].z + x.a[c].w);
       sbs += (x.b[c].x + x.b[c].y) + (x.b[c].z + x.b[c].w);
     }
     x.sa = sa;
     x.sb = sbs;
-    if (a.xn_out && blockIdx.x == 0 && sub == 0) {
-      // the sub-0 waves' lanes hold every element once
-      float4* o = reinterpret_cast<float4*>(a.xn_out + sb * 256 + kq_lane_elem<QT>(lane));
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        o[c] = x.a[c];
-        o[8 + c] = x.b[c];
-      }
-    }
   }
+  // 1/rms from the strips' sums of squares (valid after a batch barrier)
+  auto rms_inv = [&]() {
+    float tot = 0.0f;
+    for (int i = 0; i < S; i++) tot += red[i];
+    return 1.0f / sqrtf(tot / (float)a.k + a.eps);
+  };
   asm volatile("" : "+v"(x.sa), "+v"(x.sb));
   if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
   uint64_t key = 0;
@@ -416,6 +411,7 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
     }
     __syncthreads();
     const int tt = threadIdx.x;
+    const float rinv = PRO == 1 ? rms_inv() : 1.0f;
     if (EPI == EPI_SWIGLU) {
       if (tt < per_batch) {
         const int ri = batch * per_batch + tt;
@@ -424,6 +420,10 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
           for (int st = 0; st < S; st++) {
             gv += part[buf][tt * S + st][0];
             uv += part[buf][tt * S + st][1];
+          }
+          if (PRO == 1) {
+            gv *= rinv;
+            uv *= rinv;
           }
           a.y[a.row_lo + ri] = (gv / (1.0f + expf(-gv))) * uv;
         }
@@ -434,6 +434,7 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
       if (ri < nrows) {
         float v = 0.0f;
         for (int st = 0; st < S; st++) v += part[buf][su * S + st][j];
+        if (PRO == 1) v *= rinv;
         const size_t row = a.row_lo + ri;
         if (EPI == EPI_STORE && a.nseg > 1) {
           const int sg = kq_seg(a, ri);
@@ -456,6 +457,18 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
     if (batch + bstep < nbatch) {
       process(LB, batch + bstep, 1);
       if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+    }
+  }
+  if (PRO == 1 && a.xn_out && blockIdx.x == 0 && sub == 0) {
+    // the normalised x for other consumers (every workgroup processed at
+    // least one batch, so the sums of squares are visible); the sub-0
+    // waves' lanes hold every element once
+    const float rinv = rms_inv();
+    float4* o = reinterpret_cast<float4*>(a.xn_out + sb * 256 + kq_lane_elem<QT>(lane));
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      o[c] = make_float4(x.a[c].x * rinv, x.a[c].y * rinv, x.a[c].z * rinv, x.a[c].w * rinv);
+      o[8 + c] = make_float4(x.b[c].x * rinv, x.b[c].y * rinv, x.b[c].z * rinv, x.b[c].w * rinv);
     }
   }
   if (EPI == EPI_ARGMAX) {
