@@ -310,12 +310,13 @@ def test_lm_head_argmax_plain_q8_0(ctx, zo, lm_head):
     ctx.clear()
 
 
-@pytest.mark.parametrize("qt", [Q6K, Q4K])
-def test_lm_head_argmax_kquant(ctx, zo, qt):
+@pytest.mark.parametrize("qt,H", [(Q6K, 4096), (Q4K, 4096), (Q6K, 8192)])
+def test_lm_head_argmax_kquant(ctx, zo, qt, H):
     """LM head in Q6_K (the output.weight type of Q4_K_M GGUF artifacts) and
-    Q4_K (OutputQuant::Q4K, kernel/src/inference.rs:3119-3125)."""
-    rng = np.random.default_rng(5 + qt)
-    V, H = 32000, 4096
+    Q4_K (OutputQuant::Q4K, kernel/src/inference.rs:3119-3125); Q6_K at
+    in_dim 8192 takes the LDS-activation kernel with the argmax epilogue."""
+    rng = np.random.default_rng(5 + qt + H)
+    V = 32000
     w = synth.weight(rng, qt, V, H, 1)
     hidden = synth.activations(rng, H)
     norm = (1 + 0.05 * rng.standard_normal(H)).astype(np.float32)

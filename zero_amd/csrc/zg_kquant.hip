@@ -653,6 +653,155 @@ static int kq_cu_count() {
   return n;
 }
 
+// Q6_K strip GEMV with the activations in LDS.  The lane layout is
+// kq2_strip_kernel's (four lanes per superblock, 64 elements per lane, a
+// half-wave per row, so a wave decodes a row pair), but the activations are
+// staged once per workgroup into LDS in lane order (strip, quarter, float4
+// column, lane % 32) and read per quarter while the rows are decoded: a lane
+// holds 16 activations at a time instead of 64, which leaves the registers
+// to more waves per CU, and the workgroup reads x from L2 once instead of
+// once per wave.  Workgroups of S strips x WPS waves walk batches of RB row
+// pairs per wave with two batches in flight and no barrier in the loop: the
+// half-wave partials of every batch go to LDS and the strips are summed once
+// at the end.
+constexpr int kKq6Waves = 16;  // waves per workgroup (at most)
+
+__device__ __forceinline__ int kq6_lds_index(int strip, int Q, int c, int slot) {
+  return ((strip * 4 + Q) * 4 + c) * 32 + slot;  // float4 units
+}
+
+template <int EPI, int RB>
+__global__ __launch_bounds__(1024) void kq6l_kernel(GenericArgs a, int S, int WPS, int nbl) {
+  constexpr int BB = KqGeom<Q6K>::BB;
+  constexpr int RPB = 2 * RB;  // rows per wave per batch
+  extern __shared__ __attribute__((aligned(16))) float kq6_smem[];
+  float4* xl = reinterpret_cast<float4*>(kq6_smem);  // [S][4][4][32] float4
+  const int NW = S * WPS;
+  float* part = kq6_smem + S * 2048;                  // [nbl][NW][RPB]
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5, slot = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = wave % S, sub = wave / S;
+  const int nsb = (int)(a.k / 256);
+  const int sb = strip * 8 + ((lane >> 2) & 7);  // this lane's superblock
+  const size_t rowbytes = (size_t)nsb * BB;
+  const int nrows = (int)(a.row_hi - a.row_lo);
+  const int per_batch = WPS * RPB;
+  const int nbatch = (nrows + per_batch - 1) / per_batch;
+  auto load_batch = [&](Kq2Lane<Q6K> (&L)[RB], int batch) {
+    const int base = batch * per_batch + sub * RPB;
+#pragma unroll
+    for (int p = 0; p < RB; p++) {
+      const size_t row = a.row_lo + (size_t)min(base + 2 * p + half, nrows - 1);
+      kq2_load(L[p], a.w + row * rowbytes + (size_t)sb * BB, lane);
+    }
+  };
+  // first batch's weights (unconditional: the grid never exceeds the batch
+  // count), then x into LDS in lane order while they fly
+  Kq2Lane<Q6K> LA[RB], LB[RB];
+  const int b0 = blockIdx.x, bstep = gridDim.x;
+  load_batch(LA, b0);
+  {
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    for (int f = threadIdx.x; f < (int)(a.k / 4); f += blockDim.x) {
+      const int e = 4 * f;
+      const int st = e >> 11, r = e & 255, sbl = (e >> 8) & 7;
+      const int n = r >> 7, t = r & 127, Q = t >> 5, u = t & 31;
+      const int sl = (sbl << 2) | (n << 1) | (u >> 4);
+      xl[kq6_lds_index(st, Q, (u & 15) >> 2, sl)] = x4[f];
+    }
+  }
+  __syncthreads();
+  // the lane's quarter sums
+  float xs4[4];
+#pragma unroll
+  for (int Q = 0; Q < 4; Q++) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float4 v = xl[kq6_lds_index(strip, Q, c, slot)];
+      sum += (v.x + v.y) + (v.z + v.w);
+    }
+    xs4[Q] = sum;
+  }
+  asm volatile("" : "+v"(xs4[0]), "+v"(xs4[1]), "+v"(xs4[2]), "+v"(xs4[3]));
+  if (b0 + bstep < nbatch) load_batch(LB, b0 + bstep);
+  uint64_t key = 0;
+  auto process = [&](const Kq2Lane<Q6K> (&L)[RB], int bi) {
+    const int is = lane & 1;
+    float acc[RB];
+#pragma unroll
+    for (int p = 0; p < RB; p++) acc[p] = 0.0f;
+#pragma unroll
+    for (int Q = 0; Q < 4; Q++) {
+      float4 xq[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) xq[c] = xl[kq6_lds_index(strip, Q, c, slot)];
+#pragma unroll
+      for (int p = 0; p < RB; p++) {
+        const uint32_t a4[4] = {L[p].la.x, L[p].la.y, L[p].la.z, L[p].la.w};
+        const uint32_t b4[4] = {L[p].lb.x, L[p].lb.y, L[p].lb.z, L[p].lb.w};
+        const uint32_t h4[4] = {L[p].hb.x, L[p].hb.y, L[p].hb.z, L[p].hb.w};
+        uint32_t q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t lowsrc = (Q & 1) ? b4[c] : a4[c];
+          const uint32_t lo4 = (Q >= 2) ? ((lowsrc >> 4) & 0x0F0F0F0Fu) : (lowsrc & 0x0F0F0F0Fu);
+          q[c] = opaque_u32(lo4 | (((h4[c] >> (2 * Q)) & 0x03030303u) << 4));
+        }
+        const uint32_t scw[2] = {L[p].sc0, L[p].sc1};
+        const float dsc = kq_half(L[p].d) * (float)(int8_t)byte_of(scw, is + 2 * Q);
+        acc[p] = fmaf(dsc, fmaf(-32.0f, xs4[Q], u8_dot16(q, xq)), acc[p]);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < RB; p++) {
+      // sum over the half-wave: the row total lands in lanes 16..31 / 48..63
+      const float v = group_sum<32>(acc[p]);
+      if ((lane & 31) == 31) part[(bi * NW + wave) * RPB + 2 * p + half] = v;
+    }
+  };
+  int bi = 0;
+  for (int batch = b0; batch < nbatch; batch += 2 * bstep, bi += 2) {
+    process(LA, bi);
+    if (batch + 2 * bstep < nbatch) load_batch(LA, batch + 2 * bstep);
+    if (batch + bstep < nbatch) {
+      process(LB, bi + 1);
+      if (batch + 3 * bstep < nbatch) load_batch(LB, batch + 3 * bstep);
+    }
+  }
+  __syncthreads();
+  const int nb_mine = (nbatch - b0 + bstep - 1) / bstep;
+  for (int idx = threadIdx.x; idx < nb_mine * per_batch; idx += blockDim.x) {
+    const int lb = idx / per_batch, tt = idx - lb * per_batch;
+    const float* pb = part + lb * NW * RPB;
+    const int su = tt / RPB, j = tt - su * RPB;
+    const int ri = (b0 + lb * bstep) * per_batch + tt;
+    if (ri < nrows) {
+      float v = 0.0f;
+      for (int st = 0; st < S; st++) v += pb[(su * S + st) * RPB + j];
+      const size_t row = a.row_lo + ri;
+      if (EPI == EPI_RESID)
+        a.y[row] = a.resid[row] + v;
+      else if (a.y)
+        a.y[row] = v;
+      if (EPI == EPI_ARGMAX && !(v != v)) {
+        const uint64_t kk = argmax_key(v, (uint32_t)row);
+        key = kk > key ? kk : key;
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
+  }
+  (void)nbl;
+}
+
 #ifndef ZG_KQ_STRIP_WAVES_PER_CU
 #define ZG_KQ_STRIP_WAVES_PER_CU 16
 #endif
@@ -682,8 +831,49 @@ static hipError_t launch_kq_strip(const GenericArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// one row pair per wave per batch and one workgroup per CU (two workgroups
+// per CU read x twice and measured 19.9 vs 15.5 us at 4096x14336; two row
+// pairs per batch spill)
+constexpr int kKq6lRB = 1;
+constexpr int kKq6lWgPerCu = 1;
+// Q6_K with the activations in LDS (kq6l_kernel): in_dim a multiple of 2048
+// from 8192 up to 14336 (the staged x then fits 56 KB of LDS), and enough
+// rows that one workgroup per CU gets at least two batches.  Other launches
+// keep kq2_strip_kernel's wider grid: 4096x14336 15.5 vs 16.9 us, but
+// 2048x6144 6.8 vs 6.6 us, and the Q4_K_M pattern's Q6_K LM head
+// (151936x2048) made its decode 1,004 vs 1,019 tok/s.
+static bool kq6l_ok(const GenericArgs& a) {
+  if (a.k % 2048 != 0 || a.k / 2048 < 4 || a.k / 2048 > 7) return false;
+  const size_t S = a.k / 2048, rpb = (size_t)(kKq6Waves / S) * 2 * kKq6lRB;
+  return (a.row_hi - a.row_lo + rpb - 1) / rpb >= (size_t)2 * kq_cu_count() * kKq6lWgPerCu;
+}
+template <int EPI>
+static hipError_t launch_kq6l(const GenericArgs& a, hipStream_t st) {
+  constexpr int RB = kKq6lRB, RPB = 2 * RB;
+  const int S = (int)(a.k / 2048);
+  const int WPS = kKq6Waves / S;
+  const int nw = S * WPS;
+  const size_t rows = a.row_hi - a.row_lo;
+  const size_t nbatch = (rows + (size_t)WPS * RPB - 1) / ((size_t)WPS * RPB);
+  size_t grid = (size_t)kq_cu_count() * kKq6lWgPerCu;
+  if (grid > nbatch) grid = nbatch;
+  if (grid == 0) return hipSuccess;
+  const size_t xbytes = (size_t)S * 2048 * sizeof(float);
+  const size_t max_part = 8 * 1024;
+  size_t nbl = (nbatch + grid - 1) / grid;
+  if (nbl * nw * RPB * sizeof(float) > max_part) {
+    nbl = max_part / ((size_t)nw * RPB * sizeof(float));
+    grid = (nbatch + nbl - 1) / nbl;
+    nbl = (nbatch + grid - 1) / grid;
+  }
+  const size_t shm = xbytes + nbl * nw * RPB * sizeof(float);
+  hipLaunchKernelGGL((kq6l_kernel<EPI, RB>), dim3((unsigned)grid), dim3(nw * 64), shm, st, a, S, WPS, (int)nbl);
+  return hipGetLastError();
+}
+
 template <uint32_t QT, int EPI>
 static hipError_t launch_kq(const GenericArgs& a, hipStream_t st) {
+  if (QT == Q6K && kq6l_ok(a)) return launch_kq6l<EPI>(a, st);
   if (a.k % 2048 == 0 && a.k / 2048 <= 16) return launch_kq_strip<QT, EPI>(a, st);
   const size_t rows = a.row_hi - a.row_lo;
   const size_t shm = kq_lds_bytes((int)a.k);
