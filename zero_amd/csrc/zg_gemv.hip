@@ -404,11 +404,21 @@ __device__ __forceinline__ void strip_load_plain(LaneW<QT>& L, const uint8_t* bl
   L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk));
 }
 
-template <uint32_t QT>
+// Tall Q4_0 launches (a batch loop, four groups per batch) read with
+// cache-allocating loads: Q4_0X4 151936x2048 37.6 vs 40.2 us, 49152x2048
+// 15.2 vs 15.9 us; one-batch (decode-sized) launches keep nontemporal loads
+#ifndef ZG_STRIP_NT_Q4_TALL
+#define ZG_STRIP_NT_Q4_TALL 0
+#endif
+#ifndef ZG_STRIP_LD16_Q4_TALL
+#define ZG_STRIP_LD16_Q4_TALL 0
+#endif
+// TALL: a launch with a batch loop (four groups per batch)
+template <uint32_t QT, bool TALL = false>
 __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int r) {
   constexpr int QW = StripGeom<QT>::QW;
-  constexpr bool LD16 = QT == Q8_0 ? ZG_STRIP_LD16_Q8 : ZG_STRIP_LD16_Q4;
-  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : ZG_STRIP_NT_Q4;
+  constexpr bool LD16 = QT == Q8_0 ? ZG_STRIP_LD16_Q8 : (TALL ? ZG_STRIP_LD16_Q4_TALL : ZG_STRIP_LD16_Q4);
+  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : (TALL ? ZG_STRIP_NT_Q4_TALL : ZG_STRIP_NT_Q4);
   if (LD16) {
     // row quants start at 8 + 16r (Q4_0) or 8 + 32r (Q8_0): 8-byte aligned
     const u32x4a8* p = reinterpret_cast<const u32x4a8*>(blk + 8 + 4 * QW * r);
@@ -578,7 +588,7 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
         // the group's start is wave-uniform (scalar registers), the lane's
         // byte offset inside it a 32-bit vector offset
         if (IL == 4)
-          strip_load<QT>(L[j][p], sg.w + (size_t)lg * (size_t)(nb * GBY) + (uint32_t)(kb * GBY), r);
+          strip_load<QT, GBATCH == 4>(L[j][p], sg.w + (size_t)lg * (size_t)(nb * GBY) + (uint32_t)(kb * GBY), r);
         else
           strip_load_plain<QT, IL == 2>(L[j][p], sg.w + (size_t)lg * (size_t)(4 * nb * BB) +
                                                      (uint32_t)((r * nb + kb) * BB));
