@@ -258,8 +258,23 @@ zg_status zg_model_step(zg_model *m, uint32_t token, uint32_t pos, float *hidden
  * generation phase. */
 zg_status zg_model_generate(zg_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                             uint32_t *out_tokens, double *prefill_seconds, double *gen_seconds);
-/* Position reset (new sequence). */
+/* Position reset (new sequence); also clears the non-finite latch. */
 void zg_model_reset(zg_model *m);
+/* The non-finite latch, first_nonfinite_detail (inference_avx512.rs:264-275):
+ * when a model call fails with ZG_ERR_NONFINITE_LOGITS or ZG_ERR_ATTENTION,
+ * the first stage holding a NaN/Inf is found (finite_diag's stages,
+ * inference_avx512.rs:1896, 1946-1947, 1981-1982: attn_norm_in, attn_out,
+ * post_attn_residual, mlp_out, post_mlp_residual) and latched as
+ * "L{layer:02} {stage} n{0|1} i{0|1}" (the first non-finite element's
+ * NaN / Inf flags), up to 32 bytes; the failing call's zg_last_error ends
+ * with " @" and the same text.  The first failure after zg_model_create or
+ * zg_model_reset latches; later ones keep it.  Found by running the step of
+ * the first KV row holding a non-finite value (or of the failing step)
+ * again with the scans, which rewrites that row with the same values; a row
+ * written by the batched prefill is named as "k_cache[row]" /
+ * "v_cache[row]" instead.  Copies up to cap bytes (no terminator) into buf
+ * and returns the count; 0 when nothing is latched. */
+size_t zg_model_first_nonfinite(const zg_model *m, char *buf, size_t cap);
 
 /* Batched prefill.  No counterpart in the reference, which runs the prompt
  * token by token through forward_single_token_avx512

@@ -44,6 +44,7 @@
 #include <pthread.h>
 #include <sched.h>
 #include <stdatomic.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1133,7 +1134,44 @@ struct zo_model {
     float *kv;
     float *hidden, *norm, *q, *k, *v, *attn, *proj, *gate, *up, *act, *scores, *logits;
     float *inv_freqs;
+    /* the non-finite latch (FINITE_DIAG_TRIPPED / FIRST_NF_BUF,
+     * inference_avx512.rs:95, 233-235), per model */
+    int nf_tripped;
+    size_t nf_len;
+    char nf[32];
 };
+
+size_t zo_nonfinite_text(const float *buf, size_t n, int layer, const char *stage, char *out) {
+    for (size_t i = 0; i < n; i++) {
+        float v = buf[i];
+        if (isfinite(v)) continue;
+        /* finite_diag passes the first non-finite element's NaN / Inf flags
+         * (inference_avx512.rs:108-113); the text is cut at FIRST_NF_CAP */
+        char t[96];
+        int k = snprintf(t, sizeof t, "L%02d %s n%d i%d", layer, stage, isnan(v) ? 1 : 0, isinf(v) ? 1 : 0);
+        size_t len = k < 0 ? 0 : (k > 32 ? 32 : (size_t)k);
+        memcpy(out, t, len);
+        return len;
+    }
+    return 0;
+}
+
+/* finite_diag (inference_avx512.rs:101-131): the first call that finds a
+ * NaN/Inf in buf latches its text; every later call returns at once. */
+static void finite_diag(zo_model *m, const float *buf, size_t n, int layer, const char *stage) {
+    if (m->nf_tripped) return;
+    size_t len = zo_nonfinite_text(buf, n, layer, stage, m->nf);
+    if (len) {
+        m->nf_len = len;
+        m->nf_tripped = 1;
+    }
+}
+
+/* first_nonfinite_detail (inference_avx512.rs:264-275) */
+size_t zo_model_first_nonfinite(const zo_model *m, char *buf) {
+    memcpy(buf, m->nf, m->nf_len);
+    return m->nf_len;
+}
 
 zo_model *zo_model_create(const zo_model_desc *desc) {
     zo_model *m = (zo_model *)calloc(1, sizeof *m);
@@ -1269,6 +1307,7 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
         const zo_layer *L = &m->layers[l];
         const int *qt = m->quants[l].type, *il = m->quants[l].interleave;
         zo_rmsnorm(m->hidden, L->attn_norm, m->norm, H, d->rms_eps);
+        finite_diag(m, m->norm, H, l, "attn_norm_in");
         zo_segment qkv[3] = {
             {L->attn_q, m->q, qd, qt[0], il[0]},
             {L->attn_k, m->k, kvd, qt[1], il[1]},
@@ -1293,6 +1332,8 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
         if (attend(d, kc, vc, m->q, T, scale, m->scores, m->attn)) return -4;
         zo_linear_parallel(m->attn, L->attn_o, m->proj, qd, H, qt[3], il[3]);
         for (size_t i = 0; i < H; i++) m->hidden[i] = m->hidden[i] + m->proj[i];
+        finite_diag(m, m->proj, H, l, "attn_out");
+        finite_diag(m, m->hidden, H, l, "post_attn_residual");
         zo_rmsnorm(m->hidden, L->ffn_norm, m->norm, H, d->rms_eps);
         zo_segment gu[2] = {
             {L->ffn_gate, m->gate, F, qt[4], il[4]},
@@ -1302,6 +1343,8 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
         zo_silu_mul(m->gate, m->up, m->act, F);
         zo_linear_parallel(m->act, L->ffn_down, m->proj, F, H, qt[6], il[6]);
         for (size_t i = 0; i < H; i++) m->hidden[i] = m->hidden[i] + m->proj[i];
+        finite_diag(m, m->proj, H, l, "mlp_out");
+        finite_diag(m, m->hidden, H, l, "post_mlp_residual");
     }
     if (hidden_out) memcpy(hidden_out, m->hidden, H * 4);
     return 0;

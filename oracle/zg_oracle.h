@@ -182,6 +182,15 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
  * in the model for zo_model_lm_head and copied to hidden_out if non-NULL.
  * Returns -3 when a layer projection is not Q4_0 / Q8_0. */
 int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t pos0, float *hidden_out);
+/* record_first_nonfinite's text (inference_avx512.rs:237-262) for the first
+ * non-finite element of buf[0..n): "L{layer:02} {stage} n{0|1} i{0|1}" with
+ * that element's NaN / Inf flags, cut at 32 bytes, into out (no
+ * terminator); returns its length, 0 when every element is finite. */
+size_t zo_nonfinite_text(const float *buf, size_t n, int layer, const char *stage, char *out);
+/* The non-finite latch of zo_model_forward (first_nonfinite_detail,
+ * inference_avx512.rs:264-275): copies the latched text (at most 32 bytes,
+ * no terminator) into buf and returns its length, 0 when nothing tripped. */
+size_t zo_model_first_nonfinite(const zo_model *m, char *buf);
 /* final rmsnorm + LM head + argmax; returns 0 / -1 non-finite / -2 padding */
 int zo_model_lm_head(zo_model *m, float *logits_out, uint32_t *token, float *max_val);
 

@@ -82,6 +82,8 @@ _SIG = {
     "zo_model_destroy": (None, [_P]),
     "zo_model_forward": (_I, [_P, _U32, _S, _P]),
     "zo_model_lm_head": (_I, [_P, _P, C.POINTER(_U32), C.POINTER(_F)]),
+    "zo_model_first_nonfinite": (_S, [_P, C.c_char_p]),
+    "zo_nonfinite_text": (_S, [_P, _S, _I, C.c_char_p, C.c_char_p]),
     "zo_model_prefill_q8": (_I, [_P, _P, _S, _S, _P]),
     "zo_quantize_row_q8k": (None, [_P, _P, _S]),
     "zo_unpack_mins_and_scales": (None, [_P, _P]),
@@ -252,6 +254,14 @@ def linear_q4k_q8k(q8k, w, in_dim, out_dim, start=0, end=None) -> np.ndarray:
     return out
 
 
+def nonfinite_text(buf, layer: int, stage: str) -> str:
+    """The latch text finite_diag would record for buf ("" when finite)."""
+    b = np.ascontiguousarray(buf, np.float32)
+    out = C.create_string_buffer(32)
+    n = load().zo_nonfinite_text(_p(b), b.size, layer, stage.encode(), out)
+    return out.raw[:n].decode()
+
+
 def argmax(v) -> tuple[int, float]:
     v = np.ascontiguousarray(v, np.float32)
     mv = _F()
@@ -327,6 +337,16 @@ class OracleModel:
         rc = load().zo_model_forward(self.h, token, pos, _p(hid))
         assert rc == 0, rc
         return hid
+
+    def forward_status(self, token, pos) -> int:
+        """zo_model_forward's status (-4: the attention softmax failed)."""
+        return load().zo_model_forward(self.h, token, pos, None)
+
+    def first_nonfinite(self) -> str:
+        """The latch of finite_diag: e.g. "L03 attn_out n1 i0", or ""."""
+        buf = C.create_string_buffer(32)
+        n = load().zo_model_first_nonfinite(self.h, buf)
+        return buf.raw[:n].decode()
 
     def prefill_q8(self, tokens, pos0=0):
         """Batched prefill with Q8_0 activations; returns the last row's

@@ -22,6 +22,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -37,6 +39,8 @@ namespace zg {
 
 constexpr int kMaxG = 8;          // max query heads per KV head
 
+constexpr uint32_t kNoStep = 0xFFFFFFFFu;
+
 // Device-resident decode state.
 struct DevState {
   uint32_t token;    // token fed to the next forward pass
@@ -45,8 +49,8 @@ struct DevState {
   uint32_t err;      // bit 0 non-finite logits, 1 argmax in padding, 2 attention
   uint32_t n_prompt;
   uint32_t gen_cap;
-  uint32_t err_step; // gen index at the first error (valid if err != 0)
-  uint32_t pad;
+  uint32_t err_step;  // gen index of the first finalize that saw an error bit (kNoStep: none)
+  uint32_t err_first; // the error bits at that finalize: the first failure
   uint64_t best;     // last packed argmax (copy of the LM head slot)
 };
 
@@ -133,7 +137,12 @@ static_assert(kAttnDecodeSplits >= 1 && kAttnDecodeSplits <= kAttnSplits, "decod
 //             and parks them in its own LDS rows: no workgroup barrier
 //   score     lane (row r, slice s) holds float4 columns s, s+8, ... of its
 //             K row; the partial dot is summed over the row's 8 lanes by DPP;
-//             softmax as attention.rs:48-84, per wave, rescaled per round
+//             softmax as attention.rs:48-84, per wave, rescaled per round.
+//             The softmax fails there (NumericalInstability) when the max
+//             score is not finite or the exp-sum is not finite: any NaN
+//             score, or a +inf one.  Here a wave that saw a NaN score gives
+//             a NaN exp-sum (fmaxf alone would skip NaN), and the merge sets
+//             error bit 2 when the head's max or exp-sum is not finite.
 //   P.V       lane l holds dims VPL*l.. of the pass's 8 rows of V; the row
 //             weights are read out with v_readlane
 //   end       the 4 waves are merged through LDS.  A single split writes
@@ -278,6 +287,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 
   vlane_t acc = (vlane_t)(0.0f);
   float m_w = -INFINITY, l_w = 0.0f;
+  bool nan_score = false;
   for (int rb = 0; rb < n_t; rb += ROUND) {
     if (rb > 0) load_round(rb);
     float sc[NP];
@@ -306,6 +316,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
         d += dpp_f32<0x4E>(d);   // quad_perm [2,3,0,1]
         d += dpp_f32<0x141>(d);  // row_half_mirror: the 8 lanes of the row
         sc[p] = t < n_t ? d * a.scale : -INFINITY;
+        nan_score = nan_score || __builtin_isnan(sc[p]);
         cmax = fmaxf(cmax, sc[p]);
       }
     }
@@ -333,9 +344,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     m_w = m_new;
   }
   reinterpret_cast<vlane_t*>(wo[wave])[lane] = acc;
+  const bool wave_nan = __any(nan_score);
   if (lane == 0) {
     wm[wave] = m_w;
-    wl[wave] = l_w;
+    wl[wave] = wave_nan ? __builtin_nanf("") : l_w;
   }
   __syncthreads();
   if (tid < HD) {
@@ -349,7 +361,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       L = fmaf(f, wl[w], L);
       o = fmaf(f, wo[w][tid], o);
     }
-    if (tid == 0 && !isfinite(M)) atomicOr(&a.st->err, 4u);
+    if (tid == 0 && !(isfinite(M) && isfinite(L))) atomicOr(&a.st->err, 4u);
     if (PF) {
       uint32_t dbits;
       const int8_t qv = q8_0_encode_lane(o * (1.0f / L), &dbits);
@@ -447,7 +459,10 @@ __global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t voc
     if (!isfinite(v)) err = 1;
     else if (idx >= vocab_real) err = 2;
   }
-  if (err && st->err == 0) st->err_step = st->gen;
+  if ((err | st->err) && st->err_step == kNoStep) {
+    st->err_step = st->gen;
+    st->err_first = err | st->err;
+  }
   st->err |= err;
   st->best = key;
   st->token = idx;
@@ -461,6 +476,80 @@ __global__ void advance_kernel(DevState* st, const uint32_t* prompt) {
   const uint32_t p = st->pos + 1;
   st->pos = p;
   if (p < st->n_prompt) st->token = prompt[p];
+}
+
+// ---------------------------------------------------------------------------
+// Non-finite localisation.  The reference scans the activations of every
+// layer for NaN/Inf during the forward pass and latches the first stage that
+// holds one (finite_diag, inference_avx512.rs:88-131, call sites :1896,
+// :1946-1947, :1981-1982; the latch text record_first_nonfinite, :233-262).
+// Here the decode step carries no such scans: after a call fails with a
+// non-finite error, the host finds the first KV row holding a non-finite
+// value (kv_scan_kernel) and runs that row's decode step again, eagerly,
+// with nf_scan_kernel after each of the reference's stages.  The O and down
+// projections then also run once into a zeroed buffer (their residual
+// epilogue adds 0), which gives the sublayer output alone; the step's own
+// launches are unchanged, so the replay writes the bits the step wrote.
+// ---------------------------------------------------------------------------
+
+// Stages, in the reference's forward order within a layer.
+enum NfStage : uint32_t {
+  NF_ATTN_NORM_IN = 1,  // rmsnorm(hidden, attn_norm)
+  NF_ATTN_OUT,          // O projection output
+  NF_POST_ATTN,         // hidden after the attention residual add
+  NF_MLP_OUT,           // down projection output
+  NF_POST_MLP,          // hidden after the MLP residual add
+  NF_K_CACHE,           // a K cache row (rows the decode step cannot replay)
+  NF_V_CACHE,
+};
+
+// FIRST_NF_CAP (inference_avx512.rs:233): the latch text's byte capacity
+constexpr size_t kNfCap = 32;
+
+struct NfScan {
+  uint32_t tag;     // (layer << 8) | stage of the first hit; 0 none
+  uint32_t idx;     // its first non-finite element
+  uint32_t bits;    // that element's bits
+  uint32_t kv_key;  // (row << 8) | (2 * layer + 0 K / 1 V): first non-finite KV row; ~0 none
+};
+
+// One workgroup: the first non-finite element of v[0..n) latches tag,
+// unless an earlier stage has latched or attention has failed (the
+// reference's forward returns at the softmax failure, before the stages
+// after it are scanned).
+__global__ __launch_bounds__(1024) void nf_scan_kernel(const float* __restrict__ v, int n,
+                                                       const uint32_t* __restrict__ err, NfScan* res, uint32_t tag) {
+  __shared__ int first;
+  if (res->tag != 0 || (err && (*err & 4u))) return;  // uniform
+  if (threadIdx.x == 0) first = n;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x)
+    if (!isfinite(v[i])) {
+      atomicMin(&first, i);
+      break;
+    }
+  __syncthreads();
+  if (threadIdx.x == 0 && first < n) {
+    res->idx = (uint32_t)first;
+    res->bits = __float_as_uint(v[first]);
+    res->tag = tag;
+  }
+}
+
+// grid (rows, 2 * layers): whether cache row blockIdx.x of K (even y) or V
+// (odd y) of layer y / 2 holds a non-finite value; the smallest
+// (row, layer, K before V) wins.
+__global__ __launch_bounds__(256) void kv_scan_kernel(const float* __restrict__ kv, size_t max_ctx, int kvd,
+                                                      NfScan* res) {
+  const float* row = kv + ((size_t)blockIdx.y * max_ctx + blockIdx.x) * kvd;
+  int bad = 0;
+  for (int i = threadIdx.x; i < kvd; i += blockDim.x) bad |= !isfinite(row[i]);
+  if (__syncthreads_or(bad) && threadIdx.x == 0) atomicMin(&res->kv_key, (blockIdx.x << 8) | blockIdx.y);
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -673,7 +762,20 @@ struct zg_model {
   float *pf_g = nullptr, *pf_u = nullptr;
   int8_t* pf_qs = nullptr;
   uint16_t* pf_qd = nullptr;
+  // non-finite localisation: device result, [2][hidden] scan buffers
+  // (rmsnorm output, sublayer output), and per KV row the token whose step
+  // wrote it and how (kRowDecode rows can be replayed)
+  NfScan* nf = nullptr;
+  float* nf_buf = nullptr;
+  std::vector<uint32_t> row_token;
+  std::vector<uint8_t> row_kind;
+  // the latch (record_first_nonfinite, inference_avx512.rs:233-262): first
+  // localisation since the model was created or reset
+  char nf_detail[kNfCap] = {};
+  size_t nf_len = 0;
 };
+
+enum RowKind : uint8_t { kRowUnknown = 0, kRowDecode = 1, kRowBatched = 2 };
 
 // Rows per batched-prefill chunk: longer prompts run in chunks, each
 // attending to the cache rows of the chunks before it.
@@ -742,8 +844,9 @@ static zg_status head_argmax(zg_model* m, const float* x, hipStream_t st) {
                     d.rms_eps, st, kGemvStream);
 }
 
-// Record the per-token sequence on the context stream.
-static zg_status record_layers(zg_model* m, hipStream_t st) {
+// Record the per-token sequence on the context stream.  diag adds the
+// non-finite scans of a localisation replay (never captured).
+static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
   const zg_model_desc& d = m->d;
   const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
   const int qd = (int)(d.n_q_heads * d.head_dim), kvd = (int)(d.n_kv_heads * d.head_dim);
@@ -756,6 +859,20 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
   for (uint32_t l = 0; l < d.n_layers; l++) {
     const ZLayer& L = m->layers[l];
     const uint32_t *qt = L.qt, *il = L.il;
+    float* sub = m->nf_buf + H;  // diag: sublayer output alone
+    auto scan = [&](const float* v, uint32_t stage) {
+      hipLaunchKernelGGL(nf_scan_kernel, dim3(1), dim3(1024), 0, st, v, H, &m->st->err, m->nf, (l << 8) | stage);
+      return hip_check(ctx, hipGetLastError(), "scan launch");
+    };
+    auto zero_sub = [&]() {
+      hipLaunchKernelGGL(zero_kernel, dim3((H + 255) / 256), dim3(256), 0, st, sub, H);
+      return hip_check(ctx, hipGetLastError(), "zero launch");
+    };
+    if (diag) {
+      if ((s = hip_check(ctx, launch_rmsnorm(m->hidden, L.attn_norm, m->nf_buf, H, d.rms_eps, st), "rmsnorm launch")) ||
+          (s = scan(m->nf_buf, NF_ATTN_NORM_IN)))
+        return s;
+    }
     FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, qt[ZG_PROJ_Q], il[ZG_PROJ_Q]},
                        {L.k, m->k, (size_t)kvd, qt[ZG_PROJ_K], il[ZG_PROJ_K]},
                        {L.v, m->v, (size_t)kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
@@ -796,21 +913,23 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
     if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), ag, ab, 0, st, aa);
     else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
-    if (L.o_merge) {
-      if ((s = run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, m->hidden, qd, H, qt[ZG_PROJ_O],
-                          il[ZG_PROJ_O], st)))
-        return s;
-    } else {
+    // y += O * attention (y the hidden state, or the zeroed scan buffer)
+    auto o_proj = [&](float* y) -> zg_status {
+      if (L.o_merge)
+        return run_attn_o(ctx, m->part_o, m->part_ml, m->nsplit, HD, L.o, y, qd, H, qt[ZG_PROJ_O], il[ZG_PROJ_O], st);
       if (m->nsplit > 1) {
         const int thr = 256, nthr = qd / 8;
         hipLaunchKernelGGL(attn_merge_kernel, dim3((nthr + thr - 1) / thr), dim3(thr), 0, st, m->part_o, m->part_ml,
                            qd, HD, m->nsplit, m->attn);
-        if ((s = hip_check(ctx, hipGetLastError(), "attention merge launch"))) return s;
+        zg_status e = hip_check(ctx, hipGetLastError(), "attention merge launch");
+        if (e) return e;
       }
-      if ((s = run_linear(ctx, m->attn, L.o, m->hidden, qd, H, qt[ZG_PROJ_O], il[ZG_PROJ_O], 0, H, EPI_RESID,
-                          m->hidden, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
-        return s;
-    }
+      return run_linear(ctx, m->attn, L.o, y, qd, H, qt[ZG_PROJ_O], il[ZG_PROJ_O], 0, H, EPI_RESID, y, nullptr,
+                        PRO_PLAIN, nullptr, 0.0f, st);
+    };
+    if (diag && ((s = zero_sub()) || (s = o_proj(sub)) || (s = scan(sub, NF_ATTN_OUT)))) return s;
+    if ((s = o_proj(m->hidden))) return s;
+    if (diag && (s = scan(m->hidden, NF_POST_ATTN))) return s;
     if (L.gu_one) {
       FusedDev gu[2] = {{L.gate, m->act, (size_t)F, qt[ZG_PROJ_GATE], il[ZG_PROJ_GATE]},
                         {L.up, nullptr, (size_t)F, qt[ZG_PROJ_UP], il[ZG_PROJ_UP]}};
@@ -825,9 +944,13 @@ static zg_status record_layers(zg_model* m, hipStream_t st) {
       hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, st, m->act, m->up, F);
       if ((s = hip_check(ctx, hipGetLastError(), "swiglu launch"))) return s;
     }
-    if ((s = run_linear(ctx, m->act, L.down, m->hidden, F, H, qt[ZG_PROJ_DOWN], il[ZG_PROJ_DOWN], 0, H, EPI_RESID,
-                        m->hidden, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
-      return s;
+    auto down_proj = [&](float* y) {
+      return run_linear(ctx, m->act, L.down, y, F, H, qt[ZG_PROJ_DOWN], il[ZG_PROJ_DOWN], 0, H, EPI_RESID, y, nullptr,
+                        PRO_PLAIN, nullptr, 0.0f, st);
+    };
+    if (diag && ((s = zero_sub()) || (s = down_proj(sub)) || (s = scan(sub, NF_MLP_OUT)))) return s;
+    if ((s = down_proj(m->hidden))) return s;
+    if (diag && (s = scan(m->hidden, NF_POST_MLP))) return s;
   }
   return ZG_OK;
 }
@@ -1032,7 +1155,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   const size_t H = d.hidden, F = d.ffn;
   try {
     m->layers.resize(d.n_layers);
-    m->owned.reserve(32 + 4 * (size_t)d.n_layers);  // room for every buffer the model allocates
+    m->owned.reserve(40 + 4 * (size_t)d.n_layers);  // room for every buffer the model allocates
   } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
     delete m;
     return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
@@ -1104,6 +1227,16 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->out_tokens), m->out_cap * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->xn), H * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->up), F * sizeof(float));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->nf), sizeof(NfScan));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->nf_buf), 2 * H * sizeof(float));
+  if (!s) {
+    try {
+      m->row_token.assign(d.max_ctx, 0);
+      m->row_kind.assign(d.max_ctx, kRowUnknown);
+    } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
+      s = set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
+    }
+  }
   if (!s) {
     // per layer, which GEMVs are one launch with the rmsnorm (or
     // attention-merge) prologue: X4 weights, or plain Q4_0 / Q8_0 at a
@@ -1162,23 +1295,114 @@ static zg_status set_state(zg_model* m, uint32_t token, uint32_t pos, uint32_t n
   h.pos = pos;
   h.n_prompt = n_prompt;
   h.gen_cap = gen_cap;
+  h.err_step = kNoStep;
   return hip_check(m->ctx, hipMemcpyAsync(m->st, &h, sizeof h, hipMemcpyHostToDevice, m->ctx->stream), "state upload");
 }
 
-static zg_status state_status(zg_model* m, const DevState& h) {
-  if (h.err & 4u) return set_error(m->ctx, ZG_ERR_ATTENTION, "attention: non-finite scores");
-  if (h.err & 1u) return set_error(m->ctx, ZG_ERR_NONFINITE_LOGITS, "LM head: non-finite logits (step %u)", h.err_step);
-  if (h.err & 2u) return set_error(m->ctx, ZG_ERR_ARGMAX_IN_PADDING, "LM head: argmax in padding (step %u)", h.err_step);
+static const char* nf_stage_name(uint32_t stage) {
+  switch (stage) {
+    case NF_ATTN_NORM_IN: return "attn_norm_in";
+    case NF_ATTN_OUT: return "attn_out";
+    case NF_POST_ATTN: return "post_attn_residual";
+    case NF_MLP_OUT: return "mlp_out";
+    case NF_POST_MLP: return "post_mlp_residual";
+    case NF_K_CACHE: return "k_cache";
+    case NF_V_CACHE: return "v_cache";
+    default: return "?";
+  }
+}
+
+// Fills the latch after a call failed with a non-finite error whose first
+// failing step ran at position p_fail.  The first KV row (in position
+// order, then layer) holding a non-finite value is where a non-finite value
+// first reached a later step; with none, the failing step itself made it
+// (after the last layer's K/V, or in the LM head).  That row's step runs
+// again with the scans when it was a decode step (same token, same rows
+// before it, same launches: the same bits); a row written by the batched
+// prefill names the cache row instead.  A value that reached neither the
+// cache nor the logits is not seen.  Best effort: a HIP failure here leaves
+// the latch empty.
+static void localise_nonfinite(zg_model* m, uint32_t p_fail) {
+  zg_ctx* ctx = m->ctx;
+  const zg_model_desc& d = m->d;
+  hipStream_t st = ctx->stream;
+  if (m->nf_len || p_fail >= d.max_ctx || p_fail >= (1u << 24) || 2 * d.n_layers > 255) return;
+  const size_t kvd = (size_t)d.n_kv_heads * d.head_dim;
+  NfScan h{0, 0, 0, 0xFFFFFFFFu};
+  if (hipMemcpyAsync(m->nf, &h, sizeof h, hipMemcpyHostToDevice, st) != hipSuccess) return;
+  hipLaunchKernelGGL(kv_scan_kernel, dim3(p_fail + 1, 2 * d.n_layers), dim3(256), 0, st, m->kv, (size_t)d.max_ctx,
+                     (int)kvd, m->nf);
+  if (hipGetLastError() != hipSuccess || hipMemcpyAsync(&h, m->nf, sizeof h, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return;
+  const bool kv_hit = h.kv_key != 0xFFFFFFFFu;
+  const uint32_t q = kv_hit ? h.kv_key >> 8 : p_fail;
+  uint32_t row = 0;
+  if (m->row_kind[q] == kRowDecode) {
+    if (set_state(m, m->row_token[q], q, 0, 0) || record_layers(m, st, true)) return;
+  } else if (kv_hit) {
+    // a cache row the decode step cannot reproduce: name it
+    const uint32_t slot = h.kv_key & 0xFFu;
+    row = q;
+    hipLaunchKernelGGL(nf_scan_kernel, dim3(1), dim3(1024), 0, st, m->kv + ((size_t)slot * d.max_ctx + q) * kvd,
+                       (int)kvd, nullptr, m->nf, ((slot / 2) << 8) | (slot & 1 ? NF_V_CACHE : NF_K_CACHE));
+    if (hipGetLastError() != hipSuccess) return;
+  } else {
+    return;
+  }
+  if (hipMemcpyAsync(&h, m->nf, sizeof h, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess || h.tag == 0)
+    return;
+  const uint32_t stage = h.tag & 0xFFu, layer = h.tag >> 8;
+  const float v = __builtin_bit_cast(float, h.bits);
+  char name[32];
+  if (stage == NF_K_CACHE || stage == NF_V_CACHE) snprintf(name, sizeof name, "%s[%u]", nf_stage_name(stage), row);
+  else snprintf(name, sizeof name, "%s", nf_stage_name(stage));
+  // "L{:02} {} n{} i{}" (inference_avx512.rs:259), here for the first
+  // non-finite element (finite_diag's flags, :108-113)
+  char text[64];
+  const int n = snprintf(text, sizeof text, "L%02u %s n%d i%d", layer, name, std::isnan(v) ? 1 : 0, std::isinf(v) ? 1 : 0);
+  m->nf_len = n < 0 ? 0 : std::min((size_t)n, kNfCap);
+  memcpy(m->nf_detail, text, m->nf_len);
+}
+
+// Status of a finished call: its first failure, as the reference's loop
+// stops at the first error (within one step an attention failure comes
+// before the LM head's).  p_fail: the position of the step at err_step.
+static zg_status state_status(zg_model* m, const DevState& h, uint32_t p_fail) {
+  const uint32_t e = h.err_step != kNoStep ? h.err_first : h.err;
+  if (e & 5u) localise_nonfinite(m, p_fail);
+  char at[kNfCap + 3] = "";
+  if (m->nf_len) snprintf(at, sizeof at, " @%.*s", (int)m->nf_len, m->nf_detail);
+  if (e & 4u) return set_error(m->ctx, ZG_ERR_ATTENTION, "attention: non-finite scores (step %u)%s", h.err_step, at);
+  if (e & 1u) return set_error(m->ctx, ZG_ERR_NONFINITE_LOGITS, "LM head: non-finite logits (step %u)%s", h.err_step, at);
+  if (e & 2u) return set_error(m->ctx, ZG_ERR_ARGMAX_IN_PADDING, "LM head: argmax in padding (step %u)", h.err_step);
   return ZG_OK;
+}
+
+static void note_rows(zg_model* m, size_t pos0, const uint32_t* tokens, size_t n, RowKind kind) {
+  for (size_t i = 0; i < n && pos0 + i < m->row_kind.size(); i++) {
+    m->row_token[pos0 + i] = tokens[i];
+    m->row_kind[pos0 + i] = kind;
+  }
 }
 
 // Every step writes KV row `pos` before any read of rows <= pos, and every
 // step or generate call uploads its own position, so a new sequence needs
-// no device work: reset only waits for in-flight work.
+// no device work: reset waits for in-flight work and clears the non-finite
+// latch.
 extern "C" void zg_model_reset(zg_model* m) {
   if (!m) return;
   hipSetDevice(m->ctx->device);
   hipStreamSynchronize(m->ctx->stream);
+  m->nf_len = 0;
+}
+
+extern "C" size_t zg_model_first_nonfinite(const zg_model* m, char* buf, size_t cap) {
+  if (!m || !buf) return 0;
+  const size_t n = std::min(m->nf_len, cap);
+  memcpy(buf, m->nf_detail, n);
+  return n;
 }
 
 extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, float* hidden_out, float* logits,
@@ -1188,6 +1412,7 @@ extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, fl
   if (pos >= m->d.max_ctx) return set_error(ctx, ZG_ERR_CONTEXT_FULL, "position %u >= max_ctx %u", pos, m->d.max_ctx);
   if (token >= m->d.vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "token %u out of range", token);
   hipSetDevice(ctx->device);
+  note_rows(m, pos, &token, 1, kRowDecode);
   zg_status s = set_state(m, token, pos, 0, 0);
   if (s) return s;
   if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
@@ -1202,7 +1427,7 @@ extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, fl
                                                    hipMemcpyDeviceToHost, ctx->stream), "download")))
     return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
-  if ((s = state_status(m, h))) return s;
+  if ((s = state_status(m, h, pos))) return s;
   return lm_head_status(ctx, h.best, m->d.vocab_real, next_token, max_logit);
 }
 
@@ -1218,6 +1443,7 @@ extern "C" zg_status zg_model_prefill(zg_model* m, const uint32_t* tokens, size_
   for (size_t i = 0; i < n; i++)
     if (tokens[i] >= m->d.vocab_padded) return set_error(ctx, ZG_ERR_INVALID_ARG, "prefill: token %u out of range", tokens[i]);
   hipSetDevice(ctx->device);
+  note_rows(m, pos0, tokens, n, kRowBatched);
   zg_status s = hip_check(ctx, hipMemcpyAsync(m->prompt, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream),
                           "prompt upload");
   if (!s) s = set_state(m, 0, pos0 + (uint32_t)n - 1, 0, 0);
@@ -1231,7 +1457,7 @@ extern "C" zg_status zg_model_prefill(zg_model* m, const uint32_t* tokens, size_
                                                       hipMemcpyDeviceToHost, ctx->stream), "download")))
     return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
-  if ((s = state_status(m, h))) return s;
+  if ((s = state_status(m, h, pos0 + (uint32_t)n - 1))) return s;
   return lm_head_status(ctx, h.best, m->d.vocab_real, next_token, max_logit);
 }
 
@@ -1269,6 +1495,7 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
   if (batched && !m->pf_ok)
     return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "generate: the batched prefill's GEMMs take Q4_0 / Q8_0 projections");
   if (batched && (s = prefill_alloc(m))) return s;
+  note_rows(m, 0, prompt, n_prompt, batched ? kRowBatched : kRowDecode);
   if ((s = set_state(m, prompt[0], batched ? (uint32_t)n_prompt - 1 : 0, (uint32_t)n_prompt, (uint32_t)n_gen)))
     return s;
   if ((s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "sync"))) return s;
@@ -1298,5 +1525,8 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
   if ((s = hip_check(ctx, hipMemcpy(&h, m->st, sizeof h, hipMemcpyDeviceToHost), "state download"))) return s;
   if ((s = hip_check(ctx, hipMemcpy(out_tokens, m->out_tokens, n_gen * 4, hipMemcpyDeviceToHost), "tokens download")))
     return s;
-  return state_status(m, h);
+  // generated token j - 1 was the input of the step at position n_prompt - 1 + j
+  note_rows(m, n_prompt, out_tokens, n_gen - 1, kRowDecode);
+  const size_t last = n_prompt + n_gen - 2;
+  return state_status(m, h, (uint32_t)(h.err_step == kNoStep ? last : n_prompt - 1 + h.err_step));
 }

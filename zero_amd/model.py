@@ -75,6 +75,18 @@ class GpuModel:
             self.ctx.lib.zg_model_destroy(self.h)
             self.h = None
 
+    def reset(self):
+        """New sequence (zg_model_reset); also clears the non-finite latch."""
+        self.ctx.lib.zg_model_reset(self.h)
+
+    def first_nonfinite(self) -> str:
+        """The non-finite latch (zg_model_first_nonfinite): the first stage
+        that held a NaN/Inf in a failed call, e.g. "L03 attn_out n1 i0"; ""
+        when nothing is latched."""
+        buf = C.create_string_buffer(32)
+        n = self.ctx.lib.zg_model_first_nonfinite(self.h, buf, 32)
+        return buf.raw[:n].decode()
+
     def _raise(self, rc, tok):
         if rc == _lib.ZG_ERR_ARGMAX_IN_PADDING:
             raise ArgmaxInPaddingRegion(rc, self.ctx.last_error(), tok)
