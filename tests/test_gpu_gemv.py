@@ -225,6 +225,50 @@ def test_tall_q8_0_ranges(ctx, zo):
     ctx.clear()
 
 
+def _edge_activations(rng, k, kind):
+    """Activation vectors whose blocks stress the integer form of the tall
+    launches (x scaled per 32-block to 22-bit integers): a zero block, a
+    block of magnitudes below 1e-30 (no integer form: its wave decodes in
+    fp32), a block spanning eight decades, and non-finite values."""
+    x = synth.activations(rng, k)
+    x[0:32] = 0.0
+    x[64:96] = np.float32(1e-31) * rng.standard_normal(32).astype(np.float32)
+    x[128:160] *= np.float32(1e-4)
+    x[131] = 1e4
+    if kind == "inf":
+        x[700] = np.inf
+    elif kind == "nan":
+        x[1500] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("kind", ["finite", "inf", "nan"])
+@pytest.mark.parametrize("quant,rows,k", [(Q4_0, 12288, 2048), (Q8_0, 32768, 2048)])
+def test_tall_integer_activation_edges(ctx, zo, quant, rows, k, kind):
+    """Tall X4 launches take the activations as exact integers (three int8
+    digits per value, int32 dot chains).  Finite edge blocks stay within the
+    parity bar and as close to f64 as the oracle (x 4); non-finite inputs
+    give non-finite rows exactly where the oracle's do."""
+    rng = np.random.default_rng(rows + k + len(kind))
+    w = synth.weight(rng, quant, rows, k, 4)
+    x = _edge_activations(rng, k, kind)
+    ctx.register(w, quant, 4)
+    out = np.empty(rows, np.float32)
+    ctx.linear_dispatch(x, w, out, k, rows, quant)
+    ref = zo.linear_range(x, w, k, rows, quant, 4)
+    ctx.clear()
+    if kind == "finite":
+        f64 = zo.linear_f64(x, w, k, rows, quant, 4)
+        e_gpu, e_ref = rel_err(out, ref), rel_err(ref, f64)
+        print(f"{kind} quant={quant}: rel err vs oracle {e_gpu:.2e}, oracle vs f64 {e_ref:.2e}, "
+              f"gpu vs f64 {rel_err(out, f64):.2e}")
+        assert e_gpu <= REL_TOL
+        assert rel_err(out, f64) <= 4 * e_ref + 1e-6
+    else:
+        assert np.array_equal(np.isfinite(out), np.isfinite(ref))
+        assert not np.isfinite(ref).any()
+
+
 @pytest.mark.parametrize("il", [4, 1])
 def test_fused_qkv_q8_0(ctx, zo, il):
     """Config 2: fused Q|K|V Q8_0, Qwen3-1.7B attention (2048 + 1024 + 1024) x 2048,

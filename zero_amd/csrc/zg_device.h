@@ -344,4 +344,113 @@ __device__ __forceinline__ float deq_elem(const BlockRef& br, uint32_t qt, float
   }
 }
 
+// ---------------------------------------------------------------------------
+// Activations as exact integers for v_dot4_i32_i8.
+//
+// A 32-value block with largest magnitude M is scaled by 127 * 2^14 / M and
+// rounded to the nearest integer V (|V| <= 127 * 2^14: 22 significant bits,
+// an error of at most 2^-22 M per value, the order of one fp32 rounding of
+// the block's largest product).  V is split into three signed bytes,
+// V = 2^14 a + 2^7 b + c with b, c in [-64, 63] and a in [-127, 127], so
+// that sum_j q_j V_j over int8 quants q comes out of three v_dot4_i32_i8
+// chains exactly, and the row's block term is that integer times
+// d * M / (127 * 2^14).
+//
+// Lane layout: the four lanes of a quad share one block; quad lane r holds
+// the block's values 4r..4r+3 ("lo") and 16+4r..16+4r+3 ("hi").  After the
+// quad exchange every lane holds, per digit k, dwords dg[k][c] = values
+// 4c..4c+3 for c < 4 and 16+4(c-4).. for c >= 4: the order of the quant
+// dwords of a Q4_0 block (low nibbles of dword c are values 4c..4c+3, high
+// nibbles 16+4c..) and of a Q8_0 block (dword c = values 4c..4c+3).
+// ---------------------------------------------------------------------------
+struct XDig {
+  uint32_t dg[3][8];  // digits a, b, c of the block's 32 values, packed 4 per dword
+  int sum[3];         // per digit, the sum of the block's 32 digits
+  float sinv;         // M / (127 * 2^14): one unit of V
+};
+
+// Three signed base-128 digits of V, each in the low byte of an int.
+__device__ __forceinline__ void split_digits(int v, int& a, int& b, int& c) {
+  c = __builtin_amdgcn_sbfe(v, 0, 7);   // sign-extended low 7 bits: [-64, 63]
+  const int w = (v - c) >> 7;           // exact
+  b = __builtin_amdgcn_sbfe(w, 0, 7);
+  a = (w - b) >> 7;
+}
+
+// Low bytes of four ints into one dword (byte j from p[j]).
+__device__ __forceinline__ uint32_t pack_low_bytes(int p0, int p1, int p2, int p3) {
+  const uint32_t p01 = __builtin_amdgcn_perm((uint32_t)p1, (uint32_t)p0, 0x0C0C0400u);
+  const uint32_t p23 = __builtin_amdgcn_perm((uint32_t)p3, (uint32_t)p2, 0x0C0C0400u);
+  return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+}
+
+// Digits of four values at scale s, packed: out[k] holds digit k.
+__device__ __forceinline__ void digits4(float4 x, float s, uint32_t (&out)[3]) {
+  int a[4], b[4], c[4];
+  const float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int j = 0; j < 4; j++) split_digits(__float2int_rn(v[j] * s), a[j], b[j], c[j]);
+  out[0] = pack_low_bytes(a[0], a[1], a[2], a[3]);
+  out[1] = pack_low_bytes(b[0], b[1], b[2], b[3]);
+  out[2] = pack_low_bytes(c[0], c[1], c[2], c[3]);
+}
+
+template <int S>
+__device__ __forceinline__ uint32_t quad_bcast_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, S | (S << 2) | (S << 4) | (S << 6), 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ int quad_sum_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  return v;
+}
+
+// The quad's block from this lane's quarter (lo = values 4r..4r+3, hi =
+// 16+4r..16+4r+3).  Returns true when the integer form does not apply to
+// the block: a NaN or infinity among its values, or a largest magnitude
+// below 1e-30 other than zero (the scale would overflow).  The block's
+// largest magnitude is an integer max over the sign-cleared bit patterns,
+// which orders every finite value below +inf below every NaN.
+__device__ __forceinline__ bool xdig_quad(float4 lo, float4 hi, XDig& X) {
+  const uint32_t m7 = 0x7FFFFFFFu;
+  uint32_t mb = max(max(__float_as_uint(lo.x) & m7, __float_as_uint(lo.y) & m7), max(__float_as_uint(lo.z) & m7, __float_as_uint(lo.w) & m7));
+  mb = max(mb, max(max(__float_as_uint(hi.x) & m7, __float_as_uint(hi.y) & m7), max(__float_as_uint(hi.z) & m7, __float_as_uint(hi.w) & m7)));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
+  const bool bad = mb >= 0x7F800000u || (mb != 0u && mb < 0x0DA24260u);  // 1e-30f
+  const float m = __uint_as_float(mb);
+  const float s = (mb != 0u && !bad) ? (127.0f * 16384.0f) / m : 0.0f;
+  X.sinv = m * (1.0f / (127.0f * 16384.0f));
+  uint32_t dl[3], dh[3];
+  digits4(lo, s, dl);
+  digits4(hi, s, dh);
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    X.dg[k][0] = quad_bcast_u32<0>(dl[k]);
+    X.dg[k][1] = quad_bcast_u32<1>(dl[k]);
+    X.dg[k][2] = quad_bcast_u32<2>(dl[k]);
+    X.dg[k][3] = quad_bcast_u32<3>(dl[k]);
+    X.dg[k][4] = quad_bcast_u32<0>(dh[k]);
+    X.dg[k][5] = quad_bcast_u32<1>(dh[k]);
+    X.dg[k][6] = quad_bcast_u32<2>(dh[k]);
+    X.dg[k][7] = quad_bcast_u32<3>(dh[k]);
+    X.sum[k] = quad_sum_i32(__builtin_amdgcn_sdot4((int)dl[k], 0x01010101, __builtin_amdgcn_sdot4((int)dh[k], 0x01010101, 0, false), false));
+  }
+  return bad;
+}
+
+// The three digit chains of sum_j q_j V_j for a block of 32 signed int8
+// quants q, given as 8 dwords in the dg order; t0, t1, t2 enter with the
+// chains' start values.  V = 2^14 a + 2^7 b + c, so the block's integer sum
+// is 2^14 t0 + 2^7 t1 + t2.
+__device__ __forceinline__ void xdig_chains(const uint32_t (&q)[8], const XDig& X, int& t0, int& t1, int& t2) {
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    t0 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[0][c], t0, false);
+    t1 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[1][c], t1, false);
+    t2 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[2][c], t2, false);
+  }
+}
+
 }  // namespace zg

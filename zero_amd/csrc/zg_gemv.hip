@@ -17,6 +17,8 @@
 // Generic path: any layout / block type, one wave per output row, byte
 // loads.  Used for plain Q4_0/Q8_0, odd blocks-per-row and as the first
 // Q4_K/Q6_K implementation.
+#include <type_traits>
+
 #include "zg_device.h"
 #include "zg_kernels.h"
 
@@ -457,6 +459,33 @@ __device__ __forceinline__ float strip_dot(const LaneW<QT>& L, const float4* xb,
   return d * (q8u_block_dot(L.q, xb) + mterm);
 }
 
+// The same block against the activations as exact integers (XDig): the
+// three digit chains of sum_j q_j V_j with v_dot4_i32_i8, then one scale
+// d * M / (127 * 2^14).  Q4_0: the nibbles n enter as they are and the
+// chains start at -8 * sum_j V_j, so the block's integer sum is
+// sum_j (n_j - 8) V_j, |.| <= 32 * 8 * 127 * 2^14 + ... < 2^31, recombined
+// in int32.  Q8_0: quants up to 128 in magnitude, so the top digit's chain
+// joins the other two in float (one rounding).
+template <uint32_t QT>
+__device__ __forceinline__ float strip_dot_dig(const LaneW<QT>& L, const XDig& X) {
+  const float ds = scale_f32(L.d) * X.sinv;
+  if constexpr (QT == Q4_0) {
+    uint32_t q[8];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      q[c] = L.q[c] & 0x0F0F0F0Fu;
+      q[4 + c] = (L.q[c] >> 4) & 0x0F0F0F0Fu;
+    }
+    int t0 = -8 * X.sum[0], t1 = -8 * X.sum[1], t2 = -8 * X.sum[2];
+    xdig_chains(q, X, t0, t1, t2);
+    return (float)((t0 << 14) + (t1 << 7) + t2) * ds;
+  } else {
+    int t0 = 0, t1 = 0, t2 = 0;
+    xdig_chains(L.q, X, t0, t1, t2);
+    return fmaf((float)t0, 16384.0f, (float)((t1 << 7) + t2)) * ds;
+  }
+}
+
 // The same block with a Q8_0 activation block (int8 x8, fp16 scale dx,
 // sx = sum of x8): the integer dot (v_dot4_i32_i8; Q4_0 nibbles enter
 // unsigned and the -8 offset is -8 sx), then (dW dX) * isum, the per-block
@@ -523,6 +552,24 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v;
 }
 
+// The 32 activations of K-block kb as the prologue forms them: from x, times
+// the rmsnorm gain (the 1/rms factor is applied to the row totals), or from
+// the merged attention vector in LDS (xs).
+template <int PRO>
+__device__ __forceinline__ void strip_x_block(float4 (&xf)[8], const GemvArgs& a, const float* xs, int kb) {
+  const float4* x4 = reinterpret_cast<const float4*>((PRO == PRO_ATTN ? xs : a.x) + 32 * kb);
+#pragma unroll
+  for (int c = 0; c < 8; c++) xf[c] = x4[c];
+  if (PRO == PRO_RMSNORM) {
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const float4 g = g4[c];
+      xf[c] = make_float4(xf[c].x * g.x, xf[c].y * g.y, xf[c].z * g.z, xf[c].w * g.w);
+    }
+  }
+}
+
 // IL 4: X4 group-blocks; IL 1: plain row-major blocks (IL 2: the same with
 // nontemporal loads), a "group" being 4
 // consecutive rows (lane (b, r) reads block b of row 4 g + r, b = lane >> 2,
@@ -534,9 +581,13 @@ __device__ __forceinline__ float quad_sum(float v) {
 // batch), so there is no second register set and no batch loop.
 // SC: the strip count as a compile-time constant (0: the argument S_rt),
 // for the common one-batch shapes (in_dim 2048 and 6144).
+// DIG: fp32 activations as exact integers (XDig) and int8 dot chains; a
+// wave with a block that the integer form does not take (NaN, infinity, a
+// largest magnitude below 1e-30) runs the fp32 decode instead.
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4,
-          bool ONEB = false, int SC = 0>
+          bool ONEB = false, int SC = 0, bool DIG = false>
 __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) {
+  static_assert(!DIG || PRO != PRO_Q8X, "Q8_0 activations have their own integer form");
   const int S = SC ? SC : S_rt;
   constexpr int GBY = StripGeom<QT>::GB;
   constexpr int BB = QT == Q4_0 ? 18 : 34;  // plain block bytes
@@ -650,8 +701,14 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
     }
     __syncthreads();
     const float4* x4 = reinterpret_cast<const float4*>(xs + 32 * kb);
+    if (DIG) {
+      // the lane's quarter, as the global prologues load it
+      xb[0] = x4[r];
+      xb[1] = x4[4 + r];
+    } else {
 #pragma unroll
-    for (int c = 0; c < 8; c++) xb[c] = x4[c];
+      for (int c = 0; c < 8; c++) xb[c] = x4[c];
+    }
   }
   if (PRO == PRO_RMSNORM) {
     // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w.  The scalar
@@ -678,13 +735,20 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
   }
   float mterm = 0.0f;
   int sx = 0;
+  XDig xd;
+  bool fp32 = !DIG;  // wave-uniform: this wave decodes with fp32 activations
+  if (DIG) {
+    const bool bad = xdig_quad(xb[0], xb[1], xd);
+    fp32 = __builtin_amdgcn_ballot_w64(bad) != 0;
+    asm volatile("" : "+v"(xd.sum[0]), "+v"(xd.sum[1]), "+v"(xd.sum[2]), "+v"(xd.sinv));
+  }
   if (PRO == PRO_Q8X) {
 #pragma unroll
     for (int c = 0; c < 8; c++) sx = __builtin_amdgcn_sdot4((int)x8[c], 0x01010101, sx, false);
     asm volatile("" : "+v"(sx));  // computed here, not sunk below the next load
-  } else {
+  } else if (!DIG) {
     float t;
-    if (PRO == PRO_ATTN) {
+    if (PRO == PRO_ATTN && !DIG) {
       t = 0.0f;
 #pragma unroll
       for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
@@ -705,13 +769,35 @@ __global__ __launch_bounds__(MAXT) void gemv_strip_kernel(GemvArgs a, int S_rt) 
   auto process = [&](const LaneW<QT> (&L)[GBATCH][PARTS], int batch, int buf) {
     const int base = batch * per_batch + sub * GBATCH;
     float* pb = part + (size_t)buf * NW * GBATCH * PARTS * 16;
+    // in batch-loop launches (and single-projection ones) every group of the
+    // batch is decoded, also the clamped repeats past the last item (their
+    // totals are dropped in the epilogue): a skipped decode leaves its loads
+    // unconsumed, and the compiler then waits for the other batch's loads
+    // before it reuses their registers (C1 6144x2048: 3.53 vs 3.63 us; the
+    // fused Q|K|V one-batch launch keeps the skip: 3.99 vs 4.20 us)
 #pragma unroll
     for (int j = 0; j < GBATCH; j++) {
-      if (base + j < items) {
+      if (SEG1 || !ONEB || base + j < items) {
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
-          const float v = row_sum4(PRO == PRO_Q8X ? strip_dot_q8x<QT>(L[j][p], x8, dxq, sx)
-                                                  : strip_dot<QT>(L[j][p], xb, mterm));
+          float dot;
+          if (PRO == PRO_Q8X) {
+            dot = strip_dot_q8x<QT>(L[j][p], x8, dxq, sx);
+          } else if (!DIG) {
+            dot = strip_dot<QT>(L[j][p], xb, mterm);
+          } else if (!fp32) {
+            dot = strip_dot_dig<QT>(L[j][p], xd);
+          } else {
+            // the fp32 decode on the lane's whole block, reloaded per group
+            // (a wave that met a block the integer form does not take)
+            float4 xf[8];
+            strip_x_block<PRO>(xf, a, part + (size_t)2 * NW * GBATCH * PARTS * 16, kb);
+            float t = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; c++) t += (xf[c].x + xf[c].y) + (xf[c].z + xf[c].w);
+            dot = strip_dot<QT>(L[j][p], xf, (QT == Q4_0 ? -8.0f : -128.0f) * t);
+          }
+          const float v = row_sum4(dot);
           if ((lane & 15) < 4) pb[((wave * GBATCH + j) * PARTS + p) * 16 + (lane >> 4) * 4 + r] = v;
         }
       }
@@ -948,23 +1034,35 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
+#ifndef ZG_STRIP_TALL_GB
+#define ZG_STRIP_TALL_GB 4
+#endif
+
+// Which strip launches take the integer activation form: 0 none, 1 the
+// batch-loop launches, 2 every launch with fp32 activations.
+#ifndef ZG_STRIP_DIG
+#define ZG_STRIP_DIG 1
+#endif
+
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
 static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr bool DIG1 = PRO != PRO_Q8X && ZG_STRIP_DIG >= 2;  // one-batch launches
+  constexpr bool DIGL = PRO != PRO_Q8X && ZG_STRIP_DIG >= 1;  // batch-loop launches
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
   const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
   if (MAXT == 1024 && nbatch <= (size_t)cu_count() * 4) {
     // one batch per workgroup (every decode-sized launch): no batch loop
     if (S == 4)
-      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 4>), dim3((unsigned)nbatch),
-                         dim3(nw * 64), shm, st, a, S);
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 4, DIG1>),
+                         dim3((unsigned)nbatch), dim3(nw * 64), shm, st, a, S);
     else if (S == 12)
-      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 12>), dim3((unsigned)nbatch),
-                         dim3(nw * 64), shm, st, a, S);
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 12, DIG1>),
+                         dim3((unsigned)nbatch), dim3(nw * 64), shm, st, a, S);
     else
-      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true>), dim3((unsigned)nbatch),
-                         dim3(nw * 64), shm, st, a, S);
+      hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 0, DIG1>),
+                         dim3((unsigned)nbatch), dim3(nw * 64), shm, st, a, S);
     return hipGetLastError();
   }
   // about 16 resident waves per CU; the remaining batches are looped over.
@@ -975,8 +1073,8 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
     static int resident = 0;
     if (resident == 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL>, nw * 64,
-                                                       shm) !=
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, false, 0, DIGL>, nw * 64, shm) !=
               hipSuccess ||
           n <= 0)
         n = 1;
@@ -987,8 +1085,8 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   const size_t cap = (size_t)cu_count() * per_cu;
   const size_t grid = nbatch < cap ? nbatch : cap;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL>), dim3((unsigned)grid), dim3(nw * 64), shm,
-                     st, a, S);
+  hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, false, 0, DIGL>), dim3((unsigned)grid),
+                     dim3(nw * 64), shm, st, a, S);
   return hipGetLastError();
 }
 
@@ -1011,7 +1109,7 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   const size_t wps = nw / S;
   if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID) && PRO != PRO_ATTN) {
     if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
-      return launch_strip_gb<QT, PRO, EPI, 4, 1024, IL>(a, S, nw, items, st);
+      return launch_strip_gb<QT, PRO, EPI, ZG_STRIP_TALL_GB, (ZG_STRIP_DIG >= 1 ? 256 : 1024), IL>(a, S, nw, items, st);
     // one-batch launches: groups per wave ~ items / (2 CUs), 1 to 3, so
     // that every CU gets about two workgroups (C1 6144x2048: three groups
     // per wave, 512 workgroups of four waves, 3.47 vs 3.56 us at two in a
