@@ -40,6 +40,12 @@ struct GemvArgs {
   int attn_nsplit, attn_hd;
   uint32_t flags;  // kGemvStream
   const uint8_t* xq;  // PRO_Q8X: k / 32 Q8_0 blocks (34 bytes, 2-byte aligned)
+  // tagged stores (the fused Q|K|V + attention launch): each segment's y is
+  // a uint64_t array, row r holding (tag << 32) | the row's fp32 bits,
+  // stored as one agent-scope 64-bit store; tag = *sync_epoch * sync_mul +
+  // sync_add (the step counter times the layer count plus the layer)
+  const uint32_t* sync_epoch;
+  uint32_t sync_mul, sync_add;
 };
 
 // The weights are streamed without allocating in the last-level cache:

@@ -32,6 +32,7 @@
 #include "zg_device.h"
 #include "zg_internal.h"
 #include "zg_kernels.h"
+#include "zg_strip.h"
 
 using namespace zg;
 
@@ -46,7 +47,7 @@ struct DevState {
   uint32_t token;    // token fed to the next forward pass
   uint32_t pos;      // its position
   uint32_t gen;      // tokens produced by finalize so far
-  uint32_t err;      // bit 0 non-finite logits, 1 argmax in padding, 2 attention
+  uint32_t err;      // bit 0 non-finite logits, 1 argmax in padding, 2 attention, 3 fused-attention wait timeout
   uint32_t n_prompt;
   uint32_t gen_cap;
   uint32_t err_step;  // gen index of the first finalize that saw an error bit (kNoStep: none)
@@ -76,8 +77,10 @@ __device__ __forceinline__ void embed_row(const uint8_t* __restrict__ embd, uint
 __global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
                              DevState* __restrict__ st, uint64_t* __restrict__ best,
                              float* __restrict__ out, const float* __restrict__ inv_freq, int half,
-                             float* __restrict__ rope_cs) {
+                             float* __restrict__ rope_cs, uint32_t* __restrict__ epoch) {
   const uint32_t tok = st->token;
+  // the step counter of the fused Q|K|V + attention launches
+  if (threadIdx.x == 0) *epoch += 1;
   if ((int)threadIdx.x < half) {
     const float th = (float)st->pos * inv_freq[threadIdx.x];
     rope_cs[threadIdx.x] = cosf(th);
@@ -86,6 +89,10 @@ __global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int 
   embed_row(embd, qt, hidden, tok, out);
   if (threadIdx.x == 0) *best = 0;
 }
+
+// Poll bound of the fused attention's wait: 2^13 polls of ~1 us, a few ms,
+// against a wait of a few us (the GEMV it waits for has no wait).
+constexpr uint32_t kSyncSpinLimit = 1u << 13;
 
 struct AttnArgs {
   const float* q;      // raw Q projection [nq*HD]
@@ -110,6 +117,12 @@ struct AttnArgs {
   int row_stride;
   int8_t* qs;
   uint16_t* qsd;
+  // fused decode form: the GEMV's tagged Q|K|V rows ([nq*HD | nkv*HD |
+  // nkv*HD] 64-bit words: tag << 32 | fp32 bits) and the step counter; this
+  // layer's rows carry tag = *epoch * tag_mul + tag_add
+  const uint64_t* tagged;
+  const uint32_t* epoch;
+  uint32_t tag_mul, tag_add;
 };
 
 #ifndef ZG_ATTN_WAVES
@@ -166,26 +179,29 @@ __device__ __forceinline__ int attn_split_rows(int pos, int nsplit) {
   return (pos + 8 * nsplit) / (8 * nsplit) * 8;
 }
 
-template <int HD, bool PF>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
+// FUSED: the workgroup runs in the Q|K|V GEMV's launch (qkv_attn_kernel):
+// it issues its first round of K/V cache loads, then reads its Q row and
+// its KV head's K and V rows from the GEMV's tagged words (a.tagged) until
+// every word carries this step and layer's tag.  NP: passes per round.
+template <int HD, bool PF, int NP = ZG_ATTN_PASSES, bool FUSED = false>
+__device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int nq, int bz) {
   constexpr int F4 = HD / 4;            // float4 per head row
   constexpr int LPR = 8;                // lanes per row in the score layout
   constexpr int CPL = F4 / LPR;         // K float4 columns per lane
   constexpr int RPW = 64 / LPR;         // rows per wave per pass
   constexpr int NWV = kAttnWaves;
   constexpr int PASS = RPW * NWV;       // rows per pass
-  constexpr int NP = ZG_ATTN_PASSES;    // passes per round
   constexpr int ROUND = NP * PASS;      // rows per round
   constexpr int VPL = HD / 64;          // V dims per lane
   constexpr int HALF = HD / 2;
   typedef float vlane_t __attribute__((ext_vector_type(VPL)));
-  const int qh = blockIdx.x, sp = blockIdx.y, nq = gridDim.x;
+  static_assert(!(FUSED && PF), "the fused form is the decode step's");
   const int kvh = qh / a.g;
-  const int pos = PF ? a.pos0 + (int)blockIdx.z : (int)a.st->pos;
+  const int pos = PF ? a.pos0 + bz : (int)a.st->pos;
   if (PF) {
-    a.q += (size_t)blockIdx.z * a.row_stride;
-    a.qs += (size_t)blockIdx.z * a.row_stride;
-    a.qsd += (size_t)blockIdx.z * a.row_stride / 32;
+    a.q += (size_t)bz * a.row_stride;
+    a.qs += (size_t)bz * a.row_stride;
+    a.qsd += (size_t)bz * a.row_stride / 32;
   }
   const int slen = PF ? a.split_len : attn_split_rows(pos, a.nsplit);
   const int c0 = sp * slen;
@@ -227,23 +243,73 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       }
     }
   };
-  // prologue operands, then the first step's K/V loads
+  // prologue operands, then the first step's K/V loads (fused: the K/V
+  // loads first, then the wait for this head's Q|K|V rows, then those rows)
   const int hl = lane % HALF;
-  const float qx0 = a.q[qh * HD + hl], qx1 = a.q[qh * HD + hl + HALF];
+  float qx0 = 0.0f, qx1 = 0.0f;
   float kx0 = 0.0f, kx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f, cs0 = 0.0f, cs1 = 0.0f;
   vlane_t vnew = (vlane_t)(0.0f);
+  if (FUSED) {
+    load_round(0);
+    // wave 0 polls this head's Q row, its KV head's K and V rows (tagged
+    // words) until every tag is this step's, and parks the values in LDS
+    __shared__ __attribute__((aligned(16))) float qkv_s[3 * HD];
+    if (wave == 0) {
+      constexpr int NW = 3 * HD / 64;  // words per lane
+      const uint32_t ep = *a.epoch * a.tag_mul + a.tag_add;  // this step and layer's tag
+      const int nq_hd = nq * HD, kv_hd = a.nkv * HD;
+      const uint64_t* src[NW];
+#pragma unroll
+      for (int j = 0; j < NW; j++) {
+        const int e = lane + 64 * j;  // 0..3*HD-1: q | k | v
+        src[j] = e < HD ? a.tagged + qh * HD + e
+                 : e < 2 * HD ? a.tagged + nq_hd + kvh * HD + (e - HD)
+                              : a.tagged + nq_hd + kv_hd + kvh * HD + (e - 2 * HD);
+      }
+      uint64_t w[NW];
+      uint32_t spins = 0;
+      for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+          w[j] = __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // wrap-safe: the tags of earlier layers and steps are behind
+          ok = ok && (int)((uint32_t)(w[j] >> 32) - ep) >= 0;
+        }
+        if (__all(ok)) break;
+        if (++spins > kSyncSpinLimit) {
+          if (lane == 0) atomicOr(&a.st->err, 8u);
+          break;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NW; j++) qkv_s[lane + 64 * j] = __uint_as_float((uint32_t)w[j]);
+    }
+    __syncthreads();
+    qx0 = qkv_s[hl];
+    qx1 = qkv_s[hl + HALF];
+    kx0 = qkv_s[HD + hl];
+    kx1 = qkv_s[HD + hl + HALF];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) vnew[i] = qkv_s[2 * HD + VPL * lane + i];
+  } else {
+    qx0 = a.q[qh * HD + hl];
+    qx1 = a.q[qh * HD + hl + HALF];
+    if (!PF) {
+      kx0 = a.k[kvh * HD + hl];
+      kx1 = a.k[kvh * HD + hl + HALF];
+      vnew = reinterpret_cast<const vlane_t*>(a.v)[kvh * (HD / VPL) + lane];
+    }
+  }
   if (!PF) {
-    kx0 = a.k[kvh * HD + hl];
-    kx1 = a.k[kvh * HD + hl + HALF];
     qw0 = a.q_norm[hl];
     qw1 = a.q_norm[hl + HALF];
     kw0 = a.k_norm[hl];
     kw1 = a.k_norm[hl + HALF];
     cs0 = a.rope_cs[hl];
     cs1 = a.rope_cs[hl + HALF];
-    vnew = reinterpret_cast<const vlane_t*>(a.v)[kvh * (HD / VPL) + lane];
   }
-  load_round(0);
+  if (!FUSED) load_round(0);
 
   // QK-norm + RoPE of one head vector held as (x0, x1) = dims (l, l + HALF)
   // by lanes l < HALF; result into this wave's LDS row
@@ -373,6 +439,35 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       a.out[((size_t)sp * nq + qh) * HD + tid] = o;
       if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(M, L);
     }
+  }
+}
+
+template <int HD, bool PF>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
+  attn_split_body<HD, PF>(a, blockIdx.x, blockIdx.y, gridDim.x, blockIdx.z);
+}
+
+// Q|K|V GEMV and decode attention in one launch.  Workgroups 0..n_attn-1 are
+// the attention splits (query head b % nq, split b / nq), the rest the
+// one-batch strip GEMV (rmsnorm prologue, four strips: in_dim 2048, two
+// groups per batch).  The attention workgroups come first, so they are
+// dispatched first: they issue their K/V cache loads while the GEMV runs,
+// then poll the GEMV's rows, each stored once with this step and layer's
+// tag (the GEMV never waits, so every poll ends; it is also bounded).
+// One launch instead of two, and the attention's cache reads overlap the
+// GEMV.  A counter that every batch incremented serialised the 512 atomics
+// of a step on one line (19 vs 8.8 us for the two kernels).
+constexpr int kFusedAttnPasses = 2;
+
+template <uint32_t QT, int IL, int HD>
+__global__ __launch_bounds__(256) void qkv_attn_kernel(GemvArgs ga, AttnArgs aa, int n_attn) {
+  const int b = blockIdx.x;
+  if (b < n_attn) {
+    const int nq = n_attn / aa.nsplit;
+    attn_split_body<HD, false, kFusedAttnPasses, true>(aa, b % nq, b / nq, nq, 0);
+  } else {
+    gemv_strip_body<QT, PRO_RMSNORM, EPI_STORE, 2, 1024, false, IL, true, 4, false, true>(ga, 4, b - n_attn,
+                                                                                           (int)gridDim.x - n_attn);
   }
 }
 
@@ -721,6 +816,7 @@ struct ZLayer {
   bool qk_norm_v = false;                  // else Q4_K Q|K with the prologue, which leaves x' for V
   bool gu_kq = false;                      // else Q4_K gate|up with rmsnorm and SwiGLU in one launch
   bool o_merge = false;                    // the O GEMV merges the attention splits itself
+  bool qkv_attn = false;                   // Q|K|V GEMV and attention in one launch (qkv_attn_kernel)
 };
 
 struct zg_model {
@@ -741,6 +837,12 @@ struct zg_model {
   float* part_ml = nullptr;  // attention split (max, exp-sum) [nsplit][nq]
   uint64_t* best = nullptr;
   zg::DevState* st = nullptr;
+  // qkv_attn_kernel: the step counter (embed_kernel adds one per step;
+  // never reset while the model lives) and the Q|K|V rows as tagged 64-bit
+  // words (the counter of the step that stored the row << 32 | fp32 bits)
+  uint32_t* sync = nullptr;
+  uint64_t* qkv_tag = nullptr;
+  int cus = 0;  // compute units of the device
   uint32_t* prompt = nullptr;  // device prompt buffer
   size_t prompt_cap = 0;
   uint32_t* out_tokens = nullptr;
@@ -844,6 +946,64 @@ static zg_status head_argmax(zg_model* m, const float* x, hipStream_t st) {
                     d.rms_eps, st, kGemvStream);
 }
 
+// Layer l's Q|K|V GEMV (rmsnorm prologue) and decode attention as one
+// qkv_attn_kernel launch; aa holds the attention arguments.
+static zg_status run_qkv_attn(zg_model* m, uint32_t l, const ZLayer& L, AttnArgs aa, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  const int HD = (int)d.head_dim, nkv = (int)d.n_kv_heads, g = (int)(d.n_q_heads / d.n_kv_heads);
+  const size_t qd = (size_t)d.n_q_heads * HD, kvd = (size_t)nkv * HD;
+  GemvArgs ga{};
+  ga.nseg = 3;
+  ga.k = (int)d.hidden;
+  ga.x = m->hidden;
+  ga.norm_w = L.attn_norm;
+  ga.eps = d.rms_eps;
+  const uint8_t* w[3] = {L.q, L.k, L.v};
+  float* y[3] = {m->q, m->k, m->v};
+  const size_t n[3] = {qd, kvd, kvd};
+  uint32_t gb = 0;
+  for (int i = 0; i < 3; i++) {
+    ga.seg[i].w = w[i];
+    ga.seg[i].y = y[i];
+    ga.seg[i].resid = nullptr;
+    ga.seg[i].g_begin = gb;
+    ga.seg[i].row_lo = 0;
+    ga.seg[i].row_hi = (uint32_t)n[i];
+    gb += (uint32_t)(n[i] / 4);
+  }
+  ga.total_groups = gb;
+  // the GEMV's rows go to the tagged buffer only: [Q | K | V] 64-bit words
+  ga.seg[0].y = reinterpret_cast<float*>(m->qkv_tag);
+  ga.seg[1].y = reinterpret_cast<float*>(m->qkv_tag + qd);
+  ga.seg[2].y = reinterpret_cast<float*>(m->qkv_tag + qd + kvd);
+  // one tag per step and layer: the buffer is shared by the layers
+  ga.sync_epoch = m->sync;
+  ga.sync_mul = d.n_layers;
+  ga.sync_add = l;
+  aa.tagged = m->qkv_tag;
+  aa.epoch = m->sync;
+  aa.tag_mul = d.n_layers;
+  aa.tag_add = l;
+  const int n_attn = (int)d.n_q_heads * m->nsplit;
+  const dim3 grid((unsigned)(n_attn + gb / 2)), block(256);
+  const size_t shm = 2 * 4 * 2 * 16 * sizeof(float);  // the strip body's [2][4 waves][2 groups][16] partials
+  const uint32_t qt = L.qt[ZG_PROJ_Q], il = L.il[ZG_PROJ_Q];
+#define ZG_QKV_ATTN(QT, IL, HDV) hipLaunchKernelGGL((qkv_attn_kernel<QT, IL, HDV>), grid, block, shm, st, ga, aa, n_attn)
+  if (HD == 128) {
+    if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 128);
+    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 128);
+    else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 128);
+    else ZG_QKV_ATTN(Q8_0, 1, 128);
+  } else {
+    if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 64);
+    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 64);
+    else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 64);
+    else ZG_QKV_ATTN(Q8_0, 1, 64);
+  }
+#undef ZG_QKV_ATTN
+  return hip_check(m->ctx, hipGetLastError(), "qkv+attention launch");
+}
+
 // Record the per-token sequence on the context stream.  diag adds the
 // non-finite scans of a localisation replay (never captured).
 static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
@@ -852,7 +1012,7 @@ static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
   const int qd = (int)(d.n_q_heads * d.head_dim), kvd = (int)(d.n_kv_heads * d.head_dim);
   zg_ctx* ctx = m->ctx;
   hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, m->embd, d.embd_type, H, m->st, m->best, m->hidden,
-                     m->inv_freq, HD / 2, m->rope_cs);
+                     m->inv_freq, HD / 2, m->rope_cs, m->sync);
   zg_status s = hip_check(ctx, hipGetLastError(), "embed launch");
   if (s) return s;
   const float scale = 1.0f / sqrtf((float)HD);
@@ -873,25 +1033,6 @@ static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
           (s = scan(m->nf_buf, NF_ATTN_NORM_IN)))
         return s;
     }
-    FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, qt[ZG_PROJ_Q], il[ZG_PROJ_Q]},
-                       {L.k, m->k, (size_t)kvd, qt[ZG_PROJ_K], il[ZG_PROJ_K]},
-                       {L.v, m->v, (size_t)kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
-    if (L.qkv_one) {
-      if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
-    } else if (L.qkv_norm_each) {
-      for (const FusedDev& f : qkv)
-        if ((s = run_linear(ctx, m->hidden, f.w, f.y, H, f.n, f.qt, f.il, 0, f.n, EPI_STORE, nullptr, nullptr,
-                            PRO_RMSNORM, L.attn_norm, d.rms_eps, st)))
-          return s;
-    } else if (L.qk_norm_v) {
-      if ((s = run_kq_segs(ctx, m->hidden, qkv, 2, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, st, m->xn))) return s;
-      if ((s = run_linear(ctx, m->xn, qkv[2].w, qkv[2].y, H, qkv[2].n, qkv[2].qt, qkv[2].il, 0, qkv[2].n, EPI_STORE,
-                          nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
-        return s;
-    } else {
-      if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
-      if ((s = run_fused(ctx, m->xn, qkv, 3, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
-    }
     AttnArgs aa{};
     aa.q = m->q;
     aa.k = m->k;
@@ -909,10 +1050,33 @@ static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
     aa.nsplit = m->nsplit;
     aa.eps = d.rms_eps;
     aa.scale = scale;
-    const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnWaves * 64);
-    if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), ag, ab, 0, st, aa);
-    else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
-    if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
+    if (L.qkv_attn) {
+      if ((s = run_qkv_attn(m, l, L, aa, st))) return s;
+    } else {
+      FusedDev qkv[3] = {{L.q, m->q, (size_t)qd, qt[ZG_PROJ_Q], il[ZG_PROJ_Q]},
+                         {L.k, m->k, (size_t)kvd, qt[ZG_PROJ_K], il[ZG_PROJ_K]},
+                         {L.v, m->v, (size_t)kvd, qt[ZG_PROJ_V], il[ZG_PROJ_V]}};
+      if (L.qkv_one) {
+        if ((s = run_fused(ctx, m->hidden, qkv, 3, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, EPI_STORE, st))) return s;
+      } else if (L.qkv_norm_each) {
+        for (const FusedDev& f : qkv)
+          if ((s = run_linear(ctx, m->hidden, f.w, f.y, H, f.n, f.qt, f.il, 0, f.n, EPI_STORE, nullptr, nullptr,
+                              PRO_RMSNORM, L.attn_norm, d.rms_eps, st)))
+            return s;
+      } else if (L.qk_norm_v) {
+        if ((s = run_kq_segs(ctx, m->hidden, qkv, 2, H, PRO_RMSNORM, L.attn_norm, d.rms_eps, st, m->xn))) return s;
+        if ((s = run_linear(ctx, m->xn, qkv[2].w, qkv[2].y, H, qkv[2].n, qkv[2].qt, qkv[2].il, 0, qkv[2].n, EPI_STORE,
+                            nullptr, nullptr, PRO_PLAIN, nullptr, 0.0f, st)))
+          return s;
+      } else {
+        if ((s = model_rmsnorm(m, m->hidden, L.attn_norm, st))) return s;
+        if ((s = run_fused(ctx, m->xn, qkv, 3, H, PRO_PLAIN, nullptr, 0.0f, EPI_STORE, st))) return s;
+      }
+      const dim3 ag(d.n_q_heads, m->nsplit), ab(kAttnWaves * 64);
+      if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), ag, ab, 0, st, aa);
+      else hipLaunchKernelGGL((attn_split_kernel<64, false>), ag, ab, 0, st, aa);
+      if ((s = hip_check(ctx, hipGetLastError(), "attention launch"))) return s;
+    }
     // y += O * attention (y the hidden state, or the zeroed scan buffer)
     auto o_proj = [&](float* y) -> zg_status {
       if (L.o_merge)
@@ -1221,6 +1385,13 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->part_ml), (size_t)m->nsplit * d.n_q_heads * 2 * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->sync), sizeof(uint32_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->qkv_tag), (qd + 2 * kvd) * sizeof(uint64_t));
+  if (!s) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess || cus <= 0) cus = 256;
+    m->cus = cus;
+  }
   m->prompt_cap = d.max_ctx;
   m->out_cap = d.max_ctx;
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->prompt), m->prompt_cap * sizeof(uint32_t));
@@ -1264,6 +1435,15 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
                                                                  : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o))) ||
                    kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
       for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
+      // Q|K|V and attention in one launch: Q4_0 / Q8_0 of one type and
+      // layout on the one-launch strip path, in_dim 2048 (four strips, the
+      // attention's 256-thread workgroups), two-group batches that never
+      // straddle a KV head, and one batch per workgroup
+      const size_t groups = (qd + 2 * kvd) / 4;
+      L.qkv_attn = (fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM)) &&
+                   (qt[ZG_PROJ_Q] == ZG_Q4_0 || qt[ZG_PROJ_Q] == ZG_Q8_0) && il[ZG_PROJ_Q] == il[ZG_PROJ_K] &&
+                   il[ZG_PROJ_Q] == il[ZG_PROJ_V] && H == 2048 && (d.head_dim == 128 || d.head_dim == 64) &&
+                   groups / 2 <= (size_t)m->cus * 4;
     }
     m->head_norm = rmsnorm_fused_ok(d.head_type, d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
   }
@@ -1371,6 +1551,8 @@ static void localise_nonfinite(zg_model* m, uint32_t p_fail) {
 // before the LM head's).  p_fail: the position of the step at err_step.
 static zg_status state_status(zg_model* m, const DevState& h, uint32_t p_fail) {
   const uint32_t e = h.err_step != kNoStep ? h.err_first : h.err;
+  if ((h.err | e) & 8u)
+    return set_error(m->ctx, ZG_ERR_HIP, "qkv+attention: a completion wait timed out (step %u)", h.err_step);
   if (e & 5u) localise_nonfinite(m, p_fail);
   char at[kNfCap + 3] = "";
   if (m->nf_len) snprintf(at, sizeof at, " @%.*s", (int)m->nf_len, m->nf_detail);
