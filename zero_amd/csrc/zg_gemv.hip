@@ -446,6 +446,15 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
+#ifndef ZG_ONEB_PER_CU
+#define ZG_ONEB_PER_CU 4
+#endif
+#ifndef ZG_SWIGLU_GB
+#define ZG_SWIGLU_GB 2
+#endif
+#ifndef ZG_SWIGLU_DIG
+#define ZG_SWIGLU_DIG 0
+#endif
 #ifndef ZG_STRIP_TALL_GB
 #define ZG_STRIP_TALL_GB 4
 #endif
@@ -459,12 +468,12 @@ bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192;
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4>
 static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
-  constexpr bool DIG1 = PRO != PRO_Q8X && ZG_STRIP_DIG >= 2;  // one-batch launches
+  constexpr bool DIG1 = PRO != PRO_Q8X && (ZG_STRIP_DIG >= 2 || (EPI == EPI_SWIGLU && ZG_SWIGLU_DIG));  // one-batch
   constexpr bool DIGL = PRO != PRO_Q8X && ZG_STRIP_DIG >= 1;  // batch-loop launches
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
   const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
-  if (MAXT == 1024 && nbatch <= (size_t)cu_count() * 4) {
+  if (MAXT == 1024 && nbatch <= (size_t)cu_count() * ZG_ONEB_PER_CU) {
     // one batch per workgroup (every decode-sized launch): no batch loop
     if (S == 4)
       hipLaunchKernelGGL((gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, true, 4, DIG1>),
@@ -540,7 +549,7 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   // gate|up (SwiGLU): two items (a gate and an up group each) per batch,
   // 768 one-batch workgroups at Qwen3-1.7B's FFN (decode 1,326 vs 1,297
   // tok/s with one item per batch and a batch loop)
-  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, 2, 1024, IL>(a, S, nw, items, st);
+  if constexpr (EPI == EPI_SWIGLU) return launch_strip_gb<QT, PRO, EPI, ZG_SWIGLU_GB, 1024, IL>(a, S, nw, items, st);
   return launch_strip_gb<QT, PRO, EPI, 2, 1024, IL>(a, S, nw, items, st);
 }
 
@@ -560,9 +569,210 @@ static bool tall_path_ok(const GemvArgs& a) {
 #ifndef ZG_STREAM_STRIP
 #define ZG_STREAM_STRIP 1
 #endif
+#ifndef ZG_STREAM_IL
+#define ZG_STREAM_IL 3
+#endif
 static bool tall_stream_ok(const GemvArgs& a) {
   return a.nseg == 1 && (a.flags & kGemvStream) && a.k % 512 == 0 && a.k <= 2048 &&
          a.total_groups >= ZG_TALL_MIN_GROUPS;
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged strip GEMV for tall single-projection X4 launches, in_dim 2048.
+//
+// The strip kernel's per-lane loads span ~1.1 KB at a 72/136-byte stride;
+// here the workgroup streams each batch of G consecutive groups (G x 64
+// group-blocks, contiguous) into LDS with gfx950's direct global-to-LDS
+// 16-byte loads (global_load_lds_dwordx4: consecutive lanes, consecutive 16
+// bytes, no VGPR staging), double-buffered, and the lanes decode their
+// (block, row) pieces from LDS with the strip kernel's lane map (wave w =
+// strip w, lane (b, r)).  Every wave issues exactly ROUNDS loads per batch
+// (chunk indices clamped into the tensor, each buffer padded to whole
+// rounds), so one s_waitcnt count covers a batch.
+// ---------------------------------------------------------------------------
+template <uint32_t QT>
+__device__ __forceinline__ void lds_lane(LaneW<QT>& L, const uint8_t* gb, int r) {
+  constexpr int QW = StripGeom<QT>::QW;
+  const u32x2* p = reinterpret_cast<const u32x2*>(gb + 8 + 4 * QW * r);
+#pragma unroll
+  for (int i = 0; i < QW / 2; i++) {
+    const u32x2 v = p[i];
+    L.q[2 * i] = v.x;
+    L.q[2 * i + 1] = v.y;
+  }
+  L.d = *reinterpret_cast<const uint16_t*>(gb + 2 * r);
+}
+
+// Workgroup barrier after this wave's LDS reads and writes have completed
+// (its global loads may still be in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <uint32_t QT, int G>
+struct LdsGeom {
+  static constexpr int GS = 64 * StripGeom<QT>::GB;         // group stream bytes at in_dim 2048
+  static constexpr int ROUNDS = (G * GS / 16 + 255) / 256;  // 16-byte loads per thread per batch
+  static constexpr int BUF = ROUNDS * 4096;                 // buffer bytes (whole rounds)
+  static constexpr size_t SHM = 2 * (size_t)BUF + 2 * 4 * G * 16 * sizeof(float);
+};
+
+template <uint32_t QT, int PRO, int EPI, int G, bool STREAM>
+__global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
+  using Geo = LdsGeom<QT, G>;
+  constexpr int GBY = StripGeom<QT>::GB, GS = Geo::GS, ROUNDS = Geo::ROUNDS, BUF = Geo::BUF;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_stage[];  // [2][BUF] bytes, then [2][4][G][16] partials
+  float* part = reinterpret_cast<float*>(lds_stage + 2 * BUF);
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = lane >> 2, r = lane & 3;
+  const int kb = wave * 16 + b;
+  const int items = (int)a.total_groups;
+  const int nbatch = (items + G - 1) / G;
+  const size_t nchunk = (size_t)items * GS / 16;  // 16-byte chunks of the tensor
+  const uint8_t* w = a.seg[0].w;
+  // batch `batch` into buffer `buf`: chunk c of the batch (thread c % 256,
+  // round c / 256) from global chunk batch*G*GS/16 + c, clamped into the
+  // tensor (a clamped chunk lands in the padding or in a group whose
+  // result is dropped)
+  auto issue = [&](int batch, int buf) {
+    const size_t c0 = (size_t)batch * (G * GS / 16);
+#pragma unroll
+    for (int q = 0; q < ROUNDS; q++) {
+      const size_t c = min(c0 + (size_t)(q * 256 + (int)threadIdx.x), nchunk - 1);
+      __builtin_amdgcn_global_load_lds(
+          w + 16 * c,
+          (__attribute__((address_space(3))) void*)(lds_stage + buf * BUF + 16 * (q * 256 + wave * 64)), 16, 0,
+          STREAM ? 2 : 0);
+    }
+  };
+  float4 xb[2], gw[2];
+  const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
+  xb[0] = x4[r];
+  xb[1] = x4[4 + r];
+  if (PRO == PRO_RMSNORM) {
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+    gw[0] = g4[r];
+    gw[1] = g4[4 + r];
+  }
+  const int b0 = blockIdx.x, bstep = gridDim.x;
+  issue(b0, 0);
+  if (PRO == PRO_RMSNORM) {
+    float ssq = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) ssq += xb[c].x * xb[c].x + xb[c].y * xb[c].y + xb[c].z * xb[c].z + xb[c].w * xb[c].w;
+    ssq = wave_sum(ssq);
+    if (lane == 0) red[wave] = ssq;
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+      xb[c] = make_float4(xb[c].x * gw[c].x, xb[c].y * gw[c].y, xb[c].z * gw[c].z, xb[c].w * gw[c].w);
+  }
+  XDig xd;
+  const bool fp32 = __builtin_amdgcn_ballot_w64(xdig_quad(xb[0], xb[1], xd)) != 0;
+  uint64_t key = 0;
+  int i = 0;
+  for (int batch = b0; batch < nbatch; batch += bstep, i++) {
+    const int cur = i & 1;
+    const bool more = batch + bstep < nbatch;
+    if (more) {
+      issue(batch + bstep, cur ^ 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ROUNDS) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    // the batch's bytes are in LDS for every wave (a plain s_barrier: the
+    // compiler's workgroup fence would also wait for the next batch's
+    // loads, which are LDS writes to it)
+    lds_barrier();
+    float* pb = part + cur * 4 * G * 16;
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+      LaneW<QT> L;
+      lds_lane<QT>(L, lds_stage + cur * BUF + j * GS + kb * GBY, r);
+      float dot;
+      if (!fp32) {
+        dot = strip_dot_dig<QT>(L, xd);
+      } else {
+        float4 xf[8];
+        strip_x_block<PRO>(xf, a, nullptr, kb);
+        float t = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) t += (xf[c].x + xf[c].y) + (xf[c].z + xf[c].w);
+        dot = strip_dot<QT>(L, xf, (QT == Q4_0 ? -8.0f : -128.0f) * t);
+      }
+      const float v = row_sum4(dot);
+      if ((lane & 15) < 4) pb[(wave * G + j) * 16 + (lane >> 4) * 4 + r] = v;
+    }
+    lds_barrier();  // partials visible; every wave is done with this buffer
+    const int tt = threadIdx.x;
+    if (tt < G * 4) {
+      const int j = tt >> 2, rr = tt & 3;
+      const int item = batch * G + j;
+      if (item < items) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+          const float* q = pb + (st * G + j) * 16 + rr;
+          acc += (q[0] + q[4]) + (q[8] + q[12]);
+        }
+        if (PRO == PRO_RMSNORM) acc *= 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.k + a.eps);
+        const GemvSeg& sg = a.seg[0];
+        const uint32_t row = 4 * (uint32_t)item + (uint32_t)rr;
+        if (row >= sg.row_lo && row < sg.row_hi) {
+          if (EPI == EPI_RESID) {
+            sg.y[row] = sg.resid[row] + acc;
+          } else {
+            if (sg.y) sg.y[row] = acc;
+            if (EPI == EPI_ARGMAX && !(acc != acc)) {
+              const uint64_t kk = argmax_key(acc, row);
+              key = kk > key ? kk : key;
+            }
+          }
+        }
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
+  }
+}
+
+#ifndef ZG_LDS_TALL
+#define ZG_LDS_TALL 1
+#endif
+#ifndef ZG_LDS_G
+#define ZG_LDS_G 4
+#endif
+static bool lds_tall_ok(const GemvArgs& a) {
+  return ZG_LDS_TALL && (a.flags & kGemvStream) && a.nseg == 1 && a.k == 2048 &&
+         a.total_groups >= ZG_TALL_MIN_GROUPS;
+}
+
+template <uint32_t QT, int PRO, int EPI, bool STREAM>
+static hipError_t launch_lds(const GemvArgs& a, hipStream_t st) {
+  constexpr int G = ZG_LDS_G;
+  const size_t shm = LdsGeom<QT, G>::SHM;
+  static int resident = 0;
+  if (resident == 0) {
+    int n = 0;
+    if (hipFuncSetAttribute((const void*)gemv_lds_kernel<QT, PRO, EPI, G, STREAM>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_lds_kernel<QT, PRO, EPI, G, STREAM>, 256, shm) !=
+            hipSuccess ||
+        n <= 0)
+      n = 1;
+    resident = n;
+  }
+  const size_t nbatch = (a.total_groups + G - 1) / G;
+  const size_t cap = (size_t)cu_count() * resident;
+  const size_t grid = nbatch < cap ? nbatch : cap;
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemv_lds_kernel<QT, PRO, EPI, G, STREAM>), dim3((unsigned)grid), dim3(256), shm, st, a);
+  return hipGetLastError();
 }
 
 // Q4_0X4 takes the strip kernel (measured faster at every decode shape).
@@ -581,9 +791,15 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
     }
     return hipErrorInvalidValue;
   } else {
+    if constexpr ((PRO == PRO_PLAIN || PRO == PRO_RMSNORM) && (EPI == EPI_STORE || EPI == EPI_ARGMAX)) {
+      if (lds_tall_ok(a)) {
+        if (a.flags & kGemvStream) return launch_lds<QT, PRO, EPI, true>(a, st);
+        return launch_lds<QT, PRO, EPI, false>(a, st);
+      }
+    }
     if constexpr (QT == Q8_0 && (EPI == EPI_STORE || EPI == EPI_ARGMAX)) {
       if (tall_path_ok(a)) return launch_strip<QT, PRO, EPI>(a, st);
-      if (ZG_STREAM_STRIP && tall_stream_ok(a)) return launch_strip<QT, PRO, EPI, 3>(a, st);
+      if (ZG_STREAM_STRIP && tall_stream_ok(a)) return launch_strip<QT, PRO, EPI, ZG_STREAM_IL>(a, st);
     }
     if constexpr (QT == Q4_0) {
       if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);

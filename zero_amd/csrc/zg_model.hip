@@ -180,8 +180,8 @@ __device__ __forceinline__ int attn_split_rows(int pos, int nsplit) {
 }
 
 // FUSED: the workgroup runs in the Q|K|V GEMV's launch (qkv_attn_kernel):
-// it issues its first round of K/V cache loads, then reads its Q row and
-// its KV head's K and V rows from the GEMV's tagged words (a.tagged) until
+// it issues its first round of K/V cache loads, then each wave reads the
+// Q, K and V values it needs from the GEMV's tagged words (a.tagged) until
 // every word carries this step and layer's tag.  NP: passes per round.
 template <int HD, bool PF, int NP = ZG_ATTN_PASSES, bool FUSED = false>
 __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int nq, int bz) {
@@ -251,47 +251,39 @@ __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int 
   vlane_t vnew = (vlane_t)(0.0f);
   if (FUSED) {
     load_round(0);
-    // wave 0 polls this head's Q row, its KV head's K and V rows (tagged
-    // words) until every tag is this step's, and parks the values in LDS
-    __shared__ __attribute__((aligned(16))) float qkv_s[3 * HD];
-    if (wave == 0) {
-      constexpr int NW = 3 * HD / 64;  // words per lane
-      const uint32_t ep = *a.epoch * a.tag_mul + a.tag_add;  // this step and layer's tag
-      const int nq_hd = nq * HD, kv_hd = a.nkv * HD;
-      const uint64_t* src[NW];
+    // every wave polls the tagged words it needs itself (lane l: Q and K
+    // dims l, l + HALF, V dims VPL*l..) until each carries this step and
+    // layer's tag: no barrier and no LDS round trip on the way
+    const uint32_t ep = *a.epoch * a.tag_mul + a.tag_add;
+    const uint64_t* tq = a.tagged + qh * HD;
+    const uint64_t* tk = a.tagged + nq * HD + kvh * HD;
+    const uint64_t* tv = a.tagged + (nq + a.nkv) * HD + kvh * HD;
+    constexpr int NWD = 4 + VPL;
+    const uint64_t* src[NWD] = {tq + hl, tq + hl + HALF, tk + hl, tk + hl + HALF};
 #pragma unroll
-      for (int j = 0; j < NW; j++) {
-        const int e = lane + 64 * j;  // 0..3*HD-1: q | k | v
-        src[j] = e < HD ? a.tagged + qh * HD + e
-                 : e < 2 * HD ? a.tagged + nq_hd + kvh * HD + (e - HD)
-                              : a.tagged + nq_hd + kv_hd + kvh * HD + (e - 2 * HD);
+    for (int i = 0; i < VPL; i++) src[4 + i] = tv + VPL * lane + i;
+    uint64_t w[NWD];
+    uint32_t spins = 0;
+    for (;;) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < NWD; j++) {
+        w[j] = __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // wrap-safe: the tags of earlier layers and steps are behind
+        ok = ok && (int)((uint32_t)(w[j] >> 32) - ep) >= 0;
       }
-      uint64_t w[NW];
-      uint32_t spins = 0;
-      for (;;) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < NW; j++) {
-          w[j] = __hip_atomic_load(src[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          // wrap-safe: the tags of earlier layers and steps are behind
-          ok = ok && (int)((uint32_t)(w[j] >> 32) - ep) >= 0;
-        }
-        if (__all(ok)) break;
-        if (++spins > kSyncSpinLimit) {
-          if (lane == 0) atomicOr(&a.st->err, 8u);
-          break;
-        }
+      if (__all(ok)) break;
+      if (++spins > kSyncSpinLimit) {
+        if (lane == 0) atomicOr(&a.st->err, 8u);
+        break;
       }
-#pragma unroll
-      for (int j = 0; j < NW; j++) qkv_s[lane + 64 * j] = __uint_as_float((uint32_t)w[j]);
     }
-    __syncthreads();
-    qx0 = qkv_s[hl];
-    qx1 = qkv_s[hl + HALF];
-    kx0 = qkv_s[HD + hl];
-    kx1 = qkv_s[HD + hl + HALF];
+    qx0 = __uint_as_float((uint32_t)w[0]);
+    qx1 = __uint_as_float((uint32_t)w[1]);
+    kx0 = __uint_as_float((uint32_t)w[2]);
+    kx1 = __uint_as_float((uint32_t)w[3]);
 #pragma unroll
-    for (int i = 0; i < VPL; i++) vnew[i] = qkv_s[2 * HD + VPL * lane + i];
+    for (int i = 0; i < VPL; i++) vnew[i] = __uint_as_float((uint32_t)w[4 + i]);
   } else {
     qx0 = a.q[qh * HD + hl];
     qx1 = a.q[qh * HD + hl + HALF];
@@ -457,7 +449,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 // One launch instead of two, and the attention's cache reads overlap the
 // GEMV.  A counter that every batch incremented serialised the 512 atomics
 // of a step on one line (19 vs 8.8 us for the two kernels).
-constexpr int kFusedAttnPasses = 2;
+#ifndef ZG_FUSED_ATTN_PASSES
+#define ZG_FUSED_ATTN_PASSES 2
+#endif
+constexpr int kFusedAttnPasses = ZG_FUSED_ATTN_PASSES;
 
 template <uint32_t QT, int IL, int HD>
 __global__ __launch_bounds__(256) void qkv_attn_kernel(GemvArgs ga, AttnArgs aa, int n_attn) {
