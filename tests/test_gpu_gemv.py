@@ -111,6 +111,7 @@ GEMV_CASES = [
     (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
     (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
     (Q4_0, 4, 151936, 2048), # tall Q4_0X4: four groups per batch, batches looped over
+    (Q8_0, 4, 32776, 2048),  # tall Q8_0X4 at in_dim 2048: LDS-staged kernel, last batch of two groups
     # DeepSeek2 / Kimi K2 projections through linear_dispatch_avx512
     # (kernel/src/inference_avx512.rs:2101-2825): MLA kv_a_mqa, q_a, q_b,
     # the kv_b decompressions, o_proj and the MoE expert FFN, Q4_0 as GGUF
@@ -209,20 +210,21 @@ def test_row_ranges(ctx, zo, quant, il):
 
 
 def test_tall_q8_0_ranges(ctx, zo):
-    """Row ranges of a tall Q8_0X4 matrix (the LM head's strip path): rows
-    outside the range stay untouched, partial first and last groups."""
+    """Row ranges of tall Q8_0X4 matrices (the LM head's register strip and
+    LDS-staged paths): rows outside the range stay untouched, partial first
+    and last groups."""
     rng = np.random.default_rng(9)
-    rows, k = 32800, 1024
-    w = synth.weight(rng, Q8_0, rows, k, 4)
-    x = synth.activations(rng, k)
-    ctx.register(w, Q8_0, 4)
-    ref = zo.linear_range(x, w, k, rows, Q8_0, 4)
-    for s, e in ((0, rows), (1, 32799), (6, 32777)):
-        out = np.full(rows, -7.0, np.float32)
-        ctx.linear_range(x, w, out, k, rows, Q8_0, s, e)
-        assert np.all(out[:s] == -7.0) and np.all(out[e:] == -7.0)
-        assert rel_err(out[s:e], ref[s:e]) <= REL_TOL
-    ctx.clear()
+    for rows, k in ((32800, 1024), (32804, 2048)):  # register strip kernel; LDS-staged kernel
+        w = synth.weight(rng, Q8_0, rows, k, 4)
+        x = synth.activations(rng, k)
+        ctx.register(w, Q8_0, 4)
+        ref = zo.linear_range(x, w, k, rows, Q8_0, 4)
+        for s, e in ((0, rows), (1, rows - 1), (6, rows - 23)):
+            out = np.full(rows, -7.0, np.float32)
+            ctx.linear_range(x, w, out, k, rows, Q8_0, s, e)
+            assert np.all(out[:s] == -7.0) and np.all(out[e:] == -7.0)
+            assert rel_err(out[s:e], ref[s:e]) <= REL_TOL
+        ctx.clear()
 
 
 def _edge_activations(rng, k, kind):

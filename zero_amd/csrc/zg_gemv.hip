@@ -747,9 +747,17 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
 #ifndef ZG_LDS_G
 #define ZG_LDS_G 4
 #endif
+// Where the LDS-staged kernel is used (nontemporal loads): tall Q8_0X4
+// single projections (the LM head: 61.2 vs 64.2 us for the register strip
+// kernel's cache-allocating loads, 77 us for its nontemporal ones) and
+// streamed tall launches of either type.  Tall cache-allocating Q4_0X4
+// launches keep the register strip kernel (36.3 vs 38.1 us at 151936x2048),
+// and one-batch launches gain nothing from staging (C1 6144x2048: 4.8 vs
+// 3.5 us).
+template <uint32_t QT>
 static bool lds_tall_ok(const GemvArgs& a) {
-  return ZG_LDS_TALL && (a.flags & kGemvStream) && a.nseg == 1 && a.k == 2048 &&
-         a.total_groups >= ZG_TALL_MIN_GROUPS;
+  return ZG_LDS_TALL && a.nseg == 1 && a.k == 2048 && a.total_groups >= ZG_TALL_MIN_GROUPS &&
+         (QT == Q8_0 || (a.flags & kGemvStream));
 }
 
 template <uint32_t QT, int PRO, int EPI, bool STREAM>
@@ -792,10 +800,7 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
     return hipErrorInvalidValue;
   } else {
     if constexpr ((PRO == PRO_PLAIN || PRO == PRO_RMSNORM) && (EPI == EPI_STORE || EPI == EPI_ARGMAX)) {
-      if (lds_tall_ok(a)) {
-        if (a.flags & kGemvStream) return launch_lds<QT, PRO, EPI, true>(a, st);
-        return launch_lds<QT, PRO, EPI, false>(a, st);
-      }
+      if (lds_tall_ok<QT>(a)) return launch_lds<QT, PRO, EPI, true>(a, st);
     }
     if constexpr (QT == Q8_0 && (EPI == EPI_STORE || EPI == EPI_ARGMAX)) {
       if (tall_path_ok(a)) return launch_strip<QT, PRO, EPI>(a, st);
