@@ -632,13 +632,17 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
   const uint8_t* w = a.seg[0].w;
   // batch `batch` into buffer `buf`: chunk c of the batch (thread c % 256,
   // round c / 256) from global chunk batch*G*GS/16 + c, clamped into the
-  // tensor (a clamped chunk lands in the padding or in a group whose
-  // result is dropped)
+  // tensor (a clamped chunk lands in a group whose result is dropped); the
+  // padding after the batch re-reads the batch's own first chunks (lines
+  // this workgroup is fetching anyway, not the next batch's)
   auto issue = [&](int batch, int buf) {
-    const size_t c0 = (size_t)batch * (G * GS / 16);
+    constexpr int BC = G * GS / 16;  // chunks per batch
+    const size_t c0 = (size_t)batch * BC;
 #pragma unroll
     for (int q = 0; q < ROUNDS; q++) {
-      const size_t c = min(c0 + (size_t)(q * 256 + (int)threadIdx.x), nchunk - 1);
+      int cl = q * 256 + (int)threadIdx.x;
+      if (q * 256 + 255 >= BC) cl = cl >= BC ? cl - BC : cl;
+      const size_t c = min(c0 + (size_t)cl, nchunk - 1);
       __builtin_amdgcn_global_load_lds(
           w + 16 * c,
           (__attribute__((address_space(3))) void*)(lds_stage + buf * BUF + 16 * (q * 256 + wave * 64)), 16, 0,
