@@ -245,12 +245,14 @@ def _edge_activations(rng, k, kind):
 
 
 @pytest.mark.parametrize("kind", ["finite", "inf", "nan"])
-@pytest.mark.parametrize("quant,rows,k", [(Q4_0, 12288, 2048), (Q8_0, 32768, 2048)])
+@pytest.mark.parametrize("quant,rows,k", [(Q4_0, 12288, 2048), (Q4_0, 32768, 2048), (Q8_0, 32768, 2048)])
 def test_tall_integer_activation_edges(ctx, zo, quant, rows, k, kind):
     """Tall X4 launches take the activations as exact integers (three int8
-    digits per value, int32 dot chains).  Finite edge blocks stay within the
-    parity bar and as close to f64 as the oracle (x 4); non-finite inputs
-    give non-finite rows exactly where the oracle's do."""
+    digits per value, int32 dot chains): the register strip kernel's batch
+    loop (12288 rows) and the LDS-staged kernel (32768 rows).  Finite edge
+    blocks stay within the parity bar and as close to f64 as the oracle
+    (x 4); non-finite inputs give non-finite rows exactly where the
+    oracle's do."""
     rng = np.random.default_rng(rows + k + len(kind))
     w = synth.weight(rng, quant, rows, k, 4)
     x = _edge_activations(rng, k, kind)

@@ -748,16 +748,23 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
 #ifndef ZG_LDS_TALL
 #define ZG_LDS_TALL 1
 #endif
-#ifndef ZG_LDS_G
-#define ZG_LDS_G 4
-#endif
-// Where the LDS-staged kernel is used (nontemporal loads): tall Q8_0X4
-// single projections (the LM head: 61.2 vs 64.2 us for the register strip
-// kernel's cache-allocating loads, 77 us for its nontemporal ones) and
-// streamed tall launches of either type.  Tall cache-allocating Q4_0X4
-// launches keep the register strip kernel (36.3 vs 38.1 us at 151936x2048),
-// and one-batch launches gain nothing from staging (C1 6144x2048: 4.8 vs
-// 3.5 us).
+// Groups per batch: Q4_0 8 (36,864 bytes, nine whole rounds, two
+// workgroups per CU), Q8_0 4 (34,816 bytes in nine rounds, two workgroups
+// per CU; eight groups leave one workgroup per CU: 65.2 vs 58.8 us for the
+// LM head)
+template <uint32_t QT>
+constexpr int lds_groups() {
+  return QT == Q4_0 ? 8 : 4;
+}
+// The LDS-staged kernel (nontemporal loads) takes tall Q8_0X4 single
+// projections at in_dim 2048 (the LM head: 58.8 us against 64.2 us for the
+// register strip kernel's cache-allocating loads and 77 us for its
+// nontemporal ones) and streamed tall launches of either type (inside the
+// decode step its nontemporal read leaves the KV cache in the caches).
+// Tall Q4_0X4 measured within noise of the register strip kernel (35.6 -
+// 37.6 vs 36.3 us at 151936x2048; 49152x2048 slower, 14.2 vs 13.2 us) and
+// keeps it; one-batch launches gain nothing from staging (C1 6144x2048:
+// 4.8 vs 3.5 us).
 template <uint32_t QT>
 static bool lds_tall_ok(const GemvArgs& a) {
   return ZG_LDS_TALL && a.nseg == 1 && a.k == 2048 && a.total_groups >= ZG_TALL_MIN_GROUPS &&
@@ -766,7 +773,7 @@ static bool lds_tall_ok(const GemvArgs& a) {
 
 template <uint32_t QT, int PRO, int EPI, bool STREAM>
 static hipError_t launch_lds(const GemvArgs& a, hipStream_t st) {
-  constexpr int G = ZG_LDS_G;
+  constexpr int G = lds_groups<QT>();
   const size_t shm = LdsGeom<QT, G>::SHM;
   static int resident = 0;
   if (resident == 0) {
