@@ -102,7 +102,9 @@ GEMV_CASES = [
     (Q8_0, 4, 8, 32),
     (Q4_0, 1, 7, 256),       # plain layouts
     (Q8_0, 1, 100, 512),
-    (Q4K, 1, 64, 4096),
+    (Q4K, 1, 64, 4096),      # Q4_K strip path: 16 groups of four rows
+    (Q4K, 1, 36, 6144),      # twelve strips per row (the down shape's in_dim)
+    (Q4K, 1, 2052, 2048),    # 513 groups: two or three groups per workgroup, a partial last one
     (Q6K, 1, 48, 1024),
     (Q4K, 1, 33, 2304),      # 9 superblocks per row: a partial 8-superblock step
     (Q6K, 1, 17, 2304),      # odd superblocks per row: unaligned Q6_K row starts
@@ -193,7 +195,7 @@ def test_gemv_device_api_matches_host_api(ctx, zo):
     ctx.clear()
 
 
-@pytest.mark.parametrize("quant,il", [(Q4_0, 4), (Q8_0, 4), (Q4_0, 1), (Q8_0, 1), (Q6K, 1)])
+@pytest.mark.parametrize("quant,il", [(Q4_0, 4), (Q8_0, 4), (Q4_0, 1), (Q8_0, 1), (Q4K, 1), (Q6K, 1)])
 def test_row_ranges(ctx, zo, quant, il):
     rng = np.random.default_rng(2)
     rows, k = 40, 1024

@@ -339,6 +339,24 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
     return hip_check(ctx, launch_gemv_plain(a, qt, pro, epi, st), "gemv plain launch");
   }
+  if (pro == PRO_PLAIN && (epi == EPI_STORE || epi == EPI_RESID) && q4k_strip_ok(qt, il, k, n, w, x)) {
+    // Q4_K rows in fours through the strip kernel
+    const size_t rbytes = (k / 256) * 144;
+    const size_t g0 = start / 4, g1 = (end + 3) / 4;
+    GemvArgs a{};
+    a.nseg = 1;
+    a.k = (int)k;
+    a.total_groups = (uint32_t)(g1 - g0);
+    a.x = x;
+    a.flags = gemv_flags;
+    a.seg[0].w = w + 4 * g0 * rbytes;
+    a.seg[0].y = y ? y + 4 * g0 : nullptr;
+    a.seg[0].resid = resid ? resid + 4 * g0 : nullptr;
+    a.seg[0].g_begin = 0;
+    a.seg[0].row_lo = (uint32_t)(start - 4 * g0);
+    a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
+    return hip_check(ctx, launch_gemv_plain(a, qt, pro, epi, st), "gemv Q4_K strip launch");
+  }
   if (pro == PRO_RMSNORM && (epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX) && aligned16(norm_w) &&
       kq_fused_ok(qt, il, k, w, x)) {
     // Q4_K strip kernel with the rmsnorm prologue
@@ -396,7 +414,9 @@ bool zg::fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k
 bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro) {
   bool ok = nseg >= 1 && nseg <= 3 && (pro == PRO_PLAIN || pro == PRO_RMSNORM);
   for (size_t i = 0; i < nseg && ok; i++)
-    ok = plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
+    ok = (plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) ||
+          q4k_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x)) &&
+         segs[i].qt == segs[0].qt;
   return ok;
 }
 
@@ -521,6 +541,24 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
 // split merge in the strip kernel's prologue.
 zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd,
                          const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st) {
+  if (q4k_strip_ok(qt, il, k, n, w, part_o) && attn_merge_strip_ok(nsplit, hd, k)) {
+    // Q4_K rows in fours through the strip kernel, the merge in its prologue
+    GemvArgs a{};
+    a.nseg = 1;
+    a.k = (int)k;
+    a.total_groups = (uint32_t)(n / 4);
+    a.x = part_o;
+    a.attn_ml = part_ml;
+    a.attn_nsplit = nsplit;
+    a.attn_hd = hd;
+    a.seg[0].w = w;
+    a.seg[0].y = y;
+    a.seg[0].resid = y;
+    a.seg[0].g_begin = 0;
+    a.seg[0].row_lo = 0;
+    a.seg[0].row_hi = (uint32_t)n;
+    return hip_check(ctx, launch_gemv_plain(a, qt, PRO_ATTN, EPI_RESID, st), "attention-merge gemv Q4_K strip launch");
+  }
   if (qt == ZG_Q4K) {
     if (!kq_attn_o_ok(qt, il, k, nsplit, hd, w, part_o))
       return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge Q4_K GEMV: in_dim %zu not supported", k);

@@ -344,6 +344,50 @@ __device__ __forceinline__ float deq_elem(const BlockRef& br, uint32_t qt, float
   }
 }
 
+// Q4_K helpers shared by the Q4_K kernels and the strip GEMV.
+// sum_i q_i x_i over 4 dwords of unsigned bytes (q in 0..255) against
+// 16 consecutive x values.
+__device__ __forceinline__ float u8_dot16(const uint32_t* q, const float4* x) {
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t v = q[c];
+    const float4 xv = x[c];
+    float& s = (c & 1) ? s1 : s0;
+    s = fmaf(xv.x, (float)(v & 0xFFu), s);
+    s = fmaf(xv.y, (float)((v >> 8) & 0xFFu), s);
+    s = fmaf(xv.z, (float)((v >> 16) & 0xFFu), s);
+    s = fmaf(xv.w, (float)(v >> 24), s);
+  }
+  return s0 + s1;
+}
+
+// get_scale_min_k4 (dequant.rs:75-85) for the lane's sub-blocks 2j and 2j+1,
+// branch-free over the wave (j differs between lanes): for j < 2 the low six
+// bits of bytes 2j, 2j+1 of w0 (scales) and w1 (mins); for j >= 2 the low /
+// high nibbles of bytes 2j-4, 2j-3 of w2, with the top two bits of the same
+// bytes of w0 / w1 above them.
+__device__ __forceinline__ void q4k_lane_scales(uint32_t w0, uint32_t w1, uint32_t w2, int j, uint32_t& sA,
+                                                uint32_t& sB, uint32_t& nA, uint32_t& nB) {
+  const uint32_t sh = 16u * (uint32_t)(j & 1);
+  const bool lowj = j < 2;
+  const uint32_t a = w0 >> sh, b = w1 >> sh, c = w2 >> sh;
+  const uint32_t wid = lowj ? 6u : 4u;
+  const uint32_t hmask = lowj ? 0u : ~0u;
+  const uint32_t ls = lowj ? a : c, lm = lowj ? b : (c >> 4);
+  const uint32_t hs = a & hmask, hm = b & hmask;
+  sA = __builtin_amdgcn_ubfe(ls, 0, wid) | (__builtin_amdgcn_ubfe(hs, 6, 2) << 4);
+  sB = __builtin_amdgcn_ubfe(ls, 8, wid) | (__builtin_amdgcn_ubfe(hs, 14, 2) << 4);
+  nA = __builtin_amdgcn_ubfe(lm, 0, wid) | (__builtin_amdgcn_ubfe(hm, 6, 2) << 4);
+  nB = __builtin_amdgcn_ubfe(lm, 8, wid) | (__builtin_amdgcn_ubfe(hm, 14, 2) << 4);
+}
+
+// The superblock's d and dmin through the hardware fp16 conversion: exact
+// for every finite value; a NaN scale gives a NaN row either way.
+__device__ __forceinline__ float kq_half(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+}
+
 // ---------------------------------------------------------------------------
 // Activations as exact integers for v_dot4_i32_i8.
 //

@@ -446,6 +446,11 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
+// Q4_K single projections take the strip kernel
+#ifndef ZG_Q4K_STRIP
+#define ZG_Q4K_STRIP 1
+#endif
+
 #ifndef ZG_ONEB_PER_CU
 #define ZG_ONEB_PER_CU 4
 #endif
@@ -465,6 +470,9 @@ bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192;
 #ifndef ZG_STRIP_TALL_GB
 #define ZG_STRIP_TALL_GB 4
 #endif
+#ifndef ZG_Q4K_TALL_GB
+#define ZG_Q4K_TALL_GB 4
+#endif
 
 // Which strip launches take the integer activation form: 0 none, 1 the
 // batch-loop launches, 2 every launch with fp32 activations.
@@ -476,7 +484,11 @@ template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 
 static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t items, hipStream_t st) {
   constexpr int PARTS = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr bool DIG1 = PRO != PRO_Q8X && (ZG_STRIP_DIG >= 2 || (EPI == EPI_SWIGLU && ZG_SWIGLU_DIG));  // one-batch
-  constexpr bool DIGL = PRO != PRO_Q8X && ZG_STRIP_DIG >= 1;  // batch-loop launches
+  // batch-loop launches (four groups per batch spill under the 1024-thread bound)
+  constexpr bool DIGL = PRO != PRO_Q8X && ZG_STRIP_DIG >= 1 && (MAXT < 1024 || GBATCH < 4);
+  // a workgroup never exceeds the kernel's thread bound (the compiler sized
+  // its registers and index arithmetic for it)
+  if (nw * 64 > MAXT) return hipErrorInvalidConfiguration;
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
   const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
@@ -535,9 +547,17 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
   // work; with argmax epilogues two batches in flight only fit the
   // 1024-thread register budget at two groups per batch
   const size_t wps = nw / S;
-  if constexpr (QT == Q4_0 && (EPI == EPI_STORE || EPI == EPI_RESID) && PRO != PRO_ATTN) {
-    if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps)
-      return launch_strip_gb<QT, PRO, EPI, ZG_STRIP_TALL_GB, (ZG_STRIP_DIG >= 1 ? 256 : 1024), IL>(a, S, nw, items, st);
+  if constexpr ((QT == Q4_0 || QT == Q4K) && (EPI == EPI_STORE || EPI == EPI_RESID) && PRO != PRO_ATTN) {
+    // tall launches: the integer activation form needs more than the 128
+    // registers of a 1024-thread bound, so its workgroups (one wave per
+    // strip) take the tightest bound that holds them; past eight strips
+    // the fp32 form
+    if (items > (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * wps) {
+      constexpr int TGB = QT == Q4K ? ZG_Q4K_TALL_GB : ZG_STRIP_TALL_GB;
+      if (nw <= 4) return launch_strip_gb<QT, PRO, EPI, TGB, (ZG_STRIP_DIG >= 1 ? 256 : 1024), IL>(a, S, nw, items, st);
+      if (nw <= 8) return launch_strip_gb<QT, PRO, EPI, TGB, (ZG_STRIP_DIG >= 1 ? 512 : 1024), IL>(a, S, nw, items, st);
+      return launch_strip_gb<QT, PRO, EPI, TGB, 1024, IL>(a, S, nw, items, st);
+    }
     // one-batch launches: groups per wave ~ items / (2 CUs), 1 to 3, so
     // that every CU gets about two workgroups (C1 6144x2048: three groups
     // per wave, 512 workgroups of four waves, 3.47 vs 3.56 us at two in a
@@ -887,9 +907,38 @@ static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStre
   return hipErrorInvalidValue;
 }
 
+// Q4_K rows through the strip kernel (lane units of 32 elements, four rows
+// per group): in_dim a multiple of 512 up to 8192, rows in fours, weights
+// and x 16-byte aligned.
+bool q4k_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
+  if (!ZG_Q4K_STRIP || qt != Q4K || il != 1 || !strip_path_ok((int)k) || n % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+    return false;
+  // one-batch launches only (the tall batch-loop form measured slower than
+  // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096)
+  const int S = (int)k / 512, nw = S >= 3 ? S : 4;  // S >= 1 here
+  return ZG_Q4K_STRIP >= 2 || n / 4 <= (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * (size_t)(nw / S);
+}
+
+// The strip kernel's merge prologue takes these attention splits.
+bool attn_merge_strip_ok(int nsplit, int hd, size_t k) {
+  return nsplit >= 1 && nsplit <= kAttnSplits && hd > 0 && hd % 8 == 0 && k % (size_t)hd == 0;
+}
+
+static hipError_t dispatch_q4k_strip(const GemvArgs& a, int pro, int epi, hipStream_t st) {
+  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_strip<Q4K, PRO_PLAIN, EPI_STORE, 1>(a, st);
+  if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_strip<Q4K, PRO_PLAIN, EPI_RESID, 1>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_strip<Q4K, PRO_RMSNORM, EPI_STORE, 1>(a, st);
+  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_strip<Q4K, PRO_RMSNORM, EPI_SWIGLU, 1>(a, st);
+  if (pro == PRO_ATTN && epi == EPI_RESID && attn_merge_strip_ok(a.attn_nsplit, a.attn_hd, (size_t)a.k))
+    return launch_strip<Q4K, PRO_ATTN, EPI_RESID, 1>(a, st);
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv_plain(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st) {
   if (qt == Q4_0) return dispatch_plain_qt<Q4_0>(a, pro, epi, st);
   if (qt == Q8_0) return dispatch_plain_qt<Q8_0>(a, pro, epi, st);
+  if (qt == Q4K) return dispatch_q4k_strip(a, pro, epi, st);
   return hipErrorInvalidValue;
 }
 

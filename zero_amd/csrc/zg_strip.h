@@ -98,6 +98,34 @@ struct LaneW {
   uint32_t d;
 };
 
+// Q4_K (row-major 144-byte superblocks: fp16 d, fp16 dmin, 12 bytes of
+// 6-bit scales and mins, 128 quant bytes; dequant.rs:75-124).  A lane unit
+// is 32 elements of one row: the 16 quant bytes [32 j + 16 h, +16) of a
+// superblock, whose low nibbles are run A (elements 64 j + 16 h + i, in
+// sub-block 2 j) and high nibbles run B (32 elements later, sub-block
+// 2 j + 1), with the superblock's 16-byte header.  Unit kb of a row is
+// (superblock kb / 8, j = (kb / 2) % 4, h = kb % 2), so the 16 units of a
+// 512-element strip cover it once, and run B sits where the second half of
+// a 32-element block does for the other types.
+template <>
+struct LaneW<Q4K> {
+  uint32_t q[4];
+  uint32_t h[4];
+};
+
+// Element offset of lane unit kb's first half, and of its second half
+// from there.
+template <uint32_t QT>
+__device__ __forceinline__ int unit_x0(int kb) {
+  if (QT == Q4K) return 256 * (kb >> 3) + 64 * ((kb >> 1) & 3) + 16 * (kb & 1);
+  return 32 * kb;
+}
+template <uint32_t QT>
+constexpr int unit_hoff() {
+  return QT == Q4K ? 32 : 16;
+}
+
+
 // Quant loads of the strip kernels: 16-byte loads (8-byte aligned) or
 // 8-byte loads, nontemporal or not.  The scale load always uses the same
 // cache policy as the quant loads: the two share cache lines.
@@ -181,6 +209,16 @@ __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int
   L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk + 2 * r));
 }
 
+// Q4_K unit loads: the header and the unit's quant bytes, 16 bytes each
+// (16-byte aligned).  Cache-allocating unless NT.
+template <bool NT>
+__device__ __forceinline__ void strip_load_q4k(LaneW<Q4K>& L, const uint8_t* sb, int jh) {
+  const u32x4 h = ZG_LD_POL(NT, reinterpret_cast<const u32x4*>(sb));
+  const u32x4 q = ZG_LD_POL(NT, reinterpret_cast<const u32x4*>(sb + 16 + 32 * (jh >> 1) + 16 * (jh & 1)));
+  L.h[0] = h.x, L.h[1] = h.y, L.h[2] = h.z, L.h[3] = h.w;
+  L.q[0] = q.x, L.q[1] = q.y, L.q[2] = q.z, L.q[3] = q.w;
+}
+
 // The block scale through the hardware fp16 conversion: exact for every
 // finite value, subnormals and infinities; a NaN scale gives a NaN row
 // either way (only a signalling NaN's payload would differ from
@@ -244,6 +282,53 @@ __device__ __forceinline__ float strip_dot_q8x(const LaneW<QT>& L, const uint32_
   return (half_bits_to_f32(L.d) * dx) * (float)isum;
 }
 
+// Q4_K unit with fp32 activations, kq_dot's arithmetic: run A = xb[0..3],
+// run B = xb[4..7], sa and sb their sums; j the unit's sub-block pair.
+__device__ __forceinline__ float strip_dot_q4k(const LaneW<Q4K>& L, const float4* xb, float sa, float sb, int j) {
+  const float d = kq_half(L.h[0]), dmin = kq_half(L.h[0] >> 16);
+  uint32_t iA, iB, nA, nB;
+  q4k_lane_scales(L.h[1], L.h[2], L.h[3], j, iA, iB, nA, nB);
+  // high nibbles stay in place (16 x the value): the 1/16 goes into the
+  // sub-block scale (exact)
+  uint32_t lo[4], hi[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    lo[c] = opaque_u32(L.q[c] & 0x0F0F0F0Fu);
+    hi[c] = opaque_u32(L.q[c] & 0xF0F0F0F0u);
+  }
+  const float sA = u8_dot16(lo, xb);
+  const float sB = u8_dot16(hi, xb + 4);
+  float acc = (d * (float)iA) * sA;
+  acc = fmaf(-(dmin * (float)nA), sa, acc);
+  acc = fmaf((d * 0.0625f) * (float)iB, sB, acc);
+  return fmaf(-(dmin * (float)nB), sb, acc);
+}
+
+// The same unit against integer-digit activations (XDig of the unit's 32
+// values, run A first): per run the three digit chains of sum_i q_i V_i
+// (|.| <= 16 * 15 * 127 * 2^14 < 2^31, recombined in int32), then
+// d * M / (127 * 2^14) times the scaled run sums, minus the min terms on
+// the fp32 run sums.
+__device__ __forceinline__ float strip_dot_dig_q4k(const LaneW<Q4K>& L, const XDig& X, float sa, float sb, int j) {
+  const float d = kq_half(L.h[0]), dmin = kq_half(L.h[0] >> 16);
+  uint32_t iA, iB, nA, nB;
+  q4k_lane_scales(L.h[1], L.h[2], L.h[3], j, iA, iB, nA, nB);
+  int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int lo = (int)(L.q[c] & 0x0F0F0F0Fu), hi = (int)((L.q[c] >> 4) & 0x0F0F0F0Fu);
+    a0 = __builtin_amdgcn_sdot4(lo, (int)X.dg[0][c], a0, false);
+    a1 = __builtin_amdgcn_sdot4(lo, (int)X.dg[1][c], a1, false);
+    a2 = __builtin_amdgcn_sdot4(lo, (int)X.dg[2][c], a2, false);
+    b0 = __builtin_amdgcn_sdot4(hi, (int)X.dg[0][4 + c], b0, false);
+    b1 = __builtin_amdgcn_sdot4(hi, (int)X.dg[1][4 + c], b1, false);
+    b2 = __builtin_amdgcn_sdot4(hi, (int)X.dg[2][4 + c], b2, false);
+  }
+  const float IA = (float)((a0 << 14) + (a1 << 7) + a2), IB = (float)((b0 << 14) + (b1 << 7) + b2);
+  const float acc = fmaf((float)iA, IA, (float)iB * IB) * (d * X.sinv);
+  return fmaf(-dmin, fmaf((float)nA, sa, (float)nB * sb), acc);
+}
+
 // partial sums over the 4 lanes of each DPP row that share lane & 3
 // (lane l of a row holds block l >> 2; row_ror:n reads lane l - n mod 16):
 // lane l < 4 ends with (P0 + P3) + (P2 + P1) over that row's blocks P0..P3.
@@ -292,20 +377,25 @@ __device__ __forceinline__ float quad_sum(float v) {
 // The 32 activations of K-block kb as the prologue forms them: from x, times
 // the rmsnorm gain (the 1/rms factor is applied to the row totals), or from
 // the merged attention vector in LDS (xs).
-template <int PRO>
+// (Q4_K: the unit's runs A and B, as xf[0..3] and xf[4..7].)
+template <int PRO, uint32_t QT = Q4_0>
 __device__ __forceinline__ void strip_x_block(float4 (&xf)[8], const GemvArgs& a, const float* xs, int kb) {
-  const float4* x4 = reinterpret_cast<const float4*>((PRO == PRO_ATTN ? xs : a.x) + 32 * kb);
+  constexpr int H4 = unit_hoff<QT>() / 4;
+  const int x0 = unit_x0<QT>(kb);
+  const float4* x4 = reinterpret_cast<const float4*>((PRO == PRO_ATTN ? xs : a.x) + x0);
 #pragma unroll
-  for (int c = 0; c < 8; c++) xf[c] = x4[c];
+  for (int c = 0; c < 8; c++) xf[c] = x4[c < 4 ? c : c - 4 + H4];
   if (PRO == PRO_RMSNORM) {
-    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + x0);
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-      const float4 g = g4[c];
+      const float4 g = g4[c < 4 ? c : c - 4 + H4];
       xf[c] = make_float4(xf[c].x * g.x, xf[c].y * g.y, xf[c].z * g.z, xf[c].w * g.w);
     }
   }
 }
+
+__device__ __forceinline__ float f4_sum(float4 v) { return (v.x + v.y) + (v.z + v.w); }
 
 // IL 4: X4 group-blocks (IL 3: the same with nontemporal loads); IL 1:
 // plain row-major blocks (IL 2: the same with nontemporal loads), a "group"
@@ -326,6 +416,7 @@ template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 
           bool ONEB = false, int SC = 0, bool DIG = false, bool SIG = false>
 __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int bid, int nblk) {
   static_assert(!DIG || PRO != PRO_Q8X, "Q8_0 activations have their own integer form");
+  static_assert(QT != Q4K || ((IL == 1 || IL == 2) && PRO != PRO_Q8X), "Q4_K: row-major superblocks, fp32 x");
   static_assert(!SIG || EPI == EPI_STORE, "tagged stores replace plain stores");
   const int S = SC ? SC : S_rt;
   constexpr int GBY = StripGeom<QT>::GB;
@@ -377,7 +468,12 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
         const GemvSeg sg = locate(min(base + j, items - 1), p, lg);
         // the group's start is wave-uniform (scalar registers), the lane's
         // byte offset inside it a 32-bit vector offset
-        if (IL == 4 || IL == 3)
+        if constexpr (QT == Q4K)
+          // row 4 lg + r, superblock kb / 8 (rows of nb / 8 superblocks)
+          strip_load_q4k<IL == 2>(L[j][p], sg.w + (size_t)(4 * lg + (uint32_t)r) * (size_t)(nb * 18) +
+                                               (uint32_t)((kb >> 3) * 144),
+                                  kb & 7);
+        else if constexpr (IL == 4 || IL == 3)
           strip_load<QT, GBATCH == 4, IL == 3>(L[j][p], sg.w + (size_t)lg * (size_t)(nb * GBY) + (uint32_t)(kb * GBY),
                                                r);
         else
@@ -408,13 +504,14 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
     // this lane's quarter of the x-block (and of the rmsnorm gain, loaded
     // with x ahead of the barrier that waits for the sum of squares); the
     // quad shares its quarters through DPP below
-    const float4* x4 = reinterpret_cast<const float4*>(a.x + 32 * kb);
+    constexpr int H4 = unit_hoff<QT>() / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + unit_x0<QT>(kb));
     xb[0] = x4[r];
-    xb[1] = x4[4 + r];
+    xb[1] = x4[H4 + r];
     if (PRO == PRO_RMSNORM) {
-      const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + 32 * kb);
+      const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + unit_x0<QT>(kb));
       gw[0] = g4[r];
-      gw[1] = g4[4 + r];
+      gw[1] = g4[H4 + r];
     }
   }
   // two batches in flight: this workgroup's first and second
@@ -441,14 +538,15 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
       reinterpret_cast<float4*>(xs + e0)[1] = m1;
     }
     __syncthreads();
-    const float4* x4 = reinterpret_cast<const float4*>(xs + 32 * kb);
+    constexpr int H4 = unit_hoff<QT>() / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(xs + unit_x0<QT>(kb));
     if (DIG) {
       // the lane's quarter, as the global prologues load it
       xb[0] = x4[r];
-      xb[1] = x4[4 + r];
+      xb[1] = x4[H4 + r];
     } else {
 #pragma unroll
-      for (int c = 0; c < 8; c++) xb[c] = x4[c];
+      for (int c = 0; c < 8; c++) xb[c] = x4[c < 4 ? c : c - 4 + H4];
     }
   }
   if (PRO == PRO_RMSNORM) {
@@ -475,9 +573,15 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
     }
   }
   float mterm = 0.0f;
+  float xsa = 0.0f, xsb = 0.0f;  // Q4_K: the unit's run sums
   int sx = 0;
   XDig xd;
   bool fp32 = !DIG;  // wave-uniform: this wave decodes with fp32 activations
+  if (QT == Q4K && !(PRO == PRO_ATTN && !DIG)) {
+    // the quad's quarter sums: run A from the lo quarters, run B from the hi ones
+    xsa = quad_sum(f4_sum(xb[0]));
+    xsb = quad_sum(f4_sum(xb[1]));
+  }
   if (DIG) {
     const bool bad = xdig_quad(xb[0], xb[1], xd);
     fp32 = __builtin_amdgcn_ballot_w64(bad) != 0;
@@ -493,6 +597,10 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
       t = 0.0f;
 #pragma unroll
       for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
+      if (QT == Q4K) {
+        xsa = (f4_sum(xb[0]) + f4_sum(xb[1])) + (f4_sum(xb[2]) + f4_sum(xb[3]));
+        xsb = (f4_sum(xb[4]) + f4_sum(xb[5])) + (f4_sum(xb[6]) + f4_sum(xb[7]));
+      }
     } else {
       // the quad's four quarters: block sum, then the whole block in every lane
       t = quad_sum(((xb[0].x + xb[0].y) + (xb[0].z + xb[0].w)) + ((xb[1].x + xb[1].y) + (xb[1].z + xb[1].w)));
@@ -522,7 +630,20 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
           float dot;
-          if (PRO == PRO_Q8X) {
+          if constexpr (QT == Q4K) {
+            const int pj = (kb >> 1) & 3;
+            if (!DIG) {
+              dot = strip_dot_q4k(L[j][p], xb, xsa, xsb, pj);
+            } else if (!fp32) {
+              dot = strip_dot_dig_q4k(L[j][p], xd, xsa, xsb, pj);
+            } else {
+              float4 xf[8];
+              strip_x_block<PRO, QT>(xf, a, part + (size_t)2 * NW * GBATCH * PARTS * 16, kb);
+              const float fa = (f4_sum(xf[0]) + f4_sum(xf[1])) + (f4_sum(xf[2]) + f4_sum(xf[3]));
+              const float fb = (f4_sum(xf[4]) + f4_sum(xf[5])) + (f4_sum(xf[6]) + f4_sum(xf[7]));
+              dot = strip_dot_q4k(L[j][p], xf, fa, fb, pj);
+            }
+          } else if (PRO == PRO_Q8X) {
             dot = strip_dot_q8x<QT>(L[j][p], x8, dxq, sx);
           } else if (!DIG) {
             dot = strip_dot<QT>(L[j][p], xb, mterm);
