@@ -105,7 +105,9 @@ GEMV_CASES = [
     (Q4K, 1, 64, 4096),      # Q4_K strip path: 16 groups of four rows
     (Q4K, 1, 36, 6144),      # twelve strips per row (the down shape's in_dim)
     (Q4K, 1, 2052, 2048),    # 513 groups: two or three groups per workgroup, a partial last one
-    (Q6K, 1, 48, 1024),
+    (Q6K, 1, 48, 1024),      # Q6_K strip path (in_dim a multiple of 512)
+    (Q6K, 1, 2048, 6144),    # the down shape: twelve strips
+    (Q6K, 1, 1028, 2048),    # 257 groups, a partial last workgroup
     (Q4K, 1, 33, 2304),      # 9 superblocks per row: a partial 8-superblock step
     (Q6K, 1, 17, 2304),      # odd superblocks per row: unaligned Q6_K row starts
     (Q6K, 1, 8, 16384),      # in_dim above the LDS-staged limit: generic path

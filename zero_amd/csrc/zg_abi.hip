@@ -339,7 +339,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
     return hip_check(ctx, launch_gemv_plain(a, qt, pro, epi, st), "gemv plain launch");
   }
-  if (pro == PRO_PLAIN && (epi == EPI_STORE || epi == EPI_RESID) && q4k_strip_ok(qt, il, k, n, w, x)) {
+  if (pro == PRO_PLAIN && (epi == EPI_STORE || epi == EPI_RESID) && kq_strip_ok(qt, il, k, n, w, x)) {
     // Q4_K rows in fours through the strip kernel
     const size_t rbytes = (k / 256) * 144;
     const size_t g0 = start / 4, g1 = (end + 3) / 4;
@@ -415,7 +415,7 @@ bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_
   bool ok = nseg >= 1 && nseg <= 3 && (pro == PRO_PLAIN || pro == PRO_RMSNORM);
   for (size_t i = 0; i < nseg && ok; i++)
     ok = (plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) ||
-          q4k_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x)) &&
+          kq_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x)) &&
          segs[i].qt == segs[0].qt;
   return ok;
 }
@@ -541,7 +541,7 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
 // split merge in the strip kernel's prologue.
 zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml, int nsplit, int hd,
                          const uint8_t* w, float* y, size_t k, size_t n, uint32_t qt, uint32_t il, hipStream_t st) {
-  if (q4k_strip_ok(qt, il, k, n, w, part_o) && attn_merge_strip_ok(nsplit, hd, k)) {
+  if (kq_strip_ok(qt, il, k, n, w, part_o) && attn_merge_strip_ok(nsplit, hd, k)) {
     // Q4_K rows in fours through the strip kernel, the merge in its prologue
     GemvArgs a{};
     a.nseg = 1;

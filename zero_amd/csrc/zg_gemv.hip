@@ -446,7 +446,7 @@ static hipError_t launch_x4(const GemvArgs& a, hipStream_t st) {
 
 bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192; }
 
-// Q4_K single projections take the strip kernel
+// decode-sized Q4_K projections take the strip kernel
 #ifndef ZG_Q4K_STRIP
 #define ZG_Q4K_STRIP 1
 #endif
@@ -910,12 +910,15 @@ static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStre
 // Q4_K rows through the strip kernel (lane units of 32 elements, four rows
 // per group): in_dim a multiple of 512 up to 8192, rows in fours, weights
 // and x 16-byte aligned.
-bool q4k_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
+bool kq_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
   if (!ZG_Q4K_STRIP || qt != Q4K || il != 1 || !strip_path_ok((int)k) || n % 4 != 0 ||
       (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
     return false;
   // one-batch launches only (the tall batch-loop form measured slower than
-  // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096)
+  // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096).
+  // A Q6_K unit of the same shape (three 16-byte quant loads at 2-byte
+  // alignment, 15 registers per row) was slower than zg_kquant.hip's Q6_K
+  // kernels at the decode shapes: down 7.72 vs 7.25 us, attn_v 3.99 vs 3.75
   const int S = (int)k / 512, nw = S >= 3 ? S : 4;  // S >= 1 here
   return ZG_Q4K_STRIP >= 2 || n / 4 <= (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * (size_t)(nw / S);
 }

@@ -101,7 +101,7 @@ bool plain_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w,
 // in_dim accepted by the strip kernel: a multiple of 512 up to 8192
 bool strip_path_ok(int k);
 // Q4_K rows the strip kernel takes (launch_gemv_plain with qt Q4_K)
-bool q4k_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
+bool kq_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x);
 // attention splits the strip kernel's merge prologue takes
 bool attn_merge_strip_ok(int nsplit, int hd, size_t k);
 hipError_t launch_gemv_plain(const GemvArgs& a, uint32_t qt, int pro, int epi, hipStream_t st);
