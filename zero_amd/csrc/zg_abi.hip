@@ -464,6 +464,30 @@ bool zg::fused_kq_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k
 // xn_out (rmsnorm prologue only): also store the normalized x there.
 zg_status zg::run_kq_segs(zg_ctx* ctx, const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro,
                           const float* norm_w, float eps, hipStream_t st, float* xn_out) {
+  bool strip = (pro == PRO_PLAIN || (pro == PRO_RMSNORM && aligned16(norm_w) && (!xn_out || aligned16(xn_out))));
+  for (size_t i = 0; i < nseg && strip; i++) strip = kq_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x);
+  if (strip) {
+    // Q4_K segments through the strip kernel (rows in fours per segment)
+    GemvArgs a{};
+    a.nseg = (int)nseg;
+    a.k = (int)k;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.xn_out = pro == PRO_RMSNORM ? xn_out : nullptr;
+    uint32_t gb = 0;
+    for (size_t i = 0; i < nseg; i++) {
+      a.seg[i].w = segs[i].w;
+      a.seg[i].y = segs[i].y;
+      a.seg[i].resid = nullptr;
+      a.seg[i].g_begin = gb;
+      a.seg[i].row_lo = 0;
+      a.seg[i].row_hi = (uint32_t)segs[i].n;
+      gb += (uint32_t)(segs[i].n / 4);
+    }
+    a.total_groups = gb;
+    return hip_check(ctx, launch_gemv_plain(a, ZG_Q4K, pro, EPI_STORE, st), "gemv Q4_K strip segmented launch");
+  }
   GenericArgs g{};
   g.xn_out = pro == PRO_RMSNORM ? xn_out : nullptr;
   g.x = x;

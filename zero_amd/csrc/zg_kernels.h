@@ -46,6 +46,9 @@ struct GemvArgs {
   // sync_add (the step counter times the layer count plus the layer)
   const uint32_t* sync_epoch;
   uint32_t sync_mul, sync_add;
+  // PRO_RMSNORM: workgroup 0 also stores the normalized x here (k floats)
+  // when non-null, for a following GEMV without the prologue
+  float* xn_out;
 };
 
 // The weights are streamed without allocating in the last-level cache:

@@ -736,6 +736,25 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
     }
     if (lane == 0 && key) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)key);
   }
+  if (PRO == PRO_RMSNORM && a.xn_out && bid == 0 && sub == 0) {
+    // the normalized x for other consumers: (x * gain) * (1 / rms), the
+    // sums of squares having crossed the batch barrier; the quarters of the
+    // first strip set's lanes cover every element once
+    float ss = 0.0f;
+    for (int i = 0; i < S; i++) ss += red[i];
+    const float rinv = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+    constexpr int H4 = unit_hoff<QT>() / 4;
+    const int x0 = unit_x0<QT>(kb);
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + x0);
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w + x0);
+    float4* o4 = reinterpret_cast<float4*>(a.xn_out + x0);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int i = h ? H4 + r : r;
+      const float4 v = x4[i], g = g4[i];
+      o4[i] = make_float4((v.x * g.x) * rinv, (v.y * g.y) * rinv, (v.z * g.z) * rinv, (v.w * g.w) * rinv);
+    }
+  }
 }
 
 template <uint32_t QT, int PRO, int EPI, int GBATCH, int MAXT = 1024, bool SEG1 = false, int IL = 4,
