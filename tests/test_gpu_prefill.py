@@ -90,9 +90,9 @@ def test_q8_0_linears_and_q4_0_embedding(ctx, zo):
 @pytest.mark.parametrize("lin_type", [synth.Q4_0, synth.Q8_0])
 def test_plain_row_layouts(ctx, zo, lin_type):
     """Plain row-major layer linears and LM head (.smodel-v1 / GGUF layouts)
-    at strip-sized dims: the rmsnorm and SwiGLU prologue/epilogue and (Q4_0)
-    the attention-split merge run in the plain strip GEMV, the prefill GEMMs
-    read plain rows."""
+    at strip-sized dims: the model interleaves them to X4 on the device when
+    it is created; its batched prefill and decode match the oracle, which
+    reads the plain rows."""
     cfg = synth.ModelConfig(n_layers=2, hidden=512, ffn=1024, n_q_heads=8, n_kv_heads=2, head_dim=64,
                             vocab_padded=1024, vocab_real=1000, max_ctx=160, lin_type=lin_type,
                             lin_interleave=1, head_interleave=1)
@@ -181,9 +181,9 @@ def _x4_layers(model):
 
 def test_qwen3_1_7b_shape_plain_layout_bit_identical(ctx):
     """At the Qwen3-1.7B shape the plain-row Q4_0 model gives the X4 model's
-    bits: every lane of the strip GEMV reads the same block of the same row
-    in either layout, and the GEMMs are bit-exact with the oracle in both.
-    Checked on a 64-token batched prefill, then 16 decode steps."""
+    bits: the device interleave at model creation reproduces the packer's
+    X4 bytes (the X4 model here is interleaved on the host).  Checked on a
+    64-token batched prefill, then 16 decode steps."""
     cfg = synth.ModelConfig(max_ctx=128, lin_interleave=1)
     plain = synth.random_model(cfg, seed=3)
     models = [GpuModel(ctx, plain), GpuModel(ctx, _x4_layers(plain))]

@@ -466,6 +466,25 @@ __global__ __launch_bounds__(256) void qkv_attn_kernel(GemvArgs ga, AttnArgs aa,
   }
 }
 
+// Plain row-major Q4_0 / Q8_0 blocks (bb bytes: fp16 d, then the quants) to
+// the X4 layout the packer writes for .smodel-v2 (per group of four rows
+// and block: the four rows' d, then their quant bytes in row order), one
+// thread per (group, block); every field sits at an even offset.
+__global__ __launch_bounds__(256) void interleave_x4_kernel(const uint8_t* __restrict__ plain, uint8_t* __restrict__ x4,
+                                                            size_t units, int nb, int bb) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= units) return;
+  const size_t g = t / (size_t)nb;
+  const int b = (int)(t - g * (size_t)nb);
+  uint16_t* o = reinterpret_cast<uint16_t*>(x4 + t * (size_t)(4 * bb));
+  const int qh = (bb - 2) / 2;  // quant halfwords per block
+  for (int l = 0; l < 4; l++) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(plain + ((4 * g + l) * (size_t)nb + b) * (size_t)bb);
+    o[l] = src[0];
+    for (int i = 0; i < qh; i++) o[4 + l * qh + i] = src[1 + i];
+  }
+}
+
 // Split merge for O projections that cannot take the merging GEMV: thread t
 // merges dims 8t..8t+7 of the attention output.
 __global__ void attn_merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml, int k, int hd,
@@ -920,6 +939,26 @@ static zg_status weight_dev(zg_model* m, const void* key, uint32_t qt, uint32_t 
   return ZG_OK;
 }
 
+// A plain-row Q4_0 / Q8_0 tensor of rows in fours, copied to X4 into model
+// memory (*w and *il then name the copy); other tensors are left as they are.
+static zg_status repack_x4(zg_model* m, const uint8_t** w, uint32_t qt, uint32_t* il, size_t rows, size_t k) {
+  if (*il != 1 || (qt != ZG_Q4_0 && qt != ZG_Q8_0) || rows % 4 || k % 32 || (reinterpret_cast<uintptr_t>(*w) & 1u))
+    return ZG_OK;
+  const size_t bytes = tensor_bytes(qt, rows, k);
+  void* dst = nullptr;
+  zg_status s = model_alloc(m, &dst, bytes);
+  if (s) return s;
+  const int nb = (int)(k / 32), bb = qt == ZG_Q4_0 ? 18 : 34;
+  const size_t units = rows / 4 * (size_t)nb;
+  hipLaunchKernelGGL(interleave_x4_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, m->ctx->stream, *w,
+                     static_cast<uint8_t*>(dst), units, nb, bb);
+  s = hip_check(m->ctx, hipGetLastError(), "model: interleave launch");
+  if (s) return s;
+  *w = static_cast<const uint8_t*>(dst);
+  *il = 4;
+  return ZG_OK;
+}
+
 // rmsnorm of x into m->xn, for GEMVs without a rmsnorm prologue (the
 // model's own buffer: a captured graph must not hold context scratch, which
 // a later call may reallocate)
@@ -1345,6 +1384,19 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   }
   if (!s) s = weight_dev(m, d.token_embd, d.embd_type, 1, d.vocab_padded, H, &m->embd);
   if (!s) s = weight_dev(m, d.lm_head, d.head_type, d.head_interleave, d.vocab_padded, H, &m->head);
+  // plain-row Q4_0 / Q8_0 projections and LM head (the .smodel-v1 and GGUF
+  // layouts) are interleaved to X4 into memory the model owns: the X4
+  // kernels give the same bits as the plain-row ones on the same weights
+  // (lane (b, r) decodes block b of row 4 g + r in either layout) and read
+  // 16 contiguous quant bytes per lane instead of 2-byte-aligned blocks
+  for (uint32_t l = 0; l < d.n_layers && !s; l++) {
+    ZLayer& L = m->layers[l];
+    const uint8_t** w[ZG_N_PROJ] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    const size_t rows[ZG_N_PROJ] = {qd, kvd, kvd, H, F, F, H}, ks[ZG_N_PROJ] = {H, H, H, qd, H, H, F};
+    for (int p = 0; p < ZG_N_PROJ && !s; p++) s = repack_x4(m, w[p], L.qt[p], &L.il[p], rows[p], ks[p]);
+  }
+  if (!s) s = repack_x4(m, &m->head, d.head_type, &m->d.head_interleave, d.vocab_padded, H);
+  if (!s) s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "model: interleave");
   if (!s && !d.output_norm) s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null output_norm");
   if (!s) s = upload_f32(m, &m->out_norm, d.output_norm, H);
   if (!s) {
@@ -1440,7 +1492,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
                    il[ZG_PROJ_Q] == il[ZG_PROJ_V] && H == 2048 && (d.head_dim == 128 || d.head_dim == 64) &&
                    groups / 2 <= (size_t)m->cus * 4;
     }
-    m->head_norm = rmsnorm_fused_ok(d.head_type, d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
+    m->head_norm =
+        rmsnorm_fused_ok(d.head_type, m->d.head_interleave, H, d.vocab_padded, m->head, m->hidden, EPI_ARGMAX);
   }
   if (!s) s = capture(m, record_prefill, &m->g_prefill);
   if (!s) s = capture(m, record_step, &m->g_step);
