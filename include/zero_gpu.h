@@ -243,7 +243,11 @@ typedef struct zg_model zg_model;
 /* Builds device state (KV cache [L][K|V][t][kv_head][d] fp32 as
  * kv_cache.rs:17-31, scratch, norm weights) and captures the per-token
  * layer sequence of forward_single_token_avx512
- * (inference_avx512.rs:1826-1987) + lm_head_argmax_avx512 into a hipGraph. */
+ * (inference_avx512.rs:1826-1987) + lm_head_argmax_avx512 into a hipGraph.
+ * Plain-row Q4_0 / Q8_0 projections and LM head whose rows come in fours
+ * are copied once into model-owned device memory in the X4 layout (the
+ * same results bit for bit, the X4 kernels' speed): the model then holds a
+ * second copy of those weights until zg_model_destroy. */
 zg_status zg_model_create(zg_ctx *ctx, const zg_model_desc *desc, zg_model **out);
 void zg_model_destroy(zg_model *m);
 /* One token through all layers at position pos, then the LM head.
