@@ -115,6 +115,8 @@ GEMV_CASES = [
     (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
     (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
     (Q4_0, 4, 151936, 2048), # tall Q4_0X4: four groups per batch, batches looped over
+    (Q4_0, 4, 8320, 4096),   # tall at eight strips: 512-thread workgroups under a 512-thread bound
+    (Q4_0, 4, 8208, 6144),   # tall at twelve strips: the fp32 form under the 1024-thread bound
     (Q8_0, 4, 32776, 2048),  # tall Q8_0X4 at in_dim 2048: LDS-staged kernel, last batch of two groups
     # DeepSeek2 / Kimi K2 projections through linear_dispatch_avx512
     # (kernel/src/inference_avx512.rs:2101-2825): MLA kv_a_mqa, q_a, q_b,
