@@ -110,6 +110,7 @@ constexpr int lds_row() { return BK * 32 + 16; }
 // scales, NW weight block rows (raw quants + scale).
 template <uint32_t WT, int BM, int BK>
 struct GemmStage {
+  static_assert(BM * BK * 2 % 256 == 0 && kBN * BK % 256 == 0, "every thread stages whole chunks and blocks");
   static constexpr int NA = BM * BK * 2 / 256;
   static constexpr int ND = (BM * BK + 255) / 256;
   static constexpr int NW = kBN * BK / 256;
@@ -393,6 +394,11 @@ static int gemm_cu_count() {
   return n;
 }
 
+// blocks per stage of the 64-row tile (M=512 x 6144x2048: 33.0 us at 4,
+// 40.2 us at 8; the 32-row tile's 8 against 4 or 16: 42.9 / 42.7 / 42.9 us)
+#ifndef ZG_GEMM_BK64
+#define ZG_GEMM_BK64 4
+#endif
 #ifndef ZG_GEMM_SMALL_BK
 #define ZG_GEMM_SMALL_BK 8
 #endif
@@ -447,10 +453,10 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
   // 64-row tiles unless they would not give every CU three workgroups
   const size_t tiles64 = ((n + kBN - 1) / kBN) * ((m + 63) / 64);
   if (tiles64 >= (size_t)3 * gemm_cu_count()) {
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64, 4>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64, 4>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 64, 4>(a, st);
-    else launch_gemm<Q8_0, 1, 64, 4>(a, st);
+    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64, ZG_GEMM_BK64>(a, st);
+    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64, ZG_GEMM_BK64>(a, st);
+    else if (interleave == 4) launch_gemm<Q8_0, 4, 64, ZG_GEMM_BK64>(a, st);
+    else launch_gemm<Q8_0, 1, 64, ZG_GEMM_BK64>(a, st);
   } else if (((n + kBN - 1) / kBN) * ((m + 31) / 32) <= (size_t)gemm_cu_count()) {
     // at most one 32-row tile per CU: each stage's round trip is exposed,
     // so fewer, larger stages
