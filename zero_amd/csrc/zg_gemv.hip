@@ -918,7 +918,10 @@ bool kq_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, co
   // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096).
   // A Q6_K unit of the same shape (three 16-byte quant loads at 2-byte
   // alignment, 15 registers per row) was slower than zg_kquant.hip's Q6_K
-  // kernels at the decode shapes: down 7.72 vs 7.25 us, attn_v 3.99 vs 3.75
+  // kernels at the decode shapes: down 7.72 vs 7.25 us, attn_v 3.99 vs 3.75.
+  // The one-batch launches decode with fp32 activations: the integer-digit
+  // form there took the Q4_K_M decode from 1,160 to 1,007 tok/s (SwiGLU
+  // launch only) and 964 tok/s (every Q4_K launch)
   const int S = (int)k / 512, nw = S >= 3 ? S : 4;  // S >= 1 here
   return ZG_Q4K_STRIP >= 2 || n / 4 <= (size_t)cu_count() * ZG_STRIP_SMALL_ITEMS_PER_CU * (size_t)(nw / S);
 }
