@@ -1024,12 +1024,14 @@ static zg_status run_qkv_attn(zg_model* m, uint32_t l, const ZLayer& L, AttnArgs
   const uint32_t qt = L.qt[ZG_PROJ_Q], il = L.il[ZG_PROJ_Q];
 #define ZG_QKV_ATTN(QT, IL, HDV) hipLaunchKernelGGL((qkv_attn_kernel<QT, IL, HDV>), grid, block, shm, st, ga, aa, n_attn)
   if (HD == 128) {
-    if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 128);
+    if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 128);
+    else if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 128);
     else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 128);
     else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 128);
     else ZG_QKV_ATTN(Q8_0, 1, 128);
   } else {
-    if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 64);
+    if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 64);
+    else if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 64);
     else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 64);
     else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 64);
     else ZG_QKV_ATTN(Q8_0, 1, 64);
@@ -1482,13 +1484,14 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
                                                                  : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o))) ||
                    kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
       for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
-      // Q|K|V and attention in one launch: Q4_0 / Q8_0 of one type and
+      // Q|K|V and attention in one launch: Q4_0 / Q8_0 / Q4_K of one type and
       // layout on the one-launch strip path, in_dim 2048 (four strips, the
       // attention's 256-thread workgroups), two-group batches that never
       // straddle a KV head, and one batch per workgroup
       const size_t groups = (qd + 2 * kvd) / 4;
       L.qkv_attn = (fused_x4_ok(m->hidden, q3, 3, H) || fused_plain_ok(m->hidden, q3, 3, H, PRO_RMSNORM)) &&
-                   (qt[ZG_PROJ_Q] == ZG_Q4_0 || qt[ZG_PROJ_Q] == ZG_Q8_0) && il[ZG_PROJ_Q] == il[ZG_PROJ_K] &&
+                   (qt[ZG_PROJ_Q] == ZG_Q4_0 || qt[ZG_PROJ_Q] == ZG_Q8_0 || qt[ZG_PROJ_Q] == ZG_Q4K) &&
+                   il[ZG_PROJ_Q] == il[ZG_PROJ_K] &&
                    il[ZG_PROJ_Q] == il[ZG_PROJ_V] && H == 2048 && (d.head_dim == 128 || d.head_dim == 64) &&
                    groups / 2 <= (size_t)m->cus * 4;
     }
