@@ -133,7 +133,7 @@ struct AttnArgs {
 #endif
 constexpr int kAttnWaves = ZG_ATTN_WAVES;
 #ifndef ZG_ATTN_SPLITS
-#define ZG_ATTN_SPLITS 4
+#define ZG_ATTN_SPLITS 6
 #endif
 constexpr int kAttnDecodeSplits = ZG_ATTN_SPLITS;
 static_assert(kAttnDecodeSplits >= 1 && kAttnDecodeSplits <= kAttnSplits, "decode splits within the merge's capacity");
@@ -1416,7 +1416,11 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   // attention faster but the merge in the O projection's prologue slower:
   // every O workgroup reads nsplit x 8 KB of split outputs (Qwen3-1.7B,
   // eager trace: 8 splits 4.42 + 4.78 us, 4 splits 5.26 + 4.04 us with the
-  // splits cut by max_ctx)
+  // splits cut by max_ctx).  With the fused Q|K|V + attention launch, at
+  // max_ctx 384 (every split one 64-row round of K/V loads): decode 1,491 /
+  // 1,495 tok/s at 6 splits against 1,478 / 1,476 at 4 on one box, and
+  // 1,511 at 8 against 1,517 at 4 on another; token-by-token prompt steps,
+  // short contexts, lose 1.7 % at 6
   {
     const uint32_t ns = (d.max_ctx + 7) / 8;
     m->nsplit = (int)(ns < (uint32_t)kAttnDecodeSplits ? ns : (uint32_t)kAttnDecodeSplits);
