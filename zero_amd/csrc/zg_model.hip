@@ -1417,10 +1417,11 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   // every O workgroup reads nsplit x 8 KB of split outputs (Qwen3-1.7B,
   // eager trace: 8 splits 4.42 + 4.78 us, 4 splits 5.26 + 4.04 us with the
   // splits cut by max_ctx).  With the fused Q|K|V + attention launch, at
-  // max_ctx 384 (every split one 64-row round of K/V loads): decode 1,491 /
-  // 1,495 tok/s at 6 splits against 1,478 / 1,476 at 4 on one box, and
-  // 1,511 at 8 against 1,517 at 4 on another; token-by-token prompt steps,
-  // short contexts, lose 1.7 % at 6
+  // max_ctx 384 (every split one 64-row round of K/V loads at 6): decode
+  // 1,491 / 1,495 tok/s at 6 splits against 1,478 / 1,476 at 4 on one box,
+  // and 1,491 / 1,491 at 6 against 1,471 / 1,470 at 5, 1,471 / 1,469 at 7
+  // and 1,468 / 1,470 at 8 on another; token-by-token prompt steps, short
+  // contexts, lose 1.7 % at 6
   {
     const uint32_t ns = (d.max_ctx + 7) / 8;
     m->nsplit = (int)(ns < (uint32_t)kAttnDecodeSplits ? ns : (uint32_t)kAttnDecodeSplits);
