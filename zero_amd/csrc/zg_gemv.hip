@@ -460,7 +460,8 @@ bool strip_path_ok(int k) { return ZG_STRIP_ENABLE && k % 512 == 0 && k <= 8192;
 // groups per batch of the attention-merging O projection (Qwen3-1.7B
 // decode: 1,500 tok/s at 2, 1,466 at 1, 1,489 at 3, 1,482 at 4: each
 // workgroup merges the whole split output, so fewer rows per workgroup
-// re-read it more often, and more leave CUs idle)
+// re-read it more often, and more leave CUs idle; with six attention
+// splits: 1,486 at 2, 1,470 at 3, 1,472 at 4)
 #ifndef ZG_ATTN_O_GB
 #define ZG_ATTN_O_GB 2
 #endif
