@@ -916,7 +916,9 @@ bool kq_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, co
       (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
     return false;
   // one-batch launches only (the tall batch-loop form measured slower than
-  // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096).
+  // the Q4_K strip kernel of zg_kquant.hip: 13.4 vs 11.8 us at 14336x4096
+  // with four groups per batch, 13.3 at two; one group per batch 12.0, and
+  // fp32 activations at two groups 11.85 vs 11.9: no form beats it).
   // A Q6_K unit of the same shape (three 16-byte quant loads at 2-byte
   // alignment, 15 registers per row) was slower than zg_kquant.hip's Q6_K
   // kernels at the decode shapes: down 7.72 vs 7.25 us, attn_v 3.99 vs 3.75.
