@@ -58,14 +58,41 @@ struct DevState {
 // embed_lookup_dispatch (forward_pass.rs:311-370): row tok of a plain
 // token_embd (Q4_0, Q8_0, Q4_K or Q6_K), each element dequantized in the
 // reference's operation order
+// Each thread decodes eight elements per pass with all their loads issued
+// before the first store (indexes past the row clamp to its last element),
+// so the row's cache lines arrive together rather than one memory round
+// trip per element.
+template <uint32_t QT>
+__device__ __forceinline__ void embed_row_q(const uint8_t* __restrict__ embd, int hidden, uint32_t tok,
+                                            float* __restrict__ out) {
+  constexpr int be = (QT == Q4_0 || QT == Q8_0) ? 32 : 256;
+  constexpr int kPer = 8;
+  const size_t nb = (size_t)(hidden / be);
+  const int nt = (int)blockDim.x;
+  for (int e0 = 0; e0 < hidden; e0 += kPer * nt) {
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = min(e0 + (int)threadIdx.x + i * nt, hidden - 1);
+      const BlockRef br = block_ref(embd, QT, 1, tok, (size_t)(e / be), nb);
+      const float d = (QT == Q4_0 || QT == Q8_0) ? rd_half(br.d) : 0.0f;
+      v[i] = deq_elem(br, QT, d, e % be);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = e0 + (int)threadIdx.x + i * nt;
+      if (e < hidden) out[e] = v[i];
+    }
+  }
+}
+
 __device__ __forceinline__ void embed_row(const uint8_t* __restrict__ embd, uint32_t qt, int hidden, uint32_t tok,
                                           float* __restrict__ out) {
-  const int be = (qt == Q4_0 || qt == Q8_0) ? 32 : 256;
-  const size_t nb = (size_t)(hidden / be);
-  for (int e = threadIdx.x; e < hidden; e += blockDim.x) {
-    const BlockRef br = block_ref(embd, qt, 1, tok, (size_t)(e / be), nb);
-    const float d = (qt == Q4_0 || qt == Q8_0) ? rd_half(br.d) : 0.0f;
-    out[e] = deq_elem(br, qt, d, e % be);
+  switch (qt) {
+    case Q4_0: embed_row_q<Q4_0>(embd, hidden, tok, out); break;
+    case Q8_0: embed_row_q<Q8_0>(embd, hidden, tok, out); break;
+    case Q4K: embed_row_q<Q4K>(embd, hidden, tok, out); break;
+    default: embed_row_q<Q6K>(embd, hidden, tok, out); break;
   }
 }
 
