@@ -57,8 +57,7 @@ struct DevState {
 
 // embed_lookup_dispatch (forward_pass.rs:311-370): row tok of a plain
 // token_embd (Q4_0, Q8_0, Q4_K or Q6_K), each element dequantized in the
-// reference's operation order
-// Each thread decodes eight elements per pass with all their loads issued
+// reference's operation order.  Each thread decodes eight elements per pass with all their loads issued
 // before the first store (indexes past the row clamp to its last element),
 // so the row's cache lines arrive together rather than one memory round
 // trip per element.
@@ -581,8 +580,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float* __restri
 
 // After the LM head: argmax -> next token, error bits, output record, then
 // move to the next position.
-__global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t vocab_real, uint32_t* out_tokens) {
+// Every input is loaded before the first store (one memory round trip).
+__global__ void finalize_kernel(DevState* __restrict__ st, const uint64_t* __restrict__ best, uint32_t vocab_real,
+                                uint32_t* __restrict__ out_tokens) {
   const uint64_t key = *best;
+  const uint32_t err0 = st->err, err_step = st->err_step, gen = st->gen, gen_cap = st->gen_cap, pos = st->pos;
   uint32_t idx = 0;
   uint32_t err = 0;
   if (key == 0) {
@@ -595,16 +597,16 @@ __global__ void finalize_kernel(DevState* st, const uint64_t* best, uint32_t voc
     if (!isfinite(v)) err = 1;
     else if (idx >= vocab_real) err = 2;
   }
-  if ((err | st->err) && st->err_step == kNoStep) {
-    st->err_step = st->gen;
-    st->err_first = err | st->err;
+  if ((err | err0) && err_step == kNoStep) {
+    st->err_step = gen;
+    st->err_first = err | err0;
   }
-  st->err |= err;
+  st->err = err0 | err;
   st->best = key;
   st->token = idx;
-  if (out_tokens && st->gen < st->gen_cap) out_tokens[st->gen] = idx;
-  st->gen += 1;
-  st->pos += 1;
+  if (out_tokens && gen < gen_cap) out_tokens[gen] = idx;
+  st->gen = gen + 1;
+  st->pos = pos + 1;
 }
 
 // Move to the next position; during the prompt, feed the next prompt token.
