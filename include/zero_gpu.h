@@ -279,6 +279,15 @@ void zg_model_reset(zg_model *m);
  * "v_cache[row]" instead.  Copies up to cap bytes (no terminator) into buf
  * and returns the count; 0 when nothing is latched. */
 size_t zg_model_first_nonfinite(const zg_model *m, char *buf, size_t cap);
+/* Failure-path test hook; no counterpart in the reference, for tests of the
+ * timeout report only.  The fused Q|K|V + attention launch of layer `layer`
+ * (0-based) skips its tagged Q|K|V row stores, so every attention wave of
+ * that layer gives up at its bounded wait (2^13 polls) and the call returns
+ * ZG_ERR_HIP ("a completion wait timed out"): the GPU counterpart of the
+ * reference's barrier-timeout recovery (kernel/src/smp.rs:1677-1711).
+ * Every kernel still runs to its end.  layer < 0 restores the stores (the
+ * default).  Affects only layers decoded by the fused launch. */
+zg_status zg_model_test_drop_qkv_stores(zg_model *m, int32_t layer);
 
 /* Batched prefill.  No counterpart in the reference, which runs the prompt
  * token by token through forward_single_token_avx512

@@ -272,7 +272,13 @@ def test_generate_bounds(ctx, tiny):
 
 def test_qwen3_1_7b_shape_greedy_64(ctx, zo):
     """Config 3: random-init Qwen3-1.7B shape, 128-token seeded prompt, then
-    64 greedy decode steps compared token by token and logit by logit."""
+    64 greedy decode steps compared token by token and logit by logit.
+
+    Then the path the bench times: zg_model_generate (the captured step
+    graph, the next token fed back on the device) must give the oracle's
+    tokens too.  Finally the steps are replayed after zg_model_reset and
+    every logit must repeat bit for bit (the reference's bitwise-invariance
+    contract, kernel/src/smp.rs:33-40)."""
     cfg = synth.ModelConfig(max_ctx=256)
     model = synth.random_model(cfg, seed=11)
     gm = GpuModel(ctx, model)
@@ -280,24 +286,84 @@ def test_qwen3_1_7b_shape_greedy_64(ctx, zo):
     prompt = synth.prompt(12, 128, cfg.vocab_real)
     worst = 0.0
     margins = []
-    with zo.Pool(16):
+    ref_tokens, logits = [], []
+    try:
+        with zo.Pool(16):
+            for pos, t in enumerate(prompt[:-1]):
+                gm.step(int(t), pos)
+                om.forward(int(t), pos)
+            tok, pos = int(prompt[-1]), len(prompt) - 1
+            for step in range(65):
+                nxt, _, hid, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+                h_ref = om.forward(tok, pos)
+                rc, t_ref, _, lg_ref = om.lm_head()
+                assert rc == 0
+                worst = max(worst, rel_err(lg, lg_ref), rel_err(hid, h_ref))
+                top = np.sort(lg_ref)[-2:]
+                margins.append(float(top[1] - top[0]))
+                assert nxt == t_ref, (step, nxt, t_ref)
+                ref_tokens.append(t_ref)
+                logits.append(np.array(lg, np.float32))
+                tok, pos = nxt, pos + 1
+        print(f"Qwen3-1.7B shape: 65 greedy tokens identical, worst rel err {worst:.2e}, "
+              f"min top-2 logit margin {min(margins):.4f}")
+        assert worst <= REL_TOL
+
+        # the device-fed greedy loop (what bench.py times) against the oracle
+        toks, _, _ = gm.generate(prompt, 64)
+        assert np.array_equal(np.asarray(toks), np.asarray(ref_tokens[:64], np.uint32))
+        toks2, _, _ = gm.generate(prompt, 64)
+        assert np.array_equal(toks2, toks)
+
+        # the same steps again after a reset: identical logit bits
+        gm.reset()
         for pos, t in enumerate(prompt[:-1]):
             gm.step(int(t), pos)
-            om.forward(int(t), pos)
         tok, pos = int(prompt[-1]), len(prompt) - 1
         for step in range(65):
-            nxt, _, hid, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
-            h_ref = om.forward(tok, pos)
-            rc, t_ref, _, lg_ref = om.lm_head()
-            assert rc == 0
-            worst = max(worst, rel_err(lg, lg_ref), rel_err(hid, h_ref))
-            top = np.sort(lg_ref)[-2:]
-            margins.append(float(top[1] - top[0]))
-            assert nxt == t_ref, (step, nxt, t_ref)
+            nxt, _, _, lg = gm.step(tok, pos, want_logits=True)
+            assert np.array_equal(np.asarray(lg, np.float32).view(np.uint32), logits[step].view(np.uint32)), step
             tok, pos = nxt, pos + 1
-    print(f"Qwen3-1.7B shape: 65 greedy tokens identical, worst rel err {worst:.2e}, "
-          f"min top-2 logit margin {min(margins):.4f}")
-    assert worst <= REL_TOL
-    om.close()
-    gm.close()
-    ctx.clear()
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
+def test_fused_attention_wait_timeout(ctx):
+    """The bounded wait of the fused Q|K|V + attention launch, forced from
+    the host: with layer 1's tagged Q|K|V stores dropped
+    (zg_model_test_drop_qkv_stores), that layer's attention waves give up
+    after their poll bound and the step reports ZG_ERR_HIP with the timeout
+    message, the GPU counterpart of the reference's barrier-timeout recovery
+    (kernel/src/smp.rs:1677-1711).  Every kernel still runs to its end.
+    With the stores restored and a reset, the model decodes the same tokens
+    as before the failure."""
+    import zero_amd
+    from zero_amd import _lib
+    cfg = synth.ModelConfig(n_layers=3, hidden=2048, ffn=2048, vocab_padded=4096, vocab_real=4000, max_ctx=32)
+    model = synth.random_model(cfg, seed=21)
+    gm = GpuModel(ctx, model)
+    try:
+        prompt = synth.prompt(21, 6, cfg.vocab_real)
+        ref, _, _ = gm.generate(prompt, 8)
+        gm.reset()
+        assert ctx.lib.zg_model_test_drop_qkv_stores(gm.h, 1) == _lib.ZG_OK
+        with pytest.raises(zero_amd.ZgError) as e:
+            gm.step(int(prompt[0]), 0)
+        assert e.value.code == _lib.ZG_ERR_HIP
+        assert "wait timed out" in str(e.value)
+        assert ctx.lib.zg_model_test_drop_qkv_stores(gm.h, -1) == _lib.ZG_OK
+        gm.reset()
+        toks, _, _ = gm.generate(prompt, 8)
+        assert np.array_equal(toks, ref)
+        # a layer outside the model drops nothing
+        assert ctx.lib.zg_model_test_drop_qkv_stores(gm.h, 7) == _lib.ZG_OK
+        gm.reset()
+        toks, _, _ = gm.generate(prompt, 8)
+        assert np.array_equal(toks, ref)
+        assert ctx.lib.zg_model_test_drop_qkv_stores(None, 0) == _lib.ZG_ERR_INVALID_ARG
+    finally:
+        ctx.lib.zg_model_test_drop_qkv_stores(gm.h, -1)
+        gm.close()
+        ctx.clear()

@@ -145,6 +145,7 @@ SIGNATURES = {
     "zg_model_generate": (_ST, [_P, _P, _S, _S, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "zg_model_reset": (None, [_P]),
     "zg_model_first_nonfinite": (_S, [_P, C.c_char_p, _S]),
+    "zg_model_test_drop_qkv_stores": (_ST, [_P, C.c_int32]),
     "zg_model_prefill": (_ST, [_P, _P, _S, _U32, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),
     "zg_model_generate_ex": (_ST, [_P, _P, _S, _S, _U32, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "zg_linear_q8act_dev": (_ST, [_P, _P, _P, _P, _S, _S, _U32, _U32, _P]),

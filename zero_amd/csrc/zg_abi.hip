@@ -402,8 +402,8 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
 }
 
 // run_fused's one-launch forms: X4 segments through the X4 kernels, plain
-// row-major Q4_0 / Q8_0 segments through the strip kernel (rmsnorm or plain
-// prologue)
+// row-major Q4_0 / Q8_0 segments through the strip kernel (no prologue),
+// Q4_K rows through the strip kernel (rmsnorm or no prologue)
 bool zg::fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k) {
   bool ok = nseg >= 1 && nseg <= 3;
   for (size_t i = 0; i < nseg && ok; i++)
@@ -414,7 +414,7 @@ bool zg::fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k
 bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k, int pro) {
   bool ok = nseg >= 1 && nseg <= 3 && (pro == PRO_PLAIN || pro == PRO_RMSNORM);
   for (size_t i = 0; i < nseg && ok; i++)
-    ok = (plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) ||
+    ok = ((pro == PRO_PLAIN && plain_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x)) ||
           kq_strip_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x)) &&
          segs[i].qt == segs[0].qt;
   return ok;
@@ -425,7 +425,7 @@ bool zg::fused_plain_ok(const float* x, const FusedDev* segs, size_t nseg, size_
 bool zg::rmsnorm_fused_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x, int epi) {
   if (pair_path_ok(qt, il, k, n, w, x)) return true;
   if (kq_fused_ok(qt, il, k, w, x)) return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX;
-  return plain_strip_ok(qt, il, k, n, w, x) && (epi == EPI_STORE || epi == EPI_ARGMAX);
+  return plain_strip_ok(qt, il, k, n, w, x) && epi == EPI_ARGMAX;
 }
 
 // Q4_K gate|up in one launch: y[r] = silu(gate_r . x') * (up_r . x'), x' the
@@ -602,10 +602,8 @@ zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml,
     g.attn_hd = hd;
     return hip_check(ctx, launch_kq_attn_o(g, st), "attention-merge gemv_kq launch");
   }
-  const bool x4 = il == 4;
-  if (!attn_merge_gemv_ok(qt, il, k) ||
-      !(x4 ? pair_path_ok(qt, il, k, n, w, part_o) : plain_strip_ok(qt, il, k, n, w, part_o)))
-    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0 weights and a strip-sized in_dim");
+  if (!attn_merge_gemv_ok(qt, il, k) || !pair_path_ok(qt, il, k, n, w, part_o))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0X4 weights and a strip-sized in_dim");
   GemvArgs a{};
   a.nseg = 1;
   a.k = (int)k;
@@ -620,8 +618,7 @@ zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml,
   a.seg[0].g_begin = 0;
   a.seg[0].row_lo = 0;
   a.seg[0].row_hi = (uint32_t)n;
-  return hip_check(ctx, x4 ? launch_gemv_x4(a, qt, PRO_ATTN, EPI_RESID, st) : launch_gemv_plain(a, qt, PRO_ATTN, EPI_RESID, st),
-                   "attention-merge gemv launch");
+  return hip_check(ctx, launch_gemv_x4(a, qt, PRO_ATTN, EPI_RESID, st), "attention-merge gemv launch");
 }
 
 // ---------------------------------------------------------------------------

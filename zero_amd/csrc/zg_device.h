@@ -488,13 +488,24 @@ __device__ __forceinline__ bool xdig_quad(float4 lo, float4 hi, XDig& X) {
 // quants q, given as 8 dwords in the dg order; t0, t1, t2 enter with the
 // chains' start values.  V = 2^14 a + 2^7 b + c, so the block's integer sum
 // is 2^14 t0 + 2^7 t1 + t2.
+// A dependent v_dot4_i32_i8 issues ~16 cycles after its predecessor, so
+// each digit's chain is split into two (even and odd dwords; six chains in
+// flight) and the halves are added at the end: integer sums, so the result
+// is the same in any order.
 __device__ __forceinline__ void xdig_chains(const uint32_t (&q)[8], const XDig& X, int& t0, int& t1, int& t2) {
+  int u0 = 0, u1 = 0, u2 = 0;
 #pragma unroll
-  for (int c = 0; c < 8; c++) {
+  for (int c = 0; c < 8; c += 2) {
     t0 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[0][c], t0, false);
     t1 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[1][c], t1, false);
     t2 = __builtin_amdgcn_sdot4((int)q[c], (int)X.dg[2][c], t2, false);
+    u0 = __builtin_amdgcn_sdot4((int)q[c + 1], (int)X.dg[0][c + 1], u0, false);
+    u1 = __builtin_amdgcn_sdot4((int)q[c + 1], (int)X.dg[1][c + 1], u1, false);
+    u2 = __builtin_amdgcn_sdot4((int)q[c + 1], (int)X.dg[2][c + 1], u2, false);
   }
+  t0 += u0;
+  t1 += u1;
+  t2 += u2;
 }
 
 }  // namespace zg

@@ -17,7 +17,9 @@
 // Generic path: any layout / block type, one wave per output row, byte
 // loads.  Used for plain Q4_0/Q8_0, odd blocks-per-row and as the first
 // Q4_K/Q6_K implementation.
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "zg_device.h"
 #include "zg_kernels.h"
@@ -398,6 +400,34 @@ __global__ __launch_bounds__(256) void read_floor_kernel(const u32x4* __restrict
 // Host-side launchers.
 // ---------------------------------------------------------------------------
 
+// Resident workgroups per CU of kernel f at (threads, shm), queried once per
+// distinct (kernel, threads, shm) and cached under a lock: one template
+// instance can be launched with different block and LDS sizes, and several
+// host threads may launch at once.  big_lds: raise the kernel's dynamic LDS
+// limit to shm first (needed above 64 KiB).
+static int resident_per_cu(const void* f, int threads, size_t shm, bool big_lds = false) {
+  struct Entry {
+    const void* f;
+    int threads;
+    size_t shm;
+    int n;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.f == f && e.threads == threads && e.shm == shm) return e.n;
+  int n = 0;
+  if ((big_lds && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess) ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, shm) != hipSuccess || n <= 0)
+    n = 1;
+  try {
+    cache.push_back({f, threads, shm, n});
+  } catch (const std::bad_alloc&) {  // the value is still right; only the cache entry is lost
+  }
+  return n;
+}
+
 static int cu_count() {
   static int n = 0;
   if (n == 0) {
@@ -511,16 +541,9 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   // then what the occupancy query says fits.
   size_t per_cu = nw >= ZG_STRIP_WAVES_PER_CU ? 1 : (size_t)(ZG_STRIP_WAVES_PER_CU / nw);
   if (MAXT < 1024) {
-    static int resident = 0;
-    if (resident == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &n, gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, false, 0, DIGL>, nw * 64, shm) !=
-              hipSuccess ||
-          n <= 0)
-        n = 1;
-      resident = n;
-    }
+    const int resident = resident_per_cu(
+        reinterpret_cast<const void*>(gemv_strip_kernel<QT, PRO, EPI, GBATCH, MAXT, SEG1, IL, false, 0, DIGL>), nw * 64,
+        shm);
     if ((size_t)resident < per_cu) per_cu = (size_t)resident;
   }
   const size_t cap = (size_t)cu_count() * per_cu;
@@ -804,17 +827,8 @@ template <uint32_t QT, int PRO, int EPI, bool STREAM>
 static hipError_t launch_lds(const GemvArgs& a, hipStream_t st) {
   constexpr int G = lds_groups<QT>();
   const size_t shm = LdsGeom<QT, G>::SHM;
-  static int resident = 0;
-  if (resident == 0) {
-    int n = 0;
-    if (hipFuncSetAttribute((const void*)gemv_lds_kernel<QT, PRO, EPI, G, STREAM>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_lds_kernel<QT, PRO, EPI, G, STREAM>, 256, shm) !=
-            hipSuccess ||
-        n <= 0)
-      n = 1;
-    resident = n;
-  }
+  const int resident =
+      resident_per_cu(reinterpret_cast<const void*>(gemv_lds_kernel<QT, PRO, EPI, G, STREAM>), 256, shm, true);
   const size_t nbatch = (a.total_groups + G - 1) / G;
   const size_t cap = (size_t)cu_count() * resident;
   const size_t grid = nbatch < cap ? nbatch : cap;
@@ -862,7 +876,7 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
 
 // Q4_0X4 or plain Q4_0 weights
 bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k) {
-  return qt == Q4_0 && (il == 4 || il == 1) && k <= 8192 && strip_path_ok((int)k);
+  return qt == Q4_0 && il == 4 && k <= 8192 && strip_path_ok((int)k);
 }
 
 template <uint32_t QT>
@@ -886,12 +900,15 @@ bool plain_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w,
          (reinterpret_cast<uintptr_t>(w) & 1u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
+// Plain rows take no rmsnorm-store, SwiGLU or attention-merge forms: the
+// model interleaves its plain-row Q4_0 / Q8_0 tensors to X4 at creation, and
+// the operator API reaches plain rows only without a prologue or as an LM
+// head (rmsnorm + argmax).
 template <uint32_t QT>
 static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStream_t st) {
   if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_strip<QT, PRO_PLAIN, EPI_STORE, 1>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_strip<QT, PRO_PLAIN, EPI_RESID, 1>(a, st);
   if (pro == PRO_PLAIN && epi == EPI_ARGMAX) return launch_strip<QT, PRO_PLAIN, EPI_ARGMAX, 1>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_STORE) return launch_strip<QT, PRO_RMSNORM, EPI_STORE, 1>(a, st);
   if (pro == PRO_RMSNORM && epi == EPI_ARGMAX) {
     // a streamed LM head (the decode step's): 1,032 vs 1,005 tok/s for the
     // plain-layout Qwen3-1.7B-shape decode
@@ -899,12 +916,6 @@ static hipError_t dispatch_plain_qt(const GemvArgs& a, int pro, int epi, hipStre
     return launch_strip<QT, PRO_RMSNORM, EPI_ARGMAX, 1>(a, st);
   }
   if (pro == PRO_Q8X && epi == EPI_STORE) return launch_strip<QT, PRO_Q8X, EPI_STORE, 1>(a, st);
-  if (pro == PRO_RMSNORM && epi == EPI_SWIGLU) return launch_strip<QT, PRO_RMSNORM, EPI_SWIGLU, 1>(a, st);
-  if constexpr (QT == Q4_0) {
-    if (pro == PRO_ATTN && epi == EPI_RESID && a.attn_nsplit >= 1 && a.attn_nsplit <= kAttnSplits &&
-        a.attn_hd % 8 == 0 && a.k % a.attn_hd == 0)
-      return launch_strip<QT, PRO_ATTN, EPI_RESID, 1>(a, st);
-  }
   return hipErrorInvalidValue;
 }
 

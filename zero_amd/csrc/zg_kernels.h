@@ -46,6 +46,10 @@ struct GemvArgs {
   // sync_add (the step counter times the layer count plus the layer)
   const uint32_t* sync_epoch;
   uint32_t sync_mul, sync_add;
+  // tagged stores: when sync_drop is non-null and *sync_drop == sync_add + 1,
+  // the launch skips its tagged row stores (a test of the readers' bounded
+  // wait: they give up and report the timeout; 0 drops nothing)
+  const uint32_t* sync_drop;
   // PRO_RMSNORM: workgroup 0 also stores the normalized x here (k floats)
   // when non-null, for a following GEMV without the prologue
   float* xn_out;

@@ -100,20 +100,36 @@ __device__ __forceinline__ void embed_row(const uint8_t* __restrict__ embd, uint
 // as the reference builds its sin/cos table once per token
 // (trig.rs:148-216): cs[i] = cos(pos * inv_freq[i]), cs[half + i] =
 // sin(pos * inv_freq[i]).
-__global__ void embed_kernel(const uint8_t* __restrict__ embd, uint32_t qt, int hidden,
-                             DevState* __restrict__ st, uint64_t* __restrict__ best,
-                             float* __restrict__ out, const float* __restrict__ inv_freq, int half,
-                             float* __restrict__ rope_cs, uint32_t* __restrict__ epoch) {
-  const uint32_t tok = st->token;
-  // the step counter of the fused Q|K|V + attention launches
-  if (threadIdx.x == 0) *epoch += 1;
-  if ((int)threadIdx.x < half) {
-    const float th = (float)st->pos * inv_freq[threadIdx.x];
-    rope_cs[threadIdx.x] = cosf(th);
-    rope_cs[half + threadIdx.x] = sinf(th);
+struct EmbedArgs {
+  const uint8_t* embd;
+  uint32_t qt;
+  int hidden;
+  float* out;  // the residual stream
+  const float* inv_freq;
+  int half;
+  float* rope_cs;
+  uint32_t* epoch;  // step counter of the fused Q|K|V + attention launches
+  uint64_t* best;   // LM-head argmax slot
+};
+
+// The start of a step at (tok, pos): step counter, argmax slot, RoPE table,
+// embedding row.  Thread 0 writes the shared words; the caller has read
+// everything it needs from them.
+__device__ __forceinline__ void step_start(const EmbedArgs& e, uint32_t tok, uint32_t pos) {
+  if (threadIdx.x == 0) {
+    *e.epoch += 1;
+    *e.best = 0;
   }
-  embed_row(embd, qt, hidden, tok, out);
-  if (threadIdx.x == 0) *best = 0;
+  if ((int)threadIdx.x < e.half) {
+    const float th = (float)pos * e.inv_freq[threadIdx.x];
+    e.rope_cs[threadIdx.x] = cosf(th);
+    e.rope_cs[e.half + threadIdx.x] = sinf(th);
+  }
+  embed_row(e.embd, e.qt, e.hidden, tok, e.out);
+}
+
+__global__ void embed_kernel(EmbedArgs e, const DevState* __restrict__ st) {
+  step_start(e, st->token, st->pos);
 }
 
 // Poll bound of the fused attention's wait: 2^13 polls of ~1 us, a few ms,
@@ -581,22 +597,27 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float* __restri
 // After the LM head: argmax -> next token, error bits, output record, then
 // move to the next position.
 // Every input is loaded before the first store (one memory round trip).
-__global__ void finalize_kernel(DevState* __restrict__ st, const uint64_t* __restrict__ best, uint32_t vocab_real,
-                                uint32_t* __restrict__ out_tokens) {
-  const uint64_t key = *best;
-  const uint32_t err0 = st->err, err_step = st->err_step, gen = st->gen, gen_cap = st->gen_cap, pos = st->pos;
-  uint32_t idx = 0;
-  uint32_t err = 0;
+// The LM head's packed argmax key -> token, error bits 0 (non-finite or no
+// candidate) and 1 (padding row).  The token is always a row of the head
+// (0 when there is no candidate), so it indexes the embedding safely.
+__device__ __forceinline__ uint32_t argmax_token(uint64_t key, uint32_t vocab_real, uint32_t& err) {
+  err = 0;
   if (key == 0) {
     err = 1;
-  } else {
-    const uint32_t k = (uint32_t)(key >> 32);
-    const uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
-    const float v = __uint_as_float(b);
-    idx = 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu);
-    if (!isfinite(v)) err = 1;
-    else if (idx >= vocab_real) err = 2;
+    return 0;
   }
+  const uint32_t k = (uint32_t)(key >> 32);
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu);
+  if (!isfinite(__uint_as_float(b))) err = 1;
+  else if (idx >= vocab_real) err = 2;
+  return idx;
+}
+
+// The step's record: error bits, output token, next position (thread 0).
+__device__ __forceinline__ void finalize_state(DevState* __restrict__ st, uint64_t key, uint32_t idx, uint32_t err,
+                                               uint32_t err0, uint32_t err_step, uint32_t gen, uint32_t gen_cap,
+                                               uint32_t pos, uint32_t* __restrict__ out_tokens) {
   if ((err | err0) && err_step == kNoStep) {
     st->err_step = gen;
     st->err_first = err | err0;
@@ -609,11 +630,41 @@ __global__ void finalize_kernel(DevState* __restrict__ st, const uint64_t* __res
   st->pos = pos + 1;
 }
 
-// Move to the next position; during the prompt, feed the next prompt token.
-__global__ void advance_kernel(DevState* st, const uint32_t* prompt) {
-  const uint32_t p = st->pos + 1;
-  st->pos = p;
-  if (p < st->n_prompt) st->token = prompt[p];
+__global__ void finalize_kernel(DevState* __restrict__ st, const uint64_t* __restrict__ best, uint32_t vocab_real,
+                                uint32_t* __restrict__ out_tokens) {
+  const uint64_t key = *best;
+  const uint32_t err0 = st->err, err_step = st->err_step, gen = st->gen, gen_cap = st->gen_cap, pos = st->pos;
+  uint32_t err;
+  const uint32_t idx = argmax_token(key, vocab_real, err);
+  finalize_state(st, key, idx, err, err0, err_step, gen, gen_cap, pos, out_tokens);
+}
+
+// finalize_kernel and the start of the next step in one launch (the step
+// graph of the greedy loop): the token just chosen is embedded at the next
+// position.  Every thread decodes the key itself; the barrier keeps the
+// argmax slot and the state unchanged until every wave has read them.
+__global__ void finalize_embed_kernel(DevState* __restrict__ st, uint32_t vocab_real, uint32_t* __restrict__ out_tokens,
+                                      EmbedArgs e) {
+  const uint64_t key = *e.best;
+  const uint32_t err0 = st->err, err_step = st->err_step, gen = st->gen, gen_cap = st->gen_cap, pos = st->pos;
+  uint32_t err;
+  const uint32_t idx = argmax_token(key, vocab_real, err);
+  __syncthreads();
+  if (threadIdx.x == 0) finalize_state(st, key, idx, err, err0, err_step, gen, gen_cap, pos, out_tokens);
+  step_start(e, idx, pos + 1);
+}
+
+// Move to the next position; during the prompt, feed the next prompt token;
+// then start that step (embedding, RoPE table, step counter).
+__global__ void advance_embed_kernel(DevState* __restrict__ st, const uint32_t* __restrict__ prompt, EmbedArgs e) {
+  const uint32_t p = st->pos + 1, n_prompt = st->n_prompt, tok0 = st->token;
+  const uint32_t tok = p < n_prompt ? prompt[p] : tok0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    st->pos = p;
+    st->token = tok;
+  }
+  step_start(e, tok, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -880,10 +931,12 @@ struct zg_model {
   float* part_ml = nullptr;  // attention split (max, exp-sum) [nsplit][nq]
   uint64_t* best = nullptr;
   zg::DevState* st = nullptr;
-  // qkv_attn_kernel: the step counter (embed_kernel adds one per step;
-  // never reset while the model lives) and the Q|K|V rows as tagged 64-bit
-  // words (the counter of the step that stored the row << 32 | fp32 bits)
-  uint32_t* sync = nullptr;
+  // qkv_attn_kernel: the step counter (every step start adds one: the
+  // embedding launch or the previous step's last launch; never reset while
+  // the model lives) and the Q|K|V rows as tagged 64-bit words (the counter
+  // of the step that stored the row << 32 | fp32 bits)
+  uint32_t* sync = nullptr;  // [0] step counter of the fused launches; [1] test hook: layer + 1 whose
+                             // fused launch skips its tagged stores (0: none)
   uint64_t* qkv_tag = nullptr;
   int cus = 0;  // compute units of the device
   uint32_t* prompt = nullptr;  // device prompt buffer
@@ -894,12 +947,19 @@ struct zg_model {
   bool head_norm = false;  // the LM-head GEMV takes the output rmsnorm itself
   bool pf_ok = false;      // every layer projection Q4_0 / Q8_0 (the batched prefill's GEMMs)
   std::vector<void*> owned;  // device allocations to free
-  // references to the registry's uploaded weight copies this model reads:
-  // they outlive a zg_clear of the context until the model is destroyed
-  std::vector<std::shared_ptr<void>> weight_refs;
-  // g_prefill: embed + layers + advance (prompt tokens before the last);
-  // g_step: embed + layers + LM head + finalize (every step that emits a token)
-  hipGraphExec_t g_prefill = nullptr, g_step = nullptr;
+  // references to the registry's uploaded weight copies this model reads,
+  // each with the device address it resolved to: they outlive a zg_clear of
+  // the context until the model is destroyed (a tensor interleaved into
+  // model memory at creation drops its reference)
+  std::vector<std::pair<const void*, std::shared_ptr<void>>> weight_refs;
+  // Step graphs; each starts at the first layer, its embedding and RoPE
+  // table already in place (start_step before a call's first graph, then
+  // the previous graph's last launch):
+  // g_prefill: layers + advance and the next prompt token's start;
+  // g_step: layers + LM head + finalize and the chosen token's start (the
+  // greedy loop); g_step_host: layers + LM head + finalize (zg_model_step,
+  // which returns the step's final hidden state)
+  hipGraphExec_t g_prefill = nullptr, g_step = nullptr, g_step_host = nullptr;
   // batched prefill: row buffers for chunks of up to pf_cap tokens,
   // allocated on first use
   size_t pf_cap = 0;
@@ -960,7 +1020,7 @@ static zg_status weight_dev(zg_model* m, const void* key, uint32_t qt, uint32_t 
   if (got_il != il) return set_error(m->ctx, ZG_ERR_INVALID_ARG, "model: weight %p layout %u, expected %u", key, got_il, il);
   if (hold) {
     try {
-      m->weight_refs.push_back(std::move(hold));
+      m->weight_refs.emplace_back(*out, std::move(hold));
     } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
       return set_error(m->ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
     }
@@ -1041,6 +1101,7 @@ static zg_status run_qkv_attn(zg_model* m, uint32_t l, const ZLayer& L, AttnArgs
   ga.seg[2].y = reinterpret_cast<float*>(m->qkv_tag + qd + kvd);
   // one tag per step and layer: the buffer is shared by the layers
   ga.sync_epoch = m->sync;
+  ga.sync_drop = m->sync + 1;
   ga.sync_mul = d.n_layers;
   ga.sync_add = l;
   aa.tagged = m->qkv_tag;
@@ -1052,18 +1113,17 @@ static zg_status run_qkv_attn(zg_model* m, uint32_t l, const ZLayer& L, AttnArgs
   const size_t shm = 2 * 4 * 2 * 16 * sizeof(float);  // the strip body's [2][4 waves][2 groups][16] partials
   const uint32_t qt = L.qt[ZG_PROJ_Q], il = L.il[ZG_PROJ_Q];
 #define ZG_QKV_ATTN(QT, IL, HDV) hipLaunchKernelGGL((qkv_attn_kernel<QT, IL, HDV>), grid, block, shm, st, ga, aa, n_attn)
+  // Q4_K rows, or X4 Q4_0 / Q8_0 (plain-row Q4_0 / Q8_0 projections are
+  // interleaved to X4 at model creation)
+  if (qt != ZG_Q4K && il != 4) return set_error(m->ctx, ZG_ERR_UNSUPPORTED_QUANT, "qkv+attention: plain-row Q4_0/Q8_0");
   if (HD == 128) {
     if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 128);
-    else if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 128);
-    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 128);
-    else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 128);
-    else ZG_QKV_ATTN(Q8_0, 1, 128);
+    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 4, 128);
+    else ZG_QKV_ATTN(Q8_0, 4, 128);
   } else {
     if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 64);
-    else if (qt == ZG_Q4_0 && il == 4) ZG_QKV_ATTN(Q4_0, 4, 64);
-    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 1, 64);
-    else if (il == 4) ZG_QKV_ATTN(Q8_0, 4, 64);
-    else ZG_QKV_ATTN(Q8_0, 1, 64);
+    else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 4, 64);
+    else ZG_QKV_ATTN(Q8_0, 4, 64);
   }
 #undef ZG_QKV_ATTN
   return hip_check(m->ctx, hipGetLastError(), "qkv+attention launch");
@@ -1076,10 +1136,7 @@ static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
   const int H = (int)d.hidden, F = (int)d.ffn, HD = (int)d.head_dim;
   const int qd = (int)(d.n_q_heads * d.head_dim), kvd = (int)(d.n_kv_heads * d.head_dim);
   zg_ctx* ctx = m->ctx;
-  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, m->embd, d.embd_type, H, m->st, m->best, m->hidden,
-                     m->inv_freq, HD / 2, m->rope_cs, m->sync);
-  zg_status s = hip_check(ctx, hipGetLastError(), "embed launch");
-  if (s) return s;
+  zg_status s = ZG_OK;
   const float scale = 1.0f / sqrtf((float)HD);
   for (uint32_t l = 0; l < d.n_layers; l++) {
     const ZLayer& L = m->layers[l];
@@ -1184,14 +1241,52 @@ static zg_status record_layers(zg_model* m, hipStream_t st, bool diag = false) {
   return ZG_OK;
 }
 
+static EmbedArgs embed_args(const zg_model* m) {
+  EmbedArgs e;
+  e.embd = m->embd;
+  e.qt = m->d.embd_type;
+  e.hidden = (int)m->d.hidden;
+  e.out = m->hidden;
+  e.inv_freq = m->inv_freq;
+  e.half = (int)m->d.head_dim / 2;
+  e.rope_cs = m->rope_cs;
+  e.epoch = m->sync;
+  e.best = m->best;
+  return e;
+}
+
+// Start the step the state names (token, pos): issued by the host before
+// the first layer launch of a call; after that every step graph starts the
+// next step in its last launch.
+static zg_status start_step(zg_model* m, hipStream_t st) {
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, st, embed_args(m), m->st);
+  return hip_check(m->ctx, hipGetLastError(), "embed launch");
+}
+
+// A prompt token through the layers, then the next prompt token's start.
 static zg_status record_prefill(zg_model* m, hipStream_t st) {
   zg_status s = record_layers(m, st);
   if (s) return s;
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->st, m->prompt);
+  hipLaunchKernelGGL(advance_embed_kernel, dim3(1), dim3(256), 0, st, m->st, m->prompt, embed_args(m));
   return hip_check(m->ctx, hipGetLastError(), "advance launch");
 }
 
+// A token through the layers and the LM head, then the start of the step of
+// the token it chose (the greedy loop: no launch of its own for the embedding).
 static zg_status record_step(zg_model* m, hipStream_t st) {
+  const zg_model_desc& d = m->d;
+  zg_status s = record_layers(m, st);
+  if (s) return s;
+  s = head_argmax(m, m->hidden, st);
+  if (s) return s;
+  hipLaunchKernelGGL(finalize_embed_kernel, dim3(1), dim3(256), 0, st, m->st, d.vocab_real, m->out_tokens,
+                     embed_args(m));
+  return hip_check(m->ctx, hipGetLastError(), "finalize launch");
+}
+
+// The same without the next step's start: zg_model_step returns this step's
+// final hidden state, which the next embedding would overwrite.
+static zg_status record_step_host(zg_model* m, hipStream_t st) {
   const zg_model_desc& d = m->d;
   zg_status s = record_layers(m, st);
   if (s) return s;
@@ -1336,7 +1431,8 @@ static zg_status prefill_run(zg_model* m, size_t off, size_t n, uint32_t pos0, s
   if (s) return s;
   s = head_argmax(m, m->pf_x + (rows - 1) * d.hidden, st);
   if (s) return s;
-  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, st, m->st, m->best, d.vocab_real, m->out_tokens);
+  hipLaunchKernelGGL(finalize_embed_kernel, dim3(1), dim3(256), 0, st, m->st, d.vocab_real, m->out_tokens,
+                     embed_args(m));
   *last_rows = rows;
   return hip_check(m->ctx, hipGetLastError(), "finalize launch");
 }
@@ -1376,7 +1472,6 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   zg_model* m = new (std::nothrow) zg_model();
   if (!m) return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
   m->ctx = ctx;
-  ctx->live_models++;  // released by zg_model_destroy (also on the error path below)
   m->d = d;
   m->d.layers = nullptr;
   m->d.layer_quants = nullptr;
@@ -1386,9 +1481,10 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     m->layers.resize(d.n_layers);
     m->owned.reserve(40 + 4 * (size_t)d.n_layers);  // room for every buffer the model allocates
   } catch (const std::bad_alloc&) {  // no exception crosses the C ABI
-    delete m;
+    delete m;  // not yet counted: the context stays destroyable
     return set_error(ctx, ZG_ERR_OUT_OF_MEMORY, "model: host allocation");
   }
+  ctx->live_models++;  // released by zg_model_destroy (also on the error path below)
   for (uint32_t l = 0; l < d.n_layers && !s; l++) {
     const zg_layer_weights& W = d.layers[l];
     ZLayer& L = m->layers[l];
@@ -1428,6 +1524,19 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   }
   if (!s) s = repack_x4(m, &m->head, d.head_type, &m->d.head_interleave, d.vocab_padded, H);
   if (!s) s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "model: interleave");
+  if (!s) {
+    // the interleave copies have landed: registry uploads that no tensor of
+    // the model reads any more (every repacked plain-row tensor's) are
+    // released, so a zg_clear frees them instead of the model keeping two
+    // copies of those weights alive
+    std::vector<const void*> used = {m->embd, m->head};
+    for (const ZLayer& L : m->layers)
+      for (const uint8_t* w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) used.push_back(w);
+    auto unused = [&](const std::pair<const void*, std::shared_ptr<void>>& e) {
+      return std::find(used.begin(), used.end(), e.first) == used.end();
+    };
+    m->weight_refs.erase(std::remove_if(m->weight_refs.begin(), m->weight_refs.end(), unused), m->weight_refs.end());
+  }
   if (!s && !d.output_norm) s = set_error(ctx, ZG_ERR_INVALID_ARG, "model: null output_norm");
   if (!s) s = upload_f32(m, &m->out_norm, d.output_norm, H);
   if (!s) {
@@ -1468,7 +1577,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->part_ml), (size_t)m->nsplit * d.n_q_heads * 2 * sizeof(float));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->best), sizeof(uint64_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->st), sizeof(DevState));
-  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->sync), sizeof(uint32_t));
+  if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->sync), 2 * sizeof(uint32_t));
   if (!s) s = model_alloc(m, reinterpret_cast<void**>(&m->qkv_tag), (qd + 2 * kvd) * sizeof(uint64_t));
   if (!s) {
     int cus = 0;
@@ -1513,10 +1622,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       L.gu_kq = !L.gu_one && kq_swiglu_ok(qt[ZG_PROJ_GATE], qt[ZG_PROJ_UP], il[ZG_PROJ_GATE], il[ZG_PROJ_UP], H,
                                           L.gate, L.up, m->hidden, L.ffn_norm);
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
-      L.o_merge = m->nsplit > 1 &&
-                  ((attn_merge_gemv_ok(ot, oil, qd) && (oil == 4 ? pair_path_ok(ot, oil, qd, H, L.o, m->part_o)
-                                                                 : plain_strip_ok(ot, oil, qd, H, L.o, m->part_o))) ||
-                   kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
+      L.o_merge = m->nsplit > 1 && ((attn_merge_gemv_ok(ot, oil, qd) && pair_path_ok(ot, oil, qd, H, L.o, m->part_o)) ||
+                                    kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
       for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
       // Q|K|V and attention in one launch: Q4_0 / Q8_0 / Q4_K of one type and
       // layout on the one-launch strip path, in_dim 2048 (four strips, the
@@ -1534,6 +1641,7 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
   }
   if (!s) s = capture(m, record_prefill, &m->g_prefill);
   if (!s) s = capture(m, record_step, &m->g_step);
+  if (!s) s = capture(m, record_step_host, &m->g_step_host);
   if (s) {
     zg_model_destroy(m);
     return s;
@@ -1547,7 +1655,7 @@ extern "C" void zg_model_destroy(zg_model* m) {
   zg_ctx* ctx = m->ctx;
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
-  for (hipGraphExec_t g : {m->g_prefill, m->g_step})
+  for (hipGraphExec_t g : {m->g_prefill, m->g_step, m->g_step_host})
     if (g) hipGraphExecDestroy(g);
   for (void* p : m->owned) hipFree(p);
   delete m;  // drops the weight references: copies cleared from the registry are freed here
@@ -1604,7 +1712,7 @@ static void localise_nonfinite(zg_model* m, uint32_t p_fail) {
   const uint32_t q = kv_hit ? h.kv_key >> 8 : p_fail;
   uint32_t row = 0;
   if (m->row_kind[q] == kRowDecode) {
-    if (set_state(m, m->row_token[q], q, 0, 0) || record_layers(m, st, true)) return;
+    if (set_state(m, m->row_token[q], q, 0, 0) || start_step(m, st) || record_layers(m, st, true)) return;
   } else if (kv_hit) {
     // a cache row the decode step cannot reproduce: name it
     const uint32_t slot = h.kv_key & 0xFFu;
@@ -1665,6 +1773,16 @@ extern "C" void zg_model_reset(zg_model* m) {
   m->nf_len = 0;
 }
 
+extern "C" zg_status zg_model_test_drop_qkv_stores(zg_model* m, int32_t layer) {
+  if (!m) return ZG_ERR_INVALID_ARG;
+  hipSetDevice(m->ctx->device);
+  const uint32_t v = layer < 0 ? 0u : (uint32_t)layer + 1u;
+  zg_status s = hip_check(m->ctx, hipMemcpyAsync(m->sync + 1, &v, sizeof v, hipMemcpyHostToDevice, m->ctx->stream),
+                          "drop hook upload");
+  if (!s) s = hip_check(m->ctx, hipStreamSynchronize(m->ctx->stream), "drop hook upload");
+  return s;
+}
+
 extern "C" size_t zg_model_first_nonfinite(const zg_model* m, char* buf, size_t cap) {
   if (!m || !buf) return 0;
   const size_t n = std::min(m->nf_len, cap);
@@ -1681,8 +1799,9 @@ extern "C" zg_status zg_model_step(zg_model* m, uint32_t token, uint32_t pos, fl
   hipSetDevice(ctx->device);
   note_rows(m, pos, &token, 1, kRowDecode);
   zg_status s = set_state(m, token, pos, 0, 0);
+  if (!s) s = start_step(m, ctx->stream);
   if (s) return s;
-  if ((s = hip_check(ctx, hipGraphLaunch(m->g_step, ctx->stream), "graph launch"))) return s;
+  if ((s = hip_check(ctx, hipGraphLaunch(m->g_step_host, ctx->stream), "graph launch"))) return s;
   zg::DevState h{};
   if ((s = hip_check(ctx, hipMemcpyAsync(&h, m->st, sizeof h, hipMemcpyDeviceToHost, ctx->stream), "state download")))
     return s;
@@ -1775,6 +1894,7 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
   } else {
     // prompt tokens 0..n-2 through the layers one by one; the last one also
     // through the LM head, producing generated token 0
+    if ((s = start_step(m, ctx->stream))) return s;
     for (size_t i = 0; i + 1 < n_prompt; i++)
       if ((s = run_one(false))) return s;
     if ((s = run_one(true))) return s;

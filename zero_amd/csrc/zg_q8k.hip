@@ -154,12 +154,18 @@ __device__ __forceinline__ void q4k_q8k_lane(const Q4kW& L, const Q8kX& x, int l
   scale_min_i(s, 2 * j + 1, scB, mB);
   const uint32_t q[4] = {L.q.x, L.q.y, L.q.z, L.q.w};
   const uint32_t xa[4] = {x.qa.x, x.qa.y, x.qa.z, x.qa.w}, xb[4] = {x.qb.x, x.qb.y, x.qb.z, x.qb.w};
-  int sa = 0, sbv = 0;
+  // four chains (a dependent v_dot4_i32_i8 issues ~16 cycles after its
+  // predecessor); integer sums, so the split leaves the result unchanged
+  int sa = 0, sbv = 0, sa1 = 0, sb1 = 0;
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
+  for (int c = 0; c < 4; c += 2) {
     sa = __builtin_amdgcn_sdot4((int)(q[c] & 0x0F0F0F0Fu), (int)xa[c], sa, false);
     sbv = __builtin_amdgcn_sdot4((int)((q[c] >> 4) & 0x0F0F0F0Fu), (int)xb[c], sbv, false);
+    sa1 = __builtin_amdgcn_sdot4((int)(q[c + 1] & 0x0F0F0F0Fu), (int)xa[c + 1], sa1, false);
+    sb1 = __builtin_amdgcn_sdot4((int)((q[c + 1] >> 4) & 0x0F0F0F0Fu), (int)xb[c + 1], sb1, false);
   }
+  sa += sa1;
+  sbv += sb1;
   isum = scA * sa + scB * sbv;
   msum = mA * x.bsa + mB * x.bsb;
 }

@@ -267,18 +267,22 @@ __device__ __forceinline__ float strip_dot_dig(const LaneW<QT>& L, const XDig& X
 // term of zo_gemm_q8act.
 template <uint32_t QT>
 __device__ __forceinline__ float strip_dot_q8x(const LaneW<QT>& L, const uint32_t* x8, float dx, int sx) {
-  int isum = 0;
+  // four independent chains (a dependent v_dot4_i32_i8 issues ~16 cycles
+  // after its predecessor); integer sums, so the order is free
+  int s4[4] = {0, 0, 0, 0};
   if (QT == Q4_0) {
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      isum = __builtin_amdgcn_sdot4((int)(L.q[c] & 0x0F0F0F0Fu), (int)x8[c], isum, false);
-      isum = __builtin_amdgcn_sdot4((int)((L.q[c] >> 4) & 0x0F0F0F0Fu), (int)x8[4 + c], isum, false);
+      s4[(c & 1) * 2] = __builtin_amdgcn_sdot4((int)(L.q[c] & 0x0F0F0F0Fu), (int)x8[c], s4[(c & 1) * 2], false);
+      s4[(c & 1) * 2 + 1] =
+          __builtin_amdgcn_sdot4((int)((L.q[c] >> 4) & 0x0F0F0F0Fu), (int)x8[4 + c], s4[(c & 1) * 2 + 1], false);
     }
-    isum -= 8 * sx;
   } else {
 #pragma unroll
-    for (int c = 0; c < 8; c++) isum = __builtin_amdgcn_sdot4((int)L.q[c], (int)x8[c], isum, false);
+    for (int c = 0; c < 8; c++) s4[c & 3] = __builtin_amdgcn_sdot4((int)L.q[c], (int)x8[c], s4[c & 3], false);
   }
+  int isum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  if (QT == Q4_0) isum -= 8 * sx;
   return (half_bits_to_f32(L.d) * dx) * (float)isum;
 }
 
@@ -523,6 +527,7 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
   LaneW<QT> LA[GBATCH][PARTS], LB[GBATCH][PARTS];
   const int b0 = bid, bstep = nblk;
   const uint32_t sig_tag = SIG ? *a.sync_epoch * a.sync_mul + a.sync_add : 0u;  // this step and layer's tag
+  const bool sig_drop = SIG && a.sync_drop && *a.sync_drop == a.sync_add + 1;
   load_batch(LA, b0);
 
   // prologue and block sum
@@ -702,7 +707,8 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
             // step and layer's tag, as one agent-scope 64-bit store (the
             // reader takes a row once it carries that tag)
             const uint64_t tw = ((uint64_t)sig_tag << 32) | (uint64_t)__float_as_uint(v);
-            __hip_atomic_store(reinterpret_cast<uint64_t*>(sg.y) + row, tw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (!sig_drop)
+              __hip_atomic_store(reinterpret_cast<uint64_t*>(sg.y) + row, tw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else {
             if (sg.y) sg.y[row] = v;
             if (EPI == EPI_ARGMAX && !(v != v)) {
