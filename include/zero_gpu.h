@@ -196,6 +196,27 @@ zg_status zg_quantize_q8_0_split_dev(zg_ctx *ctx, const float *d_x, int8_t *d_qs
 zg_status zg_gemm_q8act_dev(zg_ctx *ctx, const int8_t *d_qs, const uint16_t *d_d, const void *d_w,
                             float *d_y, size_t m, size_t n, size_t k, uint32_t w_type,
                             uint32_t interleave, void *stream);
+/* The K-quant prefill GEMM's activation operand: quantize_row_q8k
+ * (kernel/src/arch/x86_64/math/vnni.rs:78-170, the arithmetic of
+ * zg_quantize_q8k_dev) of rows x k values (k % 256 == 0), written as three
+ * arrays: int8 qs[rows][k] (4-byte aligned; 16 for the GEMM), f32
+ * d8[rows][k/256] and int16 bs32[rows][k/32], the sums of 32 quants
+ * (bsum[2g] + bsum[2g+1] of the reference's block).  Bit-exact. */
+zg_status zg_quantize_q8k_split_dev(zg_ctx *ctx, const float *d_x, int8_t *d_qs, float *d_d8,
+                                    int16_t *d_bs32, size_t rows, size_t k, void *stream);
+/* Prefill GEMM for K-quant weights on int8 MFMA: Y[m][n] (+)= X[m] . W[n]
+ * for split Q8_K activations (zg_quantize_q8k_split_dev) and plain Q4_K or
+ * Q6_K rows (w_type 12 / 14; n % 64 == 0, k % 256 == 0, qs and d8 16-byte
+ * aligned).  Each output is linear_q4k_vnni_range's arithmetic
+ * (kernel/src/arch/x86_64/math/vnni.rs:258-476) bit for bit: per superblock
+ * the exact integer sums, then dot += (d_w d8) int_sum, min += (dmin_w d8)
+ * min_sum, y = dot - min; Q6_K the same construction with (q - 32) and its
+ * 16 int8 scales, y += (d_w d8) int_sum.  accumulate != 0 adds the result
+ * to Y.  No reference counterpart as a GEMM: the reference prefills token by
+ * token (kernel/src/inference.rs:1188-1330). */
+zg_status zg_gemm_q8k_dev(zg_ctx *ctx, const int8_t *d_qs, const float *d_d8, const int16_t *d_bs32,
+                          const void *d_w, float *d_y, size_t m, size_t n, size_t k, uint32_t w_type,
+                          int accumulate, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Forward pass.                                                        */

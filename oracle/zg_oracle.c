@@ -1119,6 +1119,48 @@ int zo_linear_q4k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, si
     return 0;
 }
 
+/* Q6_K x Q8_K: the integer construction of linear_q4k_vnni_range applied to
+ * the Q6_K layout.  No reference counterpart (the reference's integer path,
+ * vnni.rs:258-476, covers Q4_K only); it is the arithmetic of the K-quant
+ * prefill GEMM.  Element e of a superblock (dequant.rs:328-355: half n =
+ * e / 128, quarter Q = (e % 128) / 32, l = e % 32) has the 6-bit value
+ * ((ql[64n + l + 32(Q & 1)] >> 4(Q >> 1)) & 15) | (((qh[32n + l] >> 2Q) & 3) << 4)
+ * and the int8 scale sc[e / 16].  Per row, per superblock b in order:
+ * int_sum = sum_g sc_g * sum_{e in 16g..16g+15} (q6_e - 32) * q8_e (exact),
+ * sumf = sumf + (d_w * d_q8) * (float)int_sum. */
+int zo_linear_q6k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, size_t in_dim, size_t start,
+                            size_t end) {
+    if (in_dim % 256) return -1;
+    size_t nb = in_dim / 256;
+    for (size_t r = start; r < end; r++) {
+        float sumf = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t *wb = w + (r * nb + b) * 210;
+            const uint8_t *xb = q8k + b * ZO_Q8K_BYTES;
+            const uint8_t *ql = wb, *qh = wb + 128;
+            const int8_t *sc = (const int8_t *)(wb + 192);
+            const int8_t *q8 = (const int8_t *)(xb + 4);
+            float dq8;
+            memcpy(&dq8, xb, 4);
+            int64_t int_sum = 0;
+            for (int g = 0; g < 16; g++) {
+                int32_t sub = 0;
+                for (int i = 0; i < 16; i++) {
+                    int e = 16 * g + i, n = e / 128, Q = (e % 128) / 32, l = e % 32;
+                    int lo4 = (ql[64 * n + l + 32 * (Q & 1)] >> (4 * (Q >> 1))) & 15;
+                    int hi2 = (qh[32 * n + l] >> (2 * Q)) & 3;
+                    sub += ((lo4 | (hi2 << 4)) - 32) * (int32_t)q8[e];
+                }
+                int_sum += (int64_t)sub * (int64_t)sc[g];
+            }
+            float dc = rd_fp16(wb + 208) * dq8;
+            sumf = sumf + dc * (float)int_sum;
+        }
+        out[r] = sumf;
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------ */
 /* Full forward pass.  forward_single_token_avx512                      */
 /* (kernel/src/inference_avx512.rs:1826-1987) with the attention block   */

@@ -139,6 +139,10 @@ void zo_quantize_row_q8k(const float *x, uint8_t *out, size_t n);
 void zo_unpack_mins_and_scales(const uint8_t *s12, uint8_t *out16);
 int zo_linear_q4k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, size_t in_dim, size_t start,
                             size_t end);
+/* the same integer construction on Q6_K rows (no reference counterpart:
+ * the K-quant prefill GEMM's arithmetic) */
+int zo_linear_q6k_q8k_range(const uint8_t *q8k, const uint8_t *w, float *out, size_t in_dim, size_t start,
+                            size_t end);
 
 /* ---- full single-token forward pass for a Qwen3-shaped model
  *      (inference_avx512.rs:1826-1987 order; scalar crate ops for norms,

@@ -88,6 +88,7 @@ _SIG = {
     "zo_quantize_row_q8k": (None, [_P, _P, _S]),
     "zo_unpack_mins_and_scales": (None, [_P, _P]),
     "zo_linear_q4k_q8k_range": (_I, [_P, _P, _P, _S, _S, _S]),
+    "zo_linear_q6k_q8k_range": (_I, [_P, _P, _P, _S, _S, _S]),
 }
 
 _lib = None
@@ -252,6 +253,26 @@ def linear_q4k_q8k(q8k, w, in_dim, out_dim, start=0, end=None) -> np.ndarray:
     out = np.zeros(out_dim, np.float32)
     assert load().zo_linear_q4k_q8k_range(_p(q8k), _p(w), _p(out), in_dim, start, end) == 0
     return out
+
+
+def linear_q6k_q8k(q8k, w, in_dim, out_dim, start=0, end=None) -> np.ndarray:
+    """The Q6_K x Q8_K integer construction over rows [start, end)."""
+    end = out_dim if end is None else end
+    out = np.zeros(out_dim, np.float32)
+    assert load().zo_linear_q6k_q8k_range(_p(q8k), _p(w), _p(out), in_dim, start, end) == 0
+    return out
+
+
+def gemm_q8k(x, w, m, n, k, w_type) -> np.ndarray:
+    """The K-quant prefill GEMM's arithmetic, row by row: each of the m rows
+    of x (fp32, [m][k]) quantized to Q8_K, then the integer dot with the n
+    Q4_K (w_type 12) or Q6_K (14) rows of w."""
+    x = np.ascontiguousarray(x, np.float32).reshape(m, k)
+    f = linear_q4k_q8k if w_type == 12 else linear_q6k_q8k
+    y = np.empty((m, n), np.float32)
+    for i in range(m):
+        y[i] = f(quantize_q8k(x[i]), w, k, n)
+    return y
 
 
 def nonfinite_text(buf, layer: int, stage: str) -> str:

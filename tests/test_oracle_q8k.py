@@ -117,3 +117,56 @@ def test_linear_q4k_q8k_kat(zo):
     got = zo.linear_q4k_q8k(q8, blk, 256, 1)[0]
     # sc_g = 1 for g < 4 and (1 | (0 << 4)) = 1 for g >= 4: int_sum = 256 * 1 * -127
     assert got == np.float32(d8) * np.float32(256 * -127)
+
+
+@pytest.mark.parametrize("rows,k", [(16, 256), (40, 2048), (5, 6144)])
+def test_linear_q6k_q8k_vs_f64(zo, rows, k):
+    """The Q6_K x Q8_K integer construction (the K-quant prefill GEMM's
+    arithmetic) against an f64 brute force over the dequantized Q6_K weights
+    (dequant.rs:328-355, pinned by the reference's KATs) and the dequantized
+    Q8_K activations: a wrong element, scale or -32 mapping would not come
+    within 1e-5."""
+    rng = np.random.default_rng(3 * rows + k)
+    w = synth.weight(rng, 14, rows, k, 1)
+    x = synth.activations(rng, k)
+    q8 = zo.quantize_q8k(x)
+    got = zo.linear_q6k_q8k(q8, w, k, rows)
+    wd = zo.dequant(w, rows, k, 14).astype(np.float64)
+    ref = wd @ _q8k_dequant(q8, k)
+    err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    assert err < 1e-5, err
+    part = zo.linear_q6k_q8k(q8, w, k, rows, start=1, end=4)
+    assert np.array_equal(part[1:4], got[1:4]) and not part[:1].any() and not part[4:].any()
+    fp = zo.linear_range(x, w, k, rows, 14)
+    q_err = np.max(np.abs(got - fp)) / np.max(np.abs(fp))
+    assert 1e-5 < q_err < 3e-2, q_err
+
+
+def test_linear_q6k_q8k_kat(zo):
+    """One superblock, d = 1, every scale 2, every 6-bit value 33 (low
+    nibbles 1, high bits 2: q - 32 = 1); activations all 1.0 (q8 = -127,
+    d8 = -1/127): int_sum = 256 * 2 * -127, out = d8 * int_sum."""
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = 0x11
+    blk[128:192] = 0xAA
+    blk[192:208] = 2
+    blk[208:210] = np.array([0x3C00], np.uint16).view(np.uint8)
+    assert np.all(zo.dequant(blk, 1, 256, 14) == 2.0)
+    x = np.ones(256, np.float32)
+    q8 = zo.quantize_q8k(x)
+    d8 = q8[:4].view(np.float32)[0]
+    got = zo.linear_q6k_q8k(q8, blk, 256, 1)[0]
+    assert got == np.float32(np.float32(1.0) * d8) * np.float32(256 * 2 * -127)
+
+
+def test_gemm_q8k_rows_are_per_row_dots(zo):
+    """gemm_q8k is the per-row Q8_K quantization and integer dot."""
+    rng = np.random.default_rng(5)
+    m, n, k = 3, 8, 512
+    x = synth.activations(rng, m * k).reshape(m, k)
+    for wt in (12, 14):
+        w = synth.weight(rng, wt, n, k, 1)
+        y = zo.gemm_q8k(x, w, m, n, k, wt)
+        f = zo.linear_q4k_q8k if wt == 12 else zo.linear_q6k_q8k
+        for i in range(m):
+            assert np.array_equal(y[i], f(zo.quantize_q8k(x[i]), w, k, n))

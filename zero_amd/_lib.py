@@ -139,6 +139,8 @@ SIGNATURES = {
     "zg_quantize_q8_0_dev": (_ST, [_P, _P, _P, _S, _S, _P]),
     "zg_quantize_q8_0_split_dev": (_ST, [_P, _P, _P, _P, _S, _S, _P]),
     "zg_gemm_q8act_dev": (_ST, [_P, _P, _P, _P, _P, _S, _S, _S, _U32, _U32, _P]),
+    "zg_quantize_q8k_split_dev": (_ST, [_P, _P, _P, _P, _P, _S, _S, _P]),
+    "zg_gemm_q8k_dev": (_ST, [_P, _P, _P, _P, _P, _P, _S, _S, _S, _U32, C.c_int, _P]),
     "zg_model_create": (_ST, [_P, C.POINTER(zg_model_desc), C.POINTER(_P)]),
     "zg_model_destroy": (None, [_P]),
     "zg_model_step": (_ST, [_P, _U32, _U32, _P, _P, C.POINTER(_U32), C.POINTER(C.c_float)]),

@@ -508,4 +508,51 @@ __device__ __forceinline__ void xdig_chains(const uint32_t (&q)[8], const XDig& 
   t2 += u2;
 }
 
+// quantize_row_q8k (kernel/src/arch/x86_64/math/vnni.rs:78-170) for one
+// 256-value block v, one wave, four values per lane (e = v[4 lane .. + 4)):
+//   max_val  the first value of largest magnitude (strict > scan: ties keep
+//            the lower index; NaN never wins): the (|v| bits, ~index) key is
+//            order-preserving for non-negative floats
+//   q        rintf(e * iscale), iscale = -127 / max_val, clamped to
+//            [-128, 127] (NaN -> 0, as Rust's `as i32` saturates)
+//   d        1 / iscale
+// An all-zero block gives q = 0 and d = 0.  Returns the lane's four quants
+// as little-endian bytes; q holds their values.
+__device__ __forceinline__ uint32_t q8k_block_lane(const float* __restrict__ v, int lane, const float (&e)[4],
+                                                   int (&q)[4], float& d) {
+  float best = 0.0f;
+  int bi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float av = fabsf(e[i]);
+    if (av > best) {
+      best = av;
+      bi = 4 * lane + i;
+    }
+  }
+  uint64_t key = ((uint64_t)__float_as_uint(best) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)bi);
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    const uint64_t other = __shfl_xor(key, s, 64);
+    key = other > key ? other : key;
+  }
+  if (__uint_as_float((uint32_t)(key >> 32)) == 0.0f) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = 0;
+    d = 0.0f;
+    return 0u;
+  }
+  const float max_val = v[0xFFFFFFFFu - (uint32_t)key];
+  const float iscale = -127.0f / max_val;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float t = rintf(e[i] * iscale);
+    q[i] = (t != t) ? 0 : (int)fminf(fmaxf(t, -128.0f), 127.0f);
+    packed |= (uint32_t)(uint8_t)(int8_t)q[i] << (8 * i);
+  }
+  d = 1.0f / iscale;
+  return packed;
+}
+
 }  // namespace zg

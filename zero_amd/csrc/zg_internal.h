@@ -110,6 +110,13 @@ zg_status lm_head_status(zg_ctx* ctx, uint64_t packed, size_t vocab_real, uint32
 
 zg_status run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const GemmSegDev* segs, int nseg, size_t m,
                    size_t k, uint32_t w_type, uint32_t interleave, bool accumulate, hipStream_t st);
+// Q8_K split activations (qs [rows][k], d8 [rows][k/256], bs32 [rows][k/32])
+// and the K-quant (Q4_K / Q6_K, one type per call) prefill GEMM over 1..3
+// segments of widths that are multiples of 64 (zg_kgemm.hip)
+zg_status run_quantize_q8k_split(zg_ctx* ctx, const float* x, int8_t* qs, float* d8, int16_t* bs32, size_t rows,
+                                 size_t k, hipStream_t st);
+zg_status run_gemm_q8k(zg_ctx* ctx, const int8_t* qs, const float* d8, const int16_t* bs32, const GemmSegDev* segs,
+                       int nseg, size_t m, size_t k, uint32_t w_type, bool accumulate, hipStream_t st);
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t st);
 

@@ -1,0 +1,467 @@
+// zg_kgemm.hip -- batched-prefill GEMM for K-quant weights (Q4_K, Q6_K) on
+// Q8_K activations, int8 MFMA, for gfx950.
+//
+// No reference counterpart as a GEMM: the reference prefills token by token
+// (kernel/src/inference.rs:1188-1330).  Per output row it computes the
+// reference's integer Q4_K x Q8_K dot (linear_q4k_vnni_range,
+// kernel/src/arch/x86_64/math/vnni.rs:258-476): per superblock b,
+//   int_sum = sum_g sc_g * sum_{i in sub-block g} nibble_i * q8_i   (exact)
+//   min_sum = sum_g m_g * (bsum[2g] + bsum[2g+1])                  (exact)
+//   dot = dot + (d_w * d8) * (float)int_sum
+//   min = min + (dmin_w * d8) * (float)min_sum,   y = dot - min,
+// the f32 operations in that order, so every output equals the per-row
+// restatement bit for bit.  Q6_K takes the same construction on its layout
+// (dequant.rs:328-355; the reference's integer path has no Q6_K form):
+//   int_sum = sum_g sc_g * sum_{i in g} (q6_i - 32) * q8_i over the 16
+//   sub-blocks of 16, y = y + (d_w * d8) * (float)int_sum.
+//
+// MFMA form.  A weight element times its sub-block scale fits 13 bits
+// (Q4_K: nibble * sc <= 945; Q6_K: (q6 - 32) * sc in [-4096, 4064]), so it is
+// split into two int8 digits, w*sc = 128 hi + lo with lo in [0, 127].  Two
+// v_mfma_i32_16x16x64_i8 chains (one per digit) then accumulate a
+// superblock's whole integer sum, all its sub-blocks, in int32 (|sum| <
+// 256 * 4096 * 128 = 2^27), and int_sum = 128 hi_acc + lo_acc exactly.  The
+// Q4_K min term is one more pair of MFMAs per superblock: the activation's
+// 32-value sums (|s| <= 4096) split the same way against the 8 mins.  The
+// float work is then once per output and superblock, not per sub-block.
+//
+// Tiles: 64 x 64 outputs per 256-thread workgroup (2 x 2 waves of 32 x 32),
+// K staged 128 values (half a superblock) at a time, double-buffered in LDS;
+// the next stage's global loads are issued before the current stage is
+// multiplied.  The weight digits are formed once per workgroup when a stage
+// is written to LDS (packed 16-bit multiplies, two elements per operation).
+#include <hip/hip_runtime.h>
+
+#include "../../include/zero_gpu.h"
+#include "zg_device.h"
+#include "zg_internal.h"
+#include "zg_kernels.h"
+
+using namespace zg;
+
+namespace zg {
+
+constexpr int kKgBM = 64, kKgBN = 64;  // workgroup tile
+constexpr int kKgKS = 128;             // K per stage
+constexpr int kKgRP = kKgKS + 16;      // LDS row pitch (bytes)
+constexpr int kKgSegs = 3;             // weight segments per launch (Q|K|V)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
+
+// ---------------------------------------------------------------------------
+// Q8_K activations as split arrays (qs[row][k] int8, d8[row][k/256] f32,
+// bs32[row][k/32] int16: the sums of 32 quants, bsum[2g] + bsum[2g+1] of the
+// reference's block).  One wave per 256-value block, q8k_block_lane's
+// arithmetic, so the values are the reference quantizer's.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void quantize_q8k_split_kernel(const float* __restrict__ x, int8_t* __restrict__ qs,
+                                                                float* __restrict__ d8, int16_t* __restrict__ bs32,
+                                                                int k) {
+  const int nsb = k / 256;
+  const size_t row = blockIdx.x / nsb;
+  const int sb = blockIdx.x % nsb, lane = threadIdx.x;
+  const float* v = x + row * k + (size_t)sb * 256;
+  const float4 f = reinterpret_cast<const float4*>(v)[lane];
+  const float e[4] = {f.x, f.y, f.z, f.w};
+  int q[4];
+  float d;
+  const uint32_t packed = q8k_block_lane(v, lane, e, q, d);
+  reinterpret_cast<uint32_t*>(qs + row * k + (size_t)sb * 256)[lane] = packed;
+  // sums of 32: eight lanes per sub-block
+  int s = (q[0] + q[1]) + (q[2] + q[3]);
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  if ((lane & 7) == 0) bs32[row * (k / 32) + (size_t)sb * 8 + (lane >> 3)] = (int16_t)s;
+  if (lane == 0) d8[row * nsb + sb] = d;
+}
+
+// ---------------------------------------------------------------------------
+// Weight digits.
+// ---------------------------------------------------------------------------
+
+// get_scale_min_k4 (dequant.rs:75-85) for sub-block g from the Q4_K header's
+// scale words (w1 = scale bytes 0..3, w2 = 4..7, w3 = 8..11).
+__device__ __forceinline__ void kg_scale_min(uint32_t w1, uint32_t w2, uint32_t w3, int g, int& sc, int& m) {
+  const int sh = 8 * (g & 3);
+  const int b1 = (int)((w1 >> sh) & 0xFFu), b2 = (int)((w2 >> sh) & 0xFFu), b3 = (int)((w3 >> sh) & 0xFFu);
+  if (g < 4) {
+    sc = b1 & 63;
+    m = b2 & 63;
+  } else {
+    sc = (b3 & 0xF) | ((b1 >> 6) << 4);
+    m = (b3 >> 4) | ((b2 >> 6) << 4);
+  }
+}
+
+// Four unsigned weight values (one per byte of v, each < 16) times sc
+// (0..63): the digits lo = p & 127, hi = p >> 7 as packed bytes.
+__device__ __forceinline__ void digits_u4(uint32_t v, uint32_t sc2, uint32_t& lo, uint32_t& hi) {
+  const u16x2 p0 = __builtin_bit_cast(u16x2, v & 0x000F000Fu) * __builtin_bit_cast(u16x2, sc2);
+  const u16x2 p1 = __builtin_bit_cast(u16x2, (v >> 8) & 0x000F000Fu) * __builtin_bit_cast(u16x2, sc2);
+  const uint32_t q0 = __builtin_bit_cast(uint32_t, p0), q1 = __builtin_bit_cast(uint32_t, p1);
+  lo = (q0 & 0x007F007Fu) | ((q1 & 0x007F007Fu) << 8);
+  hi = __builtin_bit_cast(uint32_t, p0 >> (unsigned short)7) | (__builtin_bit_cast(uint32_t, p1 >> (unsigned short)7) << 8);
+}
+
+// Four Q6_K values (one per byte of v, each < 64) minus 32, times the signed
+// scale sc: lo = p & 127, hi = p >> 7 (arithmetic, in [-32, 31]) as bytes.
+__device__ __forceinline__ void digits_q6(uint32_t v, uint32_t sc2, uint32_t& lo, uint32_t& hi) {
+  const s16x2 off = {32, 32};
+  const s16x2 e0 = __builtin_bit_cast(s16x2, v & 0x00FF00FFu) - off;
+  const s16x2 e1 = __builtin_bit_cast(s16x2, (v >> 8) & 0x00FF00FFu) - off;
+  const s16x2 p0 = e0 * __builtin_bit_cast(s16x2, sc2), p1 = e1 * __builtin_bit_cast(s16x2, sc2);
+  const uint32_t q0 = __builtin_bit_cast(uint32_t, p0), q1 = __builtin_bit_cast(uint32_t, p1);
+  lo = (q0 & 0x007F007Fu) | ((q1 & 0x007F007Fu) << 8);
+  const uint32_t h0 = __builtin_bit_cast(uint32_t, p0 >> (short)7), h1 = __builtin_bit_cast(uint32_t, p1 >> (short)7);
+  hi = (h0 & 0x00FF00FFu) | ((h1 & 0x00FF00FFu) << 8);
+}
+
+struct KgemmArgs {
+  const int8_t* qs;     // [m][k]
+  const float* d8;      // [m][k/256]
+  const int16_t* bs32;  // [m][k/32]
+  const uint8_t* w[kKgSegs];
+  float* y[kKgSegs];
+  int seg_end[kKgSegs];  // cumulative columns (multiples of 64)
+  int nseg;
+  int accumulate;  // y += product (residual adds)
+  int m, n, k;
+};
+
+// Per-thread staging registers of one stage.
+template <uint32_t WT>
+struct KgStage;
+template <>
+struct KgStage<Q4K> {
+  u32x4 a[2];  // 32 bytes of the A tile
+  u32x4 q, h;  // 16 quant bytes and the 16-byte superblock header
+};
+template <>
+struct KgStage<Q6K> {
+  u32x4 a[2];
+  u32x4 l0, l1, h0, h1;  // 32 ql bytes, 32 qh bytes
+  uint32_t sc;           // the two scale bytes of the lane's quarter (low 16 bits)
+  uint32_t d;            // fp16 d
+};
+
+template <uint32_t WT>
+__global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
+  // the reference rounds every product and sum of the superblock terms on
+  // its own: no fused multiply-add in this function (a pragma here does not
+  // reach the operators inside HIP's __fadd_rn / __fmul_rn, which hipcc
+  // contracts after inlining)
+#pragma clang fp contract(off)
+  constexpr int BM = kKgBM, BN = kKgBN, KS = kKgKS, RP = kKgRP;
+  constexpr int MI = BM / 32, NJ = BN / 32;  // 16 x 16 tiles per wave
+  constexpr int SBB = WT == Q4K ? 144 : 210;
+  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * RP];
+  __shared__ __attribute__((aligned(16))) int8_t Bl[2][BN * RP];
+  __shared__ __attribute__((aligned(16))) int8_t Bh[2][BN * RP];
+  // per superblock (by parity): the 32-value sums split hi / lo [row][8],
+  // the mins [col][8], d8 per row, d / dmin per column
+  __shared__ __attribute__((aligned(16))) int8_t Aml[2][BM * 8], Amh[2][BM * 8], Bmn[2][BN * 8];
+  __shared__ __attribute__((aligned(16))) float Ad8[2][BM];
+  __shared__ float Bd[2][BN], Bdm[2][BN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * BM;
+  const int nt0 = blockIdx.x * BN;
+  const int sg = (a.nseg > 1 && nt0 >= a.seg_end[0]) ? ((a.nseg > 2 && nt0 >= a.seg_end[1]) ? 2 : 1) : 0;
+  const int base = sg == 0 ? 0 : a.seg_end[sg - 1];
+  const int ns = a.seg_end[sg] - base, n0 = nt0 - base;
+  const uint8_t* w = a.w[sg];
+  float* y = a.y[sg];
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const int r16 = lane & 15, rq = (lane >> 4) * 4, kq16 = (lane >> 4) * 16;
+  const int nsb = a.k / 256, nst = 2 * nsb;
+  const size_t wrow = (size_t)nsb * SBB;
+  const int wc = tid >> 2, wp = tid & 3;  // weight staging: column, part (Q4_K 16-byte chunk; Q6_K quarter)
+  const int mlast = a.m - 1;
+
+  KgStage<WT> S;
+  // unconditional loads: rows past m clamp to the last row (their outputs
+  // are dropped)
+  auto stage_load = [&](int st) {
+    const int sb = st >> 1, h = st & 1;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      S.a[i] = *reinterpret_cast<const u32x4*>(a.qs + (size_t)min(m0 + row, mlast) * a.k + sb * 256 + h * KS + ch * 16);
+    }
+    const uint8_t* blk = w + (size_t)(n0 + wc) * wrow + (size_t)sb * SBB;
+    if constexpr (WT == Q4K) {
+      S.h = *reinterpret_cast<const u32x4*>(blk);
+      S.q = *reinterpret_cast<const u32x4*>(blk + 16 + 64 * h + 16 * wp);
+    } else {
+      // quarter wp of half h: ql[64h + 32(wp & 1) .. +32], qh[32h .. +32]
+      const u32x4a2* lp = reinterpret_cast<const u32x4a2*>(blk + 64 * h + 32 * (wp & 1));
+      const u32x4a2* hp = reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * h);
+      const u32x4a2 l0 = lp[0], l1 = lp[1], h0 = hp[0], h1 = hp[1];
+      S.l0 = u32x4{l0.x, l0.y, l0.z, l0.w};
+      S.l1 = u32x4{l1.x, l1.y, l1.z, l1.w};
+      S.h0 = u32x4{h0.x, h0.y, h0.z, h0.w};
+      S.h1 = u32x4{h1.x, h1.y, h1.z, h1.w};
+      S.sc = *reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h + 2 * wp);
+      S.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    }
+  };
+  auto stage_store = [&](int st, int buf) {
+    const int sb = st >> 1, h = st & 1, sp = sb & 1;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<u32x4*>(&As[buf][row * RP + ch * 16]) = S.a[i];
+    }
+    int8_t* bl = &Bl[buf][wc * RP];
+    int8_t* bh = &Bh[buf][wc * RP];
+    if constexpr (WT == Q4K) {
+      // chunk wp: pair j = 2h + wp / 2, elements 16 (wp & 1) .. +16 of
+      // sub-blocks 2j (low nibbles) and 2j + 1 (high nibbles)
+      const int j = 2 * h + (wp >> 1);
+      int scA, mA, scB, mB;
+      kg_scale_min(S.h.y, S.h.z, S.h.w, 2 * j, scA, mA);
+      kg_scale_min(S.h.y, S.h.z, S.h.w, 2 * j + 1, scB, mB);
+      const uint32_t sA2 = (uint32_t)scA * 0x00010001u, sB2 = (uint32_t)scB * 0x00010001u;
+      const int kA = (wp >> 1) * 64 + (wp & 1) * 16, kB = kA + 32;
+      const uint32_t qv[4] = {S.q.x, S.q.y, S.q.z, S.q.w};
+      uint32_t loA[4], hiA[4], loB[4], hiB[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        digits_u4(qv[c] & 0x0F0F0F0Fu, sA2, loA[c], hiA[c]);
+        digits_u4((qv[c] >> 4) & 0x0F0F0F0Fu, sB2, loB[c], hiB[c]);
+      }
+      *reinterpret_cast<u32x4*>(bl + kA) = u32x4{loA[0], loA[1], loA[2], loA[3]};
+      *reinterpret_cast<u32x4*>(bh + kA) = u32x4{hiA[0], hiA[1], hiA[2], hiA[3]};
+      *reinterpret_cast<u32x4*>(bl + kB) = u32x4{loB[0], loB[1], loB[2], loB[3]};
+      *reinterpret_cast<u32x4*>(bh + kB) = u32x4{hiB[0], hiB[1], hiB[2], hiB[3]};
+      if (h == 0 && wp == 0) {
+        Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.h.x & 0xFFFFu));
+        Bdm[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.h.x >> 16));
+        uint32_t mw[2] = {0u, 0u};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+          int s_, m_;
+          kg_scale_min(S.h.y, S.h.z, S.h.w, g, s_, m_);
+          mw[g >> 2] |= (uint32_t)m_ << (8 * (g & 3));
+        }
+        *reinterpret_cast<uint2*>(&Bmn[sp][wc * 8]) = make_uint2(mw[0], mw[1]);
+      }
+    } else {
+      // quarter Q = wp of half h: element 128 h + 32 Q + l (l < 32) is
+      // ((ql[64 h + l + 32 (Q & 1)] >> 4 (Q >> 1)) & 15) | (((qh[32 h + l] >>
+      // 2 Q) & 3) << 4), scale sc[8 h + 2 Q + l / 16]
+      const int nsh = 4 * (wp >> 1), hsh = 2 * wp;
+      const int sc0 = (int)(int8_t)(S.sc & 0xFFu), sc1 = (int)(int8_t)(S.sc >> 8);
+      const uint32_t s02 = ((uint32_t)sc0 & 0xFFFFu) * 0x00010001u, s12 = ((uint32_t)sc1 & 0xFFFFu) * 0x00010001u;
+      const uint32_t lv[8] = {S.l0.x, S.l0.y, S.l0.z, S.l0.w, S.l1.x, S.l1.y, S.l1.z, S.l1.w};
+      const uint32_t hv[8] = {S.h0.x, S.h0.y, S.h0.z, S.h0.w, S.h1.x, S.h1.y, S.h1.z, S.h1.w};
+      uint32_t lo[8], hi[8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const uint32_t q6 = ((lv[c] >> nsh) & 0x0F0F0F0Fu) | (((hv[c] >> hsh) & 0x03030303u) << 4);
+        digits_q6(q6, c < 4 ? s02 : s12, lo[c], hi[c]);
+      }
+      const int k0 = 32 * wp;
+      *reinterpret_cast<u32x4*>(bl + k0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<u32x4*>(bl + k0 + 16) = u32x4{lo[4], lo[5], lo[6], lo[7]};
+      *reinterpret_cast<u32x4*>(bh + k0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<u32x4*>(bh + k0 + 16) = u32x4{hi[4], hi[5], hi[6], hi[7]};
+      if (h == 0 && wp == 0) Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.d & 0xFFFFu));
+    }
+    if (h == 0) {
+      if constexpr (WT == Q4K) {
+        for (int i = tid; i < BM * 8; i += 256) {
+          const int row = i >> 3, g = i & 7;
+          const int v = a.bs32[(size_t)min(m0 + row, mlast) * (a.k / 32) + sb * 8 + g];
+          Aml[sp][i] = (int8_t)(v & 127);
+          Amh[sp][i] = (int8_t)(v >> 7);
+        }
+      }
+      for (int i = tid; i < BM; i += 256) Ad8[sp][i] = a.d8[(size_t)min(m0 + i, mlast) * nsb + sb];
+    }
+  };
+
+  float fdot[MI][NJ][4], fmin[MI][NJ][4];
+  v4i ahi[MI][NJ], alo[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      ahi[i][j] = v4i{0, 0, 0, 0};
+      alo[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < 4; r++) fdot[i][j][r] = fmin[i][j][r] = 0.0f;
+    }
+  stage_load(0);
+  stage_store(0, 0);
+  __syncthreads();
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    if (st + 1 < nst) stage_load(st + 1);
+#pragma unroll
+    for (int kk = 0; kk < KS / 64; kk++) {
+      v4i av[MI], bl[NJ], bh[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; i++) av[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm + 16 * i + r16) * RP + kk * 64 + kq16]);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        bl[j] = *reinterpret_cast<const v4i*>(&Bl[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
+        bh[j] = *reinterpret_cast<const v4i*>(&Bh[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          alo[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bl[j], alo[i][j], 0, 0, 0);
+          ahi[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bh[j], ahi[i][j], 0, 0, 0);
+        }
+    }
+    if (st & 1) {
+      // superblock done: the float terms in the reference's order
+      const int sp = (st >> 1) & 1;
+      long aml[MI], amh[MI], bm[NJ];
+      if constexpr (WT == Q4K) {
+        // min_sum through one MFMA per digit: k = sub-block 0..7 in lanes
+        // 0..15, zeros elsewhere
+#pragma unroll
+        for (int i = 0; i < MI; i++) {
+          aml[i] = lane < 16 ? *reinterpret_cast<const long*>(&Aml[sp][(wm + 16 * i + r16) * 8]) : 0;
+          amh[i] = lane < 16 ? *reinterpret_cast<const long*>(&Amh[sp][(wm + 16 * i + r16) * 8]) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; j++) bm[j] = lane < 16 ? *reinterpret_cast<const long*>(&Bmn[sp][(wn + 16 * j + r16) * 8]) : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        const float4 d8v = *reinterpret_cast<const float4*>(&Ad8[sp][wm + 16 * i + rq]);
+        const float d8r[4] = {d8v.x, d8v.y, d8v.z, d8v.w};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          const float dw = Bd[sp][wn + 16 * j + r16];
+          if constexpr (WT == Q4K) {
+            const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(aml[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(amh[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+            const float dmw = Bdm[sp][wn + 16 * j + r16];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
+              const int msum = (mh[r] << 7) + ml[r];
+              const float dc = dw * d8r[r], dmc = dmw * d8r[r];
+              fdot[i][j][r] = fdot[i][j][r] + dc * (float)isum;
+              fmin[i][j][r] = fmin[i][j][r] + dmc * (float)msum;
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
+              fdot[i][j][r] = fdot[i][j][r] + (dw * d8r[r]) * (float)isum;
+            }
+          }
+          ahi[i][j] = v4i{0, 0, 0, 0};
+          alo[i][j] = v4i{0, 0, 0, 0};
+        }
+      }
+    }
+    if (st + 1 < nst) stage_store(st + 1, buf ^ 1);
+    __syncthreads();
+  }
+  // D layout of v_mfma_*_16x16*: lane l holds rows 4 (l / 16) + r, column l % 16
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int gm = m0 + wm + 16 * i + rq + r;
+        const int gn = n0 + wn + 16 * j + r16;
+        if (gm < a.m) {
+          const float v = WT == Q4K ? fdot[i][j][r] - fmin[i][j][r] : fdot[i][j][r];
+          float* o = y + (size_t)gm * ns + gn;
+          *o = a.accumulate ? *o + v : v;
+        }
+      }
+}
+
+}  // namespace zg
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+zg_status zg::run_quantize_q8k_split(zg_ctx* ctx, const float* x, int8_t* qs, float* d8, int16_t* bs32, size_t rows,
+                                     size_t k, hipStream_t st) {
+  if (!x || !qs || !d8 || !bs32) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize_q8k_split: null pointer");
+  if (k == 0 || k % 256) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize_q8k_split: k %% 256 != 0");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(qs) & 3) ||
+      (reinterpret_cast<uintptr_t>(d8) & 3) || (reinterpret_cast<uintptr_t>(bs32) & 1))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize_q8k_split: misaligned buffer");
+  if (rows == 0) return ZG_OK;
+  const size_t blocks = rows * (k / 256);
+  if (blocks > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return set_error(ctx, ZG_ERR_INVALID_ARG, "quantize_q8k_split: too large");
+  hipLaunchKernelGGL(quantize_q8k_split_kernel, dim3((unsigned)blocks), dim3(64), 0, st, x, qs, d8, bs32, (int)k);
+  return hip_check(ctx, hipGetLastError(), "quantize_q8k_split launch");
+}
+
+zg_status zg::run_gemm_q8k(zg_ctx* ctx, const int8_t* qs, const float* d8, const int16_t* bs32, const GemmSegDev* segs,
+                           int nseg, size_t m, size_t k, uint32_t w_type, bool accumulate, hipStream_t st) {
+  if (!qs || !d8 || !bs32 || !segs || nseg < 1 || nseg > kKgSegs)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: bad arguments");
+  if (w_type != ZG_Q4K && w_type != ZG_Q6K) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "gemm_q8k: weights must be Q4_K/Q6_K");
+  if (k == 0 || k % 256) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: k %% 256 != 0");
+  if ((reinterpret_cast<uintptr_t>(qs) & 15) || (k % 16) || (reinterpret_cast<uintptr_t>(d8) & 15))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: activations misaligned");
+  KgemmArgs a{};
+  a.qs = qs;
+  a.d8 = d8;
+  a.bs32 = bs32;
+  size_t n = 0;
+  for (int i = 0; i < nseg; i++) {
+    if (!segs[i].w || !segs[i].y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: null pointer");
+    if (segs[i].n == 0 || segs[i].n % kKgBN) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: width %% %d", kKgBN);
+    if (w_type == ZG_Q4K && (reinterpret_cast<uintptr_t>(segs[i].w) & 15))
+      return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: Q4_K weights misaligned");
+    if (w_type == ZG_Q6K && (reinterpret_cast<uintptr_t>(segs[i].w) & 1))
+      return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: Q6_K weights misaligned");
+    n += segs[i].n;
+    a.w[i] = segs[i].w;
+    a.y[i] = segs[i].y;
+    a.seg_end[i] = (int)n;
+  }
+  if (m == 0) return ZG_OK;
+  if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: shape too large");
+  for (int i = nseg; i < kKgSegs; i++) {
+    a.w[i] = a.w[0];
+    a.y[i] = a.y[0];
+    a.seg_end[i] = (int)n;
+  }
+  a.nseg = nseg;
+  a.accumulate = accumulate ? 1 : 0;
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  const dim3 grid((unsigned)(n / kKgBN), (unsigned)((m + kKgBM - 1) / kKgBM));
+  if (w_type == ZG_Q4K) hipLaunchKernelGGL(gemm_q8k_kernel<Q4K>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(gemm_q8k_kernel<Q6K>, grid, dim3(256), 0, st, a);
+  return hip_check(ctx, hipGetLastError(), "gemm_q8k launch");
+}
+
+static hipStream_t kg_stream(zg_ctx* ctx, void* s) { return s ? reinterpret_cast<hipStream_t>(s) : ctx->stream; }
+
+extern "C" zg_status zg_quantize_q8k_split_dev(zg_ctx* ctx, const float* d_x, int8_t* d_qs, float* d_d8,
+                                               int16_t* d_bs32, size_t rows, size_t k, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  return run_quantize_q8k_split(ctx, d_x, d_qs, d_d8, d_bs32, rows, k, kg_stream(ctx, stream));
+}
+
+extern "C" zg_status zg_gemm_q8k_dev(zg_ctx* ctx, const int8_t* d_qs, const float* d_d8, const int16_t* d_bs32,
+                                     const void* d_w, float* d_y, size_t m, size_t n, size_t k, uint32_t w_type,
+                                     int accumulate, void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_w || !d_y) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: null pointer");
+  const GemmSegDev seg{static_cast<const uint8_t*>(d_w), d_y, n};
+  return run_gemm_q8k(ctx, d_qs, d_d8, d_bs32, &seg, 1, m, k, w_type, accumulate != 0, kg_stream(ctx, stream));
+}

@@ -34,54 +34,17 @@ constexpr int kQ8kBytes = 292;
 // dword-aligned 128-bit loads (Q8_K blocks start at multiples of 4 bytes)
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
-// quantize_row_q8k: one wave per 256-value block, 4 values per lane.
-//   max_val  the first value of largest magnitude (strict > scan: ties keep
-//            the lower index; NaN never wins): the (|v| bits, ~index) key is
-//            order-preserving for non-negative floats
-//   q        rintf(v * iscale), iscale = -127 / max_val, clamped to
-//            [-128, 127] (NaN -> 0, as Rust's `as i32` saturates)
-//   d        1 / iscale; bsums are exact int sums of 16 (int16)
+// quantize_row_q8k: one wave per 256-value block, 4 values per lane
+// (q8k_block_lane); bsums are exact int sums of 16 (int16).
 __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, uint8_t* __restrict__ out) {
   const int b = blockIdx.x, lane = threadIdx.x;
   const float* v = x + (size_t)b * 256;
   uint8_t* o = out + (size_t)b * kQ8kBytes;
   const float4 f = reinterpret_cast<const float4*>(v)[lane];
   const float e[4] = {f.x, f.y, f.z, f.w};
-  float best = 0.0f;
-  int bi = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float av = fabsf(e[i]);
-    if (av > best) {
-      best = av;
-      bi = 4 * lane + i;
-    }
-  }
-  uint64_t key = ((uint64_t)__float_as_uint(best) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)bi);
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) {
-    const uint64_t other = __shfl_xor(key, s, 64);
-    key = other > key ? other : key;
-  }
-  const float amax = __uint_as_float((uint32_t)(key >> 32));
-  if (amax == 0.0f) {
-    // whole-block zero: d = 0, q = 0, sums 0
-    reinterpret_cast<uint32_t*>(o + 4)[lane] = 0u;
-    if (lane < 8) reinterpret_cast<uint32_t*>(o + 260)[lane] = 0u;
-    if (lane == 0) reinterpret_cast<uint32_t*>(o)[0] = 0u;
-    return;
-  }
-  const float max_val = v[0xFFFFFFFFu - (uint32_t)key];
-  const float iscale = -127.0f / max_val;
   int q[4];
-  uint32_t packed = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float t = rintf(e[i] * iscale);
-    q[i] = (t != t) ? 0 : (int)fminf(fmaxf(t, -128.0f), 127.0f);
-    packed |= (uint32_t)(uint8_t)(int8_t)q[i] << (8 * i);
-  }
-  reinterpret_cast<uint32_t*>(o + 4)[lane] = packed;
+  float d;
+  reinterpret_cast<uint32_t*>(o + 4)[lane] = q8k_block_lane(v, lane, e, q, d);
   // sums of 16: four lanes per group
   int s16 = (q[0] + q[1]) + (q[2] + q[3]);
   s16 += __shfl_xor(s16, 1, 64);
@@ -90,10 +53,7 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
     const int c = s16 < -32768 ? -32768 : (s16 > 32767 ? 32767 : s16);
     reinterpret_cast<int16_t*>(o + 260)[lane >> 2] = (int16_t)c;
   }
-  if (lane == 0) {
-    const float d = 1.0f / iscale;
-    reinterpret_cast<float*>(o)[0] = d;
-  }
+  if (lane == 0) reinterpret_cast<float*>(o)[0] = d;
 }
 
 // Scale and min j (0..7) of a Q4_K superblock from its 12 scale bytes

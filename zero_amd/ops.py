@@ -253,6 +253,18 @@ class Context:
         self.check(self.lib.zg_gemm_q8act_dev(self.h, _ptr(qs), _ptr(d), _ptr(w), _ptr(y), m, n, k, int(w_type),
                                               int(interleave), stream))
 
+    def quantize_q8k_split_dev(self, x, qs, d8, bs32, rows, k, stream=None):
+        """quantize_row_q8k per 256 values of rows x k floats, as the K-quant
+        GEMM's split arrays: int8 qs [rows][k], f32 d8 [rows][k/256], int16
+        bs32 [rows][k/32] (sums of 32 quants)."""
+        self.check(self.lib.zg_quantize_q8k_split_dev(self.h, _ptr(x), _ptr(qs), _ptr(d8), _ptr(bs32), rows, k,
+                                                      stream))
+
+    def gemm_q8k_dev(self, qs, d8, bs32, w, y, m, n, k, w_type, accumulate=False, stream=None):
+        """K-quant prefill GEMM: Y (+)= Xq8k . W for plain Q4_K / Q6_K rows."""
+        self.check(self.lib.zg_gemm_q8k_dev(self.h, _ptr(qs), _ptr(d8), _ptr(bs32), _ptr(w), _ptr(y), m, n, k,
+                                            int(w_type), 1 if accumulate else 0, stream))
+
     # ---- Q4_K x Q8_K integer path (kernel/src/arch/x86_64/math/vnni.rs) ----
     def linear_q4k_vnni(self, x: np.ndarray, w_blocks: np.ndarray, out: np.ndarray, in_dim: int,
                         out_dim: int) -> None:
