@@ -1392,13 +1392,67 @@ int zo_model_forward(zo_model *m, uint32_t token, size_t pos, float *hidden_out)
     return 0;
 }
 
-/* Batched prefill with Q8_0 activations (no reference counterpart: the
+typedef struct {
+    const uint8_t *xk; /* n Q8_K rows of k values */
+    const uint8_t *w;
+    float *y;          /* [n][out_dim] */
+    size_t n, out_dim, k;
+    int qt, n_eff;
+    _Atomic int rc;
+} kq_gemm_job;
+
+static void kq_gemm_work(void *p, int idx, int nt) {
+    (void)nt;
+    kq_gemm_job *j = (kq_gemm_job *)p;
+    if (idx >= j->n_eff) return;
+    size_t s, e, xb = j->k / 256 * ZO_Q8K_BYTES;
+    zo_row_range_for(j->out_dim, (uint32_t)j->n_eff, (size_t)idx, 1, &s, &e);
+    for (size_t i = 0; i < j->n && s < e; i++) {
+        int rc = j->qt == 12 ? zo_linear_q4k_q8k_range(j->xk + i * xb, j->w, j->y + i * j->out_dim, j->k, s, e)
+                             : zo_linear_q6k_q8k_range(j->xk + i * xb, j->w, j->y + i * j->out_dim, j->k, s, e);
+        if (rc) atomic_store(&j->rc, rc);
+    }
+}
+
+/* One GEMM of the batched prefill: n fp32 activation rows X ([n][k]) times
+ * the out_dim rows of w into Y ([n][out_dim]).  Q4_0 / Q8_0 weights read the
+ * rows' Q8_0 encoding xq (zo_quantize_q8_0_row of X, made by the caller)
+ * through zo_gemm_q8act; plain Q4_K / Q6_K weights read each row's Q8_K
+ * encoding (zo_quantize_row_q8k into xk, n * k / 256 blocks) through the
+ * integer dot (zo_linear_q4k_q8k_range / zo_linear_q6k_q8k_range), the
+ * output rows split over the pool (each output is one row's dot, so the
+ * split changes no bits). */
+static int prefill_gemm(const float *X, const uint8_t *xq, uint8_t *xk, const uint8_t *w, float *Y, size_t n,
+                        size_t out_dim, size_t k, int qt, int il) {
+    if (qt == 12 || qt == 14) {
+        if (il != 1 || k % 256) return -3;
+        for (size_t i = 0; i < n; i++) zo_quantize_row_q8k(X + i * k, xk + i * (k / 256) * ZO_Q8K_BYTES, k);
+        kq_gemm_job j;
+        memset(&j, 0, sizeof j);
+        j.xk = xk;
+        j.w = w;
+        j.y = Y;
+        j.n = n;
+        j.out_dim = out_dim;
+        j.k = k;
+        j.qt = qt;
+        j.n_eff = cores_for_rows(out_dim);
+        atomic_store(&j.rc, 0);
+        pool_run(kq_gemm_work, &j);
+        return atomic_load(&j.rc) ? -3 : 0;
+    }
+    return zo_gemm_q8act(xq, w, Y, n, out_dim, k, qt, il) ? -3 : 0;
+}
+
+/* Batched prefill with quantized activations (no reference counterpart: the
  * reference runs the prompt token by token).  n rows at positions
- * pos0..pos0+n-1; per layer every row is rmsnormed, quantized with the
- * packer's Q8_0 encoder (zo_quantize_q8_0_row) and multiplied by
- * zo_gemm_q8act; QK-norm, RoPE, the cache store, attention, SwiGLU and the
- * residual adds are the single-token pass's per row.  Leaves the last row's
- * final hidden state in the model (for zo_model_lm_head). */
+ * pos0..pos0+n-1; per layer every row is rmsnormed, quantized (the packer's
+ * Q8_0 encoder, zo_quantize_q8_0_row, for Q4_0 / Q8_0 weights; the
+ * reference's quantize_row_q8k for plain Q4_K / Q6_K weights) and multiplied
+ * by each projection's GEMM (prefill_gemm); QK-norm, RoPE, the cache store,
+ * attention, SwiGLU and the residual adds are the single-token pass's per
+ * row.  Leaves the last row's final hidden state in the model (for
+ * zo_model_lm_head). */
 int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t pos0, float *hidden_out) {
     const zo_model_desc *d = &m->d;
     size_t H = (size_t)d->hidden, F = (size_t)d->ffn, hd = (size_t)d->head_dim;
@@ -1409,7 +1463,9 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
         if (tokens[i] >= d->vocab_padded) return -3;
     for (int l = 0; l < d->n_layers; l++)
         for (int p = 0; p < 7; p++)
-            if (m->quants[l].type[p] != 2 && m->quants[l].type[p] != 8) return -3;
+            if (m->quants[l].type[p] != 2 && m->quants[l].type[p] != 8 && m->quants[l].type[p] != 12 &&
+                m->quants[l].type[p] != 14)
+                return -3;
     size_t be, bb;
     if (type_geom(d->embd_type, &be, &bb) || H % be) return -3;
     size_t km = H > qd ? H : qd;
@@ -1419,9 +1475,10 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
     float *A = (float *)malloc(n * qd * 4), *P = (float *)malloc(n * H * 4);
     float *G = (float *)malloc(n * F * 4), *U = (float *)malloc(n * F * 4);
     uint8_t *xq = (uint8_t *)malloc(n * (km / 32) * 34);
+    uint8_t *xk = (uint8_t *)malloc(n * (km / 256 + 1) * ZO_Q8K_BYTES);
     float *scores = (float *)malloc((pos0 + n) * 4);
     int rc = 0;
-    if (!X || !T || !Q || !K || !V || !A || !P || !G || !U || !xq || !scores) rc = -5;
+    if (!X || !T || !Q || !K || !V || !A || !P || !G || !U || !xq || !xk || !scores) rc = -5;
     for (size_t i = 0; i < n && !rc; i++)
         zo_dequant_tensor(d->token_embd + (size_t)tokens[i] * (H / be) * bb, X + i * H, 1, H, d->embd_type, 1);
     float scale = 1.0f / sqrtf((float)hd);
@@ -1433,9 +1490,9 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
         float *vc = m->kv + ((size_t)l * 2 + 1) * d->max_ctx * kvd;
         for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->attn_norm, T + i * H, H, d->rms_eps);
         zo_quantize_q8_0_row(T, xq, n * H);
-        if (zo_gemm_q8act(xq, L->attn_q, Q, n, qd, H, qt[0], il[0]) ||
-            zo_gemm_q8act(xq, L->attn_k, K, n, kvd, H, qt[1], il[1]) ||
-            zo_gemm_q8act(xq, L->attn_v, V, n, kvd, H, qt[2], il[2])) {
+        if (prefill_gemm(T, xq, xk, L->attn_q, Q, n, qd, H, qt[0], il[0]) ||
+            prefill_gemm(T, xq, xk, L->attn_k, K, n, kvd, H, qt[1], il[1]) ||
+            prefill_gemm(T, xq, xk, L->attn_v, V, n, kvd, H, qt[2], il[2])) {
             rc = -3;
             break;
         }
@@ -1460,22 +1517,31 @@ int zo_model_prefill_q8(zo_model *m, const uint32_t *tokens, size_t n, size_t po
             if (attend(d, kc, vc, Q + i * qd, pos0 + i + 1, scale, scores, A + i * qd)) rc = -4;
         if (rc) break;
         zo_quantize_q8_0_row(A, xq, n * qd);
-        zo_gemm_q8act(xq, L->attn_o, P, n, H, qd, qt[3], il[3]);
+        if (prefill_gemm(A, xq, xk, L->attn_o, P, n, H, qd, qt[3], il[3])) {
+            rc = -3;
+            break;
+        }
         for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
         for (size_t i = 0; i < n; i++) zo_rmsnorm(X + i * H, L->ffn_norm, T + i * H, H, d->rms_eps);
         zo_quantize_q8_0_row(T, xq, n * H);
-        zo_gemm_q8act(xq, L->ffn_gate, G, n, F, H, qt[4], il[4]);
-        zo_gemm_q8act(xq, L->ffn_up, U, n, F, H, qt[5], il[5]);
+        if (prefill_gemm(T, xq, xk, L->ffn_gate, G, n, F, H, qt[4], il[4]) ||
+            prefill_gemm(T, xq, xk, L->ffn_up, U, n, F, H, qt[5], il[5])) {
+            rc = -3;
+            break;
+        }
         zo_silu_mul(G, U, T, n * F);
         zo_quantize_q8_0_row(T, xq, n * F);
-        zo_gemm_q8act(xq, L->ffn_down, P, n, H, F, qt[6], il[6]);
+        if (prefill_gemm(T, xq, xk, L->ffn_down, P, n, H, F, qt[6], il[6])) {
+            rc = -3;
+            break;
+        }
         for (size_t i = 0; i < n * H; i++) X[i] = X[i] + P[i];
     }
     if (!rc) {
         memcpy(m->hidden, X + (n - 1) * H, H * 4);
         if (hidden_out) memcpy(hidden_out, m->hidden, H * 4);
     }
-    free(X); free(T); free(Q); free(K); free(V); free(A); free(P); free(G); free(U); free(xq); free(scores);
+    free(X); free(T); free(Q); free(K); free(V); free(A); free(P); free(G); free(U); free(xq); free(xk); free(scores);
     return rc;
 }
 

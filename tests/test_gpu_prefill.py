@@ -1,8 +1,8 @@
 """GPU parity of the batched prefill (zg_model_prefill, zg_model_generate_ex
 with ZG_GEN_BATCHED_PREFILL) against the oracle's zo_model_prefill_q8: the
-prompt rows go through rmsnorm, Q8_0 activation quantization and the int8
-MFMA GEMMs, with the decode step's QK-norm, RoPE, causal attention and
-SwiGLU per row.
+prompt rows go through rmsnorm, activation quantization (Q8_0 for Q4_0 /
+Q8_0 weights, Q8_K for Q4_K / Q6_K weights) and the int8 MFMA GEMMs, with
+the decode step's QK-norm, RoPE, causal attention and SwiGLU per row.
 
 Bar: the last row's hidden state and the next token's logits within rel
 1e-3 of the oracle, identical greedy tokens after the prefill; chunked calls
@@ -323,5 +323,105 @@ def test_qwen3_1_7b_shape_batched_prefill(ctx):
         print(f"batched prefill of 128 tokens: {t_pre * 1e3:.2f} ms")
         assert toks[0] == tok_b
     finally:
+        gm.close()
+        ctx.clear()
+
+
+KQ_TINY = dataclasses.replace(TINY, embd_type=synth.Q4K, head_type=synth.Q6K, head_interleave=1,
+                              layer_quants=synth.q4_k_m_layers(2))
+
+
+@pytest.mark.parametrize("n", [1, 7, 130])
+def test_k_quant_prefill_matches_oracle(ctx, zo, n):
+    """Q4_K_M-pattern layers (Q4_K, Q6_K attn_v / ffn_down on the last
+    layer): Q8_K rows into the K-quant GEMMs, then decode from the cache."""
+    model = synth.random_model(KQ_TINY, seed=30)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(50 + n, n, KQ_TINY.vocab_real)
+        tok, mv, hid = gm.prefill(prompt, want_hidden=True)
+        h_ref = om.prefill_q8(prompt)
+        rc, t_ref, m_ref, _ = om.lm_head()
+        assert rc == 0
+        print(f"K-quant n={n}: hidden rel err {rel_err(hid, h_ref):.2e}")
+        assert rel_err(hid, h_ref) <= REL_TOL
+        assert tok == t_ref and abs(mv - m_ref) <= REL_TOL * abs(m_ref)
+        pos = n
+        for _ in range(6):
+            nxt, _, h2, _ = gm.step(tok, pos, want_hidden=True)
+            h2_ref = om.forward(tok, pos)
+            rc, t2_ref, _, _ = om.lm_head()
+            assert rel_err(h2, h2_ref) <= REL_TOL and nxt == t2_ref, pos
+            tok, pos = nxt, pos + 1
+        # chunked calls give the same bits as one call
+        if n > 2:
+            gm.prefill(prompt[:n // 2])
+            t2, m2, h2 = gm.prefill(prompt[n // 2:], pos0=n // 2, want_hidden=True)
+            assert np.array_equal(h2, hid) and t2 == t_ref
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
+def test_k_quant_generate_batched_matches_oracle(ctx, zo):
+    model = synth.random_model(KQ_TINY, seed=31)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(32, 40, KQ_TINY.vocab_real)
+        toks, _, _ = gm.generate(prompt, 32, batched_prefill=True)
+        assert np.array_equal(toks, om.generate_batched(prompt, 32))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
+def test_qwen3_1_7b_shape_q4_k_m_batched_prefill_matches_oracle(ctx, zo):
+    """12-row batched prefill through all 28 Q4_K_M-pattern layers of the
+    Qwen3-1.7B shape (Q4_K projections, Q6_K attn_v / ffn_down on 14 layers,
+    Q4_K token embedding, Q6_K LM head) against zo_model_prefill_q8: last
+    hidden state within rel 1e-3 and the same next token, then 8 decode
+    steps token for token; the 128-token prefill within the Q8_K
+    activation-quantization distance of the token-by-token pass."""
+    cfg = synth.ModelConfig(max_ctx=160, embd_type=synth.Q4K, head_type=synth.Q6K, head_interleave=1,
+                            layer_quants=synth.q4_k_m_layers(28))
+    model = synth.random_model(cfg, seed=22)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(33, 12, cfg.vocab_real)
+        with zo.Pool(16):
+            tok, mv, hid = gm.prefill(prompt, want_hidden=True)
+            h_ref = om.prefill_q8(prompt)
+            rc, t_ref, m_ref, _ = om.lm_head()
+            assert rc == 0
+            err = rel_err(hid, h_ref)
+            print(f"Q4_K_M Qwen3-1.7B shape, 12-row prefill: hidden rel err {err:.2e}")
+            assert err <= REL_TOL
+            assert tok == t_ref and abs(mv - m_ref) <= REL_TOL * abs(m_ref)
+            pos = len(prompt)
+            for _ in range(8):
+                nxt, _, h2, lg = gm.step(tok, pos, want_hidden=True, want_logits=True)
+                h2_ref = om.forward(tok, pos)
+                rc, t2_ref, _, lg2_ref = om.lm_head()
+                assert rel_err(h2, h2_ref) <= REL_TOL and rel_err(lg, lg2_ref) <= REL_TOL
+                assert nxt == t2_ref, pos
+                tok, pos = nxt, pos + 1
+        long = synth.prompt(8, 128, cfg.vocab_real)
+        tok_b, _, h_b = gm.prefill(long, want_hidden=True)
+        for i, t in enumerate(long[:-1]):
+            gm.step(int(t), i)
+        tok_s, _, h_s, _ = gm.step(int(long[-1]), len(long) - 1, want_hidden=True)
+        err = rel_err(h_b, h_s)
+        print(f"Q4_K_M batched vs token-by-token hidden rel err {err:.2e}; tokens {tok_b} / {tok_s}")
+        assert 1e-5 < err < 5e-2
+        toks, t_pre, _ = gm.generate(long, 8, batched_prefill=True)
+        print(f"Q4_K_M batched prefill of 128 tokens: {t_pre * 1e3:.2f} ms")
+        assert toks[0] == tok_b
+    finally:
+        om.close()
         gm.close()
         ctx.clear()

@@ -7,9 +7,11 @@
   forward_single_token_avx512, kernel/src/inference_avx512.rs:1826-1987)
   against an independent numpy restatement written from the Qwen3 block
   definition, on a tiny random model;
-* zo_model_prefill_q8 (batched prefill with Q8_0 activations) against the
-  same numpy restatement with each matmul input quantized to Q8_0 (numpy's
-  own round-half-even and binary16 rounding), and for chunk invariance.
+* zo_model_prefill_q8 (batched prefill with quantized activations) against
+  the same numpy restatement with each matmul input quantized to Q8_0 for
+  Q4_0 / Q8_0 weights (numpy's own round-half-even and binary16 rounding) or
+  to Q8_K for Q4_K / Q6_K weights (quantize_row_q8k restated in float64),
+  and for chunk invariance.
 """
 import dataclasses
 
@@ -55,11 +57,39 @@ def _np_q8(v):
     return (q * d.astype(np.float16).astype(np.float64)).reshape(-1)
 
 
+def _np_q8k(v):
+    """Q8_K round trip of a vector (quantize_row_q8k,
+    kernel/src/arch/x86_64/math/vnni.rs:78-170): per 256 values the first
+    value of largest magnitude m, iscale = -127 / m, q = round-half-even(v *
+    iscale) clamped to [-128, 127], value q / iscale; an all-zero block stays
+    zero."""
+    b = v.reshape(-1, 256)
+    out = np.zeros_like(b)
+    for i, row in enumerate(b):
+        mx = row[int(np.argmax(np.abs(row)))]
+        if mx != 0:
+            iscale = -127.0 / mx
+            out[i] = np.clip(np.rint(row * iscale), -128, 127) / iscale
+    return out.reshape(-1)
+
+
+def test_np_q8k_matches_the_oracle_quantizer(zo):
+    x = synth.activations(np.random.default_rng(9), 2048)
+    x[300] = -9.0
+    x[301] = 9.0  # the first of equal magnitudes sets the sign
+    blocks = zo.quantize_q8k(x).reshape(-1, 292)
+    q = blocks[:, 4:260].view(np.int8).astype(np.float64)
+    d = blocks[:, :4].copy().view(np.float32).astype(np.float64)
+    want = (q * d).reshape(-1)
+    assert np.max(np.abs(_np_q8k(x.astype(np.float64)) - want)) <= 1e-6 * np.max(np.abs(want))
+
+
 def _np_forward(model, tokens, q8_rows=0):
     """Qwen3 decoder restated in numpy float64: pre-norm GQA with QK-norm,
     NeoX RoPE, causal softmax attention, SwiGLU MLP, residuals, final norm,
-    LM head.  Positions below q8_rows quantize every matmul input to Q8_0
-    first (the batched prefill's arithmetic)."""
+    LM head.  Positions below q8_rows quantize every matmul input first (the
+    batched prefill's arithmetic): to Q8_0 for Q4_0 / Q8_0 weights, to Q8_K
+    for Q4_K / Q6_K weights."""
     cfg = model.cfg
     H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q_heads, cfg.n_kv_heads
 
@@ -76,23 +106,28 @@ def _np_forward(model, tokens, q8_rows=0):
     names = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down")
     Ws = [{k: deq(getattr(L, k), *shape, *cfg.proj_quant(li, p))
            for p, (k, shape) in enumerate(zip(names, cfg.proj_shapes()))} for li, L in enumerate(model.layers)]
+    Ts = [{k: cfg.proj_quant(li, p)[0] for p, k in enumerate(names)} for li in range(len(model.layers))]
     kc = [[] for _ in model.layers]
     vc = [[] for _ in model.layers]
     logits = []
     for pos, tok in enumerate(tokens):
         h = emb[tok].copy()
         c, s = np.cos(pos * inv), np.sin(pos * inv)
-        a8 = _np_q8 if pos < q8_rows else (lambda v: v)
+
+        def a8(v, t):
+            if pos >= q8_rows:
+                return v
+            return _np_q8k(v) if t in (synth.Q4K, synth.Q6K) else _np_q8(v)
 
         def rope(v):
             a, b = v[:hd // 2], v[hd // 2:]
             return np.concatenate([a * c - b * s, a * s + b * c])
 
-        for li, (L, W) in enumerate(zip(model.layers, Ws)):
-            xn = a8(rms(h, L.attn_norm))
-            q = (W["attn_q"] @ xn).reshape(nq, hd)
-            k = (W["attn_k"] @ xn).reshape(nkv, hd)
-            v = (W["attn_v"] @ xn).reshape(nkv, hd)
+        for li, (L, W, T) in enumerate(zip(model.layers, Ws, Ts)):
+            xn = rms(h, L.attn_norm)
+            q = (W["attn_q"] @ a8(xn, T["attn_q"])).reshape(nq, hd)
+            k = (W["attn_k"] @ a8(xn, T["attn_k"])).reshape(nkv, hd)
+            v = (W["attn_v"] @ a8(xn, T["attn_v"])).reshape(nkv, hd)
             q = np.stack([rope(rms(qh, L.q_norm)) for qh in q])
             k = np.stack([rope(rms(kh, L.k_norm)) for kh in k])
             kc[li].append(k)
@@ -105,10 +140,10 @@ def _np_forward(model, tokens, q8_rows=0):
                 p = np.exp(sc - sc.max())
                 p /= p.sum()
                 out[hh] = p @ V[:, g]
-            h = h + W["attn_o"] @ a8(out.reshape(-1))
-            xn = a8(rms(h, L.ffn_norm))
-            gt, up = W["ffn_gate"] @ xn, W["ffn_up"] @ xn
-            h = h + W["ffn_down"] @ a8(gt / (1 + np.exp(-gt)) * up)
+            h = h + W["attn_o"] @ a8(out.reshape(-1), T["attn_o"])
+            xn = rms(h, L.ffn_norm)
+            gt, up = W["ffn_gate"] @ a8(xn, T["ffn_gate"]), W["ffn_up"] @ a8(xn, T["ffn_up"])
+            h = h + W["ffn_down"] @ a8(gt / (1 + np.exp(-gt)) * up, T["ffn_down"])
         logits.append(head @ rms(h, model.output_norm))
     return np.array(logits)
 
@@ -157,9 +192,44 @@ def test_model_forward_mixed_quants_vs_numpy(zo):
         assert rc == 0
         err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
         assert err < 1e-4, (pos, err)
-    # the batched prefill's GEMMs take Q4_0 / Q8_0 projections only
-    with pytest.raises(AssertionError):
-        om.prefill_q8(np.array(toks, np.uint32))
+    om.close()
+    # batched prefill over the same mixed layers: each projection's input is
+    # quantized to its weight type's activation format
+    ref = _np_forward(model, toks, q8_rows=len(toks))
+    om = zo.OracleModel(model)
+    om.prefill_q8(np.array(toks, np.uint32))
+    rc, tok, mv, lg = om.lm_head()
+    assert rc == 0
+    err = np.max(np.abs(lg - ref[-1])) / np.max(np.abs(ref[-1]))
+    assert err < 1e-3, err
+    om.close()
+
+
+def test_prefill_q4_k_m_vs_numpy(zo):
+    """Batched prefill of a Q4_K_M-pattern model (Q4_K projections, Q6_K
+    attn_v / ffn_down on the last layer): Q8_K activation rows throughout,
+    then two decode steps from the prefilled cache."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=256, vocab_real=250, max_ctx=16, embd_type=synth.Q4K, head_type=synth.Q6K,
+                            head_interleave=1, layer_quants=synth.q4_k_m_layers(2))
+    model = synth.random_model(cfg, seed=12)
+    toks = [3, 17, 101, 5, 5, 42, 9, 200, 7]
+    n = 7
+    ref = _np_forward(model, toks, q8_rows=n)
+    om = zo.OracleModel(model)
+    om.prefill_q8(np.array(toks[:n], np.uint32))
+    for pos in range(n - 1, len(toks)):
+        if pos >= n:
+            om.forward(toks[pos], pos)
+        rc, tok, mv, lg = om.lm_head()
+        assert rc == 0
+        err = np.max(np.abs(lg - ref[pos])) / np.max(np.abs(ref[pos]))
+        assert err < 1e-3, (pos, err)
+        assert tok == int(np.argmax(ref[pos][:cfg.vocab_real]))
+    # the fp32 token-by-token pass differs by the activation quantization only
+    fp = _np_forward(model, toks)
+    q_err = np.max(np.abs(ref[n - 1] - fp[n - 1])) / np.max(np.abs(fp[n - 1]))
+    assert 1e-4 < q_err < 5e-2, q_err
     om.close()
 
 

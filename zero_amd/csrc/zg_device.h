@@ -509,24 +509,26 @@ __device__ __forceinline__ void xdig_chains(const uint32_t (&q)[8], const XDig& 
 }
 
 // quantize_row_q8k (kernel/src/arch/x86_64/math/vnni.rs:78-170) for one
-// 256-value block v, one wave, four values per lane (e = v[4 lane .. + 4)):
+// 256-value block held by one wave, four values per lane (e = values
+// 4 lane .. 4 lane + 3 of the block):
 //   max_val  the first value of largest magnitude (strict > scan: ties keep
 //            the lower index; NaN never wins): the (|v| bits, ~index) key is
-//            order-preserving for non-negative floats
+//            order-preserving for non-negative floats, and the winning
+//            lane's own first largest value is max_val (read by shuffle)
 //   q        rintf(e * iscale), iscale = -127 / max_val, clamped to
 //            [-128, 127] (NaN -> 0, as Rust's `as i32` saturates)
 //   d        1 / iscale
 // An all-zero block gives q = 0 and d = 0.  Returns the lane's four quants
 // as little-endian bytes; q holds their values.
-__device__ __forceinline__ uint32_t q8k_block_lane(const float* __restrict__ v, int lane, const float (&e)[4],
-                                                   int (&q)[4], float& d) {
-  float best = 0.0f;
+__device__ __forceinline__ uint32_t q8k_block_lane(int lane, const float (&e)[4], int (&q)[4], float& d) {
+  float best = 0.0f, bval = 0.0f;
   int bi = 0;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const float av = fabsf(e[i]);
     if (av > best) {
       best = av;
+      bval = e[i];
       bi = 4 * lane + i;
     }
   }
@@ -536,13 +538,13 @@ __device__ __forceinline__ uint32_t q8k_block_lane(const float* __restrict__ v, 
     const uint64_t other = __shfl_xor(key, s, 64);
     key = other > key ? other : key;
   }
+  const float max_val = __shfl(bval, (int)((0xFFFFFFFFu - (uint32_t)key) >> 2), 64);
   if (__uint_as_float((uint32_t)(key >> 32)) == 0.0f) {
 #pragma unroll
     for (int i = 0; i < 4; i++) q[i] = 0;
     d = 0.0f;
     return 0u;
   }
-  const float max_val = v[0xFFFFFFFFu - (uint32_t)key];
   const float iscale = -127.0f / max_val;
   uint32_t packed = 0;
 #pragma unroll
@@ -553,6 +555,21 @@ __device__ __forceinline__ uint32_t q8k_block_lane(const float* __restrict__ v, 
   }
   d = 1.0f / iscale;
   return packed;
+}
+
+// One 256-value block (four values per lane, as q8k_block_lane) into the
+// K-quant GEMM's split activation arrays: the 256 int8 quants at qs, the
+// block's d at *d8, the eight sums of 32 quants at bs32[0..8).
+__device__ __forceinline__ void q8k_split_store(int lane, const float (&e)[4], int8_t* qs, float* d8, int16_t* bs32) {
+  int q[4];
+  float d;
+  reinterpret_cast<uint32_t*>(qs)[lane] = q8k_block_lane(lane, e, q, d);
+  int s = (q[0] + q[1]) + (q[2] + q[3]);
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  if ((lane & 7) == 0) bs32[lane >> 3] = (int16_t)s;
+  if (lane == 0) *d8 = d;
 }
 
 }  // namespace zg

@@ -66,17 +66,7 @@ __global__ __launch_bounds__(64) void quantize_q8k_split_kernel(const float* __r
   const float* v = x + row * k + (size_t)sb * 256;
   const float4 f = reinterpret_cast<const float4*>(v)[lane];
   const float e[4] = {f.x, f.y, f.z, f.w};
-  int q[4];
-  float d;
-  const uint32_t packed = q8k_block_lane(v, lane, e, q, d);
-  reinterpret_cast<uint32_t*>(qs + row * k + (size_t)sb * 256)[lane] = packed;
-  // sums of 32: eight lanes per sub-block
-  int s = (q[0] + q[1]) + (q[2] + q[3]);
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
-  s += __shfl_xor(s, 4, 64);
-  if ((lane & 7) == 0) bs32[row * (k / 32) + (size_t)sb * 8 + (lane >> 3)] = (int16_t)s;
-  if (lane == 0) d8[row * nsb + sb] = d;
+  q8k_split_store(lane, e, qs + row * k + (size_t)sb * 256, d8 + row * nsb + sb, bs32 + row * (k / 32) + (size_t)sb * 8);
 }
 
 // ---------------------------------------------------------------------------

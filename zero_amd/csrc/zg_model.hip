@@ -153,8 +153,9 @@ struct AttnArgs {
   float eps, scale;
   // batched prefill: query row z of the chunk sits at position pos0 + z,
   // its (already normalised and rotated) query at q + z * row_stride; its
-  // output is Q8_0-encoded into qs + z * row_stride (int8) and
-  // qsd + z * row_stride / 32 (fp16 d bits)
+  // output goes to out + z * row_stride as fp32 when out is set, else
+  // Q8_0-encoded into qs + z * row_stride (int8) and qsd + z * row_stride /
+  // 32 (fp16 d bits)
   int pos0;
   int row_stride;
   int8_t* qs;
@@ -213,8 +214,9 @@ static_assert(kAttnDecodeSplits >= 1 && kAttnDecodeSplits <= kAttnSplits, "decod
 // z attends to cache rows 0..pos0+z, all of which are in the cache already
 // (qk_rope_store_kernel ran first), and its query is already normalised and
 // rotated.  The output row goes out Q8_0-encoded for the O GEMM (each 32-lane
-// segment of the output waves is one block).  Everything else is the decode
-// kernel's arithmetic.
+// segment of the output waves is one block), or as fp32 (a.out) for a
+// K-quant O projection, whose Q8_K blocks span two heads.  Everything else is
+// the decode kernel's arithmetic.
 // Rows per split for position pos: ceil((pos + 1) / nsplit) rounded up to a
 // multiple of 8; splits starting past pos hold no row.
 __device__ __forceinline__ int attn_split_rows(int pos, int nsplit) {
@@ -462,7 +464,9 @@ __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int 
       o = fmaf(f, wo[w][tid], o);
     }
     if (tid == 0 && !(isfinite(M) && isfinite(L))) atomicOr(&a.st->err, 4u);
-    if (PF) {
+    if (PF && a.out) {
+      a.out[(size_t)bz * a.row_stride + qh * HD + tid] = o * (1.0f / L);
+    } else if (PF) {
       uint32_t dbits;
       const int8_t qv = q8_0_encode_lane(o * (1.0f / L), &dbits);
       a.qs[qh * HD + tid] = qv;
@@ -805,6 +809,18 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(QkStoreArgs a) {
   }
 }
 
+// 1 / rms of one row of n, by a 256-thread workgroup (rmsnorm_kernel's
+// arithmetic); red: 4 floats of LDS.
+__device__ __forceinline__ float row_rms_inv(const float* __restrict__ x, int n, float eps, float* red) {
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) ssq += x[i] * x[i];
+  ssq = seg_sum<64>(ssq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ssq;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  return 1.0f / sqrtf(tot / (float)n + eps);
+}
+
 // One row of n per workgroup: rmsnorm (rmsnorm_kernel's arithmetic) and the
 // Q8_0 encoding of the normalised row, 32 values per thread at a time.
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x, const float* __restrict__ w,
@@ -813,13 +829,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
   __shared__ float red[4];
   const size_t row = blockIdx.x;
   x += row * n;
-  float ssq = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) ssq += x[i] * x[i];
-  ssq = seg_sum<64>(ssq);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ssq;
-  __syncthreads();
-  const float tot = red[0] + red[1] + red[2] + red[3];
-  const float rinv = 1.0f / sqrtf(tot / (float)n + eps);
+  const float rinv = row_rms_inv(x, n, eps, red);
   for (int b = threadIdx.x; b < n / 32; b += 256) {
     const float4* x4 = reinterpret_cast<const float4*>(x + b * 32);
     const float4* w4 = reinterpret_cast<const float4*>(w + b * 32);
@@ -887,6 +897,47 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
   }
 }
 
+// Q8_K split rows for the K-quant GEMM (qs [rows][n] int8, d8 [rows][n/256]
+// f32, bs32 [rows][n/32] int16).
+struct Q8kRows {
+  int8_t* qs;
+  float* d8;
+  int16_t* bs32;
+};
+
+// One row of n (a multiple of 256) per workgroup: rmsnorm_quant_kernel's
+// normalised values, Q8_K-encoded (quantize_row_q8k,
+// kernel/src/arch/x86_64/math/vnni.rs:78-170), one wave per 256-value block.
+__global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          Q8kRows o, int n, float eps) {
+  __shared__ float red[4];
+  const size_t row = blockIdx.x;
+  x += row * n;
+  const float rinv = row_rms_inv(x, n, eps, red);
+  const int lane = threadIdx.x & 63;
+  for (int sb = threadIdx.x >> 6; sb < n / 256; sb += 4) {
+    const float4 xv = reinterpret_cast<const float4*>(x + sb * 256)[lane];
+    const float4 wv = reinterpret_cast<const float4*>(w + sb * 256)[lane];
+    const float e[4] = {xv.x * rinv * wv.x, xv.y * rinv * wv.y, xv.z * rinv * wv.z, xv.w * rinv * wv.w};
+    q8k_split_store(lane, e, o.qs + row * n + sb * 256, o.d8 + row * (n / 256) + sb, o.bs32 + row * (n / 32) + sb * 8);
+  }
+}
+
+// One row of n (a multiple of 256) per workgroup: swiglu_quant_kernel's
+// values, Q8_K-encoded, one wave per 256-value block.
+__global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                         Q8kRows o, int n) {
+  const size_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  for (int sb = threadIdx.x >> 6; sb < n / 256; sb += 4) {
+    const float4 gv = reinterpret_cast<const float4*>(g + row * n + sb * 256)[lane];
+    const float4 uv = reinterpret_cast<const float4*>(u + row * n + sb * 256)[lane];
+    const float e[4] = {(gv.x / (1.0f + expf(-gv.x))) * uv.x, (gv.y / (1.0f + expf(-gv.y))) * uv.y,
+                        (gv.z / (1.0f + expf(-gv.z))) * uv.z, (gv.w / (1.0f + expf(-gv.w))) * uv.w};
+    q8k_split_store(lane, e, o.qs + row * n + sb * 256, o.d8 + row * (n / 256) + sb, o.bs32 + row * (n / 32) + sb * 8);
+  }
+}
+
 }  // namespace zg
 
 hipError_t zg::launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t st) {
@@ -945,7 +996,8 @@ struct zg_model {
   size_t out_cap = 0;
   int nsplit = 1;
   bool head_norm = false;  // the LM-head GEMV takes the output rmsnorm itself
-  bool pf_ok = false;      // every layer projection Q4_0 / Q8_0 (the batched prefill's GEMMs)
+  bool pf_ok = false;      // every layer projection has a batched-prefill GEMM (Q4_0 / Q8_0; Q4_K / Q6_K rows)
+  bool pf_kq = false;      // some projection is Q4_K / Q6_K (Q8_K activation rows)
   std::vector<void*> owned;  // device allocations to free
   // references to the registry's uploaded weight copies this model reads,
   // each with the device address it resolved to: they outlive a zg_clear of
@@ -967,6 +1019,12 @@ struct zg_model {
   float *pf_g = nullptr, *pf_u = nullptr;
   int8_t* pf_qs = nullptr;
   uint16_t* pf_qd = nullptr;
+  // Q8_K activation rows of the K-quant GEMMs, and the attention's fp32
+  // output rows they are quantized from when the O projection is K-quant
+  int8_t* pf_ks = nullptr;
+  float* pf_k8 = nullptr;
+  int16_t* pf_kb = nullptr;
+  float* pf_a = nullptr;
   // non-finite localisation: device result, [2][hidden] scan buffers
   // (rmsnorm output, sublayer output), and per KV row the token whose step
   // wrote it and how (kRowDecode rows can be replayed)
@@ -1331,27 +1389,60 @@ static zg_status prefill_alloc(zg_model* m) {
   al(&m->pf_u, C * F * 4);
   al(&m->pf_qs, C * kmax);
   al(&m->pf_qd, C * (kmax / 32) * 2);
+  if (m->pf_kq) {
+    al(&m->pf_ks, C * kmax);
+    al(&m->pf_k8, C * (kmax / 256) * 4);
+    al(&m->pf_kb, C * (kmax / 32) * 2);
+    al(&m->pf_a, C * qd * 4);
+  }
   if (!s) m->pf_cap = C;
   return s;
 }
 
+static bool kq_type(uint32_t t) { return t == ZG_Q4K || t == ZG_Q6K; }
+
+// Which activation encodings layer projections p0..p0+nseg-1 read: Q8_0
+// rows (Q4_0 / Q8_0 weights), Q8_K rows (Q4_K / Q6_K weights).
+static void act_needs(const ZLayer& L, int p0, int nseg, bool& q80, bool& q8k) {
+  q80 = q8k = false;
+  for (int i = 0; i < nseg; i++) (kq_type(L.qt[p0 + i]) ? q8k : q80) = true;
+}
+
+// rmsnorm of the chunk's rows into the encodings projections p0..p0+nseg-1
+// read.
+static zg_status norm_rows(zg_model* m, const ZLayer& L, int p0, int nseg, const float* w, size_t n, hipStream_t st) {
+  const int H = (int)m->d.hidden;
+  bool q80, q8k;
+  act_needs(L, p0, nseg, q80, q8k);
+  if (q80)
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, w, m->pf_qs, m->pf_qd, H,
+                       m->d.rms_eps);
+  if (q8k)
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, w,
+                       Q8kRows{m->pf_ks, m->pf_k8, m->pf_kb}, H, m->d.rms_eps);
+  return hip_check(m->ctx, hipGetLastError(), "prefill rmsnorm launch");
+}
+
 // One chunk of n <= pf_cap prompt rows (device tokens) at positions
 // pos0..pos0+n-1 through every layer, leaving the final hidden states in
-// pf_x.  Per layer: rmsnorm + Q8_0 rows -> Q|K|V GEMM -> QK-norm + RoPE +
-// cache store -> causal attention + Q8_0 -> O GEMM (+= residual) ->
-// rmsnorm + Q8_0 rows -> gate|up GEMM -> SwiGLU + Q8_0 -> down GEMM
-// (+= residual).  Each fused encode gives the bits the separate quantizer
-// would give for the same fp32 row.
-// GEMMs of layer projections p0..p0+nseg-1 on the chunk's Q8_0 rows: one
-// segmented launch when they share a type and layout, else one each.
+// pf_x.  Per layer: rmsnorm + activation rows -> Q|K|V GEMM -> QK-norm +
+// RoPE + cache store -> causal attention (+ activation rows) -> O GEMM (+=
+// residual) -> rmsnorm + activation rows -> gate|up GEMM -> SwiGLU +
+// activation rows -> down GEMM (+= residual).  Activation rows are Q8_0 for
+// Q4_0 / Q8_0 weights and Q8_K for Q4_K / Q6_K weights; each fused encode
+// gives the bits the separate quantizer would give for the same fp32 row.
+// GEMMs of layer projections p0..p0+nseg-1 on the chunk's activation rows:
+// one segmented launch per run of projections that share a type and layout.
 static zg_status layer_gemm(zg_model* m, const ZLayer& L, int p0, const GemmSegDev* segs, int nseg, size_t n,
                             size_t k, bool accumulate, hipStream_t st) {
-  bool same = true;
-  for (int i = 1; i < nseg; i++) same = same && L.qt[p0 + i] == L.qt[p0] && L.il[p0 + i] == L.il[p0];
-  if (same) return run_gemm(m->ctx, m->pf_qs, m->pf_qd, segs, nseg, n, k, L.qt[p0], L.il[p0], accumulate, st);
-  for (int i = 0; i < nseg; i++) {
-    zg_status s = run_gemm(m->ctx, m->pf_qs, m->pf_qd, segs + i, 1, n, k, L.qt[p0 + i], L.il[p0 + i], accumulate, st);
+  for (int i = 0; i < nseg;) {
+    int j = i + 1;
+    while (j < nseg && L.qt[p0 + j] == L.qt[p0 + i] && L.il[p0 + j] == L.il[p0 + i]) j++;
+    const uint32_t t = L.qt[p0 + i];
+    zg_status s = kq_type(t) ? run_gemm_q8k(m->ctx, m->pf_ks, m->pf_k8, m->pf_kb, segs + i, j - i, n, k, t, accumulate, st)
+                             : run_gemm(m->ctx, m->pf_qs, m->pf_qd, segs + i, j - i, n, k, t, L.il[p0 + i], accumulate, st);
     if (s) return s;
+    i = j;
   }
   return ZG_OK;
 }
@@ -1370,9 +1461,7 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     const ZLayer& L = m->layers[l];
     float* kc = m->kv + (size_t)(2 * l) * d.max_ctx * kvd;
     float* vc = m->kv + (size_t)(2 * l + 1) * d.max_ctx * kvd;
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.attn_norm, m->pf_qs,
-                       m->pf_qd, H, d.rms_eps);
-    if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
+    if ((s = norm_rows(m, L, ZG_PROJ_Q, 3, L.attn_norm, n, st))) break;
     const GemmSegDev qkv[3] = {{L.q, m->pf_q, qd}, {L.k, m->pf_k, kvd}, {L.v, m->pf_v, kvd}};
     if ((s = layer_gemm(m, L, ZG_PROJ_Q, qkv, 3, n, H, false, st))) break;
     QkStoreArgs qa{m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm, m->inv_freq, kc, vc, nq, nkv, (int)pos0, d.rms_eps};
@@ -1384,6 +1473,8 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     aa.q = m->pf_q;
     aa.kcache = kc;
     aa.vcache = vc;
+    const bool o_kq = kq_type(L.qt[ZG_PROJ_O]);
+    aa.out = o_kq ? m->pf_a : nullptr;
     aa.qs = m->pf_qs;
     aa.qsd = m->pf_qd;
     aa.part_ml = m->part_ml;
@@ -1400,15 +1491,18 @@ static zg_status prefill_chunk(zg_model* m, const uint32_t* d_tokens, size_t n, 
     if (HD == 128) hipLaunchKernelGGL((attn_split_kernel<128, true>), ag, ab, 0, st, aa);
     else hipLaunchKernelGGL((attn_split_kernel<64, true>), ag, ab, 0, st, aa);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill attention launch"))) break;
+    if (o_kq && (s = run_quantize_q8k_split(ctx, m->pf_a, m->pf_ks, m->pf_k8, m->pf_kb, n, qd, st))) break;
     const GemmSegDev o{L.o, m->pf_x, (size_t)H};
     if ((s = layer_gemm(m, L, ZG_PROJ_O, &o, 1, n, qd, true, st))) break;
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_x, L.ffn_norm, m->pf_qs,
-                       m->pf_qd, H, d.rms_eps);
-    if ((s = hip_check(ctx, hipGetLastError(), "prefill rmsnorm launch"))) break;
+    if ((s = norm_rows(m, L, ZG_PROJ_GATE, 2, L.ffn_norm, n, st))) break;
     const GemmSegDev gu[2] = {{L.gate, m->pf_g, (size_t)F}, {L.up, m->pf_u, (size_t)F}};
     if ((s = layer_gemm(m, L, ZG_PROJ_GATE, gu, 2, n, H, false, st))) break;
-    hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_qs, m->pf_qd,
-                       F);
+    if (kq_type(L.qt[ZG_PROJ_DOWN]))
+      hipLaunchKernelGGL(swiglu_q8k_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u,
+                         Q8kRows{m->pf_ks, m->pf_k8, m->pf_kb}, F);
+    else
+      hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)n), dim3(256), 0, st, m->pf_g, m->pf_u, m->pf_qs,
+                         m->pf_qd, F);
     if ((s = hip_check(ctx, hipGetLastError(), "prefill swiglu launch"))) break;
     const GemmSegDev dn{L.down, m->pf_x, (size_t)H};
     if ((s = layer_gemm(m, L, ZG_PROJ_DOWN, &dn, 1, n, F, true, st))) break;
@@ -1624,7 +1718,14 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
       L.o_merge = m->nsplit > 1 && ((attn_merge_gemv_ok(ot, oil, qd) && pair_path_ok(ot, oil, qd, H, L.o, m->part_o)) ||
                                     kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
-      for (int p = 0; p < ZG_N_PROJ; p++) m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0);
+      // batched prefill: Q4_0 / Q8_0 any shape; Q4_K / Q6_K plain rows of a
+      // width in 64-column tiles and an in_dim in whole superblocks
+      const size_t width[ZG_N_PROJ] = {qd, kvd, kvd, H, F, F, H}, in_dim[ZG_N_PROJ] = {H, H, H, qd, H, H, F};
+      for (int p = 0; p < ZG_N_PROJ; p++) {
+        const bool kq = kq_type(qt[p]) && il[p] == 1 && width[p] % 64 == 0 && in_dim[p] % 256 == 0;
+        m->pf_ok = m->pf_ok && (qt[p] == ZG_Q4_0 || qt[p] == ZG_Q8_0 || kq);
+        m->pf_kq = m->pf_kq || kq_type(qt[p]);
+      }
       // Q|K|V and attention in one launch: Q4_0 / Q8_0 / Q4_K of one type and
       // layout on the one-launch strip path, in_dim 2048 (four strips, the
       // attention's 256-thread workgroups), two-group batches that never
@@ -1822,7 +1923,7 @@ extern "C" zg_status zg_model_prefill(zg_model* m, const uint32_t* tokens, size_
   if (!m) return ZG_ERR_INVALID_ARG;
   zg_ctx* ctx = m->ctx;
   if (!tokens || n == 0) return set_error(ctx, ZG_ERR_INVALID_ARG, "prefill: no tokens");
-  if (!m->pf_ok) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "prefill: the GEMMs take Q4_0 / Q8_0 projections");
+  if (!m->pf_ok) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "prefill: the GEMMs take Q4_0 / Q8_0 projections and plain Q4_K / Q6_K ones of widths in 64s and in_dims in 256s");
   if ((size_t)pos0 + n > m->d.max_ctx)
     return set_error(ctx, ZG_ERR_CONTEXT_FULL, "prefill: positions %u..%zu exceed max_ctx %u", pos0, pos0 + n - 1,
                      m->d.max_ctx);
@@ -1879,7 +1980,7 @@ extern "C" zg_status zg_model_generate_ex(zg_model* m, const uint32_t* prompt, s
     return hip_check(ctx, hipGraphLaunch(head ? m->g_step : m->g_prefill, ctx->stream), "graph launch");
   };
   if (batched && !m->pf_ok)
-    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "generate: the batched prefill's GEMMs take Q4_0 / Q8_0 projections");
+    return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "generate: the batched prefill's GEMMs take Q4_0 / Q8_0 and plain Q4_K / Q6_K projections");
   if (batched && (s = prefill_alloc(m))) return s;
   note_rows(m, 0, prompt, n_prompt, batched ? kRowBatched : kRowDecode);
   if ((s = set_state(m, prompt[0], batched ? (uint32_t)n_prompt - 1 : 0, (uint32_t)n_prompt, (uint32_t)n_gen)))

@@ -44,7 +44,7 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
   const float e[4] = {f.x, f.y, f.z, f.w};
   int q[4];
   float d;
-  reinterpret_cast<uint32_t*>(o + 4)[lane] = q8k_block_lane(v, lane, e, q, d);
+  reinterpret_cast<uint32_t*>(o + 4)[lane] = q8k_block_lane(lane, e, q, d);
   // sums of 16: four lanes per group
   int s16 = (q[0] + q[1]) + (q[2] + q[3]);
   s16 += __shfl_xor(s16, 1, 64);
