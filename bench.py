@@ -313,6 +313,43 @@ def bench_rows(ctx, steps: int, cpu=None):
         if cpu:
             out[f"prefill_gemm_{name}"]["cpu_baseline"] = cpu.prefill(f"{n_out}x{k} Q4_0X4 (fp32 x rows)", wh,
                                                                       xm_host, k, n_out, synth.Q4_0, 4, M)
+        del wd
+
+    # K-quant prefill GEMM, M = 512, the Qwen3-1.7B Q4_K_M FFN shapes: Q4_K
+    # gate / up 6144x2048 and Q6_K down 2048x6144, Q8_K activations
+    for name, qt, n_out, k in (("q4k_up", synth.Q4K, 6144, 2048), ("q6k_down", synth.Q6K, 2048, 6144)):
+        wh = synth.weight(rng, qt, n_out, k, 1)
+        wd = torch.from_numpy(wh).cuda()
+        xm_host = synth.activations(rng, M, k)
+        xm = torch.from_numpy(xm_host).cuda()
+        qs = torch.empty((M, k), dtype=torch.int8, device="cuda")
+        d8 = torch.empty((M, k // 256), dtype=torch.float32, device="cuda")
+        bs = torch.empty((M, k // 32), dtype=torch.int16, device="cuda")
+        ym = torch.empty((M, n_out), device="cuda")
+        ctx.quantize_q8k_split_dev(xm, qs, d8, bs, M, k)
+
+        def kgemm(i, st, wd=wd, qs=qs, d8=d8, bs=bs, ym=ym, qt=qt, n_out=n_out, k=k):
+            ctx.gemm_q8k_dev(qs, d8, bs, wd, ym, M, n_out, k, qt, stream=st)
+
+        def kquant(i, st, xm=xm, qs=qs, d8=d8, bs=bs, k=k):
+            ctx.quantize_q8k_split_dev(xm, qs, d8, bs, M, k, stream=st)
+
+        per, n, _ = _graph_time(kgemm, 16, max(64, steps // 20), 16)
+        perq, _, _ = _graph_time(kquant, 16, max(64, steps // 20), 16)
+        ops = 2 * M * n_out * k
+        tops = ops / (per * 1e-3) / 1e12
+        nbytes = wh.nbytes + M * k + M * (k // 256) * 4 + M * (k // 32) * 2 + 4 * M * n_out
+        tname = "Q4_K" if qt == synth.Q4K else "Q6_K"
+        out[f"prefill_gemm_{name}"] = {
+            "workload": f"prefill GEMM M=512 x {n_out}x{k} {tname}, Q8_K activations, int8 MFMA",
+            "us_per_launch": round(per * 1e3, 2), "int8_TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "ops_per_launch": ops, "bytes_per_launch": nbytes,
+            "quantize_us": round(perq * 1e3, 2)}
+        log(f"prefill GEMM {name}: {per * 1e3:.1f} us, {tops:.0f} TOPS; Q8_K quantize {perq * 1e3:.1f} us")
+        if cpu:
+            out[f"prefill_gemm_{name}"]["cpu_baseline"] = cpu.prefill(f"{n_out}x{k} {tname} (fp32 x rows)", wh,
+                                                                      xm_host, k, n_out, qt, 1, M)
+        del wd
     return out
 
 
@@ -327,6 +364,8 @@ def bench_read_floor(ctx, steps: int):
     out = {}
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     for key, nbytes, what in (("read_floor_7077888B", 7_077_888, "the C1 Q4_0X4 6144x2048 weights"),
+                              ("read_floor_33030144B", 33_030_144, "Q4_K 14336x4096 weights"),
+                              ("read_floor_48168960B", 48_168_960, "Q6_K 4096x14336 weights"),
                               ("read_floor_175646208B", 175_646_208, "Q4_0X4 151936x2048 weights")):
         c = _copies(nbytes)
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 0x7F) for i in range(c)]
@@ -424,6 +463,17 @@ def _profile_workloads(ctx, names, reps: int):
             ym = torch.empty((M, n_out), device="cuda")
             ctx.quantize_q8_0_split_dev(xm, qs, dd, M, k)
             run(name, lambda i: ctx.gemm_q8act_dev(qs, dd, wd, ym, M, n_out, k, synth.Q4_0, 4), 1)
+        elif name in ("kgemm_up", "kgemm_down"):
+            M = 512
+            qt, n_out, k = (synth.Q4K, 6144, 2048) if name == "kgemm_up" else (synth.Q6K, 2048, 6144)
+            wd = torch.from_numpy(synth.weight(rng, qt, n_out, k, 1)).cuda()
+            xm = torch.from_numpy(synth.activations(rng, M, k)).cuda()
+            qs = torch.empty((M, k), dtype=torch.int8, device="cuda")
+            d8 = torch.empty((M, k // 256), dtype=torch.float32, device="cuda")
+            bs = torch.empty((M, k // 32), dtype=torch.int16, device="cuda")
+            ym = torch.empty((M, n_out), device="cuda")
+            ctx.quantize_q8k_split_dev(xm, qs, d8, bs, M, k)
+            run(name, lambda i: ctx.gemm_q8k_dev(qs, d8, bs, wd, ym, M, n_out, k, qt), 1)
         elif name == "decode":
             # the decode bench's model and lengths, with the step's kernels
             # launched directly (no graph replay under the profiler); reps
@@ -504,7 +554,10 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
     kmodel = synth.random_model(kcfg, seed)
     gk = GpuModel(ctx, kmodel)
     gk.generate(prompt, 8)
-    _, _, t_gen_k = gk.generate(prompt, n_gen)
+    toks_k, t_pre_k, t_gen_k = gk.generate(prompt, n_gen)
+    # the same prompt through the batched prefill (Q8_K rows, K-quant GEMMs)
+    gk.generate(prompt, 8, batched_prefill=True)
+    toks_kb, t_pre_kb, _ = gk.generate(prompt, 8, batched_prefill=True)
     gk.close()
     k_bytes = kcfg.weight_bytes_per_token() + norms + float(np.mean(ctxs)) * kv_per_pos + kv_per_pos
     del kmodel
@@ -513,7 +566,9 @@ def bench_decode(ctx, n_prompt=128, n_gen=256, seed=0):
                                 "decode_tok_s": (n_gen - 1) / t_gen_b, "tokens_equal_to_token_by_token": agree},
             "plain_layout": {"decode_tok_s": (n_gen - 1) / t_gen_p, "tokens_equal_to_x4": agree_p},
             "q4_k_m": {"decode_tok_s": (n_gen - 1) / t_gen_k, "bytes_per_token": int(k_bytes),
-                       "gbs": k_bytes * (n_gen - 1) / t_gen_k / 1e9},
+                       "gbs": k_bytes * (n_gen - 1) / t_gen_k / 1e9, "prefill_tok_s": n_prompt / t_pre_k,
+                       "batched_prefill_tok_s": n_prompt / t_pre_kb, "batched_prefill_ms": t_pre_kb * 1e3,
+                       "batched_first_token_equal": bool(toks_kb[0] == toks_k[0])},
             "n_prompt": n_prompt,
             "n_gen": n_gen, "bytes_per_token": int(per_tok), "gbs": per_tok * tok_s / 1e9,
             "first_tokens": [int(t) for t in toks[:8]], "model": model, "prompt": prompt}
@@ -667,7 +722,8 @@ def main():
     ap.add_argument("--no-rows", action="store_true", help="skip the fused-QKV, LM-head, k-quant and GEMM lines")
     ap.add_argument("--profile", default="",
                     help="comma list of workloads to launch eagerly (no graph) for rocprofv3 counter passes, "
-                         "then exit: c1, tall, floor_c1, floor_tall, lmhead, qkv, q4k, q6k, gemm_up, gemm_down, copy")
+                         "then exit: c1, tall, floor_c1, floor_tall, lmhead, qkv, q4k, q6k, gemm_up, gemm_down, kgemm_up, "
+                         "kgemm_down, copy")
     ap.add_argument("--profile-reps", type=int, default=30)
     ap.add_argument("--pmc-calib", action="store_true",
                     help="first run one elementwise kernel that reads 256 MiB and writes 256 MiB, the "
@@ -730,7 +786,10 @@ def main():
         log(f"batched prefill: {bp['prefill_ms']:.2f} ms for {dec['n_prompt']} tokens "
             f"({bp['prefill_tok_s']:.0f} tok/s; token by token {dec['prefill_tok_s']:.0f} tok/s)")
         log(f"decode, plain v1 layout: {dec['plain_layout']['decode_tok_s']:.1f} tok/s")
-        log(f"decode, Q4_K_M pattern: {dec['q4_k_m']['decode_tok_s']:.1f} tok/s ({dec['q4_k_m']['gbs']:.0f} GB/s)")
+        log(f"decode, Q4_K_M pattern: {dec['q4_k_m']['decode_tok_s']:.1f} tok/s ({dec['q4_k_m']['gbs']:.0f} GB/s); "
+            f"batched prefill {dec['q4_k_m']['batched_prefill_ms']:.2f} ms "
+            f"({dec['q4_k_m']['batched_prefill_tok_s']:.0f} tok/s; token by token "
+            f"{dec['q4_k_m']['prefill_tok_s']:.0f} tok/s)")
         out["decode"] = {"tok_s": round(dec["tok_s"], 2), "ms_per_token": dec["ms_per_token"],
                          "prefill_tok_s": round(dec["prefill_tok_s"], 2),
                          "batched_prefill": {k: (round(v, 2) if isinstance(v, float) else v)

@@ -45,6 +45,13 @@ constexpr int kKgBM = 64, kKgBN = 64;  // workgroup tile
 constexpr int kKgKS = 128;             // K per stage
 constexpr int kKgRP = kKgKS + 16;      // LDS row pitch (bytes)
 constexpr int kKgSegs = 3;             // weight segments per launch (Q|K|V)
+#ifndef ZG_KG_PD
+#define ZG_KG_PD 2
+#endif
+constexpr int kKgPD = ZG_KG_PD;        // stages in flight
+#ifndef ZG_KG_WPE
+#define ZG_KG_WPE 1
+#endif
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -127,8 +134,10 @@ template <uint32_t WT>
 struct KgStage;
 template <>
 struct KgStage<Q4K> {
-  u32x4 a[2];  // 32 bytes of the A tile
-  u32x4 q, h;  // 16 quant bytes and the 16-byte superblock header
+  u32x4 a[2];   // 32 bytes of the A tile
+  u32x4 q, h;   // 16 quant bytes and the 16-byte superblock header
+  uint32_t bs;  // two 32-value sums of one row (int16 pair) of the stage's superblock
+  float d8;     // d8 of row tid % 64 for the stage's superblock
 };
 template <>
 struct KgStage<Q6K> {
@@ -136,10 +145,14 @@ struct KgStage<Q6K> {
   u32x4 l0, l1, h0, h1;  // 32 ql bytes, 32 qh bytes
   uint32_t sc;           // the two scale bytes of the lane's quarter (low 16 bits)
   uint32_t d;            // fp16 d
+  float d8;
 };
 
-template <uint32_t WT>
-__global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
+// PD: stages whose global loads are in flight while a stage is multiplied
+// (a ring of PD register stages; nst, the stage count, is a multiple of PD,
+// so every load is unconditional and the wait counts stay exact).
+template <uint32_t WT, int PD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))) void gemm_q8k_kernel(KgemmArgs a) {
   // the reference rounds every product and sum of the superblock terms on
   // its own: no fused multiply-add in this function (a pragma here does not
   // reach the operators inside HIP's __fadd_rn / __fmul_rn, which hipcc
@@ -148,6 +161,7 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
   constexpr int BM = kKgBM, BN = kKgBN, KS = kKgKS, RP = kKgRP;
   constexpr int MI = BM / 32, NJ = BN / 32;  // 16 x 16 tiles per wave
   constexpr int SBB = WT == Q4K ? 144 : 210;
+  static_assert(PD % 2 == 0, "stages come in superblock pairs");
   __shared__ __attribute__((aligned(16))) int8_t As[2][BM * RP];
   __shared__ __attribute__((aligned(16))) int8_t Bl[2][BN * RP];
   __shared__ __attribute__((aligned(16))) int8_t Bh[2][BN * RP];
@@ -170,40 +184,47 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
   const size_t wrow = (size_t)nsb * SBB;
   const int wc = tid >> 2, wp = tid & 3;  // weight staging: column, part (Q4_K 16-byte chunk; Q6_K quarter)
   const int mlast = a.m - 1;
+  // rows past m clamp to the last row (their outputs are dropped)
+  const int8_t* arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+    arow[i] = a.qs + (size_t)min(m0 + row, mlast) * a.k + ch * 16;
+  }
+  const float* d8row = a.d8 + (size_t)min(m0 + lane, mlast) * nsb;
+  const int16_t* bsrow = a.bs32 + (size_t)min(m0 + (tid >> 2), mlast) * (a.k / 32) + 2 * (tid & 3);
+  const uint8_t* wcol = w + (size_t)(n0 + wc) * wrow;
 
-  KgStage<WT> S;
-  // unconditional loads: rows past m clamp to the last row (their outputs
-  // are dropped)
-  auto stage_load = [&](int st) {
+  KgStage<WT> S[PD];
+  auto stage_load = [&](KgStage<WT>& R, int st) {
     const int sb = st >> 1, h = st & 1;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      S.a[i] = *reinterpret_cast<const u32x4*>(a.qs + (size_t)min(m0 + row, mlast) * a.k + sb * 256 + h * KS + ch * 16);
-    }
-    const uint8_t* blk = w + (size_t)(n0 + wc) * wrow + (size_t)sb * SBB;
+    for (int i = 0; i < 2; i++) R.a[i] = *reinterpret_cast<const u32x4*>(arow[i] + sb * 256 + h * KS);
+    const uint8_t* blk = wcol + (size_t)sb * SBB;
+    R.d8 = d8row[sb];
     if constexpr (WT == Q4K) {
-      S.h = *reinterpret_cast<const u32x4*>(blk);
-      S.q = *reinterpret_cast<const u32x4*>(blk + 16 + 64 * h + 16 * wp);
+      R.h = *reinterpret_cast<const u32x4*>(blk);
+      R.q = *reinterpret_cast<const u32x4*>(blk + 16 + 64 * h + 16 * wp);
+      R.bs = *reinterpret_cast<const uint32_t*>(bsrow + sb * 8);
     } else {
       // quarter wp of half h: ql[64h + 32(wp & 1) .. +32], qh[32h .. +32]
       const u32x4a2* lp = reinterpret_cast<const u32x4a2*>(blk + 64 * h + 32 * (wp & 1));
       const u32x4a2* hp = reinterpret_cast<const u32x4a2*>(blk + 128 + 32 * h);
       const u32x4a2 l0 = lp[0], l1 = lp[1], h0 = hp[0], h1 = hp[1];
-      S.l0 = u32x4{l0.x, l0.y, l0.z, l0.w};
-      S.l1 = u32x4{l1.x, l1.y, l1.z, l1.w};
-      S.h0 = u32x4{h0.x, h0.y, h0.z, h0.w};
-      S.h1 = u32x4{h1.x, h1.y, h1.z, h1.w};
-      S.sc = *reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h + 2 * wp);
-      S.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+      R.l0 = u32x4{l0.x, l0.y, l0.z, l0.w};
+      R.l1 = u32x4{l1.x, l1.y, l1.z, l1.w};
+      R.h0 = u32x4{h0.x, h0.y, h0.z, h0.w};
+      R.h1 = u32x4{h1.x, h1.y, h1.z, h1.w};
+      R.sc = *reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h + 2 * wp);
+      R.d = *reinterpret_cast<const uint16_t*>(blk + 208);
     }
   };
-  auto stage_store = [&](int st, int buf) {
-    const int sb = st >> 1, h = st & 1, sp = sb & 1;
+  // h: the stage's half of its superblock (0: also the superblock's terms)
+  auto stage_store = [&](const KgStage<WT>& R, int sp, int h, int buf) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<u32x4*>(&As[buf][row * RP + ch * 16]) = S.a[i];
+      *reinterpret_cast<u32x4*>(&As[buf][row * RP + ch * 16]) = R.a[i];
     }
     int8_t* bl = &Bl[buf][wc * RP];
     int8_t* bh = &Bh[buf][wc * RP];
@@ -212,11 +233,11 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
       // sub-blocks 2j (low nibbles) and 2j + 1 (high nibbles)
       const int j = 2 * h + (wp >> 1);
       int scA, mA, scB, mB;
-      kg_scale_min(S.h.y, S.h.z, S.h.w, 2 * j, scA, mA);
-      kg_scale_min(S.h.y, S.h.z, S.h.w, 2 * j + 1, scB, mB);
+      kg_scale_min(R.h.y, R.h.z, R.h.w, 2 * j, scA, mA);
+      kg_scale_min(R.h.y, R.h.z, R.h.w, 2 * j + 1, scB, mB);
       const uint32_t sA2 = (uint32_t)scA * 0x00010001u, sB2 = (uint32_t)scB * 0x00010001u;
       const int kA = (wp >> 1) * 64 + (wp & 1) * 16, kB = kA + 32;
-      const uint32_t qv[4] = {S.q.x, S.q.y, S.q.z, S.q.w};
+      const uint32_t qv[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
       uint32_t loA[4], hiA[4], loB[4], hiB[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
@@ -227,27 +248,34 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
       *reinterpret_cast<u32x4*>(bh + kA) = u32x4{hiA[0], hiA[1], hiA[2], hiA[3]};
       *reinterpret_cast<u32x4*>(bl + kB) = u32x4{loB[0], loB[1], loB[2], loB[3]};
       *reinterpret_cast<u32x4*>(bh + kB) = u32x4{hiB[0], hiB[1], hiB[2], hiB[3]};
-      if (h == 0 && wp == 0) {
-        Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.h.x & 0xFFFFu));
-        Bdm[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.h.x >> 16));
-        uint32_t mw[2] = {0u, 0u};
+      if (h == 0) {
+        if (wp == 0) {
+          Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(R.h.x & 0xFFFFu));
+          Bdm[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(R.h.x >> 16));
+          uint32_t mw[2] = {0u, 0u};
 #pragma unroll
-        for (int g = 0; g < 8; g++) {
-          int s_, m_;
-          kg_scale_min(S.h.y, S.h.z, S.h.w, g, s_, m_);
-          mw[g >> 2] |= (uint32_t)m_ << (8 * (g & 3));
+          for (int g = 0; g < 8; g++) {
+            int s_, m_;
+            kg_scale_min(R.h.y, R.h.z, R.h.w, g, s_, m_);
+            mw[g >> 2] |= (uint32_t)m_ << (8 * (g & 3));
+          }
+          *reinterpret_cast<uint2*>(&Bmn[sp][wc * 8]) = make_uint2(mw[0], mw[1]);
         }
-        *reinterpret_cast<uint2*>(&Bmn[sp][wc * 8]) = make_uint2(mw[0], mw[1]);
+        // row tid / 4, sums 2 (tid % 4) and + 1: digits lo = v & 127, hi = v >> 7
+        const int v0 = (int)(int16_t)(R.bs & 0xFFFFu), v1 = (int)(int16_t)(R.bs >> 16);
+        const int o = (tid >> 2) * 8 + 2 * (tid & 3);
+        *reinterpret_cast<uint16_t*>(&Aml[sp][o]) = (uint16_t)((v0 & 127) | ((v1 & 127) << 8));
+        *reinterpret_cast<uint16_t*>(&Amh[sp][o]) = (uint16_t)(((v0 >> 7) & 0xFF) | (((v1 >> 7) & 0xFF) << 8));
       }
     } else {
       // quarter Q = wp of half h: element 128 h + 32 Q + l (l < 32) is
       // ((ql[64 h + l + 32 (Q & 1)] >> 4 (Q >> 1)) & 15) | (((qh[32 h + l] >>
       // 2 Q) & 3) << 4), scale sc[8 h + 2 Q + l / 16]
       const int nsh = 4 * (wp >> 1), hsh = 2 * wp;
-      const int sc0 = (int)(int8_t)(S.sc & 0xFFu), sc1 = (int)(int8_t)(S.sc >> 8);
+      const int sc0 = (int)(int8_t)(R.sc & 0xFFu), sc1 = (int)(int8_t)(R.sc >> 8);
       const uint32_t s02 = ((uint32_t)sc0 & 0xFFFFu) * 0x00010001u, s12 = ((uint32_t)sc1 & 0xFFFFu) * 0x00010001u;
-      const uint32_t lv[8] = {S.l0.x, S.l0.y, S.l0.z, S.l0.w, S.l1.x, S.l1.y, S.l1.z, S.l1.w};
-      const uint32_t hv[8] = {S.h0.x, S.h0.y, S.h0.z, S.h0.w, S.h1.x, S.h1.y, S.h1.z, S.h1.w};
+      const uint32_t lv[8] = {R.l0.x, R.l0.y, R.l0.z, R.l0.w, R.l1.x, R.l1.y, R.l1.z, R.l1.w};
+      const uint32_t hv[8] = {R.h0.x, R.h0.y, R.h0.z, R.h0.w, R.h1.x, R.h1.y, R.h1.z, R.h1.w};
       uint32_t lo[8], hi[8];
 #pragma unroll
       for (int c = 0; c < 8; c++) {
@@ -259,19 +287,9 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
       *reinterpret_cast<u32x4*>(bl + k0 + 16) = u32x4{lo[4], lo[5], lo[6], lo[7]};
       *reinterpret_cast<u32x4*>(bh + k0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
       *reinterpret_cast<u32x4*>(bh + k0 + 16) = u32x4{hi[4], hi[5], hi[6], hi[7]};
-      if (h == 0 && wp == 0) Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(S.d & 0xFFFFu));
+      if (h == 0 && wp == 0) Bd[sp][wc] = (float)__builtin_bit_cast(_Float16, (unsigned short)(R.d & 0xFFFFu));
     }
-    if (h == 0) {
-      if constexpr (WT == Q4K) {
-        for (int i = tid; i < BM * 8; i += 256) {
-          const int row = i >> 3, g = i & 7;
-          const int v = a.bs32[(size_t)min(m0 + row, mlast) * (a.k / 32) + sb * 8 + g];
-          Aml[sp][i] = (int8_t)(v & 127);
-          Amh[sp][i] = (int8_t)(v >> 7);
-        }
-      }
-      for (int i = tid; i < BM; i += 256) Ad8[sp][i] = a.d8[(size_t)min(m0 + i, mlast) * nsb + sb];
-    }
+    if (h == 0 && tid < BM) Ad8[sp][tid] = R.d8;
   };
 
   float fdot[MI][NJ][4], fmin[MI][NJ][4];
@@ -285,78 +303,89 @@ __global__ __launch_bounds__(256) void gemm_q8k_kernel(KgemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) fdot[i][j][r] = fmin[i][j][r] = 0.0f;
     }
-  stage_load(0);
-  stage_store(0, 0);
+  // stage st lives in ring slot st % PD and LDS buffer st % 2
+#pragma unroll
+  for (int u = 0; u < PD; u++) stage_load(S[u], min(u, nst - 1));
+  stage_store(S[0], 0, 0, 0);
   __syncthreads();
-  for (int st = 0; st < nst; st++) {
-    const int buf = st & 1;
-    if (st + 1 < nst) stage_load(st + 1);
+  for (int s0 = 0; s0 < nst; s0 += PD) {
 #pragma unroll
-    for (int kk = 0; kk < KS / 64; kk++) {
-      v4i av[MI], bl[NJ], bh[NJ];
+    for (int u = 0; u < PD; u++) {
+      const int st = s0 + u, buf = u & 1;
+      // slot u is in LDS already: refill it PD stages ahead (clamped: the
+      // last stages reload the final stage and never store it)
+      stage_load(S[u], min(st + PD, nst - 1));
 #pragma unroll
-      for (int i = 0; i < MI; i++) av[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm + 16 * i + r16) * RP + kk * 64 + kq16]);
+      for (int kk = 0; kk < KS / 64; kk++) {
+        v4i av[MI], bl[NJ], bh[NJ];
 #pragma unroll
-      for (int j = 0; j < NJ; j++) {
-        bl[j] = *reinterpret_cast<const v4i*>(&Bl[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
-        bh[j] = *reinterpret_cast<const v4i*>(&Bh[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
-      }
-#pragma unroll
-      for (int i = 0; i < MI; i++)
+        for (int i = 0; i < MI; i++)
+          av[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm + 16 * i + r16) * RP + kk * 64 + kq16]);
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-          alo[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bl[j], alo[i][j], 0, 0, 0);
-          ahi[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bh[j], ahi[i][j], 0, 0, 0);
+          bl[j] = *reinterpret_cast<const v4i*>(&Bl[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
+          bh[j] = *reinterpret_cast<const v4i*>(&Bh[buf][(wn + 16 * j + r16) * RP + kk * 64 + kq16]);
         }
-    }
-    if (st & 1) {
-      // superblock done: the float terms in the reference's order
-      const int sp = (st >> 1) & 1;
-      long aml[MI], amh[MI], bm[NJ];
-      if constexpr (WT == Q4K) {
-        // min_sum through one MFMA per digit: k = sub-block 0..7 in lanes
-        // 0..15, zeros elsewhere
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+          for (int j = 0; j < NJ; j++) {
+            alo[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bl[j], alo[i][j], 0, 0, 0);
+            ahi[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bh[j], ahi[i][j], 0, 0, 0);
+          }
+      }
+      if (u & 1) {
+        // superblock done: the float terms in the reference's order
+        const int sp = (st >> 1) & 1;
+        long aml[MI], amh[MI], bm[NJ];
+        if constexpr (WT == Q4K) {
+          // min_sum through one MFMA per digit: k = sub-block 0..7 in lanes
+          // 0..15, zeros elsewhere
+#pragma unroll
+          for (int i = 0; i < MI; i++) {
+            aml[i] = lane < 16 ? *reinterpret_cast<const long*>(&Aml[sp][(wm + 16 * i + r16) * 8]) : 0;
+            amh[i] = lane < 16 ? *reinterpret_cast<const long*>(&Amh[sp][(wm + 16 * i + r16) * 8]) : 0;
+          }
+#pragma unroll
+          for (int j = 0; j < NJ; j++)
+            bm[j] = lane < 16 ? *reinterpret_cast<const long*>(&Bmn[sp][(wn + 16 * j + r16) * 8]) : 0;
+        }
 #pragma unroll
         for (int i = 0; i < MI; i++) {
-          aml[i] = lane < 16 ? *reinterpret_cast<const long*>(&Aml[sp][(wm + 16 * i + r16) * 8]) : 0;
-          amh[i] = lane < 16 ? *reinterpret_cast<const long*>(&Amh[sp][(wm + 16 * i + r16) * 8]) : 0;
-        }
+          const float4 d8v = *reinterpret_cast<const float4*>(&Ad8[sp][wm + 16 * i + rq]);
+          const float d8r[4] = {d8v.x, d8v.y, d8v.z, d8v.w};
 #pragma unroll
-        for (int j = 0; j < NJ; j++) bm[j] = lane < 16 ? *reinterpret_cast<const long*>(&Bmn[sp][(wn + 16 * j + r16) * 8]) : 0;
-      }
+          for (int j = 0; j < NJ; j++) {
+            const float dw = Bd[sp][wn + 16 * j + r16];
+            if constexpr (WT == Q4K) {
+              const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(aml[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+              const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(amh[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+              const float dmw = Bdm[sp][wn + 16 * j + r16];
 #pragma unroll
-      for (int i = 0; i < MI; i++) {
-        const float4 d8v = *reinterpret_cast<const float4*>(&Ad8[sp][wm + 16 * i + rq]);
-        const float d8r[4] = {d8v.x, d8v.y, d8v.z, d8v.w};
+              for (int r = 0; r < 4; r++) {
+                const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
+                const int msum = (mh[r] << 7) + ml[r];
+                const float dc = dw * d8r[r], dmc = dmw * d8r[r];
+                fdot[i][j][r] = fdot[i][j][r] + dc * (float)isum;
+                fmin[i][j][r] = fmin[i][j][r] + dmc * (float)msum;
+              }
+            } else {
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-          const float dw = Bd[sp][wn + 16 * j + r16];
-          if constexpr (WT == Q4K) {
-            const v4i ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(aml[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-            const v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(amh[i], bm[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-            const float dmw = Bdm[sp][wn + 16 * j + r16];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-              const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
-              const int msum = (mh[r] << 7) + ml[r];
-              const float dc = dw * d8r[r], dmc = dmw * d8r[r];
-              fdot[i][j][r] = fdot[i][j][r] + dc * (float)isum;
-              fmin[i][j][r] = fmin[i][j][r] + dmc * (float)msum;
+              for (int r = 0; r < 4; r++) {
+                const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
+                fdot[i][j][r] = fdot[i][j][r] + (dw * d8r[r]) * (float)isum;
+              }
             }
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-              const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
-              fdot[i][j][r] = fdot[i][j][r] + (dw * d8r[r]) * (float)isum;
-            }
+            ahi[i][j] = v4i{0, 0, 0, 0};
+            alo[i][j] = v4i{0, 0, 0, 0};
           }
-          ahi[i][j] = v4i{0, 0, 0, 0};
-          alo[i][j] = v4i{0, 0, 0, 0};
         }
       }
+      // the next stage into the other buffer (past the end: a clamped
+      // repeat that nothing reads)
+      stage_store(S[(u + 1) % PD], ((st + 1) >> 1) & 1, (u + 1) & 1, buf ^ 1);
+      __syncthreads();
     }
-    if (st + 1 < nst) stage_store(st + 1, buf ^ 1);
-    __syncthreads();
   }
   // D layout of v_mfma_*_16x16*: lane l holds rows 4 (l / 16) + r, column l % 16
 #pragma unroll
@@ -401,7 +430,8 @@ zg_status zg::run_gemm_q8k(zg_ctx* ctx, const int8_t* qs, const float* d8, const
     return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: bad arguments");
   if (w_type != ZG_Q4K && w_type != ZG_Q6K) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "gemm_q8k: weights must be Q4_K/Q6_K");
   if (k == 0 || k % 256) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: k %% 256 != 0");
-  if ((reinterpret_cast<uintptr_t>(qs) & 15) || (k % 16) || (reinterpret_cast<uintptr_t>(d8) & 15))
+  if ((reinterpret_cast<uintptr_t>(qs) & 15) || (k % 16) || (reinterpret_cast<uintptr_t>(d8) & 3) ||
+      (reinterpret_cast<uintptr_t>(bs32) & 3))
     return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm_q8k: activations misaligned");
   KgemmArgs a{};
   a.qs = qs;
@@ -434,8 +464,15 @@ zg_status zg::run_gemm_q8k(zg_ctx* ctx, const int8_t* qs, const float* d8, const
   a.n = (int)n;
   a.k = (int)k;
   const dim3 grid((unsigned)(n / kKgBN), (unsigned)((m + kKgBM - 1) / kKgBM));
-  if (w_type == ZG_Q4K) hipLaunchKernelGGL(gemm_q8k_kernel<Q4K>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(gemm_q8k_kernel<Q6K>, grid, dim3(256), 0, st, a);
+  // kKgPD stages in flight when the stage count is a multiple of it, else two
+  const bool deep = (k / 256) % (kKgPD / 2) == 0;
+  if (w_type == ZG_Q4K) {
+    if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, kKgPD>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, 2>), grid, dim3(256), 0, st, a);
+  } else {
+    if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, kKgPD>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, 2>), grid, dim3(256), 0, st, a);
+  }
   return hip_check(ctx, hipGetLastError(), "gemm_q8k launch");
 }
 
