@@ -358,7 +358,8 @@ def bench_read_floor(ctx, steps: int):
     same number of weight bytes and computes nothing (zg_read_floor_dev),
     graph-replayed over rotating copies like the headline.  Each size is
     timed with 1, 2, 4 and 8 128-bit loads per thread; the fastest is the
-    floor."""
+    floor.  Then the Q4_0X4 strip GEMV's load pattern without its decode
+    (zg_strip_loads_dev) at the C1 and LM-head heights."""
     import torch
 
     out = {}
@@ -380,6 +381,30 @@ def bench_read_floor(ctx, steps: int):
         out[key] = _row(f"read floor: {nbytes} B ({what}), best of 1/2/4/8 loads per thread", per_u[best_u],
                         nbytes, n, c, loads_per_thread=best_u,
                         us_by_loads_per_thread={u: round(v * 1e3, 3) for u, v in per_u.items()})
+        del bufs
+    # the strip GEMV's load pattern alone (zg_strip_loads_dev): the one-batch
+    # form at C1's 6144 rows and the batch-loop form at 151,936 rows, weights
+    # only and with each lane's x quarters
+    import numpy as np
+
+    from zero_amd import synth
+
+    x = torch.from_numpy(synth.activations(np.random.default_rng(5), 2048)).cuda()
+    for key, rows, what in (("strip_loads_6144x2048", 6144, "C1 form: one batch of 3 groups per workgroup"),
+                            ("strip_loads_151936x2048", 151_936, "tall form: 4-group batches, two in flight")):
+        nbytes = rows * 2048 // 32 * 18
+        c = _copies(nbytes)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 0x7F) for i in range(c)]
+        per_x = {}
+        for with_x in (False, True):
+            def ld(i, st, with_x=with_x):
+                ctx.strip_loads_dev(bufs[i], rows, x if with_x else None, sink, stream=st)
+
+            per, n, _ = _graph_time(ld, c, max(40, steps // (4 if nbytes < 1 << 24 else 40)), c)
+            per_x[with_x] = per
+        out[key] = _row(f"Q4_0X4 strip GEMV loads without the decode, {rows}x2048 ({what}), weights only",
+                        per_x[False], nbytes, n, c, us_with_x_quarters=round(per_x[True] * 1e3, 3))
+        log(f"  with the x quarters: {per_x[True] * 1e3:.2f} us")
         del bufs
     return out
 

@@ -174,6 +174,17 @@ zg_status zg_fp16_to_f32_dev(zg_ctx *ctx, const uint16_t *d_in, float *d_out, si
  * that real data never writes. */
 zg_status zg_read_floor_dev(zg_ctx *ctx, const void *d_src, size_t bytes, uint32_t loads_per_thread,
                             uint32_t *d_sink, void *stream);
+/* Measurement hook, no reference counterpart: the Q4_0X4 strip GEMV's loads
+ * without its decode, for `rows` x 2048 Q4_0X4 weights (rows % 4 == 0): the
+ * GEMV's own per-lane load instructions, cache policy and launch form (one
+ * batch of three groups per workgroup for decode-sized launches, else a
+ * loop over four-group batches with two in flight), and with d_x non-null
+ * (2048 floats) also each lane's two float4 quarters of x.  Together with
+ * zg_read_floor_dev it separates a GEMV's time into the plain read, the
+ * load pattern and the decode.  d_sink: one uint32 that real data never
+ * writes. */
+zg_status zg_strip_loads_dev(zg_ctx *ctx, const void *d_w, size_t rows, const float *d_x, uint32_t *d_sink,
+                             void *stream);
 
 /* On-the-fly Q8_0 activation quantization of rows x k values (k % 32 == 0):
  * the packer's quantize_q8_0_block (tools/silicatepack.py:893-907) bit for

@@ -136,6 +136,7 @@ SIGNATURES = {
     "zg_dequant_dev": (_ST, [_P, _P, _P, _S, _S, _U32, _U32, _P]),
     "zg_fp16_to_f32_dev": (_ST, [_P, _P, _P, _S, _P]),
     "zg_read_floor_dev": (_ST, [_P, _P, _S, _U32, _P, _P]),
+    "zg_strip_loads_dev": (_ST, [_P, _P, _S, _P, _P, _P]),
     "zg_quantize_q8_0_dev": (_ST, [_P, _P, _P, _S, _S, _P]),
     "zg_quantize_q8_0_split_dev": (_ST, [_P, _P, _P, _P, _S, _S, _P]),
     "zg_gemm_q8act_dev": (_ST, [_P, _P, _P, _P, _P, _S, _S, _S, _U32, _U32, _P]),

@@ -875,3 +875,14 @@ extern "C" zg_status zg_read_floor_dev(zg_ctx* ctx, const void* d_src, size_t by
   return hip_check(ctx, launch_read_floor(d_src, bytes, (int)loads_per_thread, d_sink, pick_stream(ctx, stream)),
                    "read_floor launch");
 }
+
+extern "C" zg_status zg_strip_loads_dev(zg_ctx* ctx, const void* d_w, size_t rows, const float* d_x, uint32_t* d_sink,
+                                        void* stream) {
+  if (!ctx) return ZG_ERR_INVALID_ARG;
+  if (!d_w || !d_sink) return set_error(ctx, ZG_ERR_INVALID_ARG, "strip_loads: null pointer");
+  if (rows % 4 || rows / 4 > (size_t)INT32_MAX || (reinterpret_cast<uintptr_t>(d_w) & 15) ||
+      (d_x && (reinterpret_cast<uintptr_t>(d_x) & 15)))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "strip_loads: rows %% 4 != 0 or misaligned buffer");
+  return hip_check(ctx, launch_strip_loads(static_cast<const uint8_t*>(d_w), d_x, rows, d_sink, pick_stream(ctx, stream)),
+                   "strip_loads launch");
+}

@@ -396,6 +396,57 @@ __global__ __launch_bounds__(256) void read_floor_kernel(const u32x4* __restrict
   if (acc == 0x9E3779B9u) *sink = acc;
 }
 
+// The strip GEMV's loads without its decode, Q4_0X4 at in_dim 2048 (four
+// strips, one wave each): lane (b, r) of wave s loads, per group, the quant
+// bytes and fp16 d of row r of block 16 s + b through strip_load (the
+// GEMV's own load instructions and cache policy) and, with X, its two
+// float4 quarters of x.  ONEB: one batch of GB groups per workgroup (the
+// decode-sized form); else a batch loop over GB-group batches, the next
+// batch's loads issued before the current one is consumed (the tall form,
+// cache-allocating loads as there).  Indices past the last group clamp.
+// The words feed a store that real data never triggers.
+template <int GB, bool ONEB, bool X>
+__global__ __launch_bounds__(256) void strip_load_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                         int groups, uint32_t* sink) {
+  constexpr size_t kGroupBytes = 64 * 72;  // 64 group-blocks of 72 bytes
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = lane >> 2, r = lane & 3, kb = wave * 16 + b;
+  uint32_t acc = 0;
+  if (X) {
+    const float4* x4 = reinterpret_cast<const float4*>(x + kb * 32);
+    const float4 xl = x4[r], xh = x4[4 + r];
+    acc = (__float_as_uint(xl.x) ^ __float_as_uint(xl.y) ^ __float_as_uint(xl.z) ^ __float_as_uint(xl.w)) ^
+          (__float_as_uint(xh.x) ^ __float_as_uint(xh.y) ^ __float_as_uint(xh.z) ^ __float_as_uint(xh.w));
+  }
+  auto load = [&](LaneW<Q4_0> (&L)[GB], int batch) {
+#pragma unroll
+    for (int j = 0; j < GB; j++) {
+      const int g = min(batch * GB + j, groups - 1);
+      strip_load<Q4_0, !ONEB>(L[j], w + (size_t)g * kGroupBytes + kb * 72, r);
+    }
+  };
+  auto consume = [&](const LaneW<Q4_0> (&L)[GB]) {
+#pragma unroll
+    for (int j = 0; j < GB; j++) acc ^= L[j].q[0] ^ L[j].q[1] ^ L[j].q[2] ^ L[j].q[3] ^ L[j].d;
+  };
+  if (ONEB) {
+    LaneW<Q4_0> L[GB];
+    load(L, blockIdx.x);
+    consume(L);
+  } else {
+    const int nbatch = (groups + GB - 1) / GB, step = gridDim.x;
+    LaneW<Q4_0> A[GB], B[GB];
+    load(A, blockIdx.x);
+    for (int bt = blockIdx.x; bt < nbatch; bt += 2 * step) {
+      load(B, min(bt + step, nbatch - 1));
+      consume(A);
+      load(A, min(bt + 2 * step, nbatch - 1));
+      consume(B);
+    }
+  }
+  if (acc == 0x9E3779B9u) *sink = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Host-side launchers.
 // ---------------------------------------------------------------------------
@@ -1010,6 +1061,24 @@ hipError_t launch_read_floor(const void* src, size_t bytes, int loads_per_thread
     case 4: hipLaunchKernelGGL(read_floor_kernel<4>, dim3(grid), dim3(256), 0, st, s4, n16, sink); break;
     case 8: hipLaunchKernelGGL(read_floor_kernel<8>, dim3(grid), dim3(256), 0, st, s4, n16, sink); break;
     default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_strip_loads(const uint8_t* w, const float* x, size_t rows, uint32_t* sink, hipStream_t st) {
+  const int groups = (int)(rows / 4);
+  if (groups == 0) return hipSuccess;
+  // the strip GEMV's forms: one batch of three groups per workgroup when
+  // that gives at most ZG_ONEB_PER_CU workgroups per CU (C1's 512), else
+  // four-group batches over four resident workgroups per CU
+  const int nb3 = (groups + 2) / 3;
+  if (nb3 <= cu_count() * ZG_ONEB_PER_CU) {
+    if (x) hipLaunchKernelGGL((strip_load_kernel<3, true, true>), dim3(nb3), dim3(256), 0, st, w, x, groups, sink);
+    else hipLaunchKernelGGL((strip_load_kernel<3, true, false>), dim3(nb3), dim3(256), 0, st, w, x, groups, sink);
+  } else {
+    const int nb4 = (groups + 3) / 4, grid = std::min(nb4, cu_count() * 4);
+    if (x) hipLaunchKernelGGL((strip_load_kernel<4, false, true>), dim3(grid), dim3(256), 0, st, w, x, groups, sink);
+    else hipLaunchKernelGGL((strip_load_kernel<4, false, false>), dim3(grid), dim3(256), 0, st, w, x, groups, sink);
   }
   return hipGetLastError();
 }

@@ -131,5 +131,6 @@ bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k);
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t v, hipStream_t st);
 hipError_t launch_read_floor(const void* src, size_t bytes, int loads_per_thread, uint32_t* sink, hipStream_t st);
+hipError_t launch_strip_loads(const uint8_t* w, const float* x, size_t rows, uint32_t* sink, hipStream_t st);
 
 }  // namespace zg

@@ -238,6 +238,12 @@ class Context:
         floor that a GEMV of the same weight bytes is measured against."""
         self.check(self.lib.zg_read_floor_dev(self.h, _ptr(src), nbytes, loads_per_thread, _ptr(sink), stream))
 
+    def strip_loads_dev(self, w, rows, x, sink, stream=None):
+        """The Q4_0X4 strip GEMV's loads alone, rows x 2048 (zg_strip_loads_dev);
+        x None: the weight loads only."""
+        self.check(self.lib.zg_strip_loads_dev(self.h, _ptr(w), rows, None if x is None else _ptr(x), _ptr(sink),
+                                               stream))
+
     def quantize_q8_0_dev(self, x, q_blocks, rows, k, stream=None):
         self.check(self.lib.zg_quantize_q8_0_dev(self.h, _ptr(x), _ptr(q_blocks), rows, k, stream))
 
