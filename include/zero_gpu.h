@@ -217,8 +217,8 @@ zg_status zg_quantize_q8k_split_dev(zg_ctx *ctx, const float *d_x, int8_t *d_qs,
                                     int16_t *d_bs32, size_t rows, size_t k, void *stream);
 /* Prefill GEMM for K-quant weights on int8 MFMA: Y[m][n] (+)= X[m] . W[n]
  * for split Q8_K activations (zg_quantize_q8k_split_dev) and plain Q4_K or
- * Q6_K rows (w_type 12 / 14; n % 64 == 0, k % 256 == 0, qs and d8 16-byte
- * aligned).  Each output is linear_q4k_vnni_range's arithmetic
+ * Q6_K rows (w_type 12 / 14; n % 64 == 0, k % 256 == 0, qs 16-byte aligned,
+ * d8 and bs32 4-byte aligned).  Each output is linear_q4k_vnni_range's arithmetic
  * (kernel/src/arch/x86_64/math/vnni.rs:258-476) bit for bit: per superblock
  * the exact integer sums, then dot += (d_w d8) int_sum, min += (dmin_w d8)
  * min_sum, y = dot - min; Q6_K the same construction with (q - 32) and its
