@@ -244,6 +244,24 @@ def bench_rows(ctx, steps: int, cpu=None):
             out[key]["cpu_baseline"] = cpu.gemv(name, wh, x_host, H, rows, synth.Q4_0, 4, wh.nbytes + 4 * H + 4 * rows)
         del wh
 
+    # the same weights in the model's split-scale X4 device layout
+    # (interleave 5: each group's quants, then its scales): the headline shape
+    # and the LM-head height, the same strip kernel with one 16-byte quant load
+    # and one contiguous scale load per lane
+    for name, key, rows in (("Q4_0 split-scale X4 6144x2048 (the model's layout of the headline weights)",
+                             "q4_0_split_6144x2048", 6144),
+                            ("Q4_0 split-scale X4 151936x2048", "q4_0_split_151936x2048", 151_936)):
+        wh = synth.x4_split(synth.weight(rng, synth.Q4_0, rows, H, 4), rows, H, synth.Q4_0)
+        wd, c = rotating(wh)
+        yk = torch.empty(rows, device="cuda")
+
+        def spl(i, st, wd=wd, yk=yk, rows=rows):
+            ctx.linear_dev(x, wd[i], yk, H, rows, synth.Q4_0, 5, stream=st)
+
+        per, n, _ = _graph_time(spl, c, max(40, steps // (4 if rows < 16384 else 20)), 8 if rows > 16384 else 40)
+        out[key] = _row(name, per, wh.nbytes + 4 * H + 4 * rows, n, c)
+        del wd, wh
+
     # k-quants at Llama-3-8B FFN shapes
     for name, qt, rows, k in (("Q4_K 14336x4096 (gate/up)", synth.Q4K, 14336, 4096),
                               ("Q6_K 4096x14336 (down)", synth.Q6K, 4096, 14336)):

@@ -187,6 +187,36 @@ def test_mixed_projection_quants(ctx, zo):
         ctx.clear()
 
 
+def test_qwen3_1_7b_shape_q8_0_projections(ctx, zo):
+    """Q8_0X4 layer projections at the Qwen3-1.7B shape (the model splits
+    them into scale-split groups, which run every layer launch on the strip
+    kernel: gate|up with SwiGLU at 3,072 groups, down at 12 strips): a
+    6-token prompt token by token, its logits at the last two positions
+    within rel 1e-3 of the oracle, then 8 greedy tokens equal to the
+    oracle's, token-by-token and batched prefill."""
+    cfg = synth.ModelConfig(n_layers=4, max_ctx=32, lin_type=synth.Q8_0)
+    model = synth.random_model(cfg, seed=13)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(13, 6, cfg.vocab_real)
+        with zo.Pool(16):
+            for i, t in enumerate(prompt):
+                nxt, _, _, lg = gm.step(int(t), i, want_logits=i >= 4)
+                om.forward(int(t), i)
+                if i >= 4:
+                    rc, t_ref, _, lg_ref = om.lm_head()
+                    assert rc == 0 and rel_err(lg, lg_ref) <= REL_TOL and nxt == t_ref
+            toks, _, _ = gm.generate(prompt, 8)
+            assert np.array_equal(toks, om.generate(prompt, 8))
+            toks_b, _, _ = gm.generate(prompt, 8, batched_prefill=True)
+            assert np.array_equal(toks_b, om.generate_batched(prompt, 8))
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
+
+
 def test_qwen3_1_7b_shape_q4_k_m(ctx, zo):
     """The reference's default dispatch at the Qwen3-1.7B shape: Q4_K layer
     projections with the Q4_K_M pattern's Q6_K attn_v / ffn_down, Q4_K token

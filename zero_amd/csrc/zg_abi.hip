@@ -276,18 +276,23 @@ zg_status zg::resolve(zg_ctx* ctx, const void* w, size_t need, uint32_t qt, cons
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// X4 (interleave 4) or split-scale X4 (interleave 5: strip-sized in_dim
+// only) Q4_0 / Q8_0 groups through the X4 dispatch
 bool zg::pair_path_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, const void* x) {
-  return il == 4 && (qt == ZG_Q4_0 || qt == ZG_Q8_0) && k % 64 == 0 && k <= kMaxPairK && n % 4 == 0 &&
-         aligned16(w) && aligned16(x) && gemv_x4_lds_bytes(qt, (int)k) <= 65536;
+  if ((qt != ZG_Q4_0 && qt != ZG_Q8_0) || n % 4 || !aligned16(w) || !aligned16(x)) return false;
+  if (il == 5) return strip_path_ok((int)k);  // strip-kernel launches only
+  return il == 4 && k % 64 == 0 && k <= kMaxPairK && gemv_x4_lds_bytes(qt, (int)k) <= 65536;
 }
 
 zg_status zg::check_shape(zg_ctx* ctx, uint32_t qt, uint32_t il, size_t k, size_t n) {
   size_t be, bb;
   if (!type_geom(qt, &be, &bb)) return set_error(ctx, ZG_ERR_UNSUPPORTED_QUANT, "unsupported quant type %u", qt);
   if (k == 0 || k % be) return set_error(ctx, ZG_ERR_INVALID_ARG, "in_dim %zu not a multiple of %zu", k, be);
-  if (il != 1 && il != 4) return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave %u", il);
-  if (il == 4 && ((qt != ZG_Q4_0 && qt != ZG_Q8_0) || n % 4))
-    return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave 4 needs Q4_0/Q8_0 and out_dim %% 4 == 0");
+  if (il != 1 && il != 4 && il != 5) return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave %u", il);
+  if ((il == 4 || il == 5) && ((qt != ZG_Q4_0 && qt != ZG_Q8_0) || n % 4))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave %u needs Q4_0/Q8_0 and out_dim %% 4 == 0", il);
+  if (il == 5 && !strip_path_ok((int)k))
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "interleave 5 needs in_dim a multiple of 512 up to 8192");
   if (k > (size_t)INT32_MAX || n > (size_t)UINT32_MAX / 2) return set_error(ctx, ZG_ERR_INVALID_ARG, "shape too large");
   return ZG_OK;
 }
@@ -308,7 +313,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.norm_w = norm_w;
     a.eps = eps;
     a.best = best;
-    a.flags = gemv_flags;
+    a.flags = gemv_flags | (il == 5 ? kGemvSplit : 0u);
     a.seg[0].w = w + g0 * gbytes;
     a.seg[0].y = y ? y + 4 * g0 : nullptr;
     a.seg[0].resid = resid ? resid + 4 * g0 : nullptr;
@@ -317,6 +322,7 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
     a.seg[0].row_hi = (uint32_t)(end - 4 * g0);
     return hip_check(ctx, launch_gemv_x4(a, qt, pro, epi, st), "gemv_x4 launch");
   }
+  if (il == 5) return set_error(ctx, ZG_ERR_INVALID_ARG, "split-scale X4 weights need 16-byte aligned w and x");
   if (plain_strip_ok(qt, il, k, n, w, x) && (pro == PRO_PLAIN || pro == PRO_RMSNORM) &&
       (epi == EPI_STORE || epi == EPI_RESID || epi == EPI_ARGMAX) && !(pro == PRO_RMSNORM && epi == EPI_RESID)) {
     // plain rows in fours: group g is rows 4g..4g+3
@@ -407,7 +413,8 @@ zg_status zg::run_linear(zg_ctx* ctx, const float* x, const uint8_t* w, float* y
 bool zg::fused_x4_ok(const float* x, const FusedDev* segs, size_t nseg, size_t k) {
   bool ok = nseg >= 1 && nseg <= 3;
   for (size_t i = 0; i < nseg && ok; i++)
-    ok = pair_path_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt;
+    ok = pair_path_ok(segs[i].qt, segs[i].il, k, segs[i].n, segs[i].w, x) && segs[i].qt == segs[0].qt &&
+         segs[i].il == segs[0].il;
   return ok;
 }
 
@@ -540,6 +547,7 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
       g += (uint32_t)(segs[i].n / 4);
     }
     a.total_groups = g;
+    if (pair && segs[0].il == 5) a.flags |= kGemvSplit;
     return hip_check(ctx, pair ? launch_gemv_x4(a, segs[0].qt, pro, epi, st) : launch_gemv_plain(a, segs[0].qt, pro, epi, st),
                      "fused gemv launch");
   }
@@ -554,6 +562,7 @@ zg_status zg::run_fused(zg_ctx* ctx, const float* x, const FusedDev* segs, size_
     }
   }
   for (size_t i = first; i < nseg; i++) {
+    // (split-scale segments that do not share a launch go one by one)
     zg_status s = run_linear(ctx, x, segs[i].w, segs[i].y, k, segs[i].n, segs[i].qt, segs[i].il, 0, segs[i].n,
                              EPI_STORE, nullptr, nullptr, pro, norm_w, eps, st);
     if (s) return s;
@@ -612,6 +621,7 @@ zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml,
   a.attn_ml = part_ml;
   a.attn_nsplit = nsplit;
   a.attn_hd = hd;
+  a.flags = il == 5 ? kGemvSplit : 0u;
   a.seg[0].w = w;
   a.seg[0].y = y;
   a.seg[0].resid = y;
@@ -797,7 +807,7 @@ extern "C" zg_status zg_linear_q8act_dev(zg_ctx* ctx, const void* d_xq, const vo
     return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_q8act: in_dim %zu (multiple of 512 up to 8192) / out_dim %zu (%% 4)",
                      in_dim, out_dim);
   const uintptr_t wa = reinterpret_cast<uintptr_t>(d_w);
-  if ((reinterpret_cast<uintptr_t>(d_xq) & 1) || (interleave == 4 ? (wa & 7) : (wa & 1)))
+  if ((reinterpret_cast<uintptr_t>(d_xq) & 1) || (interleave == 4 ? (wa & 7) : interleave == 5 ? (wa & 15) : (wa & 1)))
     return set_error(ctx, ZG_ERR_INVALID_ARG, "linear_q8act: misaligned buffer");
   if (out_dim == 0) return ZG_OK;
   GemvArgs a{};
@@ -810,8 +820,9 @@ extern "C" zg_status zg_linear_q8act_dev(zg_ctx* ctx, const void* d_xq, const vo
   a.seg[0].g_begin = 0;
   a.seg[0].row_lo = 0;
   a.seg[0].row_hi = (uint32_t)out_dim;
+  a.flags = interleave == 5 ? kGemvSplit : 0u;
   hipStream_t st = pick_stream(ctx, stream);
-  const hipError_t e = interleave == 4 ? launch_gemv_x4(a, ggml_type, PRO_Q8X, EPI_STORE, st)
+  const hipError_t e = interleave != 1 ? launch_gemv_x4(a, ggml_type, PRO_Q8X, EPI_STORE, st)
                                        : launch_gemv_plain(a, ggml_type, PRO_Q8X, EPI_STORE, st);
   return hip_check(ctx, e, "linear_q8act launch");
 }
@@ -852,6 +863,7 @@ extern "C" zg_status zg_dequant_dev(zg_ctx* ctx, const void* d_w, float* d_out, 
   if (!ctx) return ZG_ERR_INVALID_ARG;
   if (!d_w || !d_out) return set_error(ctx, ZG_ERR_INVALID_ARG, "dequant_dev: null pointer");
   zg_status s = check_shape(ctx, ggml_type, interleave, in_dim, rows);
+  if (!s && interleave == 5) s = set_error(ctx, ZG_ERR_INVALID_ARG, "dequant: interleave 5 is a GEMV layout only");
   if (s) return s;
   DequantArgs a{static_cast<const uint8_t*>(d_w), d_out, rows, in_dim, ggml_type, (int)interleave};
   const bool pair = pair_path_ok(ggml_type, interleave, in_dim, rows, d_w, d_out);

@@ -891,6 +891,16 @@ static hipError_t launch_lds(const GemvArgs& a, hipStream_t st) {
 // Q4_0X4 takes the strip kernel (measured faster at every decode shape).
 template <uint32_t QT, int PRO, int EPI>
 static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
+  if (a.flags & kGemvSplit) {
+    // split-scale groups: the strip kernel's forms only
+    if (!strip_path_ok(a.k)) return hipErrorInvalidValue;
+    if constexpr (PRO == PRO_ATTN) {
+      if (QT != Q4_0 || a.attn_nsplit < 1 || a.attn_nsplit > kAttnSplits || a.attn_hd % 8 != 0 ||
+          a.k % a.attn_hd != 0)
+        return hipErrorInvalidValue;
+    }
+    return launch_strip<QT, PRO, EPI, 5>(a, st);
+  }
   if constexpr (PRO == PRO_Q8X) {
     // Q8_0 activations: strip kernel only
     if (strip_path_ok(a.k)) return launch_strip<QT, PRO, EPI>(a, st);
@@ -927,7 +937,7 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
 
 // Q4_0X4 or plain Q4_0 weights
 bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k) {
-  return qt == Q4_0 && il == 4 && k <= 8192 && strip_path_ok((int)k);
+  return qt == Q4_0 && (il == 4 || il == 5) && k <= 8192 && strip_path_ok((int)k);
 }
 
 template <uint32_t QT>

@@ -59,6 +59,9 @@ struct GemvArgs {
 // set by the device-resident decode step, whose KV cache and activations
 // should stay cached across the 330 MB LM-head read.
 constexpr uint32_t kGemvStream = 1;
+// The weights are split-scale X4 groups (interleave 5, strip_load_split):
+// strip-kernel launches only.
+constexpr uint32_t kGemvSplit = 2;
 
 struct GenericArgs {
   const uint8_t* w;

@@ -531,6 +531,26 @@ __global__ __launch_bounds__(256) void interleave_x4_kernel(const uint8_t* __res
   }
 }
 
+// X4 group-blocks (gb bytes: 4 fp16 scales, then 4 rows of qb quant bytes)
+// to the split-scale X4 groups the strip kernel reads with one 16-byte-
+// aligned quant load and one contiguous scale load per wave (IL 5): per
+// group of nb blocks, [block][row][qb] quants, then [block][row] scales.
+// Thread t moves group-block t (group t / nb, block t % nb).
+__global__ __launch_bounds__(256) void split_x4_kernel(const uint8_t* __restrict__ x4, uint8_t* __restrict__ out,
+                                                       size_t units, int nb, int qb) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= units) return;
+  const size_t g = t / (size_t)nb;
+  const int b = (int)(t - g * (size_t)nb);
+  const size_t gb = 8 + 4 * (size_t)qb;
+  const uint8_t* src = x4 + t * gb;
+  uint8_t* grp = out + g * (size_t)nb * gb;
+  const uint2* sq = reinterpret_cast<const uint2*>(src + 8);
+  uint2* dq = reinterpret_cast<uint2*>(grp + (size_t)b * 4 * qb);
+  for (int i = 0; i < qb / 2; i++) dq[i] = sq[i];  // the 4 rows' quants, in order
+  *reinterpret_cast<uint2*>(grp + (size_t)nb * 4 * qb + 8 * (size_t)b) = *reinterpret_cast<const uint2*>(src);
+}
+
 // Split merge for O projections that cannot take the merging GEMV: thread t
 // merges dims 8t..8t+7 of the attention output.
 __global__ void attn_merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml, int k, int hd,
@@ -1106,6 +1126,37 @@ static zg_status repack_x4(zg_model* m, const uint8_t** w, uint32_t qt, uint32_t
   return ZG_OK;
 }
 
+// An X4 Q4_0 / Q8_0 layer projection of a strip-sized in_dim, copied to
+// split-scale X4 groups into model memory (*w and *il then name the copy;
+// a model-owned source is queued on *drop for release once the copy has
+// landed); other tensors are left as they are.  The strip kernel decodes the
+// same lanes from either layout, so results keep their bits.
+static zg_status split_x4(zg_model* m, const uint8_t** w, uint32_t qt, uint32_t* il, size_t rows, size_t k,
+                          std::vector<void*>* drop) {
+  if (*il != 4 || (qt != ZG_Q4_0 && qt != ZG_Q8_0) || rows % 4 || !strip_path_ok((int)k) ||
+      (reinterpret_cast<uintptr_t>(*w) & 15u))
+    return ZG_OK;
+  const size_t bytes = tensor_bytes(qt, rows, k);
+  void* dst = nullptr;
+  zg_status s = model_alloc(m, &dst, bytes);
+  if (s) return s;
+  const int nb = (int)(k / 32), qb = qt == ZG_Q4_0 ? 16 : 32;
+  const size_t units = rows / 4 * (size_t)nb;
+  hipLaunchKernelGGL(split_x4_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, m->ctx->stream, *w,
+                     static_cast<uint8_t*>(dst), units, nb, qb);
+  s = hip_check(m->ctx, hipGetLastError(), "model: split launch");
+  if (s) return s;
+  if (std::find(m->owned.begin(), m->owned.end(), static_cast<const void*>(*w)) != m->owned.end()) {
+    try {
+      drop->push_back(const_cast<uint8_t*>(*w));
+    } catch (const std::bad_alloc&) {  // the copy stays owned until the model is destroyed
+    }
+  }
+  *w = static_cast<const uint8_t*>(dst);
+  *il = 5;
+  return ZG_OK;
+}
+
 // rmsnorm of x into m->xn, for GEMVs without a rmsnorm prologue (the
 // model's own buffer: a captured graph must not hold context scratch, which
 // a later call may reallocate)
@@ -1171,16 +1222,21 @@ static zg_status run_qkv_attn(zg_model* m, uint32_t l, const ZLayer& L, AttnArgs
   const size_t shm = 2 * 4 * 2 * 16 * sizeof(float);  // the strip body's [2][4 waves][2 groups][16] partials
   const uint32_t qt = L.qt[ZG_PROJ_Q], il = L.il[ZG_PROJ_Q];
 #define ZG_QKV_ATTN(QT, IL, HDV) hipLaunchKernelGGL((qkv_attn_kernel<QT, IL, HDV>), grid, block, shm, st, ga, aa, n_attn)
-  // Q4_K rows, or X4 Q4_0 / Q8_0 (plain-row Q4_0 / Q8_0 projections are
-  // interleaved to X4 at model creation)
-  if (qt != ZG_Q4K && il != 4) return set_error(m->ctx, ZG_ERR_UNSUPPORTED_QUANT, "qkv+attention: plain-row Q4_0/Q8_0");
+  // Q4_K rows, or X4 / split-scale X4 Q4_0 / Q8_0 (plain-row Q4_0 / Q8_0
+  // projections are interleaved at model creation)
+  if (qt != ZG_Q4K && il != 4 && il != 5)
+    return set_error(m->ctx, ZG_ERR_UNSUPPORTED_QUANT, "qkv+attention: plain-row Q4_0/Q8_0");
   if (HD == 128) {
     if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 128);
+    else if (qt == ZG_Q4_0 && il == 5) ZG_QKV_ATTN(Q4_0, 5, 128);
     else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 4, 128);
+    else if (il == 5) ZG_QKV_ATTN(Q8_0, 5, 128);
     else ZG_QKV_ATTN(Q8_0, 4, 128);
   } else {
     if (qt == ZG_Q4K) ZG_QKV_ATTN(Q4K, 1, 64);
+    else if (qt == ZG_Q4_0 && il == 5) ZG_QKV_ATTN(Q4_0, 5, 64);
     else if (qt == ZG_Q4_0) ZG_QKV_ATTN(Q4_0, 4, 64);
+    else if (il == 5) ZG_QKV_ATTN(Q8_0, 5, 64);
     else ZG_QKV_ATTN(Q8_0, 4, 64);
   }
 #undef ZG_QKV_ATTN
@@ -1617,7 +1673,26 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
     for (int p = 0; p < ZG_N_PROJ && !s; p++) s = repack_x4(m, w[p], L.qt[p], &L.il[p], rows[p], ks[p]);
   }
   if (!s) s = repack_x4(m, &m->head, d.head_type, &m->d.head_interleave, d.vocab_padded, H);
+  // then the layer projections to split-scale X4 groups (the LM head keeps
+  // X4: its tall launches stream contiguous group-blocks into LDS)
+  std::vector<void*> drop;
+  for (uint32_t l = 0; l < d.n_layers && !s; l++) {
+    ZLayer& L = m->layers[l];
+    const uint8_t** w[ZG_N_PROJ] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    const size_t rows[ZG_N_PROJ] = {qd, kvd, kvd, H, F, F, H}, ks[ZG_N_PROJ] = {H, H, H, qd, H, H, F};
+    for (int p = 0; p < ZG_N_PROJ && !s; p++) s = split_x4(m, w[p], L.qt[p], &L.il[p], rows[p], ks[p], &drop);
+  }
   if (!s) s = hip_check(ctx, hipStreamSynchronize(ctx->stream), "model: interleave");
+  if (!s) {
+    // the X4 copies made from plain rows and since split are not read again
+    for (void* p : drop) {
+      auto it = std::find(m->owned.begin(), m->owned.end(), p);
+      if (it != m->owned.end()) {
+        hipFree(p);
+        m->owned.erase(it);
+      }
+    }
+  }
   if (!s) {
     // the interleave copies have landed: registry uploads that no tensor of
     // the model reads any more (every repacked plain-row tensor's) are

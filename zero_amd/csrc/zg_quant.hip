@@ -166,6 +166,20 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
           S.q[i][2 * j] = v.x;
           S.q[i][2 * j + 1] = v.y;
         }
+      } else if (IL == 5) {
+        // split-scale X4 group: [kb][row] quants, then [kb][row] fp16 scales
+        const size_t gb = (WT == Q4_0) ? 72 : 136;
+        constexpr int QB = (WT == Q4_0) ? 16 : 32;
+        const uint8_t* g = w + (size_t)(gn >> 2) * nb * gb;
+        const size_t u = (size_t)kb * 4 + (gn & 3);
+        dp = g + (size_t)nb * 4 * QB + 2 * u;
+        qp = g + u * QB;
+#pragma unroll
+        for (int j = 0; j < St::QW / 2; j++) {
+          const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * j);
+          S.q[i][2 * j] = v.x;
+          S.q[i][2 * j + 1] = v.y;
+        }
       } else {
         const size_t bb = (WT == Q4_0) ? 18 : 34;
         dp = w + ((size_t)gn * nb + kb) * bb;
@@ -416,6 +430,20 @@ static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   else hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, false>), grid, dim3(256), 0, st, a);
 }
 
+// the weight type and layout (1 plain rows, 4 X4, 5 split-scale X4)
+template <int BM, int BK>
+static void launch_gemm_il(const GemmArgs& a, uint32_t w_type, uint32_t il, hipStream_t st) {
+  if (w_type == ZG_Q4_0) {
+    if (il == 4) launch_gemm<Q4_0, 4, BM, BK>(a, st);
+    else if (il == 5) launch_gemm<Q4_0, 5, BM, BK>(a, st);
+    else launch_gemm<Q4_0, 1, BM, BK>(a, st);
+  } else {
+    if (il == 4) launch_gemm<Q8_0, 4, BM, BK>(a, st);
+    else if (il == 5) launch_gemm<Q8_0, 5, BM, BK>(a, st);
+    else launch_gemm<Q8_0, 1, BM, BK>(a, st);
+  }
+}
+
 // Checks and launches one Q8_0-activation GEMM over 1..3 weight segments.
 zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const GemmSegDev* segs, int nseg, size_t m,
                        size_t k, uint32_t w_type, uint32_t interleave, bool accumulate, hipStream_t st) {
@@ -431,7 +459,7 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
     zg_status s = check_shape(ctx, w_type, interleave, k, segs[i].n);
     if (s) return s;
     if (nseg > 1 && segs[i].n % kBN) return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: segment width %% %d", kBN);
-    if (interleave == 4 && (reinterpret_cast<uintptr_t>(segs[i].w) & 7))
+    if (interleave != 1 && (reinterpret_cast<uintptr_t>(segs[i].w) & 7))
       return set_error(ctx, ZG_ERR_INVALID_ARG, "gemm: weights misaligned");
     n += segs[i].n;
     a.w[i] = segs[i].w;
@@ -453,22 +481,13 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
   // 64-row tiles unless they would not give every CU three workgroups
   const size_t tiles64 = ((n + kBN - 1) / kBN) * ((m + 63) / 64);
   if (tiles64 >= (size_t)3 * gemm_cu_count()) {
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 64, ZG_GEMM_BK64>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 64, ZG_GEMM_BK64>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 64, ZG_GEMM_BK64>(a, st);
-    else launch_gemm<Q8_0, 1, 64, ZG_GEMM_BK64>(a, st);
+    launch_gemm_il<64, ZG_GEMM_BK64>(a, w_type, interleave, st);
   } else if (((n + kBN - 1) / kBN) * ((m + 31) / 32) <= (size_t)gemm_cu_count()) {
     // at most one 32-row tile per CU: each stage's round trip is exposed,
     // so fewer, larger stages
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32, kSmallBK>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32, kSmallBK>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 32, kSmallBK>(a, st);
-    else launch_gemm<Q8_0, 1, 32, kSmallBK>(a, st);
+    launch_gemm_il<32, kSmallBK>(a, w_type, interleave, st);
   } else {
-    if (w_type == ZG_Q4_0 && interleave == 4) launch_gemm<Q4_0, 4, 32, 4>(a, st);
-    else if (w_type == ZG_Q4_0) launch_gemm<Q4_0, 1, 32, 4>(a, st);
-    else if (interleave == 4) launch_gemm<Q8_0, 4, 32, 4>(a, st);
-    else launch_gemm<Q8_0, 1, 32, 4>(a, st);
+    launch_gemm_il<32, 4>(a, w_type, interleave, st);
   }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
 }

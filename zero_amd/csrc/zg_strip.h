@@ -209,6 +209,30 @@ __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int
   L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(blk + 2 * r));
 }
 
+// Split-scale X4 groups (the model's device layout, IL 5): a group of 4
+// rows holds its nb blocks' quants first, [kb][row][QB bytes] (QB = 16 for
+// Q4_0, 32 for Q8_0), then their fp16 scales, [kb][row], so a wave's 16
+// blocks are 16 QB contiguous quant bytes and 128 contiguous scale bytes
+// (the X4 group-block interleaves 8 scale bytes with every 4 QB quant bytes,
+// so its scale loads touch ~9 cache lines per wave instruction).  q: the
+// lane's quants (16-byte aligned), d: its scale.  Same cache policy as
+// strip_load.
+template <uint32_t QT, bool TALL = false>
+__device__ __forceinline__ void strip_load_split(LaneW<QT>& L, const uint8_t* q, const uint8_t* d) {
+  constexpr int QW = StripGeom<QT>::QW;
+  constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : (TALL ? ZG_STRIP_NT_Q4_TALL : ZG_STRIP_NT_Q4);
+  const u32x4* p = reinterpret_cast<const u32x4*>(q);
+#pragma unroll
+  for (int i = 0; i < QW / 4; i++) {
+    const u32x4 v = ZG_LD_POL(NT, p + i);
+    L.q[4 * i] = v.x;
+    L.q[4 * i + 1] = v.y;
+    L.q[4 * i + 2] = v.z;
+    L.q[4 * i + 3] = v.w;
+  }
+  L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(d));
+}
+
 // Q4_K unit loads: the header and the unit's quant bytes, 16 bytes each
 // (16-byte aligned).  Cache-allocating unless NT.
 template <bool NT>
@@ -401,9 +425,9 @@ __device__ __forceinline__ void strip_x_block(float4 (&xf)[8], const GemvArgs& a
 
 __device__ __forceinline__ float f4_sum(float4 v) { return (v.x + v.y) + (v.z + v.w); }
 
-// IL 4: X4 group-blocks (IL 3: the same with nontemporal loads); IL 1:
-// plain row-major blocks (IL 2: the same with nontemporal loads), a "group"
-// being 4
+// IL 4: X4 group-blocks (IL 3: the same with nontemporal loads); IL 5:
+// split-scale X4 groups (strip_load_split); IL 1: plain row-major blocks
+// (IL 2: the same with nontemporal loads), a "group" being 4
 // consecutive rows (lane (b, r) reads block b of row 4 g + r, b = lane >> 2,
 // r = lane & 3 in either layout, so both give the same bits).  A plain
 // mapping with 16 lanes per row (b = lane & 15, r = lane >> 4: one row's 16
@@ -480,6 +504,12 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
         else if constexpr (IL == 4 || IL == 3)
           strip_load<QT, GBATCH == 4, IL == 3>(L[j][p], sg.w + (size_t)lg * (size_t)(nb * GBY) + (uint32_t)(kb * GBY),
                                                r);
+        else if constexpr (IL == 5) {
+          constexpr int QB = 4 * StripGeom<QT>::QW;  // quant bytes per row and block
+          const uint8_t* gp = sg.w + (size_t)lg * (size_t)(nb * GBY);
+          strip_load_split<QT, GBATCH == 4>(L[j][p], gp + (uint32_t)((4 * kb + r) * QB),
+                                            gp + (uint32_t)(nb * 4 * QB + 2 * (4 * kb + r)));
+        }
         else
           strip_load_plain<QT, IL == 2>(L[j][p], sg.w + (size_t)lg * (size_t)(4 * nb * BB) +
                                                      (uint32_t)((r * nb + kb) * BB));

@@ -91,6 +91,18 @@ def weight(rng, quant: int, rows: int, k: int, interleave: int = 1) -> np.ndarra
     return interleave_x4(w, rows, k, quant) if interleave == 4 else w
 
 
+def x4_split(w_x4, rows: int, k: int, quant: int) -> np.ndarray:
+    """X4 group-blocks to split-scale X4 groups (interleave 5, the model's
+    device layout): per group of 4 rows, the nb blocks' quants
+    [block][row][qb bytes], then their fp16 scales [block][row]."""
+    qb = 16 if quant == Q4_0 else 32
+    gb, nb = 8 + 4 * qb, k // 32
+    a = np.asarray(w_x4, np.uint8).reshape(rows // 4, nb, gb)
+    q = a[:, :, 8:].reshape(rows // 4, nb * 4 * qb)
+    d = a[:, :, :8].reshape(rows // 4, nb * 8)
+    return np.ascontiguousarray(np.concatenate([q, d], axis=1).reshape(-1))
+
+
 def activations(rng, *shape) -> np.ndarray:
     return rng.standard_normal(shape, dtype=np.float32)
 
