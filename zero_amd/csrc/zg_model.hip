@@ -1131,9 +1131,12 @@ static zg_status repack_x4(zg_model* m, const uint8_t** w, uint32_t qt, uint32_t
 // a model-owned source is queued on *drop for release once the copy has
 // landed); other tensors are left as they are.  The strip kernel decodes the
 // same lanes from either layout, so results keep their bits.
+#ifndef ZG_MODEL_SPLIT
+#define ZG_MODEL_SPLIT 1
+#endif
 static zg_status split_x4(zg_model* m, const uint8_t** w, uint32_t qt, uint32_t* il, size_t rows, size_t k,
                           std::vector<void*>* drop) {
-  if (*il != 4 || (qt != ZG_Q4_0 && qt != ZG_Q8_0) || rows % 4 || !strip_path_ok((int)k) ||
+  if (!ZG_MODEL_SPLIT || *il != 4 || (qt != ZG_Q4_0 && qt != ZG_Q8_0) || rows % 4 || !strip_path_ok((int)k) ||
       (reinterpret_cast<uintptr_t>(*w) & 15u))
     return ZG_OK;
   const size_t bytes = tensor_bytes(qt, rows, k);

@@ -217,18 +217,31 @@ __device__ __forceinline__ void strip_load(LaneW<QT>& L, const uint8_t* blk, int
 // so its scale loads touch ~9 cache lines per wave instruction).  q: the
 // lane's quants (16-byte aligned), d: its scale.  Same cache policy as
 // strip_load.
+#ifndef ZG_SPLIT_LD16
+#define ZG_SPLIT_LD16 1
+#endif
 template <uint32_t QT, bool TALL = false>
 __device__ __forceinline__ void strip_load_split(LaneW<QT>& L, const uint8_t* q, const uint8_t* d) {
   constexpr int QW = StripGeom<QT>::QW;
   constexpr bool NT = QT == Q8_0 ? ZG_STRIP_NT_Q8 : (TALL ? ZG_STRIP_NT_Q4_TALL : ZG_STRIP_NT_Q4);
-  const u32x4* p = reinterpret_cast<const u32x4*>(q);
+  if (ZG_SPLIT_LD16) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(q);
 #pragma unroll
-  for (int i = 0; i < QW / 4; i++) {
-    const u32x4 v = ZG_LD_POL(NT, p + i);
-    L.q[4 * i] = v.x;
-    L.q[4 * i + 1] = v.y;
-    L.q[4 * i + 2] = v.z;
-    L.q[4 * i + 3] = v.w;
+    for (int i = 0; i < QW / 4; i++) {
+      const u32x4 v = ZG_LD_POL(NT, p + i);
+      L.q[4 * i] = v.x;
+      L.q[4 * i + 1] = v.y;
+      L.q[4 * i + 2] = v.z;
+      L.q[4 * i + 3] = v.w;
+    }
+  } else {
+    const u32x2* p = reinterpret_cast<const u32x2*>(q);
+#pragma unroll
+    for (int i = 0; i < QW / 2; i++) {
+      const u32x2 v = ZG_LD_POL(NT, p + i);
+      L.q[2 * i] = v.x;
+      L.q[2 * i + 1] = v.y;
+    }
   }
   L.d = ZG_LD_POL(NT, reinterpret_cast<const uint16_t*>(d));
 }
