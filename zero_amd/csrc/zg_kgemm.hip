@@ -52,6 +52,9 @@ constexpr int kKgPD = ZG_KG_PD;        // stages in flight
 #ifndef ZG_KG_WPE
 #define ZG_KG_WPE 1
 #endif
+#ifndef ZG_KG_GROUPS
+#define ZG_KG_GROUPS 2
+#endif
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -149,10 +152,16 @@ struct KgStage<Q6K> {
 };
 
 // PD: stages whose global loads are in flight while a stage is multiplied
-// (a ring of PD register stages; nst, the stage count, is a multiple of PD,
-// so every load is unconditional and the wait counts stay exact).
-template <uint32_t WT, int PD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))) void gemm_q8k_kernel(KgemmArgs a) {
+// (a ring of PD register stages; the stage count is a multiple of PD, so
+// every load is unconditional and the wait counts stay exact).
+// G: groups of four waves per workgroup that share the tile's superblocks,
+// group g taking superblocks g, g + G, ... (launches with few tiles: one
+// workgroup per CU walks its K range G times as fast).  The integer sums are
+// exact in any split; the float terms still enter each output in superblock
+// order: group g > 0 hands its superblock's two products to group 0 through
+// LDS, and group 0 adds its own, then group 1's, ...
+template <uint32_t WT, int PD, int G>
+__global__ __launch_bounds__(256 * G) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))) void gemm_q8k_kernel(KgemmArgs a) {
   // the reference rounds every product and sum of the superblock terms on
   // its own: no fused multiply-add in this function (a pragma here does not
   // reach the operators inside HIP's __fadd_rn / __fmul_rn, which hipcc
@@ -162,15 +171,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
   constexpr int MI = BM / 32, NJ = BN / 32;  // 16 x 16 tiles per wave
   constexpr int SBB = WT == Q4K ? 144 : 210;
   static_assert(PD % 2 == 0, "stages come in superblock pairs");
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * RP];
-  __shared__ __attribute__((aligned(16))) int8_t Bl[2][BN * RP];
-  __shared__ __attribute__((aligned(16))) int8_t Bh[2][BN * RP];
-  // per superblock (by parity): the 32-value sums split hi / lo [row][8],
-  // the mins [col][8], d8 per row, d / dmin per column
-  __shared__ __attribute__((aligned(16))) int8_t Aml[2][BM * 8], Amh[2][BM * 8], Bmn[2][BN * 8];
-  __shared__ __attribute__((aligned(16))) float Ad8[2][BM];
-  __shared__ float Bd[2][BN], Bdm[2][BN];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // per group: the stage buffers, and per superblock (by parity) the
+  // 32-value sums split hi / lo [row][8], the mins [col][8], d8 per row, d
+  // / dmin per column
+  __shared__ __attribute__((aligned(16))) int8_t AsG[G][2][BM * RP];
+  __shared__ __attribute__((aligned(16))) int8_t BlG[G][2][BN * RP];
+  __shared__ __attribute__((aligned(16))) int8_t BhG[G][2][BN * RP];
+  __shared__ __attribute__((aligned(16))) int8_t AmlG[G][2][BM * 8], AmhG[G][2][BM * 8], BmnG[G][2][BN * 8];
+  __shared__ __attribute__((aligned(16))) float Ad8G[G][2][BM];
+  __shared__ float BdG[G][2][BN], BdmG[G][2][BN];
+  // the float terms of groups 1.. for group 0: [group - 1][dot, min][output][thread]
+  constexpr int NX = WT == Q4K ? 2 : 1;
+  __shared__ float xch[G > 1 ? G - 1 : 1][NX][MI * NJ * 4][G > 1 ? 256 : 1];
+  const int grp = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);
+  const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+  auto& As = AsG[grp];
+  auto& Bl = BlG[grp];
+  auto& Bh = BhG[grp];
+  auto& Aml = AmlG[grp];
+  auto& Amh = AmhG[grp];
+  auto& Bmn = BmnG[grp];
+  auto& Ad8 = Ad8G[grp];
+  auto& Bd = BdG[grp];
+  auto& Bdm = BdmG[grp];
   const int m0 = blockIdx.y * BM;
   const int nt0 = blockIdx.x * BN;
   const int sg = (a.nseg > 1 && nt0 >= a.seg_end[0]) ? ((a.nseg > 2 && nt0 >= a.seg_end[1]) ? 2 : 1) : 0;
@@ -180,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
   float* y = a.y[sg];
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const int r16 = lane & 15, rq = (lane >> 4) * 4, kq16 = (lane >> 4) * 16;
-  const int nsb = a.k / 256, nst = 2 * nsb;
+  const int nsb = a.k / 256, nst = 2 * nsb / G;  // stages of this group
   const size_t wrow = (size_t)nsb * SBB;
   const int wc = tid >> 2, wp = tid & 3;  // weight staging: column, part (Q4_K 16-byte chunk; Q6_K quarter)
   const int mlast = a.m - 1;
@@ -197,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
 
   KgStage<WT> S[PD];
   auto stage_load = [&](KgStage<WT>& R, int st) {
-    const int sb = st >> 1, h = st & 1;
+    const int sb = (st >> 1) * G + grp, h = st & 1;
 #pragma unroll
     for (int i = 0; i < 2; i++) R.a[i] = *reinterpret_cast<const u32x4*>(arow[i] + sb * 256 + h * KS);
     const uint8_t* blk = wcol + (size_t)sb * SBB;
@@ -334,6 +357,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
             ahi[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bh[j], ahi[i][j], 0, 0, 0);
           }
       }
+      float tdot[MI][NJ][4], tmin[MI][NJ][4];  // G > 1: this group's terms of the superblock
       if (u & 1) {
         // superblock done: the float terms in the reference's order
         const int sp = (st >> 1) & 1;
@@ -366,27 +390,67 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
                 const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
                 const int msum = (mh[r] << 7) + ml[r];
                 const float dc = dw * d8r[r], dmc = dmw * d8r[r];
-                fdot[i][j][r] = fdot[i][j][r] + dc * (float)isum;
-                fmin[i][j][r] = fmin[i][j][r] + dmc * (float)msum;
+                if (G == 1) {
+                  fdot[i][j][r] = fdot[i][j][r] + dc * (float)isum;
+                  fmin[i][j][r] = fmin[i][j][r] + dmc * (float)msum;
+                } else {
+                  tdot[i][j][r] = dc * (float)isum;
+                  tmin[i][j][r] = dmc * (float)msum;
+                }
               }
             } else {
 #pragma unroll
               for (int r = 0; r < 4; r++) {
                 const int isum = (ahi[i][j][r] << 7) + alo[i][j][r];
-                fdot[i][j][r] = fdot[i][j][r] + (dw * d8r[r]) * (float)isum;
+                if (G == 1)
+                  fdot[i][j][r] = fdot[i][j][r] + (dw * d8r[r]) * (float)isum;
+                else
+                  tdot[i][j][r] = (dw * d8r[r]) * (float)isum;
               }
             }
             ahi[i][j] = v4i{0, 0, 0, 0};
             alo[i][j] = v4i{0, 0, 0, 0};
           }
         }
+        if (G > 1 && grp > 0) {
+#pragma unroll
+          for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+              for (int r = 0; r < 4; r++) {
+                const int o = (i * NJ + j) * 4 + r;
+                xch[grp - 1][0][o][tid] = tdot[i][j][r];
+                if (WT == Q4K) xch[grp - 1][NX - 1][o][tid] = tmin[i][j][r];
+              }
+        }
       }
       // the next stage into the other buffer (past the end: a clamped
       // repeat that nothing reads)
       stage_store(S[(u + 1) % PD], ((st + 1) >> 1) & 1, (u + 1) & 1, buf ^ 1);
       __syncthreads();
+      if (G > 1 && (u & 1) && grp == 0) {
+        // superblocks G j, G j + 1, ...: own terms, then each group's (the
+        // next exchange is written two barriers later)
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+          for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const int o = (i * NJ + j) * 4 + r;
+              fdot[i][j][r] = fdot[i][j][r] + tdot[i][j][r];
+              if (WT == Q4K) fmin[i][j][r] = fmin[i][j][r] + tmin[i][j][r];
+#pragma unroll
+              for (int g = 1; g < G; g++) {
+                fdot[i][j][r] = fdot[i][j][r] + xch[g - 1][0][o][tid];
+                if (WT == Q4K) fmin[i][j][r] = fmin[i][j][r] + xch[g - 1][NX - 1][o][tid];
+              }
+            }
+      }
     }
   }
+  if (grp != 0) return;
   // D layout of v_mfma_*_16x16*: lane l holds rows 4 (l / 16) + r, column l % 16
 #pragma unroll
   for (int i = 0; i < MI; i++)
@@ -409,6 +473,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZG_KG_WPE))
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+
+// compute units of the device (queried once; a thread-safe static)
+static int kg_cu_count() {
+  static const int n = [] {
+    int dev = 0, v = 0;
+    return hipGetDevice(&dev) == hipSuccess &&
+                   hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+               ? v
+               : 256;
+  }();
+  return n;
+}
 
 zg_status zg::run_quantize_q8k_split(zg_ctx* ctx, const float* x, int8_t* qs, float* d8, int16_t* bs32, size_t rows,
                                      size_t k, hipStream_t st) {
@@ -465,13 +541,19 @@ zg_status zg::run_gemm_q8k(zg_ctx* ctx, const int8_t* qs, const float* d8, const
   a.k = (int)k;
   const dim3 grid((unsigned)(n / kKgBN), (unsigned)((m + kKgBM - 1) / kKgBM));
   // kKgPD stages in flight when the stage count is a multiple of it, else two
+  // two groups per workgroup when the tiles give at most one workgroup per
+  // CU (a prefill's few rows, the narrow down projection) and the
+  // superblocks split evenly; else one
+  const bool split = ZG_KG_GROUPS > 1 && (size_t)grid.x * grid.y <= (size_t)kg_cu_count() && (k / 256) % 2 == 0;
   const bool deep = (k / 256) % (kKgPD / 2) == 0;
   if (w_type == ZG_Q4K) {
-    if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, kKgPD>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, 2>), grid, dim3(256), 0, st, a);
+    if (split) hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, 2, 2>), grid, dim3(512), 0, st, a);
+    else if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, kKgPD, 1>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_q8k_kernel<Q4K, 2, 1>), grid, dim3(256), 0, st, a);
   } else {
-    if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, kKgPD>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, 2>), grid, dim3(256), 0, st, a);
+    if (split) hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, 2, 2>), grid, dim3(512), 0, st, a);
+    else if (deep) hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, kKgPD, 1>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_q8k_kernel<Q6K, 2, 1>), grid, dim3(256), 0, st, a);
   }
   return hip_check(ctx, hipGetLastError(), "gemm_q8k launch");
 }
