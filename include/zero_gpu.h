@@ -134,7 +134,14 @@ zg_status zg_lm_head_argmax(zg_ctx *ctx, const float *hidden, const float *norm_
 
 /* ------------------------------------------------------------------ */
 /* Device-pointer API: asynchronous on `stream` (NULL = ctx stream).    */
-/* No registry; the caller states the layout.                           */
+/* No registry; the caller states the layout: 1 plain row-major, 4     */
+/* .smodel-v2 X4, or 5 for Q4_0 / Q8_0 only: split-scale X4 groups, the */
+/* model's device layout (per group of four rows, its blocks' quants    */
+/* [block][row][16 or 32 bytes], then their fp16 scales [block][row];   */
+/* the same bytes as the X4 group, regrouped; GEMV, fused, LM-head,     */
+/* Q8_0-activation GEMV and prefill-GEMM calls with in_dim a multiple   */
+/* of 512 up to 8192, 16-byte aligned w and x; no reference             */
+/* counterpart).                                                        */
 /* ------------------------------------------------------------------ */
 
 zg_status zg_linear_dev(zg_ctx *ctx, const float *d_x, const void *d_w, float *d_out,

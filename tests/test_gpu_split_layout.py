@@ -24,21 +24,6 @@ def bits(t):
     return t.cpu().numpy().view(np.uint32)
 
 
-def test_split_matches_x4_numpy():
-    rng = np.random.default_rng(1)
-    for quant in (Q4_0, Q8_0):
-        w = synth.weight(rng, quant, 8, 64, 4)
-        s = synth.x4_split(w, 8, 64, quant)
-        qb = 16 if quant == Q4_0 else 32
-        assert s.size == w.size
-        # group 1, block 1, row 2: quants and scale
-        gb = 8 + 4 * qb
-        src = w[(1 * 2 + 1) * gb:(1 * 2 + 2) * gb]
-        g = s[2 * gb:4 * gb]
-        assert np.array_equal(g[(4 * 1 + 2) * qb:(4 * 1 + 3) * qb], src[8 + 2 * qb:8 + 3 * qb])
-        assert np.array_equal(g[2 * 4 * qb + 2 * (4 * 1 + 2):2 * 4 * qb + 2 * (4 * 1 + 2) + 2], src[4:6])
-
-
 @pytest.mark.parametrize("quant,rows,k", [(Q4_0, 6144, 2048), (Q4_0, 2048, 6144), (Q4_0, 49152, 2048),
                                           (Q4_0, 1024, 512), (Q8_0, 4096, 2048), (Q8_0, 8192, 1024)])
 def test_gemv_bits_equal_x4(ctx, quant, rows, k):
