@@ -425,3 +425,25 @@ def test_qwen3_1_7b_shape_q4_k_m_batched_prefill_matches_oracle(ctx, zo):
         om.close()
         gm.close()
         ctx.clear()
+
+
+def test_k_quant_prefill_longer_than_a_chunk(ctx, zo):
+    """620 rows of a Q4_K / Q6_K model (hidden 256: whole superblocks): one
+    512-row chunk of Q8_K GEMMs, then 108 rows attending to its cache rows."""
+    cfg = synth.ModelConfig(n_layers=2, hidden=256, ffn=512, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                            vocab_padded=512, vocab_real=500, max_ctx=640, embd_type=synth.Q4K,
+                            head_type=synth.Q6K, head_interleave=1, layer_quants=synth.q4_k_m_layers(2))
+    model = synth.random_model(cfg, seed=19)
+    gm = GpuModel(ctx, model)
+    om = zo.OracleModel(model)
+    try:
+        prompt = synth.prompt(43, 620, cfg.vocab_real)
+        tok, _, hid = gm.prefill(prompt, want_hidden=True)
+        h_ref = om.prefill_q8(prompt)
+        rc, t_ref, _, _ = om.lm_head()
+        assert rc == 0
+        assert rel_err(hid, h_ref) <= REL_TOL and tok == t_ref
+    finally:
+        om.close()
+        gm.close()
+        ctx.clear()
