@@ -244,6 +244,26 @@ def bench_rows(ctx, steps: int, cpu=None):
             out[key]["cpu_baseline"] = cpu.gemv(name, wh, x_host, H, rows, synth.Q4_0, 4, wh.nbytes + 4 * H + 4 * rows)
         del wh
 
+    # the headline GEMV through the code-object route: zg_kernels.hsaco loaded
+    # with hipModuleLoad, each launch a hipModuleLaunchKernel (captured into
+    # the graph like the library's launches)
+    from zero_amd import module as zmod
+
+    km = zmod.KernelModule()
+    wh = synth.weight(rng, synth.Q4_0, ROWS, H, 4)
+    wd, c = rotating(wh)
+    yk = torch.empty(ROWS, device="cuda")
+
+    def modl(i, st, wd=wd, yk=yk):
+        km.gemv_x4(wd[i].data_ptr(), x.data_ptr(), yk.data_ptr(), ROWS, H, synth.Q4_0, stream=st)
+
+    per, n, _ = _graph_time(modl, c, steps // 4, 40)
+    out["module_q4_0x4_6144x2048"] = _row("Q4_0X4 6144x2048 through zg_kernels.hsaco (hipModuleLaunchKernel)", per,
+                                          wh.nbytes + 4 * H + 4 * ROWS, n, c,
+                                          entry=zmod.plan(synth.Q4_0, ROWS, H, km.cu_count).entry)
+    del wd, wh
+    km.close()
+
     # the same weights in the model's split-scale X4 device layout
     # (interleave 5: each group's quants, then its scales): the headline shape
     # and the LM-head height, the same strip kernel with one 16-byte quant load
