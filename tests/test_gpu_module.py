@@ -123,3 +123,15 @@ def test_module_rejects_bad_arguments(km):
         km.gemv_x4(0, x.data_ptr(), y.data_ptr(), 64, 2048, Q4_0)
     with pytest.raises(module.ModuleError):
         km.function("zg_mk_no_such_entry")
+
+
+def test_failed_module_call_leaves_no_error_behind(ctx, km):
+    """A failed module call is reported once: the library's next launch
+    check does not see it."""
+    with pytest.raises(module.ModuleError):
+        km.function("zg_mk_no_such_entry")
+    rng = np.random.default_rng(3)
+    w, x = synth.weight(rng, Q4_0, 256, 2048, 4), synth.activations(rng, 2048)
+    y = torch.empty(256, dtype=torch.float32, device="cuda")
+    ctx.linear_dev(dev(x), dev(w), y, 2048, 256, Q4_0, 4)
+    torch.cuda.synchronize()

@@ -257,11 +257,11 @@ __global__ __launch_bounds__(kNW * 64) void gemv_x4_kernel(GemvArgs a) {
         if (EPI == EPI_SWIGLU) {
           const float g = (lane == 0) ? gate[0] : (lane == 1) ? gate[1] : (lane == 2) ? gate[2] : gate[3];
           // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
-          a.seg[0].y[row] = (g / (1.0f + expf(-g))) * v;
+          store_out(a.seg[0].y + row, (g / (1.0f + expf(-g))) * v);
         } else if (EPI == EPI_RESID) {
-          sg.y[row] = sg.resid[row] + v;
+          store_out(sg.y + row, sg.resid[row] + v);
         } else {
-          if (sg.y) sg.y[row] = v;
+          if (sg.y) store_out(sg.y + row, v);
           if (EPI == EPI_ARGMAX && !(v != v)) {
             const uint64_t kk = argmax_key(v, row);
             key = kk > key ? kk : key;
@@ -307,8 +307,8 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(GenericArgs a) {
   acc = seg_sum<64>(acc);
   uint64_t key = 0;
   if (active && lane == 0) {
-    if (a.epi == EPI_RESID) a.y[row] = a.resid[row] + acc;
-    else if (a.y) a.y[row] = acc;
+    if (a.epi == EPI_RESID) store_out(a.y + row, a.resid[row] + acc);
+    else if (a.y) store_out(a.y + row, acc);
     if (a.epi == EPI_ARGMAX && !(acc != acc)) key = argmax_key(acc, (uint32_t)row);
   }
   if (a.epi == EPI_ARGMAX && lane == 0 && key)
@@ -826,9 +826,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
         const uint32_t row = 4 * (uint32_t)item + (uint32_t)rr;
         if (row >= sg.row_lo && row < sg.row_hi) {
           if (EPI == EPI_RESID) {
-            sg.y[row] = sg.resid[row] + acc;
+            store_out(sg.y + row, sg.resid[row] + acc);
           } else {
-            if (sg.y) sg.y[row] = acc;
+            if (sg.y) store_out(sg.y + row, acc);
             if (EPI == EPI_ARGMAX && !(acc != acc)) {
               const uint64_t kk = argmax_key(acc, row);
               key = kk > key ? kk : key;

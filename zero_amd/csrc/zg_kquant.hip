@@ -231,9 +231,9 @@ __global__ __launch_bounds__(kKqWaves * 64) void kq_gemv_kernel(GenericArgs a) {
       const size_t row = a.row_lo + wave_id + (u / steps) * nwaves;
       if (lane == 0) {
         if (EPI == EPI_RESID)
-          a.y[row] = a.resid[row] + v;
+          store_out(a.y + row, a.resid[row] + v);
         else if (a.y)
-          a.y[row] = v;
+          store_out(a.y + row, v);
         if (EPI == EPI_ARGMAX && !(v != v)) {
           const uint64_t kk = argmax_key(v, (uint32_t)row);
           key = kk > key ? kk : key;
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
             gv *= rinv;
             uv *= rinv;
           }
-          a.y[a.row_lo + ri] = (gv / (1.0f + expf(-gv))) * uv;
+          store_out(a.y + a.row_lo + ri, (gv / (1.0f + expf(-gv))) * uv);
         }
       }
     } else if (tt < per_batch) {
@@ -398,11 +398,11 @@ __global__ __launch_bounds__(1024) void kq_strip_kernel(GenericArgs a, int S) {
         const size_t row = a.row_lo + ri;
         if (EPI == EPI_STORE && a.nseg > 1) {
           const int sg = kq_seg(a, ri);
-          a.seg_y[sg][ri - (sg == 0 ? 0 : (int)a.seg_end[sg - 1])] = v;
+          store_out(a.seg_y[sg] + (ri - (sg == 0 ? 0 : (int)a.seg_end[sg - 1])), v);
         } else if (EPI == EPI_RESID)
-          a.y[row] = a.resid[row] + v;
+          store_out(a.y + row, a.resid[row] + v);
         else if (a.y)
-          a.y[row] = v;
+          store_out(a.y + row, v);
         if (EPI == EPI_ARGMAX && !(v != v)) {
           const uint64_t kk = argmax_key(v, (uint32_t)row);
           key = kk > key ? kk : key;
@@ -571,9 +571,9 @@ __global__ __launch_bounds__(1024) void kq2_strip_kernel(GenericArgs a, int S) {
         for (int st = 0; st < S; st++) v += part[buf][su * S + st][j];
         const size_t row = a.row_lo + ri;
         if (EPI == EPI_RESID)
-          a.y[row] = a.resid[row] + v;
+          store_out(a.y + row, a.resid[row] + v);
         else if (a.y)
-          a.y[row] = v;
+          store_out(a.y + row, v);
         if (EPI == EPI_ARGMAX && !(v != v)) {
           const uint64_t kk = argmax_key(v, (uint32_t)row);
           key = kk > key ? kk : key;
@@ -742,9 +742,9 @@ __global__ __launch_bounds__(1024) void kq6l_kernel(GenericArgs a, int S, int WP
       for (int st = 0; st < S; st++) v += pb[(su * S + st) * RPB + j];
       const size_t row = a.row_lo + ri;
       if (EPI == EPI_RESID)
-        a.y[row] = a.resid[row] + v;
+        store_out(a.y + row, a.resid[row] + v);
       else if (a.y)
-        a.y[row] = v;
+        store_out(a.y + row, v);
       if (EPI == EPI_ARGMAX && !(v != v)) {
         const uint64_t kk = argmax_key(v, (uint32_t)row);
         key = kk > key ? kk : key;

@@ -80,7 +80,7 @@ __device__ __forceinline__ void embed_row_q(const uint8_t* __restrict__ embd, in
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int e = e0 + (int)threadIdx.x + i * nt;
-      if (e < hidden) out[e] = v[i];
+      if (e < hidden) store_out(out + e, v[i]);
     }
   }
 }
@@ -117,13 +117,13 @@ struct EmbedArgs {
 // everything it needs from them.
 __device__ __forceinline__ void step_start(const EmbedArgs& e, uint32_t tok, uint32_t pos) {
   if (threadIdx.x == 0) {
-    *e.epoch += 1;
-    *e.best = 0;
+    store_out(e.epoch, *e.epoch + 1);
+    store_out(e.best, (uint64_t)0);
   }
   if ((int)threadIdx.x < e.half) {
     const float th = (float)pos * e.inv_freq[threadIdx.x];
-    e.rope_cs[threadIdx.x] = cosf(th);
-    e.rope_cs[e.half + threadIdx.x] = sinf(th);
+    store_out(e.rope_cs + threadIdx.x, cosf(th));
+    store_out(e.rope_cs + e.half + threadIdx.x, sinf(th));
   }
   embed_row(e.embd, e.qt, e.hidden, tok, e.out);
 }
@@ -253,8 +253,11 @@ __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (c0 > pos) {
     // split past the context: neutral partial (uniform per workgroup)
-    if (tid < HD) a.out[((size_t)sp * nq + qh) * HD + tid] = 0.0f;
-    if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(-INFINITY, 0.0f);
+    if (tid < HD) store_out(a.out + ((size_t)sp * nq + qh) * HD + tid, 0.0f);
+    if (tid == 0) {
+      store_out(a.part_ml + 2 * ((size_t)sp * nq + qh), -INFINITY);
+      store_out(a.part_ml + 2 * ((size_t)sp * nq + qh) + 1, 0.0f);
+    }
     return;
   }
   const int n_t = min(slen, pos + 1 - c0);
@@ -377,10 +380,12 @@ __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int 
     // KvCache::store_kv (kv_cache.rs:139-183): row `pos` of this KV head
     float* kc = a.kcache + (size_t)pos * rowf4 * 4 + kvh * HD;
     if (lane < HALF) {
-      kc[lane] = k0;
-      kc[lane + HALF] = k1;
+      store_out(kc + lane, k0);
+      store_out(kc + lane + HALF, k1);
     }
-    reinterpret_cast<vlane_t*>(a.vcache)[(size_t)pos * rowv + kvh * (HD / VPL) + lane] = vnew;
+    float* vc = a.vcache + ((size_t)pos * rowv + kvh * (HD / VPL) + lane) * VPL;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) store_out(vc + i, vnew[i]);
   }
   wave_lds_sync();
   float4 q[CPL];
@@ -472,10 +477,13 @@ __device__ __forceinline__ void attn_split_body(AttnArgs a, int qh, int sp, int 
       a.qs[qh * HD + tid] = qv;
       if ((tid & 31) == 0) a.qsd[(qh * HD + tid) / 32] = (uint16_t)dbits;
     } else if (a.nsplit == 1) {
-      a.out[qh * HD + tid] = o * (1.0f / L);
+      store_out(a.out + qh * HD + tid, o * (1.0f / L));
     } else {
-      a.out[((size_t)sp * nq + qh) * HD + tid] = o;
-      if (tid == 0) reinterpret_cast<float2*>(a.part_ml)[sp * nq + qh] = make_float2(M, L);
+      store_out(a.out + ((size_t)sp * nq + qh) * HD + tid, o);
+      if (tid == 0) {
+        store_out(a.part_ml + 2 * ((size_t)sp * nq + qh), M);
+        store_out(a.part_ml + 2 * ((size_t)sp * nq + qh) + 1, L);
+      }
     }
   }
 }
@@ -643,15 +651,15 @@ __device__ __forceinline__ void finalize_state(DevState* __restrict__ st, uint64
                                                uint32_t err0, uint32_t err_step, uint32_t gen, uint32_t gen_cap,
                                                uint32_t pos, uint32_t* __restrict__ out_tokens) {
   if ((err | err0) && err_step == kNoStep) {
-    st->err_step = gen;
-    st->err_first = err | err0;
+    store_out(&st->err_step, gen);
+    store_out(&st->err_first, err | err0);
   }
-  st->err = err0 | err;
-  st->best = key;
-  st->token = idx;
-  if (out_tokens && gen < gen_cap) out_tokens[gen] = idx;
-  st->gen = gen + 1;
-  st->pos = pos + 1;
+  store_out(&st->err, err0 | err);
+  store_out(&st->best, key);
+  store_out(&st->token, idx);
+  if (out_tokens && gen < gen_cap) store_out(out_tokens + gen, idx);
+  store_out(&st->gen, gen + 1);
+  store_out(&st->pos, pos + 1);
 }
 
 __global__ void finalize_kernel(DevState* __restrict__ st, const uint64_t* __restrict__ best, uint32_t vocab_real,
@@ -685,8 +693,8 @@ __global__ void advance_embed_kernel(DevState* __restrict__ st, const uint32_t* 
   const uint32_t tok = p < n_prompt ? prompt[p] : tok0;
   __syncthreads();
   if (threadIdx.x == 0) {
-    st->pos = p;
-    st->token = tok;
+    store_out(&st->pos, p);
+    store_out(&st->token, tok);
   }
   step_start(e, tok, p);
 }

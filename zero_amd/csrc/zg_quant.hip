@@ -307,14 +307,16 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
     const int8_t* B = Bs[buf];
     // blocks past k in the last stage hold zero quants and scales: they add
     // fma(0, 0, acc) = acc
-    // the 32-row tile's unrolled block loop lets the compiler pair the
-    // operand reads of blocks kk and kk + 1 (ds_read2_b64, 32 bytes apart),
-    // which conflict (4.7 M conflict cycles for M=512 x 2048x6144); the
-    // rolled loop has none but 13 % more VALU work and is slower (55 vs
-    // 48 us)
+    // the 32-row tile's block loop is unrolled (the rolled loop: 13 % more
+    // VALU work, 55 vs 48 us); left to itself the compiler then pairs the
+    // operand reads of blocks kk and kk + 1 into conflicting ds_read2_b64
+    // (4.7 M conflict cycles for M=512 x 2048x6144), which the clobber below
+    // prevents (down 42.0-42.3 vs 42.6 us)
     constexpr int UNR = BM == 64 ? ZG_GEMM_UNR64 : 4;
 #pragma unroll UNR
     for (int kk = 0; kk < BK; kk++) {
+      // the 32-row tile: no pairing of LDS reads across blocks
+      if constexpr (BM == 32) asm volatile("" ::: "memory");
       long av[MI], bv[2];
       float4 da[MI];
       float db[2];

@@ -742,9 +742,9 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
           if (EPI == EPI_SWIGLU) {
             const float g = tot[0];
             // activation.rs:115-148 operand order: silu = g/(1+exp(-g)), then *up
-            a.seg[0].y[row] = (g / (1.0f + expf(-g))) * v;
+            store_out(a.seg[0].y + row, (g / (1.0f + expf(-g))) * v);
           } else if (EPI == EPI_RESID) {
-            sg.y[row] = sg.resid[row] + v;
+            store_out(sg.y + row, sg.resid[row] + v);
           } else if (SIG) {
             // read by other workgroups of this launch: the value with this
             // step and layer's tag, as one agent-scope 64-bit store (the
@@ -753,7 +753,7 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
             if (!sig_drop)
               __hip_atomic_store(reinterpret_cast<uint64_t*>(sg.y) + row, tw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else {
-            if (sg.y) sg.y[row] = v;
+            if (sg.y) store_out(sg.y + row, v);
             if (EPI == EPI_ARGMAX && !(v != v)) {
               const uint64_t kk = argmax_key(v, row);
               key = kk > key ? kk : key;

@@ -106,6 +106,8 @@ def _runtime() -> C.CDLL:
     hip.hipModuleLaunchKernel.restype = I
     hip.hipGetErrorString.argtypes = [I]
     hip.hipGetErrorString.restype = C.c_char_p
+    hip.hipGetLastError.argtypes = []
+    hip.hipGetLastError.restype = I
     return hip
 
 
@@ -129,6 +131,10 @@ class KernelModule:
 
     def _check(self, err: int, what: str) -> None:
         if err != 0:
+            # a failed call also becomes the thread's last HIP error; it is
+            # reported here, so clear it rather than let the next launch
+            # check elsewhere in the process (the library's) report it again
+            self._hip.hipGetLastError()
             raise ModuleError(f"{what}: {self._hip.hipGetErrorString(err).decode()} ({err})")
 
     def function(self, name: str) -> C.c_void_p:
