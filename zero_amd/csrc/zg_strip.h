@@ -666,6 +666,10 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
   auto process = [&](const LaneW<QT> (&L)[GBATCH][PARTS], int batch, int buf) {
     const int base = batch * per_batch + sub * GBATCH;
     float* pb = part + (size_t)buf * NW * GBATCH * PARTS * 16;
+    // a single projection's stored row range, in scalar registers before
+    // the decode rather than loaded after the barrier, on the way to the
+    // stores
+    if constexpr (SEG1 && EPI != EPI_SWIGLU) asm volatile("" ::"s"(a.seg[0].row_lo), "s"(a.seg[0].row_hi));
     // in batch-loop launches (and single-projection ones) every group of the
     // batch is decoded, also the clamped repeats past the last item (their
     // totals are dropped in the epilogue): a skipped decode leaves its loads
@@ -708,7 +712,9 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
             dot = strip_dot<QT>(L[j][p], xf, (QT == Q4_0 ? -8.0f : -128.0f) * t);
           }
           const float v = row_sum4(dot);
-          if ((lane & 15) < 4) pb[((wave * GBATCH + j) * PARTS + p) * 16 + (lane >> 4) * 4 + r] = v;
+          // [wave][group][part][r][DPP row]: a row's four DPP-row sums
+          // are one 16-byte LDS read below
+          if ((lane & 15) < 4) pb[((wave * GBATCH + j) * PARTS + p) * 16 + r * 4 + (lane >> 4)] = v;
         }
       }
     }
@@ -729,8 +735,8 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
         for (int p = 0; p < PARTS; p++) {
           float acc = 0.0f;
           for (int st = 0; st < S; st++) {
-            const float* q = pb + (((su * S + st) * GBATCH + j) * PARTS + p) * 16 + rr;
-            acc += (q[0] + q[4]) + (q[8] + q[12]);
+            const float4 q = *reinterpret_cast<const float4*>(pb + (((su * S + st) * GBATCH + j) * PARTS + p) * 16 + 4 * rr);
+            acc += (q.x + q.y) + (q.z + q.w);
           }
           tot[p] = PRO == PRO_RMSNORM ? acc * rinv : acc;
         }
