@@ -46,8 +46,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# Launches per captured graph, at least: a replay's own start costs a few
+# microseconds (the 6144x2048 GEMV: 3.45 us per launch with one pass over
+# its 77 rotating copies per graph, 3.38 us with eight), which is the graph
+# API's, not the kernel's.
+MIN_GRAPH_LAUNCHES = 1024
+
+
 def _graph_time(launch, n_launch: int, steps: int, warmup: int):
-    """Mean device time per launch of `launch(i)` for i in 0..n_launch-1,
+    """Mean device time per launch of `launch(i % n_launch)`, i = 0, 1, ...,
+    whole passes over the n_launch launches (at least MIN_GRAPH_LAUNCHES)
     captured once into a graph on a side stream and replayed; HIP events on
     that stream bracket the timed replays."""
     import torch
@@ -58,10 +66,12 @@ def _graph_time(launch, n_launch: int, steps: int, warmup: int):
         for i in range(n_launch):  # eager warm-up outside capture
             launch(i, st)
     torch.cuda.synchronize()
+    n_launch_all = n_launch * max(1, math.ceil(MIN_GRAPH_LAUNCHES / n_launch))
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
-        for i in range(n_launch):
-            launch(i, st)
+        for i in range(n_launch_all):
+            launch(i % n_launch, st)
+    n_launch = n_launch_all
     reps = max(1, math.ceil(steps / n_launch))
     wreps = max(1, math.ceil(warmup / n_launch))
     with torch.cuda.stream(stream):
