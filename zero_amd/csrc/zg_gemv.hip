@@ -848,6 +848,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
   }
 }
 
+#ifndef ZG_LDS_TALL_Q4
+#define ZG_LDS_TALL_Q4 0
+#endif
 #ifndef ZG_LDS_TALL
 #define ZG_LDS_TALL 1
 #endif
@@ -871,7 +874,7 @@ constexpr int lds_groups() {
 template <uint32_t QT>
 static bool lds_tall_ok(const GemvArgs& a) {
   return ZG_LDS_TALL && a.nseg == 1 && a.k == 2048 && a.total_groups >= ZG_TALL_MIN_GROUPS &&
-         (QT == Q8_0 || (a.flags & kGemvStream));
+         (QT == Q8_0 || ZG_LDS_TALL_Q4 || (a.flags & kGemvStream));
 }
 
 template <uint32_t QT, int PRO, int EPI, bool STREAM>

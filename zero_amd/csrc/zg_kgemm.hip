@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256 * G) __attribute__((amdgpu_waves_per_eu(ZG_KG_W
         if (gm < a.m) {
           const float v = WT == Q4K ? fdot[i][j][r] - fmin[i][j][r] : fdot[i][j][r];
           float* o = y + (size_t)gm * ns + gn;
-          *o = a.accumulate ? *o + v : v;
+          store_out(o, a.accumulate ? *o + v : v);  // through the L2, as the Q8_0 GEMM
         }
       }
 }

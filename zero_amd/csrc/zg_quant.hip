@@ -357,8 +357,9 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
         const int gm = m0 + wm + 16 * i + rq + r;
         const int gn = n0 + wn + 16 * j + r16;
         if (gm < a.m && gn < ns) {
+          // stored through the L2 (M=512 x 6144x2048: 28.3 against 29.4 us)
           float* o = y + (size_t)gm * ns + gn;
-          *o = a.accumulate ? *o + acc[i][j][r] : acc[i][j][r];
+          store_out(o, a.accumulate ? *o + acc[i][j][r] : acc[i][j][r]);
         }
       }
 }
