@@ -613,6 +613,8 @@ zg_status zg::run_attn_o(zg_ctx* ctx, const float* part_o, const float* part_ml,
   }
   if (!attn_merge_gemv_ok(qt, il, k) || !pair_path_ok(qt, il, k, n, w, part_o))
     return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs Q4_0X4 weights and a strip-sized in_dim");
+  if (!attn_merge_hd_ok(qt, hd) || k % (size_t)hd != 0)
+    return set_error(ctx, ZG_ERR_INVALID_ARG, "attention-merge GEMV needs a head dim in whole 32-element blocks");
   GemvArgs a{};
   a.nseg = 1;
   a.k = (int)k;

@@ -154,6 +154,21 @@ __device__ __forceinline__ void attn_split_load(AttnSplitIn& in, const float* pa
   }
 }
 
+// The same for two 4-element pieces of one head: o[s][0] from element e_lo,
+// o[s][1] from element e_hi (the quarters of a strip lane's x-block).
+__device__ __forceinline__ void attn_split_load2(AttnSplitIn& in, const float* part_o, const float* part_ml, int k,
+                                                 int hd, int nsplit, int e_lo, int e_hi) {
+  const int nh = k / hd, h = e_lo / hd;
+#pragma unroll
+  for (int s = 0; s < kAttnSplits; s++) {
+    if (s < nsplit) {
+      in.o[s][0] = *reinterpret_cast<const float4*>(part_o + (size_t)s * k + e_lo);
+      in.o[s][1] = *reinterpret_cast<const float4*>(part_o + (size_t)s * k + e_hi);
+      in.ml[s] = reinterpret_cast<const float2*>(part_ml)[s * nh + h];
+    }
+  }
+}
+
 __device__ __forceinline__ float4 fma4(float w, float4 a, float4 acc) {
   return make_float4(fmaf(w, a.x, acc.x), fmaf(w, a.y, acc.y), fmaf(w, a.z, acc.z), fmaf(w, a.w, acc.w));
 }

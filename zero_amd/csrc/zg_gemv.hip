@@ -573,7 +573,7 @@ static hipError_t launch_strip_gb1(const GemvArgs& a, int S, int nw, size_t item
   if (nw * 64 > MAXT) return hipErrorInvalidConfiguration;
   const int wps = nw / S;
   const size_t nbatch = (items + (size_t)wps * GBATCH - 1) / ((size_t)wps * GBATCH);
-  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float) + (PRO == PRO_ATTN ? (size_t)a.k * sizeof(float) : 0);
+  const size_t shm = (size_t)2 * nw * GBATCH * PARTS * 16 * sizeof(float);
   if (MAXT == 1024 && nbatch <= (size_t)cu_count() * ZG_ONEB_PER_CU) {
     // one batch per workgroup (every decode-sized launch): no batch loop
     if (S == 4)
@@ -800,7 +800,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
         dot = strip_dot_dig<QT>(L, xd);
       } else {
         float4 xf[8];
-        strip_x_block<PRO>(xf, a, nullptr, kb);
+        strip_x_block<PRO>(xf, a, kb);
         float t = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; c++) t += (xf[c].x + xf[c].y) + (xf[c].z + xf[c].w);
@@ -898,7 +898,7 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
     // split-scale groups: the strip kernel's forms only
     if (!strip_path_ok(a.k)) return hipErrorInvalidValue;
     if constexpr (PRO == PRO_ATTN) {
-      if (QT != Q4_0 || a.attn_nsplit < 1 || a.attn_nsplit > kAttnSplits || a.attn_hd % 8 != 0 ||
+      if (QT != Q4_0 || a.attn_nsplit < 1 || a.attn_nsplit > kAttnSplits || !attn_merge_hd_ok(QT, a.attn_hd) ||
           a.k % a.attn_hd != 0)
         return hipErrorInvalidValue;
     }
@@ -911,7 +911,7 @@ static hipError_t launch_x4_any(const GemvArgs& a, hipStream_t st) {
   } else if constexpr (PRO == PRO_ATTN) {
     // only the Q4_0 strip kernel merges attention splits
     if constexpr (QT == Q4_0) {
-      if (strip_path_ok(a.k) && a.attn_nsplit >= 1 && a.attn_nsplit <= kAttnSplits && a.attn_hd % 8 == 0 &&
+      if (strip_path_ok(a.k) && a.attn_nsplit >= 1 && a.attn_nsplit <= kAttnSplits && attn_merge_hd_ok(QT, a.attn_hd) &&
           a.k % a.attn_hd == 0)
         return launch_strip<QT, PRO, EPI>(a, st);
     }
@@ -1006,7 +1006,7 @@ bool kq_strip_ok(uint32_t qt, uint32_t il, size_t k, size_t n, const void* w, co
 
 // The strip kernel's merge prologue takes these attention splits.
 bool attn_merge_strip_ok(int nsplit, int hd, size_t k) {
-  return nsplit >= 1 && nsplit <= kAttnSplits && hd > 0 && hd % 8 == 0 && k % (size_t)hd == 0;
+  return nsplit >= 1 && nsplit <= kAttnSplits && attn_merge_hd_ok(Q4K, hd) && k % (size_t)hd == 0;
 }
 
 static hipError_t dispatch_q4k_strip(const GemvArgs& a, int pro, int epi, hipStream_t st) {

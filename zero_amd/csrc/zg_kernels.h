@@ -131,6 +131,10 @@ bool kq_attn_o_ok(uint32_t qt, uint32_t il, size_t k, int nsplit, int hd, const 
 hipError_t launch_kq_attn_o(const GenericArgs& a, hipStream_t st);
 // The strip GEMV can merge attention splits in its prologue (PRO_ATTN).
 bool attn_merge_gemv_ok(uint32_t qt, uint32_t il, size_t k);
+// Its lanes merge the splits at their own x-block quarters, so a head must
+// hold whole lane units: 32 elements (Q4_0 / Q8_0 blocks), 64 (Q4_K, id 12:
+// a sub-block pair).
+inline bool attn_merge_hd_ok(uint32_t qt, int hd) { return hd > 0 && hd % (qt == 12u ? 64 : 32) == 0; }
 hipError_t launch_fp16(const uint16_t* in, float* out, size_t n, hipStream_t st);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t v, hipStream_t st);
 hipError_t launch_read_floor(const void* src, size_t bytes, int loads_per_thread, uint32_t* sink, hipStream_t st);

@@ -1802,7 +1802,8 @@ extern "C" zg_status zg_model_create(zg_ctx* ctx, const zg_model_desc* desc, zg_
       L.gu_kq = !L.gu_one && kq_swiglu_ok(qt[ZG_PROJ_GATE], qt[ZG_PROJ_UP], il[ZG_PROJ_GATE], il[ZG_PROJ_UP], H,
                                           L.gate, L.up, m->hidden, L.ffn_norm);
       const uint32_t ot = qt[ZG_PROJ_O], oil = il[ZG_PROJ_O];
-      L.o_merge = m->nsplit > 1 && ((attn_merge_gemv_ok(ot, oil, qd) && pair_path_ok(ot, oil, qd, H, L.o, m->part_o)) ||
+      L.o_merge = m->nsplit > 1 && ((attn_merge_gemv_ok(ot, oil, qd) && attn_merge_hd_ok(ot, (int)d.head_dim) &&
+                                     pair_path_ok(ot, oil, qd, H, L.o, m->part_o)) ||
                                     kq_attn_o_ok(ot, oil, qd, m->nsplit, (int)d.head_dim, L.o, m->part_o));
       // batched prefill: Q4_0 / Q8_0 any shape; Q4_K / Q6_K plain rows of a
       // width in 64-column tiles and an in_dim in whole superblocks

@@ -424,14 +424,13 @@ __device__ __forceinline__ float quad_sum(float v) {
 }
 
 // The 32 activations of K-block kb as the prologue forms them: from x, times
-// the rmsnorm gain (the 1/rms factor is applied to the row totals), or from
-// the merged attention vector in LDS (xs).
+// the rmsnorm gain (the 1/rms factor is applied to the row totals).
 // (Q4_K: the unit's runs A and B, as xf[0..3] and xf[4..7].)
 template <int PRO, uint32_t QT = Q4_0>
-__device__ __forceinline__ void strip_x_block(float4 (&xf)[8], const GemvArgs& a, const float* xs, int kb) {
+__device__ __forceinline__ void strip_x_block(float4 (&xf)[8], const GemvArgs& a, int kb) {
   constexpr int H4 = unit_hoff<QT>() / 4;
   const int x0 = unit_x0<QT>(kb);
-  const float4* x4 = reinterpret_cast<const float4*>((PRO == PRO_ATTN ? xs : a.x) + x0);
+  const float4* x4 = reinterpret_cast<const float4*>(a.x + x0);
 #pragma unroll
   for (int c = 0; c < 8; c++) xf[c] = x4[c < 4 ? c : c - 4 + H4];
   if (PRO == PRO_RMSNORM) {
@@ -545,9 +544,11 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
   uint32_t x8[8];  // PRO_Q8X: the lane's Q8_0 activation block
   float dxq = 0.0f;
   AttnSplitIn am;
-  const int e0 = min(8 * (int)threadIdx.x, a.k - 8);  // PRO_ATTN: this thread's 8 merged dims
   if (PRO == PRO_ATTN) {
-    attn_split_load(am, a.x, a.attn_ml, a.k, a.attn_hd, a.attn_nsplit, e0);
+    // the attention splits' values at this lane's two quarters of its
+    // x-block (one head: the head dim is a multiple of the unit's span)
+    const int x0 = unit_x0<QT>(kb) + 4 * r;
+    attn_split_load2(am, a.x, a.attn_ml, a.k, a.attn_hd, a.attn_nsplit, x0, x0 + unit_hoff<QT>());
   } else if (PRO == PRO_Q8X) {
     const uint8_t* xbk = a.xq + (size_t)kb * 34;
     const u32x4s2* p = reinterpret_cast<const u32x4s2*>(xbk + 2);
@@ -583,27 +584,11 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
 
   // prologue and block sum
   if (PRO == PRO_ATTN) {
-    // the workgroup merges the attention splits into LDS (thread t: dims
-    // 8t..8t+7) while its weight loads are in flight; lanes then read their
-    // x-block from there
-    float* xs = part + (size_t)2 * NW * GBATCH * PARTS * 16;
-    float4 m0, m1;
-    attn_split_merge(am, a.attn_nsplit, m0, m1);
-    if (8 * (int)threadIdx.x < a.k) {
-      reinterpret_cast<float4*>(xs + e0)[0] = m0;
-      reinterpret_cast<float4*>(xs + e0)[1] = m1;
-    }
-    __syncthreads();
-    constexpr int H4 = unit_hoff<QT>() / 4;
-    const float4* x4 = reinterpret_cast<const float4*>(xs + unit_x0<QT>(kb));
-    if (DIG) {
-      // the lane's quarter, as the global prologues load it
-      xb[0] = x4[r];
-      xb[1] = x4[H4 + r];
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; c++) xb[c] = x4[c < 4 ? c : c - 4 + H4];
-    }
+    // each lane merges the splits at its own quarters while the weight
+    // loads are in flight (no LDS staging, no workgroup barrier: the O
+    // projection 2048x2048 in a probe, 3.24 us with the workgroup merging the
+    // whole vector into LDS, 2.58 us on a plain x)
+    attn_split_merge(am, a.attn_nsplit, xb[0], xb[1]);
   }
   if (PRO == PRO_RMSNORM) {
     // ops.rs:29-52: x * (1/sqrt(mean(x^2)+eps)) * w.  The scalar
@@ -633,7 +618,7 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
   int sx = 0;
   XDig xd;
   bool fp32 = !DIG;  // wave-uniform: this wave decodes with fp32 activations
-  if (QT == Q4K && !(PRO == PRO_ATTN && !DIG)) {
+  if (QT == Q4K) {
     // the quad's quarter sums: run A from the lo quarters, run B from the hi ones
     xsa = quad_sum(f4_sum(xb[0]));
     xsb = quad_sum(f4_sum(xb[1]));
@@ -648,21 +633,11 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
     for (int c = 0; c < 8; c++) sx = __builtin_amdgcn_sdot4((int)x8[c], 0x01010101, sx, false);
     asm volatile("" : "+v"(sx));  // computed here, not sunk below the next load
   } else if (!DIG) {
-    float t;
-    if (PRO == PRO_ATTN && !DIG) {
-      t = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; c++) t += (xb[c].x + xb[c].y) + (xb[c].z + xb[c].w);
-      if (QT == Q4K) {
-        xsa = (f4_sum(xb[0]) + f4_sum(xb[1])) + (f4_sum(xb[2]) + f4_sum(xb[3]));
-        xsb = (f4_sum(xb[4]) + f4_sum(xb[5])) + (f4_sum(xb[6]) + f4_sum(xb[7]));
-      }
-    } else {
-      // the quad's four quarters: block sum, then the whole block in every lane
-      t = quad_sum(((xb[0].x + xb[0].y) + (xb[0].z + xb[0].w)) + ((xb[1].x + xb[1].y) + (xb[1].z + xb[1].w)));
-      const float4 lo = xb[0], hi = xb[1];
-      quad_gather_block(lo, hi, xb);
-    }
+    // the quad's four quarters: block sum, then the whole block in every lane
+    const float t =
+        quad_sum(((xb[0].x + xb[0].y) + (xb[0].z + xb[0].w)) + ((xb[1].x + xb[1].y) + (xb[1].z + xb[1].w)));
+    const float4 lo = xb[0], hi = xb[1];
+    quad_gather_block(lo, hi, xb);
     mterm = (QT == Q4_0 ? -8.0f : -128.0f) * t;
     asm volatile("" : "+v"(mterm));  // computed here, not sunk below the next load
   }
@@ -698,7 +673,8 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
               dot = strip_dot_dig_q4k(L[j][p], xd, xsa, xsb, pj);
             } else {
               float4 xf[8];
-              strip_x_block<PRO, QT>(xf, a, part + (size_t)2 * NW * GBATCH * PARTS * 16, kb);
+              if constexpr (PRO == PRO_ATTN) quad_gather_block(xb[0], xb[1], xf);  // the merged quarters
+              else strip_x_block<PRO, QT>(xf, a, kb);
               const float fa = (f4_sum(xf[0]) + f4_sum(xf[1])) + (f4_sum(xf[2]) + f4_sum(xf[3]));
               const float fb = (f4_sum(xf[4]) + f4_sum(xf[5])) + (f4_sum(xf[6]) + f4_sum(xf[7]));
               dot = strip_dot_q4k(L[j][p], xf, fa, fb, pj);
@@ -713,7 +689,8 @@ __device__ __forceinline__ void gemv_strip_body(const GemvArgs& a, int S_rt, int
             // the fp32 decode on the lane's whole block, reloaded per group
             // (a wave that met a block the integer form does not take)
             float4 xf[8];
-            strip_x_block<PRO>(xf, a, part + (size_t)2 * NW * GBATCH * PARTS * 16, kb);
+            if constexpr (PRO == PRO_ATTN) quad_gather_block(xb[0], xb[1], xf);  // the merged quarters
+            else strip_x_block<PRO>(xf, a, kb);
             float t = 0.0f;
 #pragma unroll
             for (int c = 0; c < 8; c++) t += (xf[c].x + xf[c].y) + (xf[c].z + xf[c].w);
