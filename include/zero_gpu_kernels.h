@@ -91,7 +91,7 @@ static inline int zg_mk_plan(uint32_t qtype, uint32_t rows, uint32_t k, uint32_t
     else if (nw <= 8) maxt = 512;
   } else if (qtype == ZG_MK_Q4_0) {
     per = items / (cu_count * 2u * wps);
-    gb = per >= 3 ? 3 : (per < 2 ? 1 : 2);
+    gb = per >= 3 ? 3 : ((per < 2 && !(S >= 8 && per >= 1)) ? 1 : 2);
   } else {
     gb = 2;
   }

@@ -40,7 +40,8 @@ CASES = [
     (Q4_0, 6144, 2048, True),     # oneb_g3_k2048 (the headline GEMV)
     (Q4_0, 4096, 2048, True),     # oneb_g2_k2048
     (Q4_0, 2048, 2048, True),     # oneb_g1_k2048
-    (Q4_0, 2048, 6144, True),     # oneb_g1_k6144
+    (Q4_0, 1024, 6144, True),     # oneb_g1_k6144
+    (Q4_0, 2048, 6144, True),     # oneb_g2_k6144 (the decode's down projection)
     (Q4_0, 4096, 6144, True),     # oneb_g2_k6144
     (Q4_0, 6144, 6144, True),     # oneb_g3_k6144
     (Q4_0, 12288, 6144, True),    # oneb_g4_k6144 (tall, twelve strips, one batch)

@@ -118,9 +118,9 @@ def test_plans_are_the_library_launches():
     lp = module.plan(module.Q4_0, 6144, 2048, 256)
     assert (lp.entry, lp.block, lp.nbatch, lp.one_batch, lp.shm_bytes) == ("zg_mk_q4_0x4_oneb_g3_k2048", 256, 512,
                                                                            True, 2 * 4 * 3 * 16 * 4)
-    # down 2048x6144: twelve strips, one group per wave
+    # down 2048x6144: twelve strips, two groups per wave
     lp = module.plan(module.Q4_0, 2048, 6144, 256)
-    assert (lp.entry, lp.block, lp.nbatch) == ("zg_mk_q4_0x4_oneb_g1_k6144", 768, 512)
+    assert (lp.entry, lp.block, lp.nbatch) == ("zg_mk_q4_0x4_oneb_g2_k6144", 768, 256)
     # the LM-head height: a batch loop over four-group batches, 256 threads
     lp = module.plan(module.Q4_0, 151936, 2048, 256)
     assert (lp.entry, lp.block, lp.one_batch, lp.occupancy_bound) == ("zg_mk_q4_0x4_tall_t256", 256, False, True)

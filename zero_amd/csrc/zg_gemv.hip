@@ -639,7 +639,11 @@ static hipError_t launch_strip(const GemvArgs& a, hipStream_t st) {
     // probe)
     const size_t per = items / ((size_t)cu_count() * 2 * wps);
     if (per >= 3) return launch_strip_gb<QT, PRO, EPI, 3, 1024, IL>(a, S, nw, items, st);
-    if (per < 2) return launch_strip_gb<QT, PRO, EPI, 1, 1024, IL>(a, S, nw, items, st);
+    // one group per wave for the smallest launches, but two from 8 strips
+    // on once every CU gets a workgroup: a wave's x quarters (2 KB) then
+    // outweigh one group's weights (1.15 KB) (the 2048x6144 down projection:
+    // 3.71 against 3.91 us in a probe)
+    if (per < 2 && !(S >= 8 && per >= 1)) return launch_strip_gb<QT, PRO, EPI, 1, 1024, IL>(a, S, nw, items, st);
   }
   if constexpr (QT == Q8_0 && EPI != EPI_SWIGLU && PRO != PRO_ATTN) {
     // tall Q8_0X4 (the LM head): four groups per batch with 16-byte loads

@@ -76,7 +76,7 @@ def plan(qtype: int, rows: int, k: int, cu_count: int) -> Launch:
             maxt = 512
     elif qtype == Q4_0:
         per = items // (cu_count * 2 * wps)
-        gb = 3 if per >= 3 else (1 if per < 2 else 2)
+        gb = 3 if per >= 3 else (1 if (per < 2 and not (S >= 8 and per >= 1)) else 2)
     else:
         gb = 2
     nbatch = -(-items // (wps * gb))
