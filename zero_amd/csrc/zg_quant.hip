@@ -9,6 +9,7 @@
 // round() is round-half-even (rint), and d is stored as the
 // round-to-nearest-even binary16 of the double d.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 
 #include "../../include/zero_gpu.h"
 #include "zg_device.h"
@@ -77,6 +78,14 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(QuantArgs a) {
 // 32 x 32 (2 x 2 MFMA tiles), 4 blocks (128 K) staged in LDS per step.
 // ---------------------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// The 64-row tile's waves each own a 32 x 32 output block and multiply one
+// 32-element block with a single v_mfma_i32_32x32x32_i8 (32 cycles for the
+// 32 x 32 outputs, where four v_mfma_i32_16x16x32_i8 take 64).
+#ifndef ZG_GEMM_MFMA32
+#define ZG_GEMM_MFMA32 1
+#endif
 
 // Up to three weight matrices that share the activations (Q|K|V, gate|up)
 // in one launch: the output columns are the concatenation of the segments,
@@ -106,14 +115,14 @@ constexpr int lds_row() { return BK * 32 + 16; }
 
 // One stage's global operands held in registers between the load and the
 // LDS store (so that the next stage's loads fly while the current stage is
-// multiplied).  Per thread: NA 16-byte activation chunks, ND activation
-// scales, NW weight block rows (raw quants + scale).
-template <uint32_t WT, int BM, int BK>
+// multiplied).  Per thread of NT: NA 16-byte activation chunks, ND
+// activation scales, NW weight block rows (raw quants + scale).
+template <uint32_t WT, int BM, int BK, int NT>
 struct GemmStage {
-  static_assert(BM * BK * 2 % 256 == 0 && kBN * BK % 256 == 0, "every thread stages whole chunks and blocks");
-  static constexpr int NA = BM * BK * 2 / 256;
-  static constexpr int ND = (BM * BK + 255) / 256;
-  static constexpr int NW = kBN * BK / 256;
+  static_assert(BM * BK * 2 % NT == 0 && kBN * BK % NT == 0, "every thread stages whole chunks and blocks");
+  static constexpr int NA = BM * BK * 2 / NT;
+  static constexpr int ND = (BM * BK + NT - 1) / NT;
+  static constexpr int NW = kBN * BK / NT;
   static constexpr int QW = WT == Q4_0 ? 4 : 8;
   u32x4 a[NA];
   uint32_t ad[ND];
@@ -123,14 +132,14 @@ struct GemmStage {
 
 // FULL: the whole tile lies inside the matrix and k is a whole number of
 // stages, so every load is in bounds and none is guarded
-template <uint32_t WT, int IL, int BM, int BK, bool FULL>
-__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const GemmArgs& a, const uint8_t* w, int ns,
-                                                int m0, int n0, int b0, int tid) {
-  using St = GemmStage<WT, BM, BK>;
+template <uint32_t WT, int IL, int BM, int BK, bool FULL, int NT>
+__device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK, NT>& S, const GemmArgs& a, const uint8_t* w,
+                                                int ns, int m0, int n0, int b0, int tid) {
+  using St = GemmStage<WT, BM, BK, NT>;
   const int nb = a.k / 32;
 #pragma unroll
   for (int i = 0; i < St::NA; i++) {
-    const int c = tid + 256 * i, row = c / (BK * 2), ch = c % (BK * 2);
+    const int c = tid + NT * i, row = c / (BK * 2), ch = c % (BK * 2);
     const int gm = m0 + row, kb = b0 + ch / 2;
     S.a[i] = u32x4{0, 0, 0, 0};
     if (FULL || (gm < a.m && kb < nb))
@@ -141,13 +150,13 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
   // 64-row tile had 0.59 M conflict cycles with the block index fastest)
 #pragma unroll
   for (int i = 0; i < St::ND; i++) {
-    const int c = tid + 256 * i, row = c % BM, kk = c / BM;
+    const int c = tid + NT * i, row = c % BM, kk = c / BM;
     const int gm = m0 + row, kb = b0 + kk;
     S.ad[i] = (kk < BK && (FULL || (gm < a.m && kb < nb))) ? (uint32_t)a.xd[(size_t)gm * nb + kb] : 0u;
   }
 #pragma unroll
   for (int i = 0; i < St::NW; i++) {
-    const int c = tid + 256 * i, row = c % kBN, kk = c / kBN;
+    const int c = tid + NT * i, row = c % kBN, kk = c / kBN;
     const int gn = n0 + row, kb = b0 + kk;
 #pragma unroll
     for (int j = 0; j < St::QW; j++) S.q[i][j] = 0;
@@ -199,6 +208,12 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK>& S, const 
 #ifndef ZG_GEMM_UNR64
 #define ZG_GEMM_UNR64 1
 #endif
+// block-loop unroll of the 32 x 32 form (M=512 x 6144x2048: 25.5-25.7 us by
+// 2, 26.1-26.4 us rolled; by 4 the registers of a stage pair grow to 356
+// and one wave fits a SIMD)
+#ifndef ZG_GEMM_UNR32
+#define ZG_GEMM_UNR32 2
+#endif
 
 // Block scales: the hardware fp16 conversion when ZG_GEMM_HWCVT (exact
 // for every finite value; a NaN scale gives a NaN output either way), else
@@ -212,34 +227,35 @@ __device__ __forceinline__ float gemm_scale(uint32_t h) {
   return half_bits_to_f32(h);
 }
 
-template <uint32_t WT, int BM, int BK>
-__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S, int8_t* As, int8_t* Bs, float* Ad,
+template <uint32_t WT, int BM, int BK, int NT>
+__device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK, NT>& S, int8_t* As, int8_t* Bs, float* Ad,
                                                  float* Bd, int tid) {
-  using St = GemmStage<WT, BM, BK>;
+  using St = GemmStage<WT, BM, BK, NT>;
   constexpr int R = lds_row<BK>();
 #pragma unroll
   for (int i = 0; i < St::NA; i++) {
-    const int c = tid + 256 * i, row = c / (BK * 2), ch = c % (BK * 2);
+    const int c = tid + NT * i, row = c / (BK * 2), ch = c % (BK * 2);
     *reinterpret_cast<u32x4*>(As + row * R + ch * 16) = S.a[i];
   }
 #pragma unroll
   for (int i = 0; i < St::ND; i++) {
-    const int c = tid + 256 * i, row = c % BM, kk = c / BM;
+    const int c = tid + NT * i, row = c % BM, kk = c / BM;
     if (kk < BK) Ad[kk * BM + row] = gemm_scale(S.ad[i]);
   }
 #pragma unroll
   for (int i = 0; i < St::NW; i++) {
-    const int c = tid + 256 * i, row = c % kBN, kk = c / kBN;
+    const int c = tid + NT * i, row = c % kBN, kk = c / kBN;
     uint32_t q[8];
     if (WT == Q4_0) {
-      // (nibble - 8) as a signed byte: bytewise n - 8 without borrow across
-      // bytes is (n + 0x78) ^ 0x80
+      // nibble n as the signed byte (n ^ 8) << 4 = 16 (n - 8): the block's
+      // integer dot is 16 times the oracle's, and the weight scale is stored
+      // divided by 16 (both exact: |16 isum| < 2^24, and dX dW is exact in
+      // fp32), so every fma sees the same real product dX dW isum.
+      // v_bitop3_b32 table 0x6A is (a & b) ^ c.
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t lo = S.q[i][j] & 0x0F0F0F0Fu;         // elements 4j..4j+3
-        const uint32_t hi = (S.q[i][j] >> 4) & 0x0F0F0F0Fu;  // elements 16+4j..
-        q[j] = ((lo + 0x78787878u) ^ 0x80808080u);
-        q[4 + j] = ((hi + 0x78787878u) ^ 0x80808080u);
+        q[j] = __builtin_amdgcn_bitop3_b32(S.q[i][j] << 4, 0xF0F0F0F0u, 0x80808080u, 0x6A);  // elements 4j..4j+3
+        q[4 + j] = __builtin_amdgcn_bitop3_b32(S.q[i][j], 0xF0F0F0F0u, 0x80808080u, 0x6A);   // elements 16+4j..
       }
     } else {
 #pragma unroll
@@ -248,28 +264,32 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK>& S,
     u32x4* dst = reinterpret_cast<u32x4*>(Bs + row * R + kk * 32);
     dst[0] = u32x4{q[0], q[1], q[2], q[3]};
     dst[1] = u32x4{q[4], q[5], q[6], q[7]};
-    Bd[kk * kBN + row] = gemm_scale(S.wd[i]);
+    Bd[kk * kBN + row] = WT == Q4_0 ? gemm_scale(S.wd[i]) * 0.0625f : gemm_scale(S.wd[i]);
   }
 }
 
-// Workgroup tile BM (m) x 64 (n), 4 waves of BM/2 x 32 (BM/32 x 2 MFMA
-// tiles), BK blocks (BK * 32 of K) per stage, double-buffered in LDS; the
-// next stage's global loads are issued before the current stage is
-// multiplied.  Per 32-K block: v_mfma_i32_16x16x32_i8 gives the block's
-// integer dots, and every output adds dX*dW*isum with one fma, blocks in
-// ascending order.  Shapes:
-//   BM 64, BK 4   large M: ~100 VGPRs, four workgroups per CU; the block
-//                 loop is not unrolled (M=512 x 6144: all 768 tiles
-//                 resident at once; 34.7 vs 41-43 us unrolled)
-//   BM 32, BK 4   few 64-row tiles per CU (M=512 x 2048x6144: 46.5 us)
-//   BM 32, BK 8   at most one 32-row tile per CU (the batched prefill's 128
-//                 rows): each stage is one exposed memory round trip, so
-//                 256 K per stage halves the trips (128-token prefill 3.72
-//                 ms vs 4.24 with 4-block stages; 16-block stages, at one
-//                 workgroup per CU, were slower still)
-template <uint32_t WT, int IL, int BM, int BK, bool FULL>
-__global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
-  constexpr int MI = BM / 32;  // 16-row MFMA tiles per wave
+// Workgroup tile BM (m) x 64 (n) of NT threads, BK blocks (BK * 32 of K) per
+// stage, double-buffered in LDS; the next stage's global loads are issued
+// before the current stage is multiplied.  Per 32-K block an MFMA gives the
+// block's integer dots, and every output adds dX*dW*isum with one fma,
+// blocks in ascending order.  Shapes (M=512 times the Qwen3-1.7B FFN
+// matrices, graph replays):
+//   BM 64, BK 4, 256   large M: four waves of 32 x 32, one
+//                      v_mfma_i32_32x32x32_i8 per block; three workgroups
+//                      per CU (6144x2048: 25.5-25.9 us, against 27.1 us
+//                      with four v_mfma_i32_16x16x32_i8 per block)
+//   BM 32, BK 8, 512   fewer 64-row tiles: eight waves of 16 x 16, four
+//                      waves per SIMD at two workgroups per CU (2048x6144:
+//                      31.5 us, against 35.4 us with four waves of 16 x 32
+//                      and 4-block stages); also at most one tile per CU
+//                      (the batched prefill's 128 rows: 2.84 against 3.03
+//                      ms with four waves)
+template <uint32_t WT, int IL, int BM, int BK, bool FULL, int NT>
+__global__ __launch_bounds__(NT) void gemm_q8act_kernel(GemmArgs a) {
+  // waves: two along m, NT / 128 along n; each wave owns WR x WC outputs
+  constexpr int WGN = NT / 128, WR = BM / 2, WC = kBN / WGN;
+  constexpr int MI = WR / 16, NJ = WC / 16;  // 16 x 16 MFMA tiles per wave (16 x 16 form)
+  constexpr bool W32 = BM == 64 && NT == 256 && ZG_GEMM_MFMA32;
   constexpr int R = lds_row<BK>();
   __shared__ __attribute__((aligned(16))) int8_t As[2][BM * R];
   __shared__ __attribute__((aligned(16))) int8_t Bs[2][kBN * R];
@@ -286,22 +306,27 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
   float* y = a.y[sg];
   const int nb = a.k / 32;
   const int nst = (nb + BK - 1) / BK;
-  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
+  const int wm = (wave / WGN) * WR, wn = (wave % WGN) * WC;
   const int r16 = lane & 15, kq = (lane >> 4) * 8, rq = (lane >> 4) * 4;
-  float acc[MI][2][4];
+  const int r32 = lane & 31, h32 = lane >> 5;
+  // 16 x 16 form: acc[(i * NJ + j) * 4 + r] is row wm + 16 i + rq + r,
+  // column wn + 16 j + r16; 32 x 32 form: acc[4 g + r] is row wm + 8 g +
+  // 4 h32 + r, column wn + r32
+  constexpr int NACC = MI * NJ * 4;
+  float acc[NACC];
 #pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
+  for (int i = 0; i < NACC; i++) acc[i] = 0.0f;
 
-  GemmStage<WT, BM, BK> S;
+  GemmStage<WT, BM, BK, NT> S;
   gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, 0, tid);
   gemm_stage_store<WT, BM, BK>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
-  for (int st = 0; st < nst; st++) {
-    const int buf = st & 1;
+  // One stage: the next stage's global loads are issued, this stage's blocks
+  // are multiplied out of LDS buffer buf, the next stage is stored to the
+  // other buffer.  Stages run in pairs so that buf is a constant and every
+  // LDS address is a fixed register plus an immediate offset.
+  auto stage = [&](auto bufc, int st) {
+    constexpr int buf = decltype(bufc)::value;
     if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
@@ -312,56 +337,79 @@ __global__ __launch_bounds__(256) void gemm_q8act_kernel(GemmArgs a) {
     // operand reads of blocks kk and kk + 1 into conflicting ds_read2_b64
     // (4.7 M conflict cycles for M=512 x 2048x6144), which the clobber below
     // prevents (down 42.0-42.3 vs 42.6 us)
-    constexpr int UNR = BM == 64 ? ZG_GEMM_UNR64 : 4;
+    constexpr int UNR = W32 ? ZG_GEMM_UNR32 : BM == 64 ? ZG_GEMM_UNR64 : 4;
 #pragma unroll UNR
     for (int kk = 0; kk < BK; kk++) {
+      if constexpr (W32) {
+        // lane: operand row r32, bytes 16 h32..16 h32 + 15 of the block (the
+        // same K order in both operands, so the dot is the block's)
+        const v4i av = *reinterpret_cast<const v4i*>(A + (wm + r32) * R + kk * 32 + h32 * 16);
+        const v4i bv = *reinterpret_cast<const v4i*>(B + (wn + r32) * R + kk * 32 + h32 * 16);
+        float4 da[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) da[g] = *reinterpret_cast<const float4*>(&Ad[buf][kk * BM + wm + 8 * g + 4 * h32]);
+        const float db = Bd[buf][kk * kBN + wn + r32];
+        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0},
+                                                             0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float dag[4] = {da[g].x, da[g].y, da[g].z, da[g].w};
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[4 * g + r] = fmaf(__fmul_rn(dag[r], db), (float)c[4 * g + r], acc[4 * g + r]);
+        }
+        continue;
+      }
       // the 32-row tile: no pairing of LDS reads across blocks
       if constexpr (BM == 32) asm volatile("" ::: "memory");
-      long av[MI], bv[2];
+      long av[MI], bv[NJ];
       float4 da[MI];
-      float db[2];
+      float db[NJ];
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         av[i] = *reinterpret_cast<const long*>(A + (wm + 16 * i + r16) * R + kk * 32 + kq);
         da[i] = *reinterpret_cast<const float4*>(&Ad[buf][kk * BM + wm + 16 * i + rq]);
       }
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
+      for (int j = 0; j < NJ; j++) {
         bv[j] = *reinterpret_cast<const long*>(B + (wn + 16 * j + r16) * R + kk * 32 + kq);
         db[j] = Bd[buf][kk * kBN + wn + 16 * j + r16];
       }
-      v4i c[MI][2];
+      v4i c[MI][NJ];
 #pragma unroll
       for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+        for (int j = 0; j < NJ; j++) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv[j], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         const float dai[4] = {da[i].x, da[i].y, da[i].z, da[i].w};
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(__fmul_rn(dai[r], db[j]), (float)c[i][j][r], acc[i][j][r]);
+          for (int r = 0; r < 4; r++)
+            acc[(i * NJ + j) * 4 + r] = fmaf(__fmul_rn(dai[r], db[j]), (float)c[i][j][r], acc[(i * NJ + j) * 4 + r]);
       }
     }
     if (st + 1 < nst) gemm_stage_store<WT, BM, BK>(S, As[buf ^ 1], Bs[buf ^ 1], Ad[buf ^ 1], Bd[buf ^ 1], tid);
     __syncthreads();
+  };
+  int st = 0;
+  for (; st + 2 <= nst; st += 2) {
+    stage(std::integral_constant<int, 0>{}, st);
+    stage(std::integral_constant<int, 1>{}, st + 1);
   }
-  // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16
+  if (st < nst) stage(std::integral_constant<int, 0>{}, st);
+  // D layout of v_mfma_*_16x16*: lane l holds rows 4*(l/16)+r, column l%16;
+  // of v_mfma_*_32x32*: element 4g+r of lane l is row 8g+4*(l/32)+r, column
+  // l%32.  Stored through the L2 (M=512 x 6144x2048: 28.3 against 29.4 us).
 #pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int gm = m0 + wm + 16 * i + rq + r;
-        const int gn = n0 + wn + 16 * j + r16;
-        if (gm < a.m && gn < ns) {
-          // stored through the L2 (M=512 x 6144x2048: 28.3 against 29.4 us)
-          float* o = y + (size_t)gm * ns + gn;
-          store_out(o, a.accumulate ? *o + acc[i][j][r] : acc[i][j][r]);
-        }
-      }
+  for (int e = 0; e < NACC; e++) {
+    const int gm = m0 + wm + (W32 ? 8 * (e >> 2) + 4 * h32 + (e & 3) : 16 * (e / (NJ * 4)) + rq + (e & 3));
+    const int gn = n0 + wn + (W32 ? r32 : 16 * ((e >> 2) % NJ) + r16);
+    if (gm < a.m && gn < ns) {
+      float* o = y + (size_t)gm * ns + gn;
+      store_out(o, a.accumulate ? *o + acc[e] : acc[e]);
+    }
+  }
 }
 
 }  // namespace zg
@@ -420,30 +468,38 @@ static int gemm_cu_count() {
 #define ZG_GEMM_SMALL_BK 8
 #endif
 constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row tile
+// the 32-row tile with eight waves of 16 x 16 outputs and 8-block stages
+// (twice the waves per SIMD of the four-wave tile)
+#ifndef ZG_GEMM_W8
+#define ZG_GEMM_W8 1
+#endif
+#ifndef ZG_GEMM_W8S
+#define ZG_GEMM_W8S 1
+#endif
 
 // Every tile full (m a multiple of the tile rows, each segment's width a
 // multiple of 64, k a whole number of stages): the kernel form with
 // unguarded loads.
-template <uint32_t WT, int IL, int BM, int BK>
+template <uint32_t WT, int IL, int BM, int BK, int NT>
 static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
   bool full = a.m % BM == 0 && (a.k / 32) % BK == 0;
   for (int i = 0, lo = 0; i < a.nseg; lo = a.seg_end[i], i++) full = full && (a.seg_end[i] - lo) % kBN == 0;
-  if (full) hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, false>), grid, dim3(256), 0, st, a);
+  if (full) hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, true, NT>), grid, dim3(NT), 0, st, a);
+  else hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, false, NT>), grid, dim3(NT), 0, st, a);
 }
 
 // the weight type and layout (1 plain rows, 4 X4, 5 split-scale X4)
-template <int BM, int BK>
+template <int BM, int BK, int NT = 256>
 static void launch_gemm_il(const GemmArgs& a, uint32_t w_type, uint32_t il, hipStream_t st) {
   if (w_type == ZG_Q4_0) {
-    if (il == 4) launch_gemm<Q4_0, 4, BM, BK>(a, st);
-    else if (il == 5) launch_gemm<Q4_0, 5, BM, BK>(a, st);
-    else launch_gemm<Q4_0, 1, BM, BK>(a, st);
+    if (il == 4) launch_gemm<Q4_0, 4, BM, BK, NT>(a, st);
+    else if (il == 5) launch_gemm<Q4_0, 5, BM, BK, NT>(a, st);
+    else launch_gemm<Q4_0, 1, BM, BK, NT>(a, st);
   } else {
-    if (il == 4) launch_gemm<Q8_0, 4, BM, BK>(a, st);
-    else if (il == 5) launch_gemm<Q8_0, 5, BM, BK>(a, st);
-    else launch_gemm<Q8_0, 1, BM, BK>(a, st);
+    if (il == 4) launch_gemm<Q8_0, 4, BM, BK, NT>(a, st);
+    else if (il == 5) launch_gemm<Q8_0, 5, BM, BK, NT>(a, st);
+    else launch_gemm<Q8_0, 1, BM, BK, NT>(a, st);
   }
 }
 
@@ -488,9 +544,11 @@ zg_status zg::run_gemm(zg_ctx* ctx, const int8_t* qs, const uint16_t* xd, const 
   } else if (((n + kBN - 1) / kBN) * ((m + 31) / 32) <= (size_t)gemm_cu_count()) {
     // at most one 32-row tile per CU: each stage's round trip is exposed,
     // so fewer, larger stages
-    launch_gemm_il<32, kSmallBK>(a, w_type, interleave, st);
+    if (ZG_GEMM_W8S) launch_gemm_il<32, 8, 512>(a, w_type, interleave, st);
+    else launch_gemm_il<32, kSmallBK>(a, w_type, interleave, st);
   } else {
-    launch_gemm_il<32, 4>(a, w_type, interleave, st);
+    if (ZG_GEMM_W8) launch_gemm_il<32, 8, 512>(a, w_type, interleave, st);
+    else launch_gemm_il<32, 4>(a, w_type, interleave, st);
   }
   return hip_check(ctx, hipGetLastError(), "gemm launch");
 }
