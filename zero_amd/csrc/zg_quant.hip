@@ -203,10 +203,107 @@ __device__ __forceinline__ void gemm_stage_load(GemmStage<WT, BM, BK, NT>& S, co
   }
 }
 
+// A full tile's loads (FULL below, with activations and every weight
+// segment under 2 GB): each thread's byte offsets from the per-stage bases
+// are fixed for the whole kernel, so a stage's loads take a wave-uniform
+// base (scalar registers, advanced once per stage) plus a fixed 32-bit
+// per-lane offset, and cost no vector address arithmetic.
+template <uint32_t WT, int IL, int BM, int BK, int NT>
+struct GemmOffs {
+  using St = GemmStage<WT, BM, BK, NT>;
+  uint32_t a[St::NA], ad[St::ND], q[St::NW], d[St::NW];
+};
+
+template <uint32_t WT, int IL, int BM, int BK, int NT>
+__device__ __forceinline__ void gemm_offsets(GemmOffs<WT, IL, BM, BK, NT>& O, const GemmArgs& a, int m0, int n0,
+                                             int tid) {
+  using St = GemmStage<WT, BM, BK, NT>;
+  const uint32_t nb = (uint32_t)a.k / 32;
+  constexpr uint32_t gb = WT == Q4_0 ? 72 : 136, QB = WT == Q4_0 ? 16 : 32, bb = WT == Q4_0 ? 18 : 34;
+#pragma unroll
+  for (int i = 0; i < St::NA; i++) {
+    const int c = tid + NT * i, row = c / (BK * 2), ch = c % (BK * 2);
+    O.a[i] = (uint32_t)(m0 + row) * (uint32_t)a.k + (uint32_t)(ch / 2) * 32 + (uint32_t)(ch & 1) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < St::ND; i++) {
+    const int c = tid + NT * i, row = c % BM, kk = c / BM;
+    O.ad[i] = ((uint32_t)(m0 + row) * nb + (uint32_t)kk) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < St::NW; i++) {
+    const int c = tid + NT * i, row = c % kBN, kk = c / kBN;
+    const uint32_t gn = (uint32_t)(n0 + row);
+    if (IL == 4) {
+      const uint32_t g = (gn >> 2) * nb * gb + (uint32_t)kk * gb;
+      O.d[i] = g + 2 * (gn & 3);
+      O.q[i] = g + 8 + (gn & 3) * QB;
+    } else if (IL == 5) {
+      const uint32_t g = (gn >> 2) * nb * gb, u = (uint32_t)kk * 4 + (gn & 3);
+      O.q[i] = g + u * QB;
+      O.d[i] = g + nb * 4 * QB + 2 * u;
+    } else {
+      O.d[i] = (gn * nb + (uint32_t)kk) * bb;
+      O.q[i] = O.d[i] + 2;
+    }
+  }
+}
+
+// The offset as a 32-bit value defined where it is used, so that the load
+// is selected as a scalar base plus a 32-bit vector offset (hoisted out of
+// the stage loop it would be widened to a 64-bit vector add per load).
+// Raw buffer loads with the stage advance as the scalar offset measured
+// slower (M=512 x 2048x6144: 32.4 against 30.9 us).
+__device__ __forceinline__ uint32_t pin_off(uint32_t o) {
+  asm volatile("" : "+v"(o));
+  return o;
+}
+
+template <uint32_t WT, int IL, int BM, int BK, int NT>
+__device__ __forceinline__ void gemm_stage_load_full(GemmStage<WT, BM, BK, NT>& S, const GemmOffs<WT, IL, BM, BK, NT>& O,
+                                                     const GemmArgs& a, const uint8_t* w, int b0, int tid) {
+  using St = GemmStage<WT, BM, BK, NT>;
+  constexpr uint32_t gb = WT == Q4_0 ? 72 : 136, QB = WT == Q4_0 ? 16 : 32, bb = WT == Q4_0 ? 18 : 34;
+  const int8_t* xa = a.xq + (size_t)b0 * 32;
+  const uint8_t* xd = reinterpret_cast<const uint8_t*>(a.xd) + (size_t)b0 * 2;
+  const uint8_t* wq = w + (size_t)b0 * (IL == 4 ? gb : IL == 5 ? 4 * QB : bb);
+  const uint8_t* wd = IL == 5 ? w + (size_t)b0 * 8 : wq;
+#pragma unroll
+  for (int i = 0; i < St::NA; i++) S.a[i] = *reinterpret_cast<const u32x4*>(xa + pin_off(O.a[i]));
+#pragma unroll
+  for (int i = 0; i < St::ND; i++) {
+    const int kk = (tid + NT * i) / BM;
+    S.ad[i] = kk < BK ? (uint32_t)*reinterpret_cast<const uint16_t*>(xd + pin_off(O.ad[i])) : 0u;
+  }
+#pragma unroll
+  for (int i = 0; i < St::NW; i++) {
+    const uint8_t* qp = wq + pin_off(O.q[i]);
+    const uint8_t* dp = wd + pin_off(O.d[i]);
+    if (IL == 4 || IL == 5) {
+#pragma unroll
+      for (int j = 0; j < St::QW / 2; j++) {
+        const uint2 v = *reinterpret_cast<const uint2*>(qp + 8 * j);
+        S.q[i][2 * j] = v.x;
+        S.q[i][2 * j + 1] = v.y;
+      }
+      S.wd[i] = *reinterpret_cast<const uint16_t*>(dp);
+    } else {
+#pragma unroll
+      for (int j = 0; j < St::QW; j++)
+        S.q[i][j] = (uint32_t)qp[4 * j] | ((uint32_t)qp[4 * j + 1] << 8) | ((uint32_t)qp[4 * j + 2] << 16) |
+                    ((uint32_t)qp[4 * j + 3] << 24);
+      S.wd[i] = (uint32_t)dp[0] | ((uint32_t)dp[1] << 8);
+    }
+  }
+}
+
 // block-loop unroll of the 64-row tile (unrolled by 4: M=512 x 6144x2048
 // 41.2 vs 35.0 us rolled; by 2: 36.5 us)
 #ifndef ZG_GEMM_UNR64
 #define ZG_GEMM_UNR64 1
+#endif
+#ifndef ZG_GEMM_OFFS
+#define ZG_GEMM_OFFS 1
 #endif
 // block-loop unroll of the 32 x 32 form (M=512 x 6144x2048: 25.5-25.7 us by
 // 2, 26.1-26.4 us rolled; by 4 the registers of a stage pair grow to 356
@@ -276,11 +373,11 @@ __device__ __forceinline__ void gemm_stage_store(const GemmStage<WT, BM, BK, NT>
 // matrices, graph replays):
 //   BM 64, BK 4, 256   large M: four waves of 32 x 32, one
 //                      v_mfma_i32_32x32x32_i8 per block; three workgroups
-//                      per CU (6144x2048: 25.5-25.9 us, against 27.1 us
-//                      with four v_mfma_i32_16x16x32_i8 per block)
+//                      per CU (6144x2048: 25.5 us, against 27.1 us with
+//                      four v_mfma_i32_16x16x32_i8 per block)
 //   BM 32, BK 8, 512   fewer 64-row tiles: eight waves of 16 x 16, four
 //                      waves per SIMD at two workgroups per CU (2048x6144:
-//                      31.5 us, against 35.4 us with four waves of 16 x 32
+//                      30.9 us, against 35.4 us with four waves of 16 x 32
 //                      and 4-block stages); also at most one tile per CU
 //                      (the batched prefill's 128 rows: 2.84 against 3.03
 //                      ms with four waves)
@@ -318,7 +415,13 @@ __global__ __launch_bounds__(NT) void gemm_q8act_kernel(GemmArgs a) {
   for (int i = 0; i < NACC; i++) acc[i] = 0.0f;
 
   GemmStage<WT, BM, BK, NT> S;
-  gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, 0, tid);
+  GemmOffs<WT, IL, BM, BK, NT> O;
+  if constexpr (FULL && ZG_GEMM_OFFS) gemm_offsets<WT, IL, BM, BK, NT>(O, a, m0, n0, tid);
+  auto load = [&](int b0) {
+    if constexpr (FULL && ZG_GEMM_OFFS) gemm_stage_load_full<WT, IL, BM, BK, NT>(S, O, a, w, b0, tid);
+    else gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, b0, tid);
+  };
+  load(0);
   gemm_stage_store<WT, BM, BK>(S, As[0], Bs[0], Ad[0], Bd[0], tid);
   __syncthreads();
   // One stage: the next stage's global loads are issued, this stage's blocks
@@ -327,7 +430,7 @@ __global__ __launch_bounds__(NT) void gemm_q8act_kernel(GemmArgs a) {
   // LDS address is a fixed register plus an immediate offset.
   auto stage = [&](auto bufc, int st) {
     constexpr int buf = decltype(bufc)::value;
-    if (st + 1 < nst) gemm_stage_load<WT, IL, BM, BK, FULL>(S, a, w, ns, m0, n0, (st + 1) * BK, tid);
+    if (st + 1 < nst) load((st + 1) * BK);
     const int8_t* A = As[buf];
     const int8_t* B = Bs[buf];
     // blocks past k in the last stage hold zero quants and scales: they add
@@ -483,8 +586,10 @@ constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row ti
 template <uint32_t WT, int IL, int BM, int BK, int NT>
 static void launch_gemm(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
-  bool full = a.m % BM == 0 && (a.k / 32) % BK == 0;
-  for (int i = 0, lo = 0; i < a.nseg; lo = a.seg_end[i], i++) full = full && (a.seg_end[i] - lo) % kBN == 0;
+  // every tile whole, and every byte offset from a stage base under 2^31
+  bool full = a.m % BM == 0 && (a.k / 32) % BK == 0 && (size_t)a.m * (size_t)a.k < ((size_t)1 << 31);
+  for (int i = 0, lo = 0; i < a.nseg; lo = a.seg_end[i], i++)
+    full = full && (a.seg_end[i] - lo) % kBN == 0 && (size_t)(a.seg_end[i] - lo) * (size_t)(a.k / 32) * 34 < ((size_t)1 << 31);
   if (full) hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, true, NT>), grid, dim3(NT), 0, st, a);
   else hipLaunchKernelGGL((gemm_q8act_kernel<WT, IL, BM, BK, false, NT>), grid, dim3(NT), 0, st, a);
 }
