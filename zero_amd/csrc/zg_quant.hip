@@ -103,7 +103,30 @@ struct GemmArgs {
   int nseg;
   int accumulate;  // 1: y += result (residual add), 0: y = result
   int m, n, k;     // n: total columns
+  // XCD rectangles: 0, or the tile grid cut into 8 rectangles of rx x ry
+  // tiles, one per XCD (see gemm_tile)
+  int rx, ry;
 };
+
+// The tile of this workgroup.  Workgroups go to the eight XCDs round-robin
+// in dispatch order, so with the plain order XCD j holds the column tiles
+// j, j + 8, ... of every row tile and each XCD's L2 fetches every
+// activation row.  With rectangles, the k-th workgroup of XCD j takes tile
+// k of rectangle j (row-major inside it): each XCD reads the activation
+// rows and weight columns of one rectangle only.  Both orders cover every
+// tile once.
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, int& tx, int& ty) {
+  if (a.rx == 0) {
+    tx = blockIdx.x;
+    ty = blockIdx.y;
+    return;
+  }
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int j = lin & 7, k = lin >> 3;
+  const int rects_x = gridDim.x / a.rx;
+  tx = (j % rects_x) * a.rx + k % a.rx;
+  ty = (j / rects_x) * a.ry + k / a.rx;
+}
 
 constexpr int kBN = 64;  // tile columns (tile rows BM: 64 or 32)
 // LDS row stride in bytes for BK blocks of 32 per stage (padded, 16-B aligned)
@@ -393,9 +416,11 @@ __global__ __launch_bounds__(NT) void gemm_q8act_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float Ad[2][BK * BM];   // [kk][row]
   __shared__ __attribute__((aligned(16))) float Bd[2][BK * kBN];  // [kk][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * BM;
+  int tx, ty;
+  gemm_tile(a, tx, ty);
+  const int m0 = ty * BM;
   // this tile's segment (uniform): its weights, output and local columns
-  const int nt0 = blockIdx.x * kBN;
+  const int nt0 = tx * kBN;
   const int sg = (a.nseg > 1 && nt0 >= a.seg_end[0]) ? ((a.nseg > 2 && nt0 >= a.seg_end[1]) ? 2 : 1) : 0;
   const int base = sg == 0 ? 0 : a.seg_end[sg - 1];
   const int ns = a.seg_end[sg] - base, n0 = nt0 - base;
@@ -571,6 +596,9 @@ static int gemm_cu_count() {
 #define ZG_GEMM_SMALL_BK 8
 #endif
 constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row tile
+#ifndef ZG_GEMM_XCD_RECT
+#define ZG_GEMM_XCD_RECT 1
+#endif
 // the 32-row tile with eight waves of 16 x 16 outputs and 8-block stages
 // (twice the waves per SIMD of the four-wave tile)
 #ifndef ZG_GEMM_W8
@@ -583,9 +611,34 @@ constexpr int kSmallBK = ZG_GEMM_SMALL_BK;  // blocks per stage of the 32-row ti
 // Every tile full (m a multiple of the tile rows, each segment's width a
 // multiple of 64, k a whole number of stages): the kernel form with
 // unguarded loads.
+// XCD rectangles for a grid of gx x gy tiles (gx a multiple of 8): of the
+// rx x ry (rx dividing gx, eight rectangles covering the grid) the one whose
+// activation rows and weight columns are the fewest bytes, when that is
+// fewer than the plain order's share (column tiles j, j + 8, ... of every
+// row tile); else 0 x 0, the plain order.  wb: weight bytes per element.
+static void gemm_rects(GemmArgs& a, int gx, int gy, int bm, double wb) {
+  a.rx = a.ry = 0;
+  if (!ZG_GEMM_XCD_RECT || (long)gx * gy % 8 || gx % 8) return;
+  const double xrow = 1.0625 * a.k * bm, wcol = wb * a.k * kBN;  // bytes of a row tile / column tile
+  double best = (double)gy * xrow + (double)(gx / 8) * wcol;    // plain order
+  for (int rx = 1; rx <= gx; rx++) {
+    if (gx % rx) continue;
+    const int nx = gx / rx;
+    if (8 % nx || gy % (8 / nx)) continue;
+    const int ry = gy / (8 / nx);
+    const double bytes = (double)ry * xrow + (double)rx * wcol;
+    if (bytes < best) {
+      best = bytes;
+      a.rx = rx;
+      a.ry = ry;
+    }
+  }
+}
+
 template <uint32_t WT, int IL, int BM, int BK, int NT>
-static void launch_gemm(const GemmArgs& a, hipStream_t st) {
+static void launch_gemm(GemmArgs a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + BM - 1) / BM));
+  gemm_rects(a, (int)grid.x, (int)grid.y, BM, WT == Q4_0 ? 0.5625 : 1.0625);
   // every tile whole, and every byte offset from a stage base under 2^31
   bool full = a.m % BM == 0 && (a.k / 32) % BK == 0 && (size_t)a.m * (size_t)a.k < ((size_t)1 << 31);
   for (int i = 0, lo = 0; i < a.nseg; lo = a.seg_end[i], i++)
@@ -596,7 +649,7 @@ static void launch_gemm(const GemmArgs& a, hipStream_t st) {
 
 // the weight type and layout (1 plain rows, 4 X4, 5 split-scale X4)
 template <int BM, int BK, int NT = 256>
-static void launch_gemm_il(const GemmArgs& a, uint32_t w_type, uint32_t il, hipStream_t st) {
+static void launch_gemm_il(GemmArgs& a, uint32_t w_type, uint32_t il, hipStream_t st) {
   if (w_type == ZG_Q4_0) {
     if (il == 4) launch_gemm<Q4_0, 4, BM, BK, NT>(a, st);
     else if (il == 5) launch_gemm<Q4_0, 5, BM, BK, NT>(a, st);
