@@ -35,11 +35,11 @@ ROWS, K = 6144, 2048
 GEMV_BYTES = ROWS * (K // 32) * 18 + 4 * K + 4 * ROWS
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the GEMV kernel, from rocprofv3 --pmc FETCH_SIZE
-# (3,516 KiB x 2.00) and WRITE_SIZE (32 KiB x 1.00) over the eager `--profile
+# (3,508 KiB x 2.00) and WRITE_SIZE (32 KiB x 1.00) over the eager `--profile
 # c1` launches; the factors come from the same counters read on an
 # elementwise kernel that reads and writes 256 MiB (`--profile copy`).
-# 1.02 x GEMV_BYTES: the weights are read exactly once.
-GEMV_TRAFFIC_BYTES = 7_233_432
+# 1.01 x GEMV_BYTES: the weights are read exactly once.
+GEMV_TRAFFIC_BYTES = 7_216_029
 
 
 def log(*a):
