@@ -72,6 +72,13 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// A quad_perm read whose every source lane is valid: bound_ctrl on, so no
+// old value is set up and the move can fold into its user.
+template <int CTRL>
+__device__ __forceinline__ float quad_pick(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
 // Full wave64 sum, wave-uniform result: xor-1 and xor-2 within quads
 // (quad_perm), half-row and row mirrors give every lane its 16-lane row
 // sum, then the four row sums are read out with v_readlane.
@@ -421,6 +428,21 @@ __device__ __forceinline__ void q4k_lane_scales(uint32_t w0, uint32_t w1, uint32
 
 // The superblock's d and dmin through the hardware fp16 conversion: exact
 // for every finite value; a NaN scale gives a NaN row either way.
+// get_scale_min_k4 (dequant.rs:75-85) for one sub-block sbi (0..7) of the
+// 12 scale bytes w0..w2; the shifts and widths depend on sbi only, so they
+// are constant per lane where sbi is: sbi < 4 takes the low six bits of
+// byte sbi of w0 (scale) and w1 (min); sbi >= 4 the low / high nibble of
+// byte sbi - 4 of w2, with the top two bits of byte sbi - 4 of w0 / w1
+// above them (a zero-width field is 0).
+__device__ __forceinline__ void q4k_sub_scale(uint32_t w0, uint32_t w1, uint32_t w2, int sbi, uint32_t& sc,
+                                              uint32_t& mn) {
+  const bool low = sbi < 4;
+  const uint32_t o = 8u * (uint32_t)(sbi & 3);
+  const uint32_t wid = low ? 6u : 4u, hw = low ? 0u : 2u;
+  sc = __builtin_amdgcn_ubfe(low ? w0 : w2, o, wid) | (__builtin_amdgcn_ubfe(w0, o + 6u, hw) << 4);
+  mn = __builtin_amdgcn_ubfe(low ? w1 : w2, low ? o : o + 4u, wid) | (__builtin_amdgcn_ubfe(w1, o + 6u, hw) << 4);
+}
+
 __device__ __forceinline__ float kq_half(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
 }

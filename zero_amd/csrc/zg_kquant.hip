@@ -121,12 +121,21 @@ struct KqX {
 
 
 __device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const KqX& x, int lane) {
-  const int j = (lane >> 1) & 3;
+  const int j = (lane >> 1) & 3, h = lane & 1;
   const float d = kq_half(L.hdr.x), dmin = kq_half(L.hdr.x >> 16);
-  uint32_t iA, iB, nA, nB;
-  q4k_lane_scales(L.hdr.y, L.hdr.z, L.hdr.w, j, iA, iB, nA, nB);
-  // high nibbles stay in place (16 x the value): the 1/16 goes into the
-  // sub-block scale (exact)
+  // The two lanes of a sub-block pair (h = 0, 1; quad lanes 0,1 and 2,3)
+  // each decode one of its sub-blocks, 2j + h, into the factors d*sc and
+  // dmin*m, and take the pair's factors by DPP: sub-block 2j's from the
+  // even lane (quad_perm [0,0,2,2]), 2j + 1's from the odd lane ([1,1,3,3]).
+  // High nibbles stay in place (16 x the value): the 1/16 goes into
+  // sub-block 2j + 1's scale (exact).  The same products as decoding both
+  // sub-blocks in every lane, in the same order (8.6 % fewer VALU in the
+  // 14336x4096 loop; 10.90-11.03 against 11.03-11.15 us).
+  uint32_t sc, mn;
+  q4k_sub_scale(L.hdr.y, L.hdr.z, L.hdr.w, 2 * j + h, sc, mn);
+  const float ds = (d * (h ? 0.0625f : 1.0f)) * (float)sc, dm = dmin * (float)mn;
+  const float dA = quad_pick<0xA0>(ds), mA = quad_pick<0xA0>(dm);
+  const float dB = quad_pick<0xF5>(ds), mB = quad_pick<0xF5>(dm);
   const uint32_t q[4] = {L.q.x, L.q.y, L.q.z, L.q.w};
   uint32_t lo[4], hi[4];
 #pragma unroll
@@ -136,10 +145,10 @@ __device__ __forceinline__ float kq_dot(const KqLane<Q4K>& L, const KqX& x, int 
   }
   const float sA = u8_dot16(lo, x.a);
   const float sB = u8_dot16(hi, x.b);
-  float acc = (d * (float)iA) * sA;
-  acc = fmaf(-(dmin * (float)nA), x.sa, acc);
-  acc = fmaf((d * 0.0625f) * (float)iB, sB, acc);
-  return fmaf(-(dmin * (float)nB), x.sb, acc);
+  float acc = dA * sA;
+  acc = fmaf(-mA, x.sa, acc);
+  acc = fmaf(dB, sB, acc);
+  return fmaf(-mB, x.sb, acc);
 }
 
 __device__ __forceinline__ float kq_dot(const KqLane<Q6K>& L, const KqX& x, int lane) {
