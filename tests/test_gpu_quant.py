@@ -81,6 +81,7 @@ GEMM_CASES = [
     (512, 2048, 6144, Q4_0, 4),  # down-proj shape
     (512, 6144, 2048, Q8_0, 1),  # the 64-row tile, plain Q8_0 rows
     (700, 6100, 1024, Q8_0, 4),  # the 64-row tile with ragged M and N (guarded loads and stores)
+    (512, 2048, 1024, Q4_0, 1),  # the eight-wave 32-row tile, plain rows, XCD rectangles of 8x8 tiles
     (65, 100, 256, Q8_0, 1),     # ragged M and N, plain Q8_0
     (1, 64, 96, Q4_0, 4),        # M=1, odd blocks per row
     (70, 132, 64, Q8_0, 4),
