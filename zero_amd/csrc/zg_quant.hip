@@ -320,11 +320,12 @@ __device__ __forceinline__ void gemm_stage_load_full(GemmStage<WT, BM, BK, NT>& 
   }
 }
 
-// block-loop unroll of the 64-row tile (unrolled by 4: M=512 x 6144x2048
-// 41.2 vs 35.0 us rolled; by 2: 36.5 us)
+// block-loop unroll of the 64-row tile's 16 x 16 form (ZG_GEMM_MFMA32 0;
+// unrolled by 4: M=512 x 6144x2048 41.2 vs 35.0 us rolled; by 2: 36.5 us)
 #ifndef ZG_GEMM_UNR64
 #define ZG_GEMM_UNR64 1
 #endif
+// full tiles load through gemm_offsets / gemm_stage_load_full
 #ifndef ZG_GEMM_OFFS
 #define ZG_GEMM_OFFS 1
 #endif
