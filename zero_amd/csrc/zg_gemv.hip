@@ -853,32 +853,44 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
 }
 
 #ifndef ZG_LDS_TALL_Q4
-#define ZG_LDS_TALL_Q4 0
+#define ZG_LDS_TALL_Q4 1
 #endif
 #ifndef ZG_LDS_TALL
 #define ZG_LDS_TALL 1
 #endif
-// Groups per batch: Q4_0 8 (36,864 bytes, nine whole rounds, two
-// workgroups per CU), Q8_0 4 (34,816 bytes in nine rounds, two workgroups
-// per CU; eight groups leave one workgroup per CU: 65.2 vs 58.8 us for the
-// LM head)
+// Groups per batch.  Q4_0 4 (18,432 bytes in five rounds, three workgroups
+// per CU): 151936x2048 31.0-31.6 us against 31.8 with eight (36,864 bytes,
+// two workgroups per CU), 31.1-31.4 with three, 32.9 with two.  Q8_0 4
+// (34,816 bytes in nine rounds, two workgroups per CU; eight groups leave
+// one workgroup per CU: 65.2 vs 58.8 us for the LM head).
+#ifndef ZG_LDS_G_Q4
+#define ZG_LDS_G_Q4 4
+#endif
+#ifndef ZG_LDS_G_Q8
+#define ZG_LDS_G_Q8 4
+#endif
 template <uint32_t QT>
 constexpr int lds_groups() {
-  return QT == Q4_0 ? 8 : 4;
+  return QT == Q4_0 ? ZG_LDS_G_Q4 : ZG_LDS_G_Q8;
 }
-// The LDS-staged kernel (nontemporal loads) takes tall Q8_0X4 single
-// projections at in_dim 2048 (the LM head: 58.8 us against 64.2 us for the
-// register strip kernel's cache-allocating loads and 77 us for its
-// nontemporal ones) and streamed tall launches of either type (inside the
+// Q4_0X4 launches of at least this many groups take the LDS-staged kernel
+// (151936x2048: 31.1-31.6 against 32.2 us for the register strip kernel in
+// the same runs); shorter ones keep the strip kernel (49152x2048: 12.4
+// against 12.9-13.1 us staged).
+#ifndef ZG_LDS_Q4_MIN_GROUPS
+#define ZG_LDS_Q4_MIN_GROUPS 24576
+#endif
+// The LDS-staged kernel takes tall Q8_0X4 single projections at in_dim 2048
+// (the LM head: 58.8 us against 64.2 us for the register strip kernel's
+// cache-allocating loads and 77 us for its nontemporal ones), the tallest
+// Q4_0X4 ones, and streamed tall launches of either type (inside the
 // decode step its nontemporal read leaves the KV cache in the caches).
-// Tall Q4_0X4 measured within noise of the register strip kernel (35.6 -
-// 37.6 vs 36.3 us at 151936x2048; 49152x2048 slower, 14.2 vs 13.2 us) and
-// keeps it; one-batch launches gain nothing from staging (C1 6144x2048:
-// 4.8 vs 3.5 us).
+// One-batch launches gain nothing from staging (C1 6144x2048: 4.8 vs
+// 3.5 us).
 template <uint32_t QT>
 static bool lds_tall_ok(const GemvArgs& a) {
   return ZG_LDS_TALL && a.nseg == 1 && a.k == 2048 && a.total_groups >= ZG_TALL_MIN_GROUPS &&
-         (QT == Q8_0 || ZG_LDS_TALL_Q4 || (a.flags & kGemvStream));
+         (QT == Q8_0 || (ZG_LDS_TALL_Q4 && a.total_groups >= ZG_LDS_Q4_MIN_GROUPS) || (a.flags & kGemvStream));
 }
 
 template <uint32_t QT, int PRO, int EPI, bool STREAM>
