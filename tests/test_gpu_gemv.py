@@ -114,7 +114,8 @@ GEMV_CASES = [
     (Q8_0, 4, 32768, 512),   # tall Q8_0X4 (LM-head strip path): one strip, four waves per strip
     (Q8_0, 4, 33000, 1024),  # tall strip path, last batch of two groups
     (Q8_0, 4, 32772, 4096),  # tall but in_dim above 2048: segment kernel, last group alone
-    (Q4_0, 4, 151936, 2048), # tall Q4_0X4: four groups per batch, batches looped over
+    (Q4_0, 4, 151936, 2048), # tall Q4_0X4: the LDS-staged kernel, four groups per batch
+    (Q4_0, 4, 49152, 2048),  # tall Q4_0X4 below the staging threshold: strip kernel batch loop
     (Q4_0, 4, 8320, 4096),   # tall at eight strips: 512-thread workgroups under a 512-thread bound
     (Q4_0, 4, 8208, 6144),   # tall at twelve strips: the fp32 form under the 1024-thread bound
     (Q8_0, 4, 32776, 2048),  # tall Q8_0X4 at in_dim 2048: LDS-staged kernel, last batch of two groups
@@ -251,11 +252,12 @@ def _edge_activations(rng, k, kind):
 
 
 @pytest.mark.parametrize("kind", ["finite", "inf", "nan"])
-@pytest.mark.parametrize("quant,rows,k", [(Q4_0, 12288, 2048), (Q4_0, 32768, 2048), (Q8_0, 32768, 2048)])
+@pytest.mark.parametrize("quant,rows,k", [(Q4_0, 12288, 2048), (Q4_0, 98304, 2048), (Q8_0, 32768, 2048)])
 def test_tall_integer_activation_edges(ctx, zo, quant, rows, k, kind):
     """Tall X4 launches take the activations as exact integers (three int8
     digits per value, int32 dot chains): the register strip kernel's batch
-    loop (12288 rows) and the LDS-staged kernel (32768 rows).  Finite edge
+    loop (12288 rows) and the LDS-staged kernel (98304 Q4_0 rows, 32768
+    Q8_0 rows).  Finite edge
     blocks stay within the parity bar and as close to f64 as the oracle
     (x 4); non-finite inputs give non-finite rows exactly where the
     oracle's do."""
