@@ -880,6 +880,9 @@ constexpr int lds_groups() {
 #ifndef ZG_LDS_Q4_MIN_GROUPS
 #define ZG_LDS_Q4_MIN_GROUPS 24576
 #endif
+// The LDS-staged kernel streams with nontemporal loads also outside the
+// decode step (cache-allocating: the LM head 60.9 against 54.8 us,
+// 151936x2048 Q4_0X4 32.6 against 30.9 us).
 // The LDS-staged kernel takes tall Q8_0X4 single projections at in_dim 2048
 // (the LM head: 58.8 us against 64.2 us for the register strip kernel's
 // cache-allocating loads and 77 us for its nontemporal ones), the tallest
