@@ -20,9 +20,9 @@
  * library applies to the same shape, so an entry launched as planned gives
  * the library's bits.  The module carries the strip kernel's forms only:
  * where the library takes another kernel for a shape (its LDS-staged tall
- * Q8_0X4 launch at in_dim 2048, its segment kernel for mid-sized Q8_0X4 at
- * in_dim above 2048) the planned strip form gives results within the same
- * tolerance, not the same bits.
+ * launch at in_dim 2048: Q8_0X4, and Q4_0X4 of at least 24,576 groups; its
+ * segment kernel for mid-sized Q8_0X4 at in_dim above 2048) the planned
+ * strip form gives results within the same tolerance, not the same bits.
  *
  * Pure host code: nothing here calls HIP.
  */

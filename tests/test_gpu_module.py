@@ -50,6 +50,7 @@ CASES = [
     (Q4_0, 4096, 3072, True),     # oneb_g2 (six strips)
     (Q4_0, 6144, 3072, True),     # oneb_g3
     (Q4_0, 49152, 2048, True),    # tall_t256
+    (Q4_0, 151936, 2048, False),  # tall_t256 (the library takes its LDS-staged kernel)
     (Q4_0, 16384, 4096, True),    # tall_t512
     (Q4_0, 32768, 6144, True),    # tall_t1024
     (Q8_0, 4096, 2048, True),     # q8 oneb_g2_k2048 (fused-QKV size)
