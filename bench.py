@@ -236,8 +236,9 @@ def bench_rows(ctx, steps: int, cpu=None):
             out[key]["cpu_baseline"] = cpu.gemv(name, wh, xk_host, k, rows, synth.Q4_0, 1,
                                                 wh.nbytes + 4 * k + 4 * rows)
 
-    # the headline kernel on taller Q4_0X4 matrices (8x the headline rows, and
-    # the LM head's height): the same strip GEMV with more bytes per launch
+    # the headline GEMV on taller Q4_0X4 matrices (8x the headline rows, and
+    # the LM head's height) with more bytes per launch: the strip kernel's
+    # batch loop at 49152 rows, the LDS-staged streaming kernel at 151936
     for name, key, rows in (("Q4_0X4 49152x2048 (8x the headline rows)", "q4_0x4_49152x2048", 49152),
                             ("Q4_0X4 151936x2048 (LM-head height)", "q4_0x4_151936x2048", 151_936)):
         wh = synth.weight(rng, synth.Q4_0, rows, H, 4)
