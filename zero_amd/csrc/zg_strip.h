@@ -62,7 +62,9 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* qs, const float4* 
 }
 
 // Q8_0 block sum with the int8 quants read as unsigned bytes (q ^ 0x80 =
-// q + 128); the caller subtracts 128 * sum(x).
+// q + 128); the caller subtracts 128 * sum(x).  (Converting them as
+// sign-extended bytes, v_cvt_f32_i32 with an SDWA byte select, and dropping
+// the offset term measured slower: fused Q|K|V Q8_0X4 4.01 against 3.87 us.)
 __device__ __forceinline__ float q8u_block_dot(const uint32_t* qs, const float4* xb) {
   float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
